@@ -1,0 +1,94 @@
+"""Builds the native libraries in-tree.
+
+  ai_amd/_lib/libfa_rocm.so   HIP kernels + C ABI (include/fa_rocm.h), gfx950
+  ai_amd/_lib/libfa_synth.so  seeded synthetic inputs (include/fa_synth.h), host only
+
+Compiles every source on every call (the driver's "does it build" check).
+Usage: python -m ai_amd.build [-v]
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "ai_amd")
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "_lib")
+BUILD = os.path.join(ROOT, "_build")
+INCLUDE = os.path.join(ROOT, "include")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# Packed-FP32 instructions are disabled for device code (they are generated
+# from ordinary float code at -O3 otherwise).
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", INCLUDE, "-I", CSRC,
+]
+
+ROCM_SOURCES = ["context.cpp", "model.cpp", "gemm.hip", "rowops.hip", "attention.hip", "score.hip"]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def build_rocm(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(LIB, exist_ok=True)
+    objs = []
+    jobs = []
+    for src in ROCM_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".", "_") + ".o")
+        objs.append(obj)
+        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        jobs.append([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+    workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        for f in [ex.submit(_run, j, verbose) for j in jobs]:
+            f.result()
+    out = os.path.join(LIB, "libfa_rocm.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def build_synth(verbose: bool = False) -> str:
+    os.makedirs(LIB, exist_ok=True)
+    out = os.path.join(LIB, "libfa_synth.so")
+    tmp = out + ".tmp"
+    cxx = shutil.which("g++") or "g++"
+    _run([cxx, "-O3", "-std=c++17", "-fPIC", "-fopenmp", "-shared", "-Wall", "-I", INCLUDE,
+          os.path.join(CSRC, "synth.cpp"), "-o", tmp], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def build_oracle(verbose: bool = False) -> None:
+    """The CPU oracle is test infrastructure; it is built beside the product."""
+    _run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle"), "-j2"], verbose)
+
+
+def build_all(verbose: bool = False) -> None:
+    build_synth(verbose)
+    build_rocm(verbose)
+    build_oracle(verbose)
+
+
+if __name__ == "__main__":
+    build_all(verbose="-v" in sys.argv)
+    print("built", os.listdir(LIB))

@@ -1,0 +1,372 @@
+// Context, errors, device buffers and the tensor-level C-ABI entry points
+// (host pointers in, host pointers out).
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "fa_internal.h"
+
+namespace fa {
+
+namespace {
+thread_local std::string tls_error;
+}
+
+int set_error(fa_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->last_error = buf;
+  tls_error = buf;
+  return code;
+}
+
+int DevBuf::ensure(fa_ctx* ctx, size_t need) {
+  if (need <= bytes && ptr) return FA_OK;
+  if (ptr) {
+    hipError_t e = hipStreamSynchronize(ctx->stream);  // in-flight work may still read it
+    if (e != hipSuccess) return set_error(ctx, FA_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  size_t sz = need < 256 ? 256 : need;
+  sz = (sz + 255) & ~size_t(255);
+  hipError_t e = hipMalloc(&ptr, sz);
+  if (e != hipSuccess) {
+    ptr = nullptr;
+    return set_error(ctx, FA_ERR_OOM, "hipMalloc(%zu): %s", sz, hipGetErrorString(e));
+  }
+  bytes = sz;
+  return FA_OK;
+}
+
+void DevBuf::release() {
+  if (ptr) (void)hipFree(ptr);
+  ptr = nullptr;
+  bytes = 0;
+}
+
+int stage_h2d(fa_ctx* ctx, size_t slot, const void* src, size_t bytes, void** out) {
+  DevBuf& b = ctx->slot(slot);
+  int rc = b.ensure(ctx, bytes);
+  if (rc) return rc;
+  if (bytes) FA_HIP_CHECK(ctx, hipMemcpyAsync(b.ptr, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  *out = b.ptr;
+  return FA_OK;
+}
+
+// float64 angle tables rounded to float32 (tensor/rope.go:36-50).
+void rope_tables_host(double base, const int32_t* positions, int T, int D, std::vector<float>& cs,
+                      std::vector<float>& sn) {
+  const int half = D / 2;
+  std::vector<double> inv(half);
+  for (int i = 0; i < half; i++) inv[i] = std::pow(base, -(double)(2 * i) / (double)D);
+  cs.resize((size_t)T * half);
+  sn.resize((size_t)T * half);
+  for (int t = 0; t < T; t++) {
+    const double p = (double)positions[t];
+    for (int i = 0; i < half; i++) {
+      const double a = p * inv[i];
+      cs[(size_t)t * half + i] = (float)std::cos(a);
+      sn[(size_t)t * half + i] = (float)std::sin(a);
+    }
+  }
+}
+
+}  // namespace fa
+
+using fa::set_error;
+
+// Scratch slots used by the host-pointer entry points.
+enum { S_A = 0, S_B, S_C, S_BIAS, S_ROWSCALE, S_MUL, S_RES, S_X, S_G, S_OUT, S_COS, S_SIN, S_Q, S_K, S_V, S_MASK };
+
+extern "C" {
+
+const char* fa_version(void) { return "fa_rocm 0.1 gfx950"; }
+
+int fa_create(int device, fa_ctx** out) {
+  if (!out) return set_error(nullptr, FA_ERR_ARG, "fa_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return set_error(nullptr, FA_ERR_HIP, "hipGetDeviceCount: %s", hipGetErrorString(e));
+  if (device < 0 || device >= n)
+    return set_error(nullptr, FA_ERR_ARG, "fa_create: device %d outside 0..%d", device, n - 1);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return set_error(nullptr, FA_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
+  fa_ctx* c = new fa_ctx();
+  c->device = device;
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return set_error(nullptr, FA_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->cu_count = prop.multiProcessorCount;
+  *out = c;
+  return FA_OK;
+}
+
+void fa_destroy(fa_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (auto& b : ctx->scratch) b.release();
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char* fa_last_error(const fa_ctx* ctx) {
+  if (ctx) return ctx->last_error.c_str();
+  return fa::tls_error.c_str();
+}
+
+void* fa_stream(fa_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int fa_sync(fa_ctx* ctx) {
+  if (!ctx) return set_error(nullptr, FA_ERR_ARG, "fa_sync: ctx is NULL");
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_device_alloc(fa_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return set_error(ctx, FA_ERR_ARG, "fa_device_alloc: NULL argument");
+  hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+  if (e != hipSuccess) return set_error(ctx, FA_ERR_OOM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  return FA_OK;
+}
+
+int fa_device_free(fa_ctx* ctx, void* ptr) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "fa_device_free: ctx is NULL");
+  if (!ptr) return FA_OK;
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  FA_HIP_CHECK(ctx, hipFree(ptr));
+  return FA_OK;
+}
+
+int fa_memcpy_h2d(fa_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "fa_memcpy_h2d: ctx is NULL");
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_memcpy_d2h(fa_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "fa_memcpy_d2h: ctx is NULL");
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
+                    int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "MatMulFused: ctx is NULL");
+  if (m < 0 || n < 0 || k < 0)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: negative size [%lld x %lld] . [%lld x %lld]", (long long)m,
+                     (long long)k, (long long)k, (long long)n);
+  if (b_dtype != FA_DT_F32 && b_dtype != FA_DT_BF16)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown B dtype %d", b_dtype);
+  if (b_layout != FA_B_KN && b_layout != FA_B_NK)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown B layout %d", b_layout);
+  if (lda < (k > 0 ? k : 1) && m > 0)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: lda %lld < k %lld", (long long)lda, (long long)k);
+  const int64_t brow = b_layout == FA_B_KN ? n : k, bcnt = b_layout == FA_B_KN ? k : n;
+  if (ldb < brow && bcnt > 0)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: ldb %lld too small", (long long)ldb);
+  if (ldc < n && m > 0) return set_error(ctx, FA_ERR_ARG, "MatMulFused: ldc %lld < n %lld", (long long)ldc, (long long)n);
+  if (e && e->act != FA_ACT_NONE && e->act != FA_ACT_RELU && e->act != FA_ACT_GELU)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown activation %d", e->act);
+  if (e && e->mul && e->ldm < n) return set_error(ctx, FA_ERR_ARG, "MatMulFused: Mul leading dimension < n");
+  if (e && e->residual && e->ldr < n)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: Residual leading dimension < n");
+  if (m == 0 || n == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  const size_t esz = b_dtype == FA_DT_BF16 ? 2 : 4;
+  void *da = nullptr, *db = nullptr, *dc = nullptr;
+  int rc;
+  const size_t abytes = (size_t)((m - 1) * lda + k) * 4;
+  const size_t bbytes = bcnt > 0 ? (size_t)((bcnt - 1) * ldb + brow) * esz : 0;
+  const size_t cbytes = (size_t)((m - 1) * ldc + n) * 4;
+  if ((rc = fa::stage_h2d(ctx, S_A, a, k > 0 ? abytes : 0, &da))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_B, b, bbytes, &db))) return rc;
+  if ((rc = ctx->slot(S_C).ensure(ctx, cbytes))) return rc;
+  dc = ctx->slot(S_C).ptr;
+  fa::GemmArgs g;
+  g.m = m; g.n = n; g.k = k;
+  g.a = (const float*)da; g.lda = lda; g.b = db; g.ldb = ldb; g.b_dtype = b_dtype; g.b_layout = b_layout;
+  g.c = (float*)dc; g.ldc = ldc;
+  g.epi = fa::Epi::None;
+  if (e && (e->bias || e->row_scale || e->act != FA_ACT_NONE || e->mul || e->residual)) {
+    g.epi = fa::Epi::Generic;
+    void* p;
+    if (e->bias) { if ((rc = fa::stage_h2d(ctx, S_BIAS, e->bias, (size_t)n * 4, &p))) return rc; g.bias = (const float*)p; }
+    if (e->row_scale) { if ((rc = fa::stage_h2d(ctx, S_ROWSCALE, e->row_scale, (size_t)m * 4, &p))) return rc; g.row_scale = (const float*)p; }
+    if (e->mul) { if ((rc = fa::stage_h2d(ctx, S_MUL, e->mul, (size_t)((m - 1) * e->ldm + n) * 4, &p))) return rc; g.mul = (const float*)p; g.ldm = e->ldm; }
+    if (e->residual) { if ((rc = fa::stage_h2d(ctx, S_RES, e->residual, (size_t)((m - 1) * e->ldr + n) * 4, &p))) return rc; g.residual = (const float*)p; g.ldr = e->ldr; }
+    g.act = e->act;
+  }
+  if (ldc != n) {
+    // rows of C with gaps: keep the caller's bytes between rows
+    FA_HIP_CHECK(ctx, hipMemcpyAsync(dc, c, cbytes, hipMemcpyHostToDevice, ctx->stream));
+  }
+  if ((rc = fa::launch_gemm(ctx, g, ctx->stream))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(c, dc, cbytes, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "RowSumSquares: ctx is NULL");
+  if (m < 0 || n < 0) return set_error(ctx, FA_ERR_ARG, "RowSumSquares: negative shape");
+  if (m == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  void *dx, *dout;
+  int rc;
+  if ((rc = fa::stage_h2d(ctx, S_X, x, (size_t)(m * n) * 4, &dx))) return rc;
+  if ((rc = ctx->slot(S_OUT).ensure(ctx, (size_t)m * 4))) return rc;
+  dout = ctx->slot(S_OUT).ptr;
+  if ((rc = fa::launch_row_sum_squares(ctx, (const float*)dx, m, n, (float*)dout, ctx->stream))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(out, dout, (size_t)m * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64_t rows, int64_t n, float* out) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "RMSNorm: ctx is NULL");
+  if (n <= 0) return set_error(ctx, FA_ERR_ARG, "RMSNorm: expected at least a 1-D input");
+  if (rows < 0) return set_error(ctx, FA_ERR_ARG, "RMSNorm: negative row count");
+  if (!g) return set_error(ctx, FA_ERR_ARG, "RMSNorm: g must have %lld elements", (long long)n);
+  if (rows == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  void *dx, *dg, *dout;
+  int rc;
+  if ((rc = fa::stage_h2d(ctx, S_X, x, (size_t)(rows * n) * 4, &dx))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_G, g, (size_t)n * 4, &dg))) return rc;
+  if ((rc = ctx->slot(S_OUT).ensure(ctx, (size_t)(rows * n) * 4))) return rc;
+  dout = ctx->slot(S_OUT).ptr;
+  if ((rc = fa::launch_rmsnorm(ctx, (const float*)dx, (const float*)dg, eps, rows, n, (float*)dout, ctx->stream)))
+    return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(out, dout, (size_t)(rows * n) * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_rope(fa_ctx* ctx, const float* x, double base, const int32_t* positions, int64_t rows, int32_t T, int32_t D,
+            float* out) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "RoPE: ctx is NULL");
+  if (D <= 0 || T <= 0 || rows < 0) return set_error(ctx, FA_ERR_ARG, "RoPE: expected at least a 2-D input");
+  if (D % 2 != 0) return set_error(ctx, FA_ERR_ARG, "RoPE: head dimension %d must be even", D);
+  if (rows % T != 0) return set_error(ctx, FA_ERR_ARG, "RoPE: %lld rows are not a multiple of T=%d", (long long)rows, T);
+  if (!positions) return set_error(ctx, FA_ERR_ARG, "RoPE: got 0 positions for %d slots", T);
+  if (rows == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  std::vector<float> cs, sn;
+  fa::rope_tables_host(base, positions, T, D, cs, sn);
+  void *dx, *dc, *ds, *dout;
+  int rc;
+  if ((rc = fa::stage_h2d(ctx, S_X, x, (size_t)(rows * D) * 4, &dx))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_COS, cs.data(), cs.size() * 4, &dc))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_SIN, sn.data(), sn.size() * 4, &ds))) return rc;
+  if ((rc = ctx->slot(S_OUT).ensure(ctx, (size_t)(rows * D) * 4))) return rc;
+  dout = ctx->slot(S_OUT).ptr;
+  if ((rc = fa::launch_rope(ctx, (const float*)dx, (const float*)dc, (const float*)ds, rows, T, D, (float*)dout,
+                            ctx->stream)))
+    return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(out, dout, (size_t)(rows * D) * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));  // also keeps cs/sn alive until the copies ran
+  return FA_OK;
+}
+
+// Bytes spanned by a strided [B, H, R, C] operand with unit stride on C.
+static size_t span4(int32_t B, int32_t H, int32_t R, int32_t C, int64_t sb, int64_t sh, int64_t sr, int64_t sc) {
+  if (B == 0 || H == 0 || R == 0 || C == 0) return 0;
+  int64_t last = (B - 1) * sb + (H - 1) * sh + (int64_t)(R - 1) * sr + (int64_t)(C - 1) * sc;
+  return (size_t)(last + 1) * 4;
+}
+
+int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, int32_t B, int32_t H, int32_t T,
+                 int32_t S, int32_t D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t v_sb,
+                 int64_t v_sh, const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_sr, int64_t m_sc, float scale,
+                 float* out) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "Attention: ctx is NULL");
+  if (B < 0 || H < 0 || T < 0 || S < 0 || D < 0)
+    return set_error(ctx, FA_ERR_ARG, "Attention: negative shape");
+  if (q_sb < 0 || q_sh < 0 || k_sb < 0 || k_sh < 0 || v_sb < 0 || v_sh < 0 || m_sb < 0 || m_sh < 0 || m_sr < 0 ||
+      m_sc < 0)
+    return set_error(ctx, FA_ERR_ARG, "Attention: negative stride");
+  if ((int64_t)B * H * T == 0 || D == 0) return FA_OK;
+  if (S == 0) return set_error(ctx, FA_ERR_ARG, "Attention: no keys (S = 0)");
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  void *dq, *dk, *dv, *dm = nullptr, *dout;
+  int rc;
+  if ((rc = fa::stage_h2d(ctx, S_Q, q, span4(B, H, T, D, q_sb, q_sh, D, 1), &dq))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_K, k, span4(B, H, S, D, k_sb, k_sh, D, 1), &dk))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_V, v, span4(B, H, S, D, v_sb, v_sh, D, 1), &dv))) return rc;
+  if (mask && (rc = fa::stage_h2d(ctx, S_MASK, mask, span4(B, H, T, S, m_sb, m_sh, m_sr, m_sc), &dm))) return rc;
+  const size_t obytes = (size_t)B * H * T * D * 4;
+  if ((rc = ctx->slot(S_OUT).ensure(ctx, obytes))) return rc;
+  dout = ctx->slot(S_OUT).ptr;
+  fa::AttnGenericArgs a;
+  a.q = (const float*)dq; a.k = (const float*)dk; a.v = (const float*)dv; a.mask = (const float*)dm;
+  a.B = B; a.H = H; a.T = T; a.S = S; a.D = D;
+  a.q_sb = q_sb; a.q_sh = q_sh; a.k_sb = k_sb; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sh = v_sh;
+  a.m_sb = m_sb; a.m_sh = m_sh; a.m_sr = m_sr; a.m_sc = m_sc;
+  a.scale = scale;
+  a.out = (float*)dout;
+  if ((rc = fa::launch_attention_generic(ctx, a, ctx->stream))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(out, dout, obytes, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
+                             int32_t topk, int32_t* idx, float* val) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "Similarities: ctx is NULL");
+  if (nq < 0 || nd <= 0 || d <= 0)
+    return set_error(ctx, FA_ERR_ARG, "Similarities: shapes [%lld x %d] and [%lld x %d]", (long long)nq, d,
+                     (long long)nd, d);
+  if (topk < 1 || topk > 32 || topk > nd)
+    return set_error(ctx, FA_ERR_ARG, "Similarities top-k: k=%d outside 1..min(32, %lld)", topk, (long long)nd);
+  if (nq == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  int rc;
+  fa::DevBuf& sc = ctx->slot(S_C);
+  if ((rc = sc.ensure(ctx, (size_t)(nq * nd) * 4))) return rc;
+  fa::GemmArgs g;
+  g.m = nq; g.n = nd; g.k = d;
+  g.a = queries; g.lda = d; g.b = docs; g.ldb = d; g.b_dtype = FA_DT_F32; g.b_layout = FA_B_NK;
+  g.c = sc.as<float>(); g.ldc = nd;
+  if ((rc = fa::launch_gemm(ctx, g, ctx->stream))) return rc;
+  return fa::launch_topk(ctx, sc.as<float>(), nq, nd, topk, idx, val, ctx->stream);
+}
+
+int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
+                         int32_t topk, int32_t* idx, float* val) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "Similarities: ctx is NULL");
+  if (nq < 0 || nd <= 0 || d <= 0)
+    return set_error(ctx, FA_ERR_ARG, "Similarities: shapes [%lld x %d] and [%lld x %d]", (long long)nq, d,
+                     (long long)nd, d);
+  if (topk < 1 || topk > 32 || topk > nd)
+    return set_error(ctx, FA_ERR_ARG, "Similarities top-k: k=%d outside 1..min(32, %lld)", topk, (long long)nd);
+  if (nq == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  void *dq, *dd;
+  int rc;
+  if ((rc = fa::stage_h2d(ctx, S_Q, queries, (size_t)(nq * d) * 4, &dq))) return rc;
+  if ((rc = fa::stage_h2d(ctx, S_K, docs, (size_t)(nd * d) * 4, &dd))) return rc;
+  const size_t ib = (size_t)nq * topk * 4;
+  if ((rc = ctx->slot(S_OUT).ensure(ctx, 2 * ib))) return rc;
+  int32_t* di = ctx->slot(S_OUT).as<int32_t>();
+  float* dv = (float*)((char*)ctx->slot(S_OUT).ptr + ib);
+  if ((rc = fa_similarities_topk_dev(ctx, (const float*)dq, nq, (const float*)dd, nd, d, topk, di, dv))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(idx, di, ib, hipMemcpyDeviceToHost, ctx->stream));
+  if (val) FA_HIP_CHECK(ctx, hipMemcpyAsync(val, dv, ib, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+}  // extern "C"

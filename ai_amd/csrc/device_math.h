@@ -1,0 +1,69 @@
+// Device-side math shared by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace fa {
+
+// tanh as the reference computes it (internal/kernel/generic.go:313-359):
+// identity below |x| < 4e-4, +-1 from |x| >= 9, otherwise an odd degree-13
+// over even degree-6 rational after clamping to +-7.99881172180175781 (the
+// published Eigen float approximation).
+__device__ __forceinline__ float tanh_ref(float v) {
+  if (v > -0.0004f && v < 0.0004f) return v;
+  if (v >= 9.f) return 1.f;
+  if (v <= -9.f) return -1.f;
+  v = fminf(fmaxf(v, -7.99881172180175781f), 7.99881172180175781f);
+  const float v2 = v * v;
+  float p = -2.76076847742355e-16f;
+  p = fmaf(p, v2, 2.00018790482477e-13f);
+  p = fmaf(p, v2, -8.60467152213735e-11f);
+  p = fmaf(p, v2, 5.12229709037114e-08f);
+  p = fmaf(p, v2, 1.48572235717979e-05f);
+  p = fmaf(p, v2, 6.37261928875436e-04f);
+  p = fmaf(p, v2, 4.89352455891786e-03f);
+  p *= v;
+  float q = 1.19825839466702e-06f;
+  q = fmaf(q, v2, 1.18534705686654e-04f);
+  q = fmaf(q, v2, 2.26843463243900e-03f);
+  q = fmaf(q, v2, 4.89352518554385e-03f);
+  return p / q;
+}
+
+// tanh-GELU, 0.5*x*(1 + tanh(sqrt(2/pi)*(x + 0.044715*x^3)))
+// (internal/kernel/math.go:117-143).
+__device__ __forceinline__ float gelu_tanh_ref(float x) {
+  float u = x * x * x * 0.044715f + x;
+  u *= 0.7978845608028654f;
+  return (tanh_ref(u) + 1.f) * x * 0.5f;
+}
+
+// exp with the reference's flush: inputs below -87 give exactly 0
+// (internal/kernel/generic.go:278-307), so masked softmax weights are exact
+// zeros. Computed as 2^(x*log2 e) on the hardware exp2.
+__device__ __forceinline__ float exp_flush(float x) {
+  return x < -87.f ? 0.f : exp2f(x * 1.4426950408889634f);
+}
+
+// Sum over the 64 lanes of a wavefront (result in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// 1/sqrt(ss/n + eps) with the quotient in float32 and the square root and
+// reciprocal in float64, rounded to float32 (models/gemma/embed.go:432-438,
+// tensor/attention.go:328).
+__device__ __forceinline__ float rms_inv(float ss, int n, float eps) {
+  float t = ss / (float)n + eps;
+  return (float)(1.0 / sqrt((double)t));
+}
+
+}  // namespace fa

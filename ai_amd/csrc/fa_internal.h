@@ -1,0 +1,177 @@
+// Internal declarations shared by the translation units of libfa_rocm.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "fa_rocm.h"
+
+namespace fa {
+
+// ---- errors ----------------------------------------------------------------
+
+struct Status {
+  int code = FA_OK;
+  std::string msg;
+};
+
+// Records msg as the last error of ctx (or of the thread when ctx is null)
+// and returns code.
+int set_error(fa_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+
+#define FA_HIP_CHECK(ctx, expr)                                                                        \
+  do {                                                                                                 \
+    hipError_t _e = (expr);                                                                            \
+    if (_e != hipSuccess)                                                                              \
+      return ::fa::set_error((ctx), FA_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__, \
+                             __LINE__);                                                                \
+  } while (0)
+
+#define FA_CHECK_LAUNCH(ctx) FA_HIP_CHECK(ctx, hipGetLastError())
+
+// ---- scratch arena ---------------------------------------------------------
+
+// A device buffer that only grows. Used for the copies of host operands in
+// the drop-in entry points and for the model's activations.
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  int ensure(fa_ctx* ctx, size_t need);
+  void release();
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
+}  // namespace fa
+
+struct fa_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  std::vector<fa::DevBuf> scratch;  // per-slot scratch for host-pointer entry points
+  int cu_count = 0;
+  fa::DevBuf& slot(size_t i) {
+    if (scratch.size() <= i) scratch.resize(i + 1);
+    return scratch[i];
+  }
+};
+
+namespace fa {
+
+// Copies host data into scratch slot `slot` (grown as needed) and returns
+// the device pointer via *out.
+int stage_h2d(fa_ctx* ctx, size_t slot, const void* src, size_t bytes, void** out);
+
+// float64 RoPE angle tables rounded to float32, [T, D/2] each (tensor/rope.go:36-50).
+void rope_tables_host(double base, const int32_t* positions, int T, int D, std::vector<float>& cs,
+                      std::vector<float>& sn);
+
+// ---- kernels (launchers) -----------------------------------------------------
+
+enum class Epi { None = 0, Generic = 1, GeGLU = 2 };
+
+struct GemmArgs {
+  int64_t m = 0, n = 0, k = 0;
+  const float* a = nullptr;
+  int64_t lda = 0;
+  const void* b = nullptr;  // bf16 or f32
+  int64_t ldb = 0;
+  int b_dtype = FA_DT_BF16;
+  int b_layout = FA_B_NK;
+  float* c = nullptr;
+  int64_t ldc = 0;
+  // Generic epilogue
+  const float* bias = nullptr;
+  const float* row_scale = nullptr;
+  int act = FA_ACT_NONE;
+  const float* mul = nullptr;
+  int64_t ldm = 0;
+  const float* residual = nullptr;
+  int64_t ldr = 0;
+  Epi epi = Epi::None;
+};
+
+// Launches C = epi(A . B) on stream. For Epi::GeGLU, B is the interleaved
+// gate/up weight [2F x K] (32-row groups alternating gate, up) and C is
+// [m x F] = gelu(gate) * up.
+int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t stream);
+
+int launch_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out, hipStream_t s);
+int launch_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64_t rows, int64_t n, float* out,
+                   hipStream_t s);
+int launch_rope(fa_ctx* ctx, const float* x, const float* cos_t, const float* sin_t, int64_t rows, int32_t T,
+                int32_t D, float* out, hipStream_t s);
+
+struct AttnGenericArgs {
+  const float *q, *k, *v, *mask;
+  int32_t B, H, T, S, D;
+  int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, m_sb, m_sh, m_sr, m_sc;
+  float scale;
+  float* out;
+};
+int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s);
+
+int launch_topk(fa_ctx* ctx, const float* scores, int64_t nq, int64_t nd, int32_t topk, int32_t* idx, float* val,
+                hipStream_t s);
+
+// ---- model-path kernels -------------------------------------------------------
+
+// For packed row r of sequence b at position t (cu_seqlens[b] <= r <
+// cu_seqlens[b+1], t = r - cu_seqlens[b]): row_src[r] = b*T + t, pos[r] = t.
+int launch_row_plan(fa_ctx* ctx, const int32_t* cu_seqlens, int32_t nseq, int32_t T, int64_t rows, int32_t* row_src,
+                    int32_t* pos, hipStream_t s);
+
+// Embedding gather of packed tokens: x[r] = E[ids_packed[r]] * scale and
+// xn[r] = x[r] * rms_inv(x[r]) * g (the first layer's input norm).
+int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_src, const uint16_t* E,
+                        int64_t vocab, int64_t rows, int32_t d, float scale, const float* g_next, float eps, float* x,
+                        float* xn, hipStream_t s);
+
+// q/k RMSNorm with (1+g) and RoPE on the packed qkv buffer [rows x (H+2*Hkv)*D],
+// in place; positions from d_pos.
+int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t Hkv, int32_t D, const float* gq,
+                       const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
+                       hipStream_t s);
+
+// x += RMSNorm(o; g_post); then xn = RMSNorm(x; g_next) (g_next may be null:
+// then xn is not written).
+int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
+                         const float* g_post, const float* g_next, float eps, hipStream_t s);
+
+// Fused varlen attention over packed tokens. qkv [rows x (H+2Hkv)*D]; out
+// [rows x H*D]; cu_seqlens [nseq+1]; window: keys with |i-j| >= window are
+// masked (window <= 0: none).
+struct AttnVarlenArgs {
+  const float* qkv;
+  float* out;
+  const int32_t* cu_seqlens;
+  int32_t nseq, max_len, H, Hkv, D;
+  int32_t window;
+  float scale;
+};
+// d_items holds n_items pairs (sequence, first query) of 64-query blocks.
+int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const int32_t* d_items, int32_t n_items,
+                                  hipStream_t s);
+// Queries per workgroup of the varlen kernel (the item granularity).
+int attention_varlen_qblock();
+
+// Masked mean pooling of the final normed hidden states over each
+// sequence's valid rows: pooled[b] = sum rows * (1/L_b).
+int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t nseq, int32_t d, float* pooled,
+                hipStream_t s);
+
+// out[b, :dim] = y[b, :dim] / sqrt(sum y^2 + 1e-12)
+int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int32_t dim, float* out, hipStream_t s);
+
+// Final RMSNorm with (1+g) of x rows into h.
+int launch_final_norm(fa_ctx* ctx, const float* x, int64_t rows, int32_t d, const float* g, float eps, float* h,
+                      hipStream_t s);
+
+}  // namespace fa

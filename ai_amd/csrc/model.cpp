@@ -1,0 +1,645 @@
+// The EmbeddingGemma encoder on one GPU: bf16-resident weights, packed
+// variable-length token rows, and the forward pass
+//   gather*sqrt(d) -> 24 x [qkv GEMM, qk-norm+RoPE, attention, o GEMM,
+//   post-norm+residual(+next pre-norm), gate|up GEMM with GeGLU epilogue,
+//   down GEMM, post-norm+residual(+next pre-norm)] -> mean pool -> Dense head
+//   -> L2
+// following models/gemma/embed.go:160-240,381-475 and model.go:76-232.
+//
+// Layout in HBM (M = sum of valid lengths; padding rows are never stored):
+//   x   [M, d] fp32   residual stream
+//   xn  [M, d] fp32   RMSNorm(x; 1+g) feeding the next product (the
+//                     reference folds 1+g into the weights and applies the
+//                     row scale in the product's epilogue, model.go:210-222,
+//                     embed.go:193-197; the values agree to rounding)
+//   qkv [M, (H+2Hkv)*D] fp32   q | k | v per token, normed and rotated in place
+//   att [M, H*D] fp32, o [M, d] fp32, gu [M, F] fp32
+// Weights: [out, in] bf16 as in the checkpoint; q|k|v stacked into one
+// [(H+2Hkv)*D, d] matrix, gate and up interleaved in 32-row groups into one
+// [2F, d] matrix (see gemm.hip), 1+w norm vectors in fp32.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "fa_internal.h"
+
+namespace fa {
+
+namespace {
+
+bool bf16_exact(float f, uint16_t* out) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if (u & 0xFFFFu) return false;
+  *out = (uint16_t)(u >> 16);
+  return true;
+}
+
+struct Layer {
+  uint16_t* wqkv = nullptr;   // [(H+2Hkv)*D, d]
+  uint16_t* wo = nullptr;     // [d, H*D]
+  uint16_t* wgu = nullptr;    // [2F, d], 32-row groups gate/up alternating
+  uint16_t* wdown = nullptr;  // [d, F]
+  float *g_in = nullptr, *g_post_attn = nullptr, *g_pre_ffn = nullptr, *g_post_ffn = nullptr;
+  float *g_q = nullptr, *g_k = nullptr;
+};
+
+struct KernelStat {
+  int64_t launches = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+
+struct PendingEvent {
+  hipEvent_t a, b;
+  int kind;
+  double flops, bytes;
+};
+
+}  // namespace
+}  // namespace fa
+
+struct fa_model {
+  fa_ctx* ctx = nullptr;
+  fa_gemma_config cfg{};
+  int width_qkv = 0;
+  std::vector<void*> allocations;
+  uint16_t* embed = nullptr;
+  std::vector<fa::Layer> layers;
+  float* g_final = nullptr;
+  std::vector<uint16_t*> dense;
+  std::vector<int> dense_in, dense_out;
+  float *cos_local = nullptr, *sin_local = nullptr, *cos_global = nullptr, *sin_global = nullptr;
+  std::set<std::string> seen;
+  bool finalized = false;
+  // workspace
+  fa::DevBuf ws, plan_dev;
+  int64_t ws_rows = 0, ws_seqs = 0;
+  int32_t* plan_host = nullptr;  // pinned
+  size_t plan_host_ints = 0;
+  hipEvent_t plan_done = nullptr;
+  bool plan_pending = false;
+  fa::DevBuf ids_dev, out_dev;
+  // profiling
+  bool profiling = false;
+  std::vector<hipEvent_t> event_pool;
+  std::vector<fa::PendingEvent> pending;
+  fa::KernelStat stats[FA_K_COUNT];
+};
+
+namespace fa {
+namespace {
+
+int alloc_dev(fa_model* m, size_t bytes, void** out) {
+  hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+  if (e != hipSuccess) return set_error(m->ctx, FA_ERR_OOM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  m->allocations.push_back(*out);
+  return FA_OK;
+}
+
+hipEvent_t take_event(fa_model* m) {
+  if (!m->event_pool.empty()) {
+    hipEvent_t e = m->event_pool.back();
+    m->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets one launch with events when profiling.
+struct Probe {
+  fa_model* m;
+  hipEvent_t a = nullptr;
+  int kind;
+  double flops, bytes;
+  Probe(fa_model* mm, int k, double f, double b) : m(mm), kind(k), flops(f), bytes(b) {
+    if (m->profiling) {
+      a = take_event(m);
+      if (a) (void)hipEventRecord(a, m->ctx->stream);
+    }
+  }
+  void done() {
+    if (!a) return;
+    hipEvent_t b = take_event(m);
+    if (!b) return;
+    (void)hipEventRecord(b, m->ctx->stream);
+    m->pending.push_back({a, b, kind, flops, bytes});
+    a = nullptr;
+  }
+};
+
+int collect_stats(fa_model* m) {
+  if (m->pending.empty()) return FA_OK;
+  FA_HIP_CHECK(m->ctx, hipStreamSynchronize(m->ctx->stream));
+  for (auto& p : m->pending) {
+    float ms = 0;
+    if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+      KernelStat& s = m->stats[p.kind];
+      s.launches++;
+      s.ms += ms;
+      s.flops += p.flops;
+      s.bytes += p.bytes;
+    }
+    m->event_pool.push_back(p.a);
+    m->event_pool.push_back(p.b);
+  }
+  m->pending.clear();
+  return FA_OK;
+}
+
+int parse_layer(const std::string& s, int nl, int* l, std::string* rest) {
+  if (s.rfind("layers.", 0) != 0) return -1;
+  size_t dot = s.find('.', 7);
+  if (dot == std::string::npos) return -1;
+  char* end = nullptr;
+  long v = std::strtol(s.c_str() + 7, &end, 10);
+  if (end != s.c_str() + dot || v < 0 || v >= nl) return -1;
+  *l = (int)v;
+  *rest = s.substr(dot + 1);
+  return 0;
+}
+
+}  // namespace
+}  // namespace fa
+
+using fa::set_error;
+
+extern "C" {
+
+int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
+  if (!ctx || !cfg || !out) return set_error(ctx, FA_ERR_ARG, "gemma: NULL argument");
+  *out = nullptr;
+  const fa_gemma_config& c = *cfg;
+  if (c.hidden_size <= 0 || c.num_hidden_layers <= 0 || c.num_attention_heads <= 0 || c.num_key_value_heads <= 0 ||
+      c.head_dim <= 0 || c.intermediate_size <= 0 || c.vocab_size <= 0)
+    return set_error(ctx, FA_ERR_ARG, "gemma: config sizes must be positive");
+  if (c.hidden_size % 256 != 0 || c.hidden_size > 1024)
+    return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden_size %d not in {256,512,768,1024}", c.hidden_size);
+  if (c.head_dim != 256) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d != 256", c.head_dim);
+  if (c.num_attention_heads % c.num_key_value_heads != 0)
+    return set_error(ctx, FA_ERR_ARG, "gemma: %d heads not a multiple of %d kv heads", c.num_attention_heads,
+                     c.num_key_value_heads);
+  if (c.intermediate_size % 32 != 0)
+    return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: intermediate_size %d not a multiple of 32", c.intermediate_size);
+  if (c.n_dense < 0 || c.n_dense > 4) return set_error(ctx, FA_ERR_ARG, "gemma: n_dense %d outside 0..4", c.n_dense);
+  if (c.max_tokens <= 0) return set_error(ctx, FA_ERR_ARG, "gemma: max_tokens must be positive");
+  if (c.query_pre_attn_scalar <= 0) return set_error(ctx, FA_ERR_ARG, "gemma: query_pre_attn_scalar must be > 0");
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  fa_model* m = new fa_model();
+  m->ctx = ctx;
+  m->cfg = c;
+  if (m->cfg.sliding_window_pattern <= 0) m->cfg.sliding_window_pattern = 6;
+  const int d = c.hidden_size, H = c.num_attention_heads, Hkv = c.num_key_value_heads, D = c.head_dim,
+            F = c.intermediate_size;
+  m->width_qkv = (H + 2 * Hkv) * D;
+  int rc = FA_OK;
+  void* p;
+  auto A = [&](size_t bytes) -> void* {
+    if (rc) return nullptr;
+    rc = fa::alloc_dev(m, bytes, &p);
+    return rc ? nullptr : p;
+  };
+  m->embed = (uint16_t*)A((size_t)c.vocab_size * d * 2);
+  m->layers.resize(c.num_hidden_layers);
+  for (auto& L : m->layers) {
+    L.wqkv = (uint16_t*)A((size_t)m->width_qkv * d * 2);
+    L.wo = (uint16_t*)A((size_t)d * H * D * 2);
+    L.wgu = (uint16_t*)A((size_t)2 * F * d * 2);
+    L.wdown = (uint16_t*)A((size_t)d * F * 2);
+    L.g_in = (float*)A(d * 4);
+    L.g_post_attn = (float*)A(d * 4);
+    L.g_pre_ffn = (float*)A(d * 4);
+    L.g_post_ffn = (float*)A(d * 4);
+    L.g_q = (float*)A(D * 4);
+    L.g_k = (float*)A(D * 4);
+  }
+  m->g_final = (float*)A(d * 4);
+  int in = d;
+  for (int i = 0; i < c.n_dense; i++) {
+    if (c.dense_out[i] <= 0) rc = set_error(ctx, FA_ERR_ARG, "gemma: dense_out[%d] = %d", i, c.dense_out[i]);
+    m->dense_in.push_back(in);
+    m->dense_out.push_back(c.dense_out[i]);
+    m->dense.push_back((uint16_t*)A((size_t)in * c.dense_out[i] * 2));
+    in = c.dense_out[i];
+  }
+  const size_t tab = (size_t)c.max_tokens * (D / 2) * 4;
+  m->cos_local = (float*)A(tab);
+  m->sin_local = (float*)A(tab);
+  m->cos_global = (float*)A(tab);
+  m->sin_global = (float*)A(tab);
+  if (!rc && hipEventCreateWithFlags(&m->plan_done, hipEventDisableTiming) != hipSuccess)
+    rc = set_error(ctx, FA_ERR_HIP, "hipEventCreate failed");
+  if (rc) {
+    fa_gemma_destroy(m);
+    return rc;
+  }
+  *out = m;
+  return FA_OK;
+}
+
+void fa_gemma_destroy(fa_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipStreamSynchronize(m->ctx->stream);
+  for (void* p : m->allocations) (void)hipFree(p);
+  m->ws.release();
+  m->plan_dev.release();
+  m->ids_dev.release();
+  m->out_dev.release();
+  if (m->plan_host) (void)hipHostFree(m->plan_host);
+  if (m->plan_done) (void)hipEventDestroy(m->plan_done);
+  for (auto& p : m->pending) {
+    m->event_pool.push_back(p.a);
+    m->event_pool.push_back(p.b);
+  }
+  for (hipEvent_t e : m->event_pool) (void)hipEventDestroy(e);
+  delete m;
+}
+
+int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t* shape, int32_t ndim,
+                        const void* data) {
+  if (!m || !name || !data || (ndim > 0 && !shape)) return set_error(m ? m->ctx : nullptr, FA_ERR_ARG, "gemma: NULL argument");
+  fa_ctx* ctx = m->ctx;
+  if (dtype != FA_DT_F32 && dtype != FA_DT_BF16) return set_error(ctx, FA_ERR_ARG, "gemma: weight %s: dtype %d", name, dtype);
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  const fa_gemma_config& c = m->cfg;
+  const int d = c.hidden_size, H = c.num_attention_heads, Hkv = c.num_key_value_heads, D = c.head_dim,
+            F = c.intermediate_size;
+  const std::string s(name);
+  auto shape_is = [&](std::initializer_list<int64_t> want) {
+    if ((size_t)ndim != want.size()) return false;
+    int i = 0;
+    for (int64_t w : want)
+      if (shape[i++] != w) return false;
+    return true;
+  };
+  auto shape_str = [&]() {
+    std::string r = "[";
+    for (int i = 0; i < ndim; i++) r += (i ? "," : "") + std::to_string(shape[i]);
+    return r + "]";
+  };
+  // matrix [rows, cols] -> bf16 rows at dst (row stride cols), with an
+  // optional row remap (dst row of source row r)
+  auto put_matrix = [&](uint16_t* dst, int64_t rows, int64_t cols, auto&& dst_row) -> int {
+    std::vector<uint16_t> tmp((size_t)rows * cols);
+    if (dtype == FA_DT_BF16) {
+      const uint16_t* src = (const uint16_t*)data;
+      for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[(size_t)dst_row(r) * cols], src + r * cols, cols * 2);
+    } else {
+      const float* src = (const float*)data;
+      for (int64_t r = 0; r < rows; r++)
+        for (int64_t k = 0; k < cols; k++)
+          if (!fa::bf16_exact(src[r * cols + k], &tmp[(size_t)dst_row(r) * cols + k]))
+            return set_error(ctx, FA_ERR_UNSUPPORTED,
+                             "gemma: weight %s is not exactly representable in bf16 (row %lld col %lld); this build "
+                             "keeps matrices bf16-resident",
+                             name, (long long)r, (long long)k);
+    }
+    FA_HIP_CHECK(ctx, hipMemcpy(dst, tmp.data(), tmp.size() * 2, hipMemcpyHostToDevice));
+    return FA_OK;
+  };
+  auto identity = [](int64_t r) { return r; };
+  auto put_norm = [&](float* dst, int64_t n) -> int {
+    std::vector<float> v(n);
+    for (int64_t i = 0; i < n; i++) {
+      float w;
+      if (dtype == FA_DT_BF16) {
+        uint32_t u = (uint32_t)((const uint16_t*)data)[i] << 16;
+        std::memcpy(&w, &u, 4);
+      } else {
+        w = ((const float*)data)[i];
+      }
+      v[i] = w + 1.0f;  // Gemma's (1 + w) (model.go:131-140)
+    }
+    FA_HIP_CHECK(ctx, hipMemcpy(dst, v.data(), n * 4, hipMemcpyHostToDevice));
+    return FA_OK;
+  };
+  int rc = FA_OK;
+  int l;
+  std::string rest;
+  if (s == "embed_tokens.weight") {
+    if (!shape_is({c.vocab_size, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+    rc = put_matrix(m->embed, c.vocab_size, d, identity);
+  } else if (s == "norm.weight") {
+    if (!shape_is({d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+    rc = put_norm(m->g_final, d);
+  } else if (s.rfind("dense.", 0) == 0 && s.size() > 6) {
+    char* end = nullptr;
+    long i = std::strtol(s.c_str() + 6, &end, 10);
+    if (i < 0 || i >= c.n_dense || std::string(end) != ".linear.weight")
+      return set_error(ctx, FA_ERR_ARG, "gemma: weight %q not found", name);
+    if (!shape_is({m->dense_out[i], m->dense_in[i]}))
+      return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+    rc = put_matrix(m->dense[i], m->dense_out[i], m->dense_in[i], identity);
+  } else if (fa::parse_layer(s, c.num_hidden_layers, &l, &rest) == 0) {
+    fa::Layer& L = m->layers[l];
+    if (rest == "input_layernorm.weight" || rest == "post_attention_layernorm.weight" ||
+        rest == "pre_feedforward_layernorm.weight" || rest == "post_feedforward_layernorm.weight") {
+      if (!shape_is({d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      float* dst = rest[0] == 'i' ? L.g_in : rest[1] == 'o' ? (rest[5] == 'a' ? L.g_post_attn : L.g_post_ffn) : L.g_pre_ffn;
+      rc = put_norm(dst, d);
+    } else if (rest == "self_attn.q_norm.weight" || rest == "self_attn.k_norm.weight") {
+      if (!shape_is({D})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_norm(rest[10] == 'q' ? L.g_q : L.g_k, D);
+    } else if (rest == "self_attn.q_proj.weight") {
+      if (!shape_is({H * D, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wqkv, H * D, d, identity);
+    } else if (rest == "self_attn.k_proj.weight") {
+      if (!shape_is({Hkv * D, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wqkv + (size_t)H * D * d, Hkv * D, d, identity);
+    } else if (rest == "self_attn.v_proj.weight") {
+      if (!shape_is({Hkv * D, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wqkv + (size_t)(H + Hkv) * D * d, Hkv * D, d, identity);
+    } else if (rest == "self_attn.o_proj.weight") {
+      if (!shape_is({d, H * D})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wo, d, H * D, identity);
+    } else if (rest == "mlp.gate_proj.weight" || rest == "mlp.up_proj.weight") {
+      if (!shape_is({F, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      const int64_t off = rest[4] == 'g' ? 0 : 32;  // gate rows first in each 64-row group, then up
+      rc = put_matrix(L.wgu, F, d, [off](int64_t r) { return (r / 32) * 64 + off + (r % 32); });
+    } else if (rest == "mlp.down_proj.weight") {
+      if (!shape_is({d, F})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wdown, d, F, identity);
+    } else {
+      return set_error(ctx, FA_ERR_ARG, "gemma: weight \"%s\" not found", name);
+    }
+  } else {
+    return set_error(ctx, FA_ERR_ARG, "gemma: weight \"%s\" not found", name);
+  }
+  if (rc) return rc;
+  m->seen.insert(s);
+  m->finalized = false;
+  return FA_OK;
+}
+
+int fa_gemma_finalize(fa_model* m) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  fa_ctx* ctx = m->ctx;
+  const fa_gemma_config& c = m->cfg;
+  const size_t expected = 2 + (size_t)c.n_dense + 13 * (size_t)c.num_hidden_layers;
+  if (m->seen.size() != expected)
+    return set_error(ctx, FA_ERR_STATE, "gemma: %zu of %zu weights set", m->seen.size(), expected);
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  std::vector<int32_t> pos(c.max_tokens);
+  for (int t = 0; t < c.max_tokens; t++) pos[t] = t;
+  std::vector<float> cs, sn;
+  const double local = c.rope_local_base_freq != 0 ? c.rope_local_base_freq : 10000.0;
+  const double global = c.rope_theta != 0 ? c.rope_theta : 10000.0;
+  fa::rope_tables_host(local, pos.data(), c.max_tokens, c.head_dim, cs, sn);
+  FA_HIP_CHECK(ctx, hipMemcpy(m->cos_local, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  FA_HIP_CHECK(ctx, hipMemcpy(m->sin_local, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  fa::rope_tables_host(global, pos.data(), c.max_tokens, c.head_dim, cs, sn);
+  FA_HIP_CHECK(ctx, hipMemcpy(m->cos_global, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  FA_HIP_CHECK(ctx, hipMemcpy(m->sin_global, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  m->finalized = true;
+  return FA_OK;
+}
+
+int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
+                           int32_t dim, float* d_out) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  fa_ctx* ctx = m->ctx;
+  const fa_gemma_config& c = m->cfg;
+  if (!m->finalized) return set_error(ctx, FA_ERR_STATE, "gemma: embed before every weight was set (finalize)");
+  if (B < 0 || T < 0) return set_error(ctx, FA_ERR_ARG, "gemma: negative batch shape [%d x %d]", B, T);
+  if (B == 0) return FA_OK;
+  if (!d_ids || !lengths || !d_out) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
+  if (T > c.max_tokens) return set_error(ctx, FA_ERR_ARG, "gemma: T=%d exceeds max_tokens %d", T, c.max_tokens);
+  const int d = c.hidden_size, H = c.num_attention_heads, Hkv = c.num_key_value_heads, D = c.head_dim,
+            F = c.intermediate_size;
+  const int full = c.n_dense > 0 ? m->dense_out.back() : d;
+  if (dim <= 0) dim = full;
+  if (dim > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
+  // ---- plan (host): cu_seqlens and attention work items ----
+  const int qblk = fa::attention_varlen_qblock();
+  int64_t M = 0, n_items = 0;
+  for (int b = 0; b < B; b++) {
+    if (lengths[b] < 1 || lengths[b] > T)
+      return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
+    M += lengths[b];
+    n_items += (lengths[b] + qblk - 1) / qblk;
+  }
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  const size_t plan_ints = (size_t)(B + 1) + 2 * (size_t)n_items;
+  if (m->plan_pending) {
+    FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
+    m->plan_pending = false;
+  }
+  if (plan_ints > m->plan_host_ints) {
+    if (m->plan_host) (void)hipHostFree(m->plan_host);
+    m->plan_host = nullptr;
+    size_t n = plan_ints * 2;
+    FA_HIP_CHECK(ctx, hipHostMalloc((void**)&m->plan_host, n * 4, hipHostMallocDefault));
+    m->plan_host_ints = n;
+  }
+  int32_t* cu_h = m->plan_host;
+  int32_t* items_h = m->plan_host + (B + 1);
+  cu_h[0] = 0;
+  int64_t it = 0;
+  for (int b = 0; b < B; b++) {
+    cu_h[b + 1] = cu_h[b] + lengths[b];
+    for (int q0 = 0; q0 < lengths[b]; q0 += qblk) {
+      items_h[2 * it] = b;
+      items_h[2 * it + 1] = q0;
+      it++;
+    }
+  }
+  int rc;
+  if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
+  int32_t* cu_d = m->plan_dev.as<int32_t>();
+  int32_t* items_d = cu_d + (B + 1);
+  int32_t* row_src_d = cu_d + plan_ints;   // [M] b*T + t
+  int32_t* pos_d = row_src_d + M;          // [M] t
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(cu_d, m->plan_host, plan_ints * 4, hipMemcpyHostToDevice, ctx->stream));
+  FA_HIP_CHECK(ctx, hipEventRecord(m->plan_done, ctx->stream));
+  m->plan_pending = true;
+  // ---- workspace ----
+  const int64_t ncols = 2LL * d + m->width_qkv + (int64_t)H * D + d + F;
+  const int maxw = std::max(d, std::max(full, c.n_dense > 0 ? *std::max_element(m->dense_out.begin(), m->dense_out.end()) : d));
+  const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw)) * 4 + 4096;
+  if ((rc = m->ws.ensure(ctx, ws_bytes))) return rc;
+  float* x = m->ws.as<float>();
+  float* xn = x + M * d;
+  float* qkv = xn + M * d;
+  float* att = qkv + M * m->width_qkv;
+  float* o = att + M * H * D;
+  float* gu = o + M * d;
+  float* pooled = gu + M * F;
+  float* hbuf0 = pooled + (size_t)B * d;
+  float* hbuf1 = hbuf0 + (size_t)B * maxw;
+  hipStream_t s = ctx->stream;
+  // ---- row plan on device ----
+  if ((rc = fa::launch_row_plan(ctx, cu_d, B, T, M, row_src_d, pos_d, s))) return rc;
+  const float eps = c.rms_norm_eps;
+  const float emb_scale = (float)std::sqrt((double)d);  // embed.go:176
+  const float att_scale = (float)(1.0 / std::sqrt(c.query_pre_attn_scalar));  // model.go:100
+  const int wbound = c.use_bidirectional ? c.sliding_window / 2 + 1 : c.sliding_window;  // config.go:331-339
+  {
+    fa::Probe pr(m, FA_K_GATHER, 0, (double)M * (2.0 * d + 8.0 * d + 4));
+    if ((rc = fa::launch_embed_gather(ctx, d_ids, row_src_d, m->embed, c.vocab_size, M, d, emb_scale,
+                                      m->layers[0].g_in, eps, x, xn, s)))
+      return rc;
+    pr.done();
+  }
+  for (int l = 0; l < c.num_hidden_layers; l++) {
+    const fa::Layer& L = m->layers[l];
+    const bool sliding = (l + 1) % m->cfg.sliding_window_pattern != 0;  // config.go:213-225
+    {
+      fa::GemmArgs g;
+      g.m = M; g.n = m->width_qkv; g.k = d; g.a = xn; g.lda = d; g.b = L.wqkv; g.ldb = d; g.c = qkv; g.ldc = m->width_qkv;
+      fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * M * m->width_qkv * d, 0);
+      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      pr.done();
+    }
+    {
+      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)M * (H + Hkv) * D * 8.0);
+      if ((rc = fa::launch_qknorm_rope(ctx, qkv, M, H, Hkv, D, L.g_q, L.g_k, eps, pos_d,
+                                       sliding ? m->cos_local : m->cos_global, sliding ? m->sin_local : m->sin_global,
+                                       s)))
+        return rc;
+      pr.done();
+    }
+    {
+      fa::AttnVarlenArgs a;
+      a.qkv = qkv; a.out = att; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
+      a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
+      a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
+      double pairs = 0;
+      for (int b = 0; b < B; b++) {
+        const double Lb = lengths[b];
+        if (a.window > 0 && Lb > a.window) {
+          // sum over i of |{j : |i-j| < w}| = L(2w-1) - w(w-1)
+          pairs += Lb * (2.0 * a.window - 1) - (double)a.window * (a.window - 1);
+        } else {
+          pairs += Lb * Lb;
+        }
+      }
+      fa::Probe pr(m, FA_K_ATTENTION, pairs * 4.0 * H * D, 0);
+      if ((rc = fa::launch_attention_varlen_items(ctx, a, items_d, (int32_t)n_items, s))) return rc;
+      pr.done();
+    }
+    {
+      fa::GemmArgs g;
+      g.m = M; g.n = d; g.k = H * D; g.a = att; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = o; g.ldc = d;
+      fa::Probe pr(m, FA_K_GEMM_O, 2.0 * M * d * H * D, 0);
+      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      pr.done();
+    }
+    {
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
+      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_attn, L.g_pre_ffn, eps, s))) return rc;
+      pr.done();
+    }
+    {
+      fa::GemmArgs g;
+      g.m = M; g.n = 2 * F; g.k = d; g.a = xn; g.lda = d; g.b = L.wgu; g.ldb = d; g.c = gu; g.ldc = F;
+      g.epi = fa::Epi::GeGLU;
+      fa::Probe pr(m, FA_K_GEMM_GATEUP, 2.0 * M * 2 * F * d, 0);
+      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      pr.done();
+    }
+    {
+      fa::GemmArgs g;
+      g.m = M; g.n = d; g.k = F; g.a = gu; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = o; g.ldc = d;
+      fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * M * d * F, 0);
+      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      pr.done();
+    }
+    {
+      // the last layer's "next norm" is the final RMSNorm (embed.go:237): xn = h
+      const float* g_next = (l + 1 < c.num_hidden_layers) ? m->layers[l + 1].g_in : m->g_final;
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
+      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_ffn, g_next, eps, s))) return rc;
+      pr.done();
+    }
+  }
+  {
+    fa::Probe pr(m, FA_K_POOL_L2, 0, (double)M * d * 4.0 + (double)B * d * 4.0);
+    if ((rc = fa::launch_pool(ctx, xn, cu_d, B, d, pooled, s))) return rc;
+    pr.done();
+  }
+  const float* cur = pooled;
+  int cur_w = d;
+  float* bufs[2] = {hbuf0, hbuf1};
+  for (int i = 0; i < c.n_dense; i++) {
+    fa::GemmArgs g;
+    g.m = B; g.n = m->dense_out[i]; g.k = cur_w; g.a = cur; g.lda = cur_w; g.b = m->dense[i]; g.ldb = cur_w;
+    g.c = bufs[i & 1]; g.ldc = m->dense_out[i];
+    fa::Probe pr(m, FA_K_GEMM_HEAD, 2.0 * B * m->dense_out[i] * cur_w, 0);
+    if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+    pr.done();
+    cur = bufs[i & 1];
+    cur_w = m->dense_out[i];
+  }
+  {
+    fa::Probe pr(m, FA_K_POOL_L2, 0, (double)B * dim * 8.0);
+    if ((rc = fa::launch_l2norm(ctx, cur, B, cur_w, dim, d_out, s))) return rc;
+    pr.done();
+  }
+  return FA_OK;
+}
+
+int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, int32_t B, int32_t T, int32_t dim,
+                       float* out) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  fa_ctx* ctx = m->ctx;
+  if (B < 0 || T < 0) return set_error(ctx, FA_ERR_ARG, "gemma: negative batch shape [%d x %d]", B, T);
+  if (B == 0) return FA_OK;
+  if (!ids || !lengths || !out) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
+  const fa_gemma_config& c = m->cfg;
+  const int full = c.n_dense > 0 ? m->dense_out.back() : c.hidden_size;
+  const int dd = dim <= 0 ? full : dim;
+  // validate ids on the host: an out-of-range id would read outside the table
+  for (int b = 0; b < B; b++) {
+    if (lengths[b] < 1 || lengths[b] > T)
+      return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
+    for (int t = 0; t < lengths[b]; t++) {
+      int32_t id = ids[(size_t)b * T + t];
+      if (id < 0 || id >= c.vocab_size)
+        return set_error(ctx, FA_ERR_ARG, "gemma: token id %d at [%d,%d] outside 0..%d", id, b, t, c.vocab_size - 1);
+    }
+  }
+  if (dd > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  int rc;
+  if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
+  if ((rc = m->out_dev.ensure(ctx, (size_t)B * dd * 4))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, ids, (size_t)B * T * 4, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = fa_gemma_embed_ids_dev(m, m->ids_dev.as<int32_t>(), lengths, B, T, dd, m->out_dev.as<float>()))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(out, m->out_dev.ptr, (size_t)B * dd * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
+int fa_gemma_set_profiling(fa_model* m, int enabled) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  m->profiling = enabled != 0;
+  return FA_OK;
+}
+
+int fa_gemma_kernel_stats(fa_model* m, int kind, int64_t* launches, double* ms, double* flops, double* bytes) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  if (kind < 0 || kind >= FA_K_COUNT) return set_error(m->ctx, FA_ERR_ARG, "gemma: kernel kind %d", kind);
+  int rc = fa::collect_stats(m);
+  if (rc) return rc;
+  const fa::KernelStat& s = m->stats[kind];
+  if (launches) *launches = s.launches;
+  if (ms) *ms = s.ms;
+  if (flops) *flops = s.flops;
+  if (bytes) *bytes = s.bytes;
+  return FA_OK;
+}
+
+int fa_gemma_reset_stats(fa_model* m) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  int rc = fa::collect_stats(m);
+  for (auto& s : m->stats) s = fa::KernelStat{};
+  return rc;
+}
+
+}  // extern "C"

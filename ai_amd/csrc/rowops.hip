@@ -1,0 +1,345 @@
+// Bandwidth-bound row kernels: one wavefront per row (or per head of a row),
+// 16-byte coalesced loads, wavefront reductions, rows held in registers
+// between the reduction and the write.
+//
+//   row_sum_squares  (*Tensor).RowSumSquares   tensor/matmul_fused.go:125-143
+//   rmsnorm          tensor.RMSNorm             tensor/attention.go:292-337
+//   rope             tensor.RoPE                tensor/rope.go:20-87
+//   embed_gather     E.Rows(ids)*sqrt(d) + the first pre-norm   models/gemma/embed.go:175-176,193-194
+//   qknorm_rope      RMSNorm(q|k; 1+g) then RoPE, in place      embed.go:198-207
+//   residual_norm    x += RMSNorm(o; 1+g_post); xn = RMSNorm(x; 1+g_next)   embed.go:216-225,231-237
+//   pool             masked mean                embed.go:381-404
+//   l2norm           y/sqrt(sum y^2 + 1e-12)    embed.go:472-475
+
+#include "fa_internal.h"
+#include "device_math.h"
+
+namespace fa {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---- RowSumSquares -----------------------------------------------------------
+__global__ __launch_bounds__(256) void row_sum_squares_kernel(const float* __restrict__ x, int64_t m, int64_t n,
+                                                              float* __restrict__ out) {
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (row >= m) return;
+  const float* r = x + row * n;
+  float s = 0.f;
+  for (int64_t i = lane; i < n; i += kWave) s = fmaf(r[i], r[i], s);
+  s = wave_sum(s);
+  if (lane == 0) out[row] = s;
+}
+
+// ---- RMSNorm (generic n) -----------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ g,
+                                                      float eps, int64_t rows, int64_t n, float* __restrict__ out) {
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* r = x + row * n;
+  float s = 0.f;
+  for (int64_t i = lane; i < n; i += kWave) s = fmaf(r[i], r[i], s);
+  s = wave_sum(s);
+  const float inv = rms_inv(s, (int)n, eps);
+  float* o = out + row * n;
+  for (int64_t i = lane; i < n; i += kWave) o[i] = r[i] * inv * g[i];
+}
+
+// ---- RoPE (generic) -------------------------------------------------------------
+// One thread per rotated pair (row, i < D/2); tables are [T, D/2].
+__global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, const float* __restrict__ cs,
+                                                   const float* __restrict__ sn, int64_t rows, int T, int D,
+                                                   float* __restrict__ out) {
+  const int half = D / 2;
+  int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= rows * half) return;
+  int64_t row = gid / half;
+  int i = (int)(gid - row * half);
+  int t = (int)(row % T);
+  float c = cs[(int64_t)t * half + i], s = sn[(int64_t)t * half + i];
+  const float* so = x + row * D;
+  float x1 = so[i], x2 = so[i + half];
+  out[row * D + i] = x1 * c - x2 * s;
+  out[row * D + i + half] = x1 * s + x2 * c;
+}
+
+// ---- model-path kernels (hidden size a multiple of 256, at most 1024) -----------
+// NC = hidden/256 float4 chunks per lane.
+
+template <int NC>
+__device__ __forceinline__ float sumsq(const f32x4 (&v)[NC]) {
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    s = fmaf(v[c].x, v[c].x, s);
+    s = fmaf(v[c].y, v[c].y, s);
+    s = fmaf(v[c].z, v[c].z, s);
+    s = fmaf(v[c].w, v[c].w, s);
+  }
+  return wave_sum(s);
+}
+
+// x[r] = E[ids[src[r]]] * scale; xn[r] = x[r] * rms_inv(x[r]) * g.
+template <int NC>
+__global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* __restrict__ ids,
+                                                           const int32_t* __restrict__ row_src,
+                                                           const uint16_t* __restrict__ E, int64_t vocab,
+                                                           int64_t rows, float scale,
+                                                           const float* __restrict__ g, float eps,
+                                                           float* __restrict__ x, float* __restrict__ xn) {
+  constexpr int d = NC * 256;
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  // ids on the device are not validated by the host: clamp so a bad id
+  // cannot read outside the table
+  const int64_t id = min(max((int64_t)ids[row_src[row]], (int64_t)0), vocab - 1);
+  const uint16_t* e = E + id * d;
+  f32x4 v[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    uint2 h = *reinterpret_cast<const uint2*>(e + c * 256 + lane * 4);
+    v[c].x = __uint_as_float(h.x << 16) * scale;
+    v[c].y = __uint_as_float(h.x & 0xFFFF0000u) * scale;
+    v[c].z = __uint_as_float(h.y << 16) * scale;
+    v[c].w = __uint_as_float(h.y & 0xFFFF0000u) * scale;
+  }
+  const float inv = rms_inv(sumsq<NC>(v), d, eps);
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    *reinterpret_cast<f32x4*>(x + row * d + col) = v[c];
+    f32x4 gg = *reinterpret_cast<const f32x4*>(g + col);
+    f32x4 o;
+    o.x = v[c].x * inv * gg.x; o.y = v[c].y * inv * gg.y; o.z = v[c].z * inv * gg.z; o.w = v[c].w * inv * gg.w;
+    *reinterpret_cast<f32x4*>(xn + row * d + col) = o;
+  }
+}
+
+// x += RMSNorm(o; g_post); xn = RMSNorm(x; g_next) when g_next != null.
+template <int NC>
+__global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ o, float* __restrict__ x,
+                                                            float* __restrict__ xn, int64_t rows,
+                                                            const float* __restrict__ g_post,
+                                                            const float* __restrict__ g_next, float eps) {
+  constexpr int d = NC * 256;
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  f32x4 ov[NC], xv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    ov[c] = *reinterpret_cast<const f32x4*>(o + row * d + col);
+    xv[c] = *reinterpret_cast<const f32x4*>(x + row * d + col);
+  }
+  const float inv = rms_inv(sumsq<NC>(ov), d, eps);
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    f32x4 gg = *reinterpret_cast<const f32x4*>(g_post + col);
+    xv[c].x = xv[c].x + ov[c].x * inv * gg.x;
+    xv[c].y = xv[c].y + ov[c].y * inv * gg.y;
+    xv[c].z = xv[c].z + ov[c].z * inv * gg.z;
+    xv[c].w = xv[c].w + ov[c].w * inv * gg.w;
+    *reinterpret_cast<f32x4*>(x + row * d + col) = xv[c];
+  }
+  if (g_next == nullptr) return;
+  const float inv2 = rms_inv(sumsq<NC>(xv), d, eps);
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    f32x4 gg = *reinterpret_cast<const f32x4*>(g_next + col);
+    f32x4 r;
+    r.x = xv[c].x * inv2 * gg.x; r.y = xv[c].y * inv2 * gg.y; r.z = xv[c].z * inv2 * gg.z; r.w = xv[c].w * inv2 * gg.w;
+    *reinterpret_cast<f32x4*>(xn + row * d + col) = r;
+  }
+}
+
+// Per (token, head): RMSNorm over D=256 with (1+g), then rotate-half RoPE at
+// the token's position. One wavefront holds the head's 256 values (4 per
+// lane); the rotation partner of element i (< 128) is i+128, held by lane+32.
+// Block = one token: waves 0..H-1 are the query heads, H..H+Hkv-1 the keys.
+__global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qkv, int64_t rows, int H, int Hkv,
+                                                          const float* __restrict__ gq, const float* __restrict__ gk,
+                                                          float eps, const int32_t* __restrict__ pos,
+                                                          const float* __restrict__ cs, const float* __restrict__ sn) {
+  constexpr int D = 256, half = 128;
+  const int64_t row = blockIdx.x;
+  const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows || head >= H + Hkv) return;
+  const int width = (H + 2 * Hkv) * D;
+  float* p = qkv + row * width + (int64_t)head * D;
+  const float* g = head < H ? gq : gk;
+  f32x4 v = *reinterpret_cast<const f32x4*>(p + lane * 4);
+  float s = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
+  s = wave_sum(s);
+  const float inv = rms_inv(s, D, eps);
+  f32x4 gg = *reinterpret_cast<const f32x4*>(g + lane * 4);
+  v.x = v.x * inv * gg.x; v.y = v.y * inv * gg.y; v.z = v.z * inv * gg.z; v.w = v.w * inv * gg.w;
+  f32x4 w;
+  w.x = __shfl_xor(v.x, 32, 64); w.y = __shfl_xor(v.y, 32, 64);
+  w.z = __shfl_xor(v.z, 32, 64); w.w = __shfl_xor(v.w, 32, 64);
+  const int t = pos[row];
+  const int i0 = (lane & 31) * 4;
+  f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
+  f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
+  f32x4 r;
+  if (lane < 32) {  // y_i = x_i c - x_{i+h} s
+    r.x = v.x * c.x - w.x * sv.x; r.y = v.y * c.y - w.y * sv.y;
+    r.z = v.z * c.z - w.z * sv.z; r.w = v.w * c.w - w.w * sv.w;
+  } else {  // y_{i+h} = x_i s + x_{i+h} c
+    r.x = w.x * sv.x + v.x * c.x; r.y = w.y * sv.y + v.y * c.y;
+    r.z = w.z * sv.z + v.z * c.z; r.w = w.w * sv.w + v.w * c.w;
+  }
+  *reinterpret_cast<f32x4*>(p + lane * 4) = r;
+}
+
+// pooled[b, c] = (sum over the sequence's rows of h[., c]) * (1/L_b), each
+// thread summing one column in row order.
+__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ cu,
+                                                   int d, float* __restrict__ pooled) {
+  const int b = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= d) return;
+  const int r0 = cu[b], r1 = cu[b + 1];
+  float s = 0.f;
+  for (int r = r0; r < r1; r++) s += h[(int64_t)r * d + c];
+  const int n = r1 - r0 > 0 ? r1 - r0 : 1;
+  pooled[(int64_t)b * d + c] = s * (1.f / (float)n);
+}
+
+// out[b, :dim] = y[b, :dim] / sqrt(sum(y[b, :dim]^2) + 1e-12); one wave per row.
+__global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ y, int nseq, int width, int dim,
+                                                     float* __restrict__ out) {
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= nseq) return;
+  const float* r = y + (int64_t)b * width;
+  float s = 0.f;
+  for (int i = lane; i < dim; i += kWave) s = fmaf(r[i], r[i], s);
+  s = wave_sum(s);
+  const float nrm = sqrtf(s + 1e-12f);
+  for (int i = lane; i < dim; i += kWave) out[(int64_t)b * dim + i] = r[i] / nrm;
+}
+
+__global__ __launch_bounds__(256) void row_plan_kernel(const int32_t* __restrict__ cu, int nseq, int T, int64_t rows,
+                                                       int32_t* __restrict__ row_src, int32_t* __restrict__ pos) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  int lo = 0, hi = nseq;  // cu[lo] <= r < cu[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cu[mid] <= r) lo = mid; else hi = mid;
+  }
+  const int t = (int)(r - cu[lo]);
+  row_src[r] = lo * T + t;
+  pos[r] = t;
+}
+
+int blocks_for(int64_t rows, int per) { return (int)((rows + per - 1) / per); }
+
+}  // namespace
+
+int launch_row_plan(fa_ctx* ctx, const int32_t* cu_seqlens, int32_t nseq, int32_t T, int64_t rows, int32_t* row_src,
+                    int32_t* pos, hipStream_t s) {
+  if (rows == 0) return FA_OK;
+  hipLaunchKernelGGL(row_plan_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0, s, cu_seqlens, nseq, T, rows, row_src,
+                     pos);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out, hipStream_t s) {
+  if (m == 0) return FA_OK;
+  hipLaunchKernelGGL(row_sum_squares_kernel, dim3(blocks_for(m, 4)), dim3(256), 0, s, x, m, n, out);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64_t rows, int64_t n, float* out,
+                   hipStream_t s) {
+  if (rows == 0 || n == 0) return FA_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, g, eps, rows, n, out);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_rope(fa_ctx* ctx, const float* x, const float* cos_t, const float* sin_t, int64_t rows, int32_t T,
+                int32_t D, float* out, hipStream_t s) {
+  int64_t work = rows * (D / 2);
+  if (work == 0) return FA_OK;
+  hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(work, 256)), dim3(256), 0, s, x, cos_t, sin_t, rows, T, D, out);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_src, const uint16_t* E,
+                        int64_t vocab, int64_t rows, int32_t d, float scale, const float* g_next, float eps, float* x,
+                        float* xn, hipStream_t s) {
+  if (rows == 0) return FA_OK;
+  dim3 grid(blocks_for(rows, 4)), block(256);
+  switch (d) {
+    case 256: hipLaunchKernelGGL(embed_gather_kernel<1>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 512: hipLaunchKernelGGL(embed_gather_kernel<2>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 768: hipLaunchKernelGGL(embed_gather_kernel<3>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 1024: hipLaunchKernelGGL(embed_gather_kernel<4>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
+    default: return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden size %d not in {256,512,768,1024}", d);
+  }
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
+                         const float* g_post, const float* g_next, float eps, hipStream_t s) {
+  if (rows == 0) return FA_OK;
+  dim3 grid(blocks_for(rows, 4)), block(256);
+  switch (d) {
+    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
+    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
+    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
+    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
+    default: return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden size %d not in {256,512,768,1024}", d);
+  }
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t Hkv, int32_t D, const float* gq,
+                       const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
+                       hipStream_t s) {
+  if (D != 256) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d != 256", D);
+  if (rows == 0) return FA_OK;
+  dim3 grid((unsigned)rows, (unsigned)((H + Hkv + 3) / 4)), block(256);
+  hipLaunchKernelGGL(qknorm_rope_kernel, grid, block, 0, s, qkv, rows, H, Hkv, gq, gk, eps, d_pos, cos_t, sin_t);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t nseq, int32_t d, float* pooled,
+                hipStream_t s) {
+  if (nseq == 0) return FA_OK;
+  dim3 grid(nseq, (d + 255) / 256), block(256);
+  hipLaunchKernelGGL(pool_kernel, grid, block, 0, s, h, cu_seqlens, d, pooled);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int32_t dim, float* out, hipStream_t s) {
+  if (nseq == 0) return FA_OK;
+  hipLaunchKernelGGL(l2norm_kernel, dim3(blocks_for(nseq, 4)), dim3(256), 0, s, y, nseq, width, dim, out);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_final_norm(fa_ctx* ctx, const float* x, int64_t rows, int32_t d, const float* g, float eps, float* h,
+                      hipStream_t s) {
+  return launch_rmsnorm(ctx, x, g, eps, rows, d, h, s);
+}
+
+}  // namespace fa

@@ -1,0 +1,235 @@
+/* fa_rocm.h — C ABI of libfa_rocm.so, the MI355X (gfx950) implementation of
+ * fiber/ai's EmbeddingGemma encoder path.
+ *
+ * Plain C: pointers, sizes and status codes; no C++ or torch types. Every
+ * entry point returns 0 (FA_OK) on success or an FA_ERR_* code, with a
+ * message available from fa_last_error(ctx). Argument errors the reference
+ * reports by panicking with *tensor.Error{Op, Msg} (tensor/errors.go:5-31)
+ * return FA_ERR_ARG here with the same kind of message, prefixed by the
+ * reference's Op name; a cgo shim turns them back into that panic.
+ *
+ * Memory: "host" entry points (the drop-in replacements of the reference's
+ * tensor/gemma functions) take host pointers, copy them to the device,
+ * compute on the context's HIP stream and copy the result back before
+ * returning, like the reference's functions return filled slices. The
+ * "_dev" entry points take device pointers and only enqueue work on the
+ * context's stream (fa_stream()); they are what a caller keeping data
+ * resident in HBM uses.
+ *
+ * Threading: a context owns one HIP stream and per-call scratch; calls on
+ * one context must be serialised by the caller (the reference's Embed is not
+ * documented as goroutine-safe either, models/gemma/embed.go:15). Distinct
+ * contexts may be used from distinct threads.
+ */
+#ifndef FA_ROCM_H
+#define FA_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FA_OK = 0,
+  FA_ERR_ARG = 1,         /* bad shape/argument: the reference panics with *tensor.Error */
+  FA_ERR_HIP = 2,         /* HIP runtime error (message carries hipGetErrorString) */
+  FA_ERR_OOM = 3,         /* device allocation failed */
+  FA_ERR_STATE = 4,       /* call out of order (e.g. embed before every weight is set) */
+  FA_ERR_UNSUPPORTED = 5  /* a configuration this build does not implement */
+};
+
+enum { FA_DT_F32 = 0, FA_DT_BF16 = 1 };
+
+/* Activation of a fused product: tensor.NoAct/ReLUAct/GELUAct
+ * (tensor/matmul_fused.go:25-32). GELU is the tanh approximation
+ * (internal/kernel/math.go:117-143). */
+enum { FA_ACT_NONE = 0, FA_ACT_RELU = 1, FA_ACT_GELU = 2 };
+
+/* Layout of a product's right operand B (logical shape [k x n]):
+ * FA_B_KN: row-major [k x n] with leading dimension ldb (the reference's
+ *          w[in,out], tensor/matmul.go:42-72);
+ * FA_B_NK: row-major [n x k] (a transposed view, i.e. a checkpoint's
+ *          [out,in] weight or cluster.Similarities' docs, cluster.go:185-190). */
+enum { FA_B_KN = 0, FA_B_NK = 1 };
+
+typedef struct fa_ctx fa_ctx;
+typedef struct fa_model fa_model;
+
+/* ---- context -------------------------------------------------------- */
+
+/* Create a context on HIP device `device` (one stream, default priority). */
+int fa_create(int device, fa_ctx** out);
+void fa_destroy(fa_ctx* ctx);
+/* Last error message of ctx, or of the calling thread when ctx is NULL
+ * (for fa_create failures). Never NULL. */
+const char* fa_last_error(const fa_ctx* ctx);
+/* The context's HIP stream, as an opaque pointer (hipStream_t). */
+void* fa_stream(fa_ctx* ctx);
+/* Block until the context's stream is idle. */
+int fa_sync(fa_ctx* ctx);
+/* Version string of the library build. */
+const char* fa_version(void);
+
+/* Device memory helpers for callers without a HIP runtime of their own. */
+int fa_device_alloc(fa_ctx* ctx, size_t bytes, void** out);
+int fa_device_free(fa_ctx* ctx, void* ptr);
+int fa_memcpy_h2d(fa_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+int fa_memcpy_d2h(fa_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+
+/* ---- tensor-level operators (drop-ins, host pointers) ------------------ */
+
+/* Epilogue of a fused product, applied in the reference's order
+ * Bias -> RowScale -> Act -> Mul -> Residual (internal/blas/gemm.go:276-347,
+ * tensor.Fused, tensor/matmul_fused.go:11-23). Null pointers are skipped. */
+typedef struct fa_epilogue {
+  const float* bias;      /* [n] */
+  const float* row_scale; /* [m] */
+  int act;                /* FA_ACT_* */
+  const float* mul;       /* [m x n], leading dimension ldm */
+  int64_t ldm;
+  const float* residual;  /* [m x n], leading dimension ldr */
+  int64_t ldr;
+} fa_epilogue;
+
+/* C[m x n] = epilogue(A[m x k] . B) with A row-major (lda), B of dtype
+ * b_dtype (FA_DT_F32 or FA_DT_BF16) in layout b_layout, C row-major (ldc).
+ * Replaces tensor.MatMulFused (tensor/matmul_fused.go:40-96) and, with
+ * e == NULL, the 2-D case of tensor.MatMul (tensor/matmul.go:19-72).
+ * fp32 accumulation on the MFMA units; bf16 B is widened exactly. */
+int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
+                    int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc);
+
+/* out[i] = sum_j x[i,j]^2 for row-major x [m x n].
+ * Replaces (*Tensor).RowSumSquares (tensor/matmul_fused.go:125-143). */
+int fa_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out);
+
+/* out = x / sqrt(mean(x^2) + eps) * g over the last dimension n of
+ * row-major x [rows x n]; g has n elements (the caller passes 1+w for
+ * Gemma). Replaces tensor.RMSNorm (tensor/attention.go:292-337). */
+int fa_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64_t rows, int64_t n, float* out);
+
+/* Rotary embedding, rotate-half convention, on contiguous x [rows x D]
+ * whose row r sits at position positions[r % T] (x is [..., T, D]).
+ * Angle tables in float64 rounded to float32 as the reference's.
+ * Replaces tensor.RoPE (tensor/rope.go:20-61). */
+int fa_rope(fa_ctx* ctx, const float* x, double base, const int32_t* positions, int64_t rows, int32_t T, int32_t D,
+            float* out);
+
+/* out = softmax(scale * q.k^T + mask) . v per (batch, head).
+ * q: [B, H, T, D] with element strides (q_sb, q_sh) on the two lead
+ * dimensions and rows of D contiguous at stride D; k, v: [B, H, S, D]
+ * likewise (a head stride of 0 expresses grouped-query attention, the
+ * reference's Expand). mask: additive, NULL or strides (m_sb, m_sh, m_sr,
+ * m_sc) over [B, H, T, S] (0 where broadcast). out: [B, H, T, D]
+ * contiguous. Masked weights are exactly 0 (exp of inputs below -87 flushes
+ * to 0, internal/kernel/generic.go:278-307).
+ * Replaces tensor.AttentionScaled (tensor/attention.go:67-83,130-287). */
+int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, int32_t B, int32_t H, int32_t T,
+                 int32_t S, int32_t D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t v_sb,
+                 int64_t v_sh, const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_sr, int64_t m_sc, float scale,
+                 float* out);
+
+/* Scores queries [nq x d] against docs [nd x d] (dot products, the rows
+ * being unit length as cluster.Similarities requires, cluster.go:180-190) and
+ * returns, per query, the topk largest scores in descending order with their
+ * doc indices; equal scores are ordered by the lower index (the first-max
+ * rule of (*Tensor).Argmax, tensor/reduce.go:269-297). 1 <= topk <= 32. */
+int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
+                         int32_t topk, int32_t* idx, float* val);
+
+/* Device-pointer variant of fa_similarities_topk (enqueue only). */
+int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
+                             int32_t topk, int32_t* idx, float* val);
+
+/* ---- the EmbeddingGemma model (models/gemma) ------------------------- */
+
+/* Hyper-parameters as read from config.json by gemma.LoadConfig
+ * (models/gemma/config.go:19-58,153-227), Variant 0 (Gemma 3 text encoder),
+ * plus the sentence-transformers head (model.go:236-310). */
+typedef struct fa_gemma_config {
+  int32_t hidden_size;            /* 768 */
+  int32_t num_hidden_layers;      /* 24 */
+  int32_t num_attention_heads;    /* 3 */
+  int32_t num_key_value_heads;    /* 1 */
+  int32_t head_dim;               /* 256 */
+  int32_t intermediate_size;      /* 1152 */
+  int32_t vocab_size;             /* 262144 */
+  int32_t sliding_window;         /* 512 */
+  int32_t use_bidirectional;      /* 1: window bound sliding_window/2+1 (config.go:331-339) */
+  int32_t sliding_window_pattern; /* 6: layer l is full attention iff (l+1)%6 == 0 (config.go:213-225) */
+  double rope_local_base_freq;    /* 1e4 */
+  double rope_theta;              /* 1e6 */
+  double query_pre_attn_scalar;   /* 256: score scale 1/sqrt(256) (model.go:100) */
+  float rms_norm_eps;             /* 1e-6 */
+  int32_t max_tokens;             /* 2048 (model.go:102-104) */
+  int32_t n_dense;                /* head Dense layers (2: 768->3072->768), identity activation */
+  int32_t dense_out[4];
+} fa_gemma_config;
+
+/* Create an empty model on ctx (no weights yet). Replaces the allocation
+ * part of gemma.Load (models/gemma/model.go:76-232). */
+int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out);
+void fa_gemma_destroy(fa_model* m);
+
+/* Upload one checkpoint tensor by its Hugging Face name, as gemma.Load
+ * reads them (model.go:142-191): "embed_tokens.weight", "norm.weight",
+ * "layers.<i>.{input_layernorm,post_attention_layernorm,
+ * pre_feedforward_layernorm,post_feedforward_layernorm}.weight",
+ * "layers.<i>.self_attn.{q,k,v,o}_proj.weight", "layers.<i>.self_attn.
+ * {q,k}_norm.weight", "layers.<i>.mlp.{gate,up,down}_proj.weight", and the
+ * head's "dense.<i>.linear.weight" (model.go:277-304). Shapes are the
+ * checkpoint's ([out, in] for matrices). Matrices are kept bf16-resident:
+ * FA_DT_BF16 data is stored as is; FA_DT_F32 data must be exactly
+ * representable in bf16 (else FA_ERR_UNSUPPORTED). Norm vectors are kept
+ * in float32 with Gemma's 1+w applied (model.go:131-140). */
+int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t* shape, int32_t ndim,
+                        const void* data);
+
+/* Check that every tensor was set and prepare the device-side tables
+ * (RoPE cos/sin for both bases). */
+int fa_gemma_finalize(fa_model* m);
+
+/* Embeddings of B token-id sequences: ids [B x T] row-major, right-padded
+ * (any pad value), lengths [B] with 1 <= lengths[b] <= T <= max_tokens;
+ * out [B x dim], 1 <= dim <= final width (Matryoshka truncation before L2,
+ * embed.go:421-427); dim <= 0 means the full width. Runs the encoder, masked
+ * mean pooling, the Dense head and L2 normalisation. Host pointers; returns
+ * when out is filled. Replaces (*Model).embedBatch (models/gemma/embed.go:
+ * 118-157), the ids-level core of (*Model).Embed (embed.go:15-80). */
+int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, int32_t B, int32_t T, int32_t dim,
+                       float* out);
+
+/* Same computation on device-resident data: d_ids [B x T] on the device,
+ * lengths on the HOST (they set the launch shapes), d_out [B x dim] on the
+ * device. Enqueues on fa_stream(ctx) and returns without waiting. */
+int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
+                           int32_t dim, float* d_out);
+
+/* Per-kernel timing with HIP events on the model's stream, for roofline
+ * reporting: when enabled, each kernel launch of the forward pass is
+ * bracketed by events and its duration accumulated under its kind. */
+enum {
+  FA_K_GEMM_QKV = 0,
+  FA_K_GEMM_O = 1,
+  FA_K_GEMM_GATEUP = 2,
+  FA_K_GEMM_DOWN = 3,
+  FA_K_GEMM_HEAD = 4,
+  FA_K_ATTENTION = 5,
+  FA_K_QKNORM_ROPE = 6,
+  FA_K_RESIDUAL_NORM = 7,
+  FA_K_GATHER = 8,
+  FA_K_POOL_L2 = 9,
+  FA_K_COUNT = 10
+};
+int fa_gemma_set_profiling(fa_model* m, int enabled);
+/* Accumulated launches, milliseconds, flops and bytes (algorithmic) for one
+ * kind since the last reset; synchronises the stream. */
+int fa_gemma_kernel_stats(fa_model* m, int kind, int64_t* launches, double* ms, double* flops, double* bytes);
+int fa_gemma_reset_stats(fa_model* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

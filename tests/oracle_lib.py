@@ -1,0 +1,231 @@
+"""Loader for the CPU oracle (oracle/libfa_oracle_v{3,4}.so).
+
+Test infrastructure: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it, as the checker.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+
+i32, i64, f32, f64, vp = C.c_int32, C.c_int64, C.c_float, C.c_double, C.c_void_p
+
+_SIGS = {
+    "orc_exp": (None, [vp, vp, i64]),
+    "orc_tanh": (None, [vp, vp, i64]),
+    "orc_gelu": (None, [vp, vp, i64]),
+    "orc_row_sum_squares": (None, [vp, i64, i64, i64, vp]),
+    "orc_rms_scale": (None, [vp, i64, C.c_int, f32, vp]),
+    "orc_rmsnorm": (None, [vp, vp, f32, i64, i64, vp]),
+    "orc_rope": (C.c_int, [vp, f64, vp, i64, C.c_int, C.c_int, vp]),
+    "orc_padding_mask": (None, [vp, C.c_int, C.c_int, vp]),
+    "orc_window_mask": (None, [C.c_int, C.c_int, vp]),
+    "orc_causal_mask": (None, [C.c_int, vp]),
+    "orc_gemm": (C.c_int, [i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, vp, C.c_int, vp, i64, vp, i64]),
+    "orc_attention": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, i64, i64, i64, i64, i64, i64,
+                                vp, i64, i64, i64, i64, f32, vp]),
+    "orc_similarities_topk": (C.c_int, [vp, i64, vp, i64, C.c_int, C.c_int, vp, vp]),
+    "orc_model_create": (vp, [C.c_int] * 10 + [f64, f64, f64, f32, C.c_int, vp]),
+    "orc_model_destroy": (None, [vp]),
+    "orc_model_set": (C.c_int, [vp, C.c_char_p, vp, i64]),
+    "orc_model_finalize": (C.c_int, [vp]),
+    "orc_model_embed": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "orc_num_threads": (C.c_int, []),
+}
+
+_lib = None
+
+
+def _has_avx512() -> bool:
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    return all(f in flags for f in (" avx512f", " avx512bw", " avx512dq", " avx512vl"))
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        name = "libfa_oracle_v4.so" if _has_avx512() else "libfa_oracle_v3.so"
+        p = os.path.join(ORACLE_DIR, name)
+        if not os.path.exists(p):
+            raise RuntimeError(f"{p} missing: run `make -C oracle`")
+        l = C.CDLL(p)
+        for n, (res, args) in _SIGS.items():
+            fn = getattr(l, n)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def isa() -> str:
+    return "avx512 (x86-64-v4)" if _has_avx512() else "avx2 (x86-64-v3)"
+
+
+def P(a):
+    return None if a is None else a.ctypes.data
+
+
+def f32c(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def exp(x):
+    x = f32c(x); z = np.empty_like(x); lib().orc_exp(P(x), P(z), x.size); return z
+
+
+def tanh(x):
+    x = f32c(x); z = np.empty_like(x); lib().orc_tanh(P(x), P(z), x.size); return z
+
+
+def gelu(x):
+    x = f32c(x); z = np.empty_like(x); lib().orc_gelu(P(x), P(z), x.size); return z
+
+
+def row_sum_squares(x):
+    x = f32c(x); out = np.empty(x.shape[0], np.float32)
+    lib().orc_row_sum_squares(P(x), x.shape[0], x.shape[1], x.shape[1], P(out)); return out
+
+
+def rms_scale(ss, n, eps):
+    ss = f32c(ss); out = np.empty_like(ss); lib().orc_rms_scale(P(ss), ss.size, n, eps, P(out)); return out
+
+
+def rmsnorm(x, g, eps):
+    x = f32c(x); g = f32c(g); out = np.empty_like(x); n = x.shape[-1]
+    lib().orc_rmsnorm(P(x), P(g), eps, x.size // n, n, P(out)); return out
+
+
+def rope(x, base, positions):
+    x = f32c(x); pos = np.ascontiguousarray(positions, np.int32); out = np.empty_like(x)
+    T, D = x.shape[-2], x.shape[-1]
+    rc = lib().orc_rope(P(x), base, P(pos), x.size // D, T, D, P(out))
+    assert rc == 0
+    return out
+
+
+def padding_mask(lengths, n):
+    l = np.ascontiguousarray(lengths, np.int32); out = np.empty((l.size, 1, 1, n), np.float32)
+    lib().orc_padding_mask(P(l), l.size, n, P(out)); return out
+
+
+def window_mask(n, w):
+    out = np.empty((n, n), np.float32); lib().orc_window_mask(n, w, P(out)); return out
+
+
+def causal_mask(n):
+    out = np.empty((n, n), np.float32); lib().orc_causal_mask(n, P(out)); return out
+
+
+def gemm(a, b, bias=None, rowscale=None, act=0, mul=None, residual=None):
+    """epilogue(a . b), b [k x n] row-major."""
+    a = f32c(a); b = f32c(b)
+    m, k = a.shape
+    n = b.shape[1]
+    out = np.empty((m, n), np.float32)
+    keep = [f32c(t) if t is not None else None for t in (bias, rowscale, mul, residual)]
+    rc = lib().orc_gemm(m, n, k, P(a), k, P(b), n, P(out), n, P(keep[0]), P(keep[1]), act, P(keep[2]), n, P(keep[3]), n)
+    assert rc == 0
+    return out
+
+
+def attention(q, k, v, mask, scale):
+    """q [B,H,T,D], k/v [B,H,S,D] (broadcast views allowed on H), mask broadcastable to [B,H,T,S] or None."""
+    q = f32c(q)
+    k = np.asarray(k, np.float32); v = np.asarray(v, np.float32)
+    B, H, T, D = q.shape
+    S = k.shape[2]
+
+    def st(a):
+        return tuple(s // 4 for s in a.strides)
+    if k.strides[-1] != 4 or k.strides[-2] != D * 4:
+        k = np.ascontiguousarray(k)
+    if v.strides[-1] != 4 or v.strides[-2] != D * 4:
+        v = np.ascontiguousarray(v)
+    ks, vs = st(k), st(v)
+    out = np.empty((B, H, T, D), np.float32)
+    mp, ms = None, (0, 0, 0, 0)
+    if mask is not None:
+        m = np.asarray(mask, np.float32)
+        while m.ndim < 4:
+            m = m[None]
+        m = np.ascontiguousarray(m)
+        mb = np.broadcast_to(m, (B, H, T, S))
+        ms = st(mb)
+        mp = m
+    rc = lib().orc_attention(P(q), k.ctypes.data, v.ctypes.data, B, H, T, S, D, H * T * D, T * D, ks[0], ks[1], vs[0],
+                             vs[1], None if mp is None else mp.ctypes.data, *ms, scale, P(out))
+    assert rc == 0
+    return out
+
+
+def similarities_topk(q, docs, k):
+    q = f32c(q); docs = f32c(docs)
+    idx = np.empty((q.shape[0], k), np.int32); val = np.empty((q.shape[0], k), np.float32)
+    rc = lib().orc_similarities_topk(P(q), q.shape[0], P(docs), docs.shape[0], q.shape[1], k, P(idx), P(val))
+    assert rc == 0
+    return idx, val
+
+
+class OracleModel:
+    """The oracle's EmbeddingGemma (fp32 weights; pre-norms folded as the reference does)."""
+
+    def __init__(self, shape):
+        s = shape
+        do = (C.c_int * 4)(*(list(s.dense_out) + [0] * (4 - len(s.dense_out))))
+        self._do = do
+        self.h = lib().orc_model_create(s.hidden_size, s.num_hidden_layers, s.num_attention_heads,
+                                        s.num_key_value_heads, s.head_dim, s.intermediate_size, s.vocab_size,
+                                        s.sliding_window, s.use_bidirectional, s.sliding_window_pattern,
+                                        s.rope_local_base_freq, s.rope_theta, s.query_pre_attn_scalar,
+                                        s.rms_norm_eps, len(s.dense_out), C.cast(do, vp))
+        assert self.h
+        self.shape = shape
+
+    def set(self, name, data):
+        a = f32c(data)
+        rc = lib().orc_model_set(self.h, name.encode(), P(a), a.size)
+        if rc != 0:
+            raise ValueError(f"oracle set {name}: {rc}")
+
+    def finalize(self):
+        rc = lib().orc_model_finalize(self.h)
+        if rc != 0:
+            raise ValueError(f"oracle finalize: {rc}")
+
+    def load_synthetic(self, seed=None):
+        from ai_amd import synth as S
+        seed = S.WEIGHT_SEED if seed is None else seed
+        for name, shp, kind in S.weight_specs(self.shape):
+            w = S.make_weight(name, shp, kind, seed)
+            self.set(name, S.bf16_to_f32(w) if kind == "m" else w)
+        self.finalize()
+
+    def embed(self, ids, lengths, dim=0):
+        ids = np.ascontiguousarray(ids, np.int32); lengths = np.ascontiguousarray(lengths, np.int32)
+        B, T = ids.shape
+        full = self.shape.dense_out[-1] if self.shape.dense_out else self.shape.hidden_size
+        d = full if dim == 0 else dim
+        out = np.empty((B, d), np.float32)
+        rc = lib().orc_model_embed(self.h, P(ids), P(lengths), B, T, d, P(out))
+        if rc != 0:
+            raise ValueError(f"oracle embed: {rc}")
+        return out
+
+    def close(self):
+        if self.h:
+            lib().orc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

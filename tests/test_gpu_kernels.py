@@ -1,0 +1,232 @@
+"""GPU parity of the tensor-level operators against the CPU oracle.
+
+Every call goes through the C ABI (libfa_rocm.so) on the device. Tolerances
+are the reference's: |gpu - want| <= 1e-4 * (1 + |want|) for products
+(internal/blas/gemm_test.go:39-56), 1e-5/1e-6 for RMSNorm and RoPE
+(tensor/rope_test.go:83-102), 1e-4 for attention
+(tensor/attention_test.go:64-91). Max |delta| is printed for each case.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from ai_amd import _native as N
+from ai_amd import synth as S
+from ai_amd import tensor as T
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def close(got, want, tol=1e-4, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    d = np.abs(got - want)
+    lim = tol * (1 + np.abs(want))
+    worst = float(d.max()) if d.size else 0.0
+    rel = float((d / np.maximum(np.abs(want), 1e-30)).max()) if d.size else 0.0
+    print(f"{what}: max|d|={worst:.3g} max rel={rel:.3g}", flush=True)
+    bad = np.argwhere(d > lim)
+    assert bad.size == 0, f"{what}: {bad.shape[0]} elements out of tolerance, first {bad[0]}: got {got[tuple(bad[0])]} want {want[tuple(bad[0])]}"
+    return worst
+
+
+# The reference's GEMM test shapes (internal/blas/gemm_test.go:75-79), m, n, k.
+REF_SHAPES = [(1, 1, 1), (1, 1, 100), (1, 17, 5), (1, 100, 300), (5, 1, 7), (300, 1, 100), (3, 3, 3), (4, 16, 1),
+              (6, 16, 7), (8, 12, 3), (12, 32, 9), (13, 33, 9), (5, 17, 9), (7, 37, 19), (64, 64, 64),
+              (129, 65, 33), (133, 257, 300), (100, 20, 513), (257, 33, 1), (31, 4097, 7), (300, 300, 300)]
+
+
+@pytest.mark.parametrize("m,n,k", REF_SHAPES)
+def test_matmul_reference_shapes_f32(ctx, m, n, k):
+    r = rng(m * 10007 + n * 101 + k)
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    close(T.MatMul(a, b, ctx=ctx), want, what=f"f32 KN {m}x{n}x{k}")
+    close(T.MatMul(a, np.ascontiguousarray(b.T), w_layout=N.FA_B_NK, ctx=ctx), want, what=f"f32 NK {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (13, 33, 9), (129, 65, 33), (133, 257, 300), (300, 300, 300)])
+def test_matmul_bf16_weights(ctx, m, n, k):
+    r = rng(7 + m)
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    wb = S.normal_bf16(11, f"w{m}", 0.5, (n, k))
+    wf = S.bf16_to_f32(wb)
+    want = a.astype(np.float64) @ wf.T.astype(np.float64)
+    close(T.MatMul(a, wb, w_layout=N.FA_B_NK, ctx=ctx), want, what=f"bf16 NK {m}x{n}x{k}")
+    close(T.MatMul(a, np.ascontiguousarray(wb.T), w_layout=N.FA_B_KN, ctx=ctx), want, what=f"bf16 KN {m}x{n}x{k}")
+
+
+# The encoder's product shapes at the configs (M rows; K, N) with bf16 weights.
+@pytest.mark.parametrize("M", [128, 5120, 8192, 16384, 32768])
+@pytest.mark.parametrize("K,N", [(768, 1280), (768, 768), (768, 256), (768, 2304), (1152, 768)])
+def test_matmul_config_shapes_vs_oracle(ctx, M, K, N):
+    r = rng(M + K + N)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    wb = S.normal_bf16(5, f"cfg{K}x{N}", 0.02, (N, K))
+    wf = S.bf16_to_f32(wb)
+    got = T.MatMul(a, wb, w_layout=N.FA_B_NK, ctx=ctx)
+    want = O.gemm(a, np.ascontiguousarray(wf.T))
+    close(got, want, what=f"config M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("act", [T.NoAct, T.ReLUAct, T.GELUAct])
+def test_matmul_fused_epilogue_vs_oracle(ctx, act):
+    r = rng(30 + act)
+    m, n, k = 133, 257, 300
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    bias = r.uniform(-1, 1, n).astype(np.float32)
+    rs = r.uniform(0.5, 1.5, m).astype(np.float32)
+    mul = r.uniform(-1, 1, (m, n)).astype(np.float32)
+    res = r.uniform(-1, 1, (m, n)).astype(np.float32)
+    got = T.MatMulFused(a, b, T.Fused(Bias=bias, RowScale=rs, Act=act, Mul=mul, Residual=res), ctx=ctx)
+    want = O.gemm(a, b, bias, rs, act, mul, res)
+    close(got, want, what=f"epilogue act={act}")
+    # each field alone
+    for f, args in [(T.Fused(Bias=bias), dict(bias=bias)), (T.Fused(RowScale=rs), dict(rowscale=rs)),
+                    (T.Fused(Act=act), dict(act=act)), (T.Fused(Mul=mul), dict(mul=mul)),
+                    (T.Fused(Residual=res), dict(residual=res))]:
+        close(T.MatMulFused(a, b, f, ctx=ctx), O.gemm(a, b, **args), what=f"epilogue single {list(args)}")
+
+
+def test_matmul_padding_untouched(ctx):
+    """A C with row gaps keeps the bytes between rows (gemm_test.go:50-55)."""
+    r = rng(99)
+    m, n, k = 37, 45, 64
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    ldc = n + 7
+    c = np.full(m * ldc, 123.0, np.float32)
+    rc = N.lib().fa_matmul_fused(ctx.h, m, n, k, N.ptr(a), k, N.ptr(b), n, N.FA_DT_F32, N.FA_B_KN, None, N.ptr(c), ldc)
+    N.check(ctx.h, rc)
+    cm = c.reshape(m, ldc)
+    close(cm[:, :n], a.astype(np.float64) @ b, what="ldc>n")
+    assert np.all(cm[:, n:] == 123.0)
+
+
+def test_matmul_errors(ctx):
+    with pytest.raises(T.TensorError):
+        T.MatMul(np.zeros((2, 3), np.float32), np.zeros((4, 5), np.float32), ctx=ctx)
+    with pytest.raises(T.TensorError):
+        T.MatMulFused(np.zeros((2, 3), np.float32), np.zeros((3, 5), np.float32),
+                      T.Fused(Bias=np.zeros(4, np.float32)), ctx=ctx)
+
+
+def test_row_sum_squares_kat(ctx):
+    """tensor/matmul_fused_test.go:62-71."""
+    x = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    assert T.RowSumSquares(x, ctx=ctx).tolist() == [14, 77]
+    assert T.RowSumSquares(x.T, ctx=ctx).tolist() == [17, 29, 45]
+
+
+@pytest.mark.parametrize("rows,n", [(20, 64), (3 * 8, 16), (5, 768), (1000, 256), (7, 1)])
+def test_rmsnorm_vs_oracle(ctx, rows, n):
+    r = rng(rows * n)
+    x = (r.standard_normal((rows, n)) * 2).astype(np.float32)
+    g = r.standard_normal(n).astype(np.float32)
+    got = T.RMSNorm(x, g, 1e-6, ctx=ctx)
+    close(got, O.rmsnorm(x, g, 1e-6), tol=1e-5, what=f"rmsnorm {rows}x{n}")
+
+
+def test_rope_known(ctx):
+    """tensor/rope_test.go:9-25."""
+    got = T.RoPE(np.array([[1, 0]], np.float32), 10000, [1], ctx=ctx)
+    assert abs(got[0, 0] - np.float32(np.cos(1))) <= 1e-6 and abs(got[0, 1] - np.float32(np.sin(1))) <= 1e-6
+    ident = T.RoPE(np.array([[3, -4, 5, 6]], np.float32), 10000, [0], ctx=ctx)
+    assert np.abs(ident - np.array([[3, -4, 5, 6]])).max() <= 1e-6
+
+
+@pytest.mark.parametrize("base", [1e4, 1e6])
+def test_rope_vs_oracle(ctx, base):
+    r = rng(int(base))
+    x = r.standard_normal((2, 3, 8, 256)).astype(np.float32)
+    pos = [0, 5, 9, 100, 500, 1000, 2047, 7]
+    got = T.RoPE(x, base, pos, ctx=ctx)
+    close(got, O.rope(x, base, pos), tol=1e-5, what=f"rope base={base}")
+    # norm preservation (rope_test.go:27-38)
+    xn = (x.astype(np.float64) ** 2).sum(-1)
+    yn = (got.astype(np.float64) ** 2).sum(-1)
+    assert np.all(np.abs(xn - yn) <= 1e-3 * (xn + 1))
+
+
+def test_attention_matches_naive_float64(ctx):
+    """tensor/attention_test.go:56-92: B=2, H=3, T=5, S=7, D=4, with/without padding mask."""
+    r = rng(41)
+    B, H, Tq, Sk, D = 2, 3, 5, 7, 4
+    q = r.standard_normal((B, H, Tq, D)).astype(np.float32)
+    k = r.standard_normal((B, H, Sk, D)).astype(np.float32)
+    v = r.standard_normal((B, H, Sk, D)).astype(np.float32)
+    for mask in (None, T.PaddingMask([Sk, 3], Sk)):
+        got = T.Attention(q, k, v, mask, ctx=ctx)
+        s = np.einsum("bhtd,bhsd->bhts", q.astype(np.float64), k.astype(np.float64)) / np.sqrt(D)
+        if mask is not None:
+            s = s + mask.astype(np.float64)
+        s = s - s.max(-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(-1, keepdims=True)
+        want = np.einsum("bhts,bhsd->bhtd", p, v.astype(np.float64))
+        close(got, want, what=f"attention naive mask={mask is not None}")
+
+
+@pytest.mark.parametrize("B,H,Tq,Sk,D", [(2, 3, 65, 65, 256), (1, 3, 300, 300, 256), (2, 2, 17, 100, 64)])
+def test_attention_vs_oracle_gqa_window_padding(ctx, B, H, Tq, Sk, D):
+    r = rng(B * H * Tq)
+    q = r.standard_normal((B, H, Tq, D)).astype(np.float32)
+    k1 = r.standard_normal((B, 1, Sk, D)).astype(np.float32)
+    v1 = r.standard_normal((B, 1, Sk, D)).astype(np.float32)
+    k = np.broadcast_to(k1, (B, H, Sk, D))  # the reference's Expand
+    v = np.broadcast_to(v1, (B, H, Sk, D))
+    lengths = [Sk] + [max(1, Sk // 3)] * (B - 1)
+    pad = T.PaddingMask(lengths, Sk)
+    masks = [None, pad]
+    if Tq == Sk:
+        masks.append(pad + T.WindowMask(Tq, 17).reshape(1, 1, Tq, Tq))
+    for mask in masks:
+        got = T.AttentionScaled(q, k, v, mask, 0.0625, ctx=ctx)
+        want = O.attention(q, k, v, mask, 0.0625)
+        close(got, want, what=f"attention oracle {B},{H},{Tq},{Sk},{D}")
+
+
+def test_masked_attention_weights_are_exact_zeros(ctx):
+    """tensor/attention_test.go:266-285: causal position 0 reproduces v[0]."""
+    r = rng(11)
+    n, d = 64, 16
+    q, k, v = (r.standard_normal((1, 1, n, d)).astype(np.float32) for _ in range(3))
+    out = T.Attention(q, k, v, T.CausalMask(n), ctx=ctx)
+    assert np.abs(out[0, 0, 0] - v[0, 0, 0]).max() <= 1e-6
+
+
+def test_similarities_topk_vs_oracle(ctx):
+    r = rng(5)
+    q = r.standard_normal((33, 96)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    docs = r.standard_normal((5000, 96)).astype(np.float32)
+    docs /= np.linalg.norm(docs, axis=1, keepdims=True)
+    idx = np.empty((33, 10), np.int32)
+    val = np.empty((33, 10), np.float32)
+    N.check(ctx.h, N.lib().fa_similarities_topk(ctx.h, N.ptr(q), 33, N.ptr(docs), 5000, 96, 10, N.ptr(idx),
+                                                N.ptr(val)))
+    oi, ov = O.similarities_topk(q, docs, 10)
+    s64 = q.astype(np.float64) @ docs.T.astype(np.float64)
+    for i in range(33):
+        if not np.array_equal(idx[i], oi[i]):
+            # only a near-tie may reorder: the scores must agree to rounding
+            assert np.allclose(s64[i, idx[i]], s64[i, oi[i]], atol=1e-6), (i, idx[i], oi[i])
+    assert np.abs(val - ov).max() <= 1e-5
+
+
+def test_topk_ties_lower_index_first(ctx):
+    q = np.ones((1, 4), np.float32) * 0.5
+    docs = np.zeros((300, 4), np.float32)
+    docs[[7, 3, 250, 100], :] = 0.5  # equal best scores
+    idx = np.empty((1, 5), np.int32)
+    val = np.empty((1, 5), np.float32)
+    N.check(ctx.h, N.lib().fa_similarities_topk(ctx.h, N.ptr(q), 1, N.ptr(docs), 300, 4, 5, N.ptr(idx), N.ptr(val)))
+    assert idx[0, :4].tolist() == [3, 7, 100, 250]
+    assert idx[0, 4] == 0  # first of the zero scores
