@@ -283,24 +283,30 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
     for (int i = 0; i < ndim; i++) r += (i ? "," : "") + std::to_string(shape[i]);
     return r + "]";
   };
-  // matrix [rows, cols] -> bf16 rows at dst (row stride cols), with an
-  // optional row remap (dst row of source row r)
+  // matrix [rows, cols] -> bf16 rows at dst (row stride cols); source row r
+  // goes to destination row dst_row(r), copied in runs of consecutive rows
   auto put_matrix = [&](uint16_t* dst, int64_t rows, int64_t cols, auto&& dst_row) -> int {
-    std::vector<uint16_t> tmp((size_t)rows * cols);
-    if (dtype == FA_DT_BF16) {
-      const uint16_t* src = (const uint16_t*)data;
-      for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[(size_t)dst_row(r) * cols], src + r * cols, cols * 2);
-    } else {
+    std::vector<uint16_t> tmp;
+    const uint16_t* src16 = (const uint16_t*)data;
+    if (dtype == FA_DT_F32) {
+      tmp.resize((size_t)rows * cols);
       const float* src = (const float*)data;
       for (int64_t r = 0; r < rows; r++)
         for (int64_t k = 0; k < cols; k++)
-          if (!fa::bf16_exact(src[r * cols + k], &tmp[(size_t)dst_row(r) * cols + k]))
+          if (!fa::bf16_exact(src[r * cols + k], &tmp[(size_t)r * cols + k]))
             return set_error(ctx, FA_ERR_UNSUPPORTED,
                              "gemma: weight %s is not exactly representable in bf16 (row %lld col %lld); this build "
                              "keeps matrices bf16-resident",
                              name, (long long)r, (long long)k);
+      src16 = tmp.data();
     }
-    FA_HIP_CHECK(ctx, hipMemcpy(dst, tmp.data(), tmp.size() * 2, hipMemcpyHostToDevice));
+    for (int64_t r0 = 0; r0 < rows;) {
+      int64_t r1 = r0 + 1;
+      while (r1 < rows && dst_row(r1) == dst_row(r1 - 1) + 1) r1++;
+      FA_HIP_CHECK(ctx, hipMemcpy(dst + (size_t)dst_row(r0) * cols, src16 + (size_t)r0 * cols,
+                                  (size_t)(r1 - r0) * cols * 2, hipMemcpyHostToDevice));
+      r0 = r1;
+    }
     return FA_OK;
   };
   auto identity = [](int64_t r) { return r; };

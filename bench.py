@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Throughput of the EmbeddingGemma encoder forward on one MI355X.
+
+One step = one forward pass (token ids -> 768-d L2-normalised embeddings) of
+the BASELINE.json workload named by --config (default C2: batch 32 x seq 256,
+lengths uniform in [64, 256], Zipf ids), with random-init bf16-resident
+weights of the EmbeddingGemma-300M architecture. Inputs are resident in HBM
+before the timed region; outputs stay there.
+
+Prints ONE JSON line (the driver's contract) with:
+  value            sentences/s over the timed steps (whole job, 1 GPU)
+  roofline         the dominant kernel (the gate|up GEMM with the GeGLU
+                   epilogue) timed with HIP events on the library's stream:
+                   algorithmic flops (2*M*N*K) / mean launch duration vs the
+                   157.3 TFLOP/s fp32-MFMA peak
+  cpu_baseline     the CPU oracle (a port of the reference's Go path, the Go
+                   toolchain being absent) on a bounded sample of the same
+                   workload, on this host's cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP32_MFMA_PEAK = 157.3e12  # MI355X dense fp32 matrix, FLOP/s
+HBM_PEAK = 8.0e12          # MI355X HBM3E, B/s
+
+METRIC = "sentences/sec @ batch32×seq256 on 1 MI355X; GEMM % of fp32 MFMA peak"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--profile-pass", action="store_true", default=True)
+    return p.parse_args()
+
+
+def cpu_baseline(batch, budget_s: float) -> dict:
+    """The oracle on consecutive groups of 4 sequences of the workload (each
+    padded to its own longest, as the reference's embedBatch pads), until the
+    budget is spent. Test infrastructure used as the checker-side baseline."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    from ai_amd import synth as S
+    om = O.OracleModel(S.ModelShape())
+    om.load_synthetic()
+    group = 4
+    done = tokens = 0
+    elapsed = 0.0
+    i = 0
+    while elapsed < budget_s or done == 0:
+        sl = slice(i, i + group)
+        L = batch.lengths[sl]
+        if L.size == 0:
+            i = 0
+            continue
+        Tm = int(L.max())
+        t0 = time.perf_counter()
+        om.embed(batch.ids[sl, :Tm], L)
+        elapsed += time.perf_counter() - t0
+        done += L.size
+        tokens += int(L.sum())
+        i += group
+    om.close()
+    threads = O.lib().orc_num_threads()
+    return {"value": round(done / elapsed, 3), "unit": "sentences/s", "cores": threads, "kind": "port",
+            "sample": f"{done} sequences of {batch.name} in groups of {group}, each padded to its group's max "
+                      f"length ({tokens} valid tokens, {elapsed:.1f} s, {O.isa()}, OMP threads {threads})",
+            "tokens_per_s": round(tokens / elapsed, 1)}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); data-parallel sharding over "
+              f"sentences is described in DESIGN.md but not run", file=sys.stderr)
+        sys.exit(2)
+    from ai_amd import _native as N
+    from ai_amd import gemma as G
+    from ai_amd import synth as S
+
+    ctx = N.Context(0)
+    shape = S.ModelShape()
+    model = G.Model(shape, ctx)
+    model.load_synthetic()
+    batch = S.make_batch(a.config, with_corpus=False)
+    B, T = batch.B, batch.T
+    # inputs resident in HBM before timing
+    import ctypes as C
+    d_ids, d_out = C.c_void_p(), C.c_void_p()
+    N.check(ctx.h, N.lib().fa_device_alloc(ctx.h, batch.ids.nbytes, C.byref(d_ids)))
+    N.check(ctx.h, N.lib().fa_device_alloc(ctx.h, B * model.Dim() * 4, C.byref(d_out)))
+    N.check(ctx.h, N.lib().fa_memcpy_h2d(ctx.h, d_ids, batch.ids.ctypes.data, batch.ids.nbytes))
+
+    def step():
+        model.embed_ids_dev(d_ids.value, batch.lengths, B, T, d_out.value)
+
+    for _ in range(a.warmup):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / a.steps * 1e3
+    sent_s = B * a.steps / elapsed
+    tok_s = batch.tokens * a.steps / elapsed
+
+    # Second pass over the same steps with every launch bracketed by HIP events.
+    model.set_profiling(True)
+    model.reset_stats()
+    t1 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    ctx.sync()
+    prof_ms = (time.perf_counter() - t1) / a.steps * 1e3
+    stats = model.kernel_stats()
+    model.set_profiling(False)
+
+    def kstat(name):
+        s = stats[name]
+        avg_ms = s["ms"] / max(1, s["launches"])
+        per = s["flops"] / max(1, s["launches"])
+        perb = s["bytes"] / max(1, s["launches"])
+        return s, avg_ms, per, perb
+
+    gs, g_ms, g_flops, _ = kstat("gemm_gateup")
+    achieved = g_flops / (g_ms * 1e-3) if g_ms > 0 else 0.0
+    roofline = {"kernel": "gemm_kernel<bf16,NK,fast,GeGLU> (gate|up, M=%d N=2304 K=768)" % batch.tokens,
+                "bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": FP32_MFMA_PEAK / 1e12,
+                "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK, 4), "traffic": None,
+                "launch_ms": round(g_ms, 4), "flops_per_launch": g_flops}
+    kernels = {}
+    gemm_fl = gemm_ms = 0.0
+    for name in N.KERNEL_KINDS:
+        s, avg_ms, per, perb = kstat(name)
+        if s["launches"] == 0:
+            continue
+        e = {"launches_per_step": s["launches"] / a.steps, "ms_per_step": round(s["ms"] / a.steps, 4)}
+        if s["flops"]:
+            e["tflops"] = round(s["flops"] / (s["ms"] * 1e-3) / 1e12, 2)
+            e["frac_fp32_mfma"] = round(s["flops"] / (s["ms"] * 1e-3) / FP32_MFMA_PEAK, 4)
+        if s["bytes"]:
+            e["GBps"] = round(s["bytes"] / (s["ms"] * 1e-3) / 1e9, 1)
+            e["frac_hbm"] = round(s["bytes"] / (s["ms"] * 1e-3) / HBM_PEAK, 4)
+        kernels[name] = e
+        if name.startswith("gemm"):
+            gemm_fl += s["flops"]
+            gemm_ms += s["ms"]
+    gemm_all = {"tflops": round(gemm_fl / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else 0,
+                "frac_fp32_mfma": round(gemm_fl / (gemm_ms * 1e-3) / FP32_MFMA_PEAK, 4) if gemm_ms else 0,
+                "ms_per_step": round(gemm_ms / a.steps, 3)}
+
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(batch, a.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(sent_s, 2),
+        "unit": "sentences/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init bf16 weights N(0,0.02), Zipf(1.1) token ids; seeded)",
+        "config": {"workload": f"{a.config}: EmbeddingGemma-300M encoder forward, batch {B} x seq {T}, "
+                               f"lengths {int(batch.lengths.min())}..{int(batch.lengths.max())}",
+                   "batch": B, "seq_len": T, "valid_tokens": batch.tokens},
+        "tokens_per_s": round(tok_s, 1),
+        "roofline": roofline,
+        "gemm_all": gemm_all,
+        "kernels": kernels,
+        "profiled_ms_per_step": round(prof_ms, 3),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    N.lib().fa_device_free(ctx.h, d_ids)
+    N.lib().fa_device_free(ctx.h, d_out)
+    model.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

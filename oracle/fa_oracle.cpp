@@ -537,8 +537,9 @@ ORC_API void orc_model_destroy(void* p) { delete (OrcModel*)p; }
 // transpose [out, in] -> [in, out] (model.go:121-127)
 static std::vector<float> transpose_w(const float* w, int out, int in) {
   std::vector<float> t((size_t)in * out);
-  for (int o = 0; o < out; o++)
-    for (int i = 0; i < in; i++) t[(size_t)i * out + o] = w[(size_t)o * in + i];
+#pragma omp parallel for schedule(static)
+  for (int i = 0; i < in; i++)
+    for (int o = 0; o < out; o++) t[(size_t)i * out + o] = w[(size_t)o * in + i];
   return t;
 }
 // norm: w + 1 (model.go:131-140)
@@ -598,6 +599,7 @@ ORC_API int orc_model_set(void* p, const char* name, const float* data, i64 nume
 // [in, out] (model.go:210-222).
 static std::vector<float> fold(const std::vector<float>& w, const std::vector<float>& g, int in, int out) {
   std::vector<float> r((size_t)in * out);
+#pragma omp parallel for schedule(static)
   for (int i = 0; i < in; i++)
     for (int o = 0; o < out; o++) r[(size_t)i * out + o] = w[(size_t)i * out + o] * g[i];
   return r;
