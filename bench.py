@@ -35,6 +35,12 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, B/s
 
 METRIC = "sentences/sec @ batch32×seq256 on 1 MI355X; GEMM % of fp32 MFMA peak"
 
+# HBM bytes per launch of the gate|up GEMM at C2, from rocprofv3 FETCH_SIZE
+# (x2.000) + WRITE_SIZE (x1.000) runs scaled by a 1 GiB copy kernel's
+# readings; see profiles/gemm_gateup_c2_hbm_traffic.md. Re-measured whenever
+# the kernel changes; applies to the C2 workload only.
+GATEUP_TRAFFIC_C2 = {"bytes": (75.3 + 24.2) * 2 ** 20, "kernel_rev": "gemm128x128x32-v1"}
+
 
 def parse():
     p = argparse.ArgumentParser()
@@ -44,8 +50,22 @@ def parse():
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--profile-pass", action="store_true", default=True)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 1 GiB device copy (torch) 3 times: the reference kernel for scaling "
+                        "rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     return p.parse_args()
+
+
+def calibrate_copy() -> None:
+    import torch
+    n = 1 << 28  # floats: 1 GiB
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 3}))
 
 
 def cpu_baseline(batch, budget_s: float) -> dict:
@@ -84,6 +104,9 @@ def cpu_baseline(batch, budget_s: float) -> dict:
 
 def main():
     a = parse()
+    if a.calibrate_copy:
+        calibrate_copy()
+        return
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); data-parallel sharding over "
               f"sentences is described in DESIGN.md but not run", file=sys.stderr)
@@ -142,7 +165,8 @@ def main():
     achieved = g_flops / (g_ms * 1e-3) if g_ms > 0 else 0.0
     roofline = {"kernel": "gemm_kernel<bf16,NK,fast,GeGLU> (gate|up, M=%d N=2304 K=768)" % batch.tokens,
                 "bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": FP32_MFMA_PEAK / 1e12,
-                "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK, 4),
+                "traffic": GATEUP_TRAFFIC_C2["bytes"] if a.config == "C2" else None,
                 "launch_ms": round(g_ms, 4), "flops_per_launch": g_flops}
     kernels = {}
     gemm_fl = gemm_ms = 0.0
