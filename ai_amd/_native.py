@@ -65,6 +65,8 @@ _SIGS = {
     "fa_memcpy_d2h": (C.c_int, [vp, vp, vp, C.c_size_t]),
     "fa_matmul_fused": (C.c_int, [vp, i64, i64, i64, vp, i64, vp, i64, C.c_int, C.c_int, C.POINTER(Epilogue), vp,
                                   i64]),
+    "fa_matmul_fused_dev": (C.c_int, [vp, i64, i64, i64, vp, i64, vp, i64, C.c_int, C.c_int, C.POINTER(Epilogue),
+                                      vp, i64]),
     "fa_row_sum_squares": (C.c_int, [vp, vp, i64, i64, vp]),
     "fa_rmsnorm": (C.c_int, [vp, vp, vp, f32, i64, i64, vp]),
     "fa_rope": (C.c_int, [vp, vp, f64, vp, i64, i32, i32, vp]),

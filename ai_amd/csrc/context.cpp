@@ -219,6 +219,33 @@ int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a
   return FA_OK;
 }
 
+int fa_matmul_fused_dev(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
+                        int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "MatMulFused: ctx is NULL");
+  if (m < 0 || n < 0 || k < 0) return set_error(ctx, FA_ERR_ARG, "MatMulFused: negative size");
+  if (b_dtype != FA_DT_F32 && b_dtype != FA_DT_BF16)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown B dtype %d", b_dtype);
+  if (b_layout != FA_B_KN && b_layout != FA_B_NK)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown B layout %d", b_layout);
+  const int64_t brow = b_layout == FA_B_KN ? n : k, bcnt = b_layout == FA_B_KN ? k : n;
+  if ((lda < k && m > 0) || (ldb < brow && bcnt > 0) || (ldc < n && m > 0))
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: leading dimension too small");
+  if (e && e->act != FA_ACT_NONE && e->act != FA_ACT_RELU && e->act != FA_ACT_GELU)
+    return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown activation %d", e->act);
+  if (m == 0 || n == 0) return FA_OK;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  fa::GemmArgs g;
+  g.m = m; g.n = n; g.k = k;
+  g.a = a; g.lda = lda; g.b = b; g.ldb = ldb; g.b_dtype = b_dtype; g.b_layout = b_layout;
+  g.c = c; g.ldc = ldc;
+  if (e && (e->bias || e->row_scale || e->act != FA_ACT_NONE || e->mul || e->residual)) {
+    g.epi = fa::Epi::Generic;
+    g.bias = e->bias; g.row_scale = e->row_scale; g.act = e->act;
+    g.mul = e->mul; g.ldm = e->ldm; g.residual = e->residual; g.ldr = e->ldr;
+  }
+  return fa::launch_gemm(ctx, g, ctx->stream);
+}
+
 int fa_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out) {
   if (!ctx) return set_error(ctx, FA_ERR_ARG, "RowSumSquares: ctx is NULL");
   if (m < 0 || n < 0) return set_error(ctx, FA_ERR_ARG, "RowSumSquares: negative shape");

@@ -1,14 +1,17 @@
 // fp32-accumulate MFMA GEMM for gfx950: C = epilogue(A . B).
 //
 // A: fp32 [m x k] row-major. B: logical [k x n], stored bf16 or fp32, either
-// as [n x k] rows (checkpoint [out,in] weights, docs) or [k x n] rows. The
-// workgroup computes a 128x128 tile of C with four waves (2x2), each wave a
-// 64x64 sub-tile as 2x2 blocks of v_mfma_f32_32x32x2_f32 (16 accumulators
-// per lane per block). K advances in slabs of 32 through two LDS buffers:
-// the next slab's global loads are issued before the current slab's MFMAs
-// and written to the other buffer afterwards, so one barrier per slab
-// suffices. bf16 weights are widened to fp32 (exact) when they are written
-// to LDS, so the MFMA operands are always fp32.
+// as [n x k] rows (checkpoint [out,in] weights, docs) or [k x n] rows. A
+// workgroup computes a BM x BN tile of C with WM x WN waves; each wave owns a
+// (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks of v_mfma_f32_32x32x2_f32
+// (16 accumulators per lane per block). K advances in slabs of BK through two
+// LDS buffers: the next slab's global loads are issued at the top of a slab,
+// written to the other buffer before the slab's last MFMA step, and one
+// barrier per slab separates the buffers. The first operand reads of the next
+// slab are issued right after that barrier, so their latency overlaps the
+// current slab's last MFMAs; within a slab the operands of step s+1 are read
+// while the MFMAs of step s run. bf16 weights are widened to fp32 (exact) when
+// written to LDS, so the MFMA operands are always fp32.
 //
 // MFMA operand layout (32x32x2, one block): lane l supplies A[row l%32][k]
 // and B[k][col l%32] with k = l/32; the 16 results of lane l are C[row][col]
@@ -18,11 +21,23 @@
 // k = 8s..8s+3 and lanes 32-63 take k = 8s+4..8s+7, and MFMA number c (0..3)
 // pairs k = 8s+c with 8s+4+c on both operands.
 //
+// Work distribution: one workgroup per tile, XCD-aware tile order. The tile
+// shape is chosen per call from the output's tile count: 64x64 tiles (four
+// or more resident workgroups per CU, fine-grained balance over the 256 CUs)
+// until the 128x128 tiles fill several rounds of the CUs, 128x128 beyond.
+// A stream-K distribution (equal shares of (tile, K-slab) units plus a fixup
+// pass over split tiles) measured slower at these sizes: the fixup pass alone
+// costs 45-60 us at the C2 shapes.
+//
 // Epilogues: None; Generic (bias, row scale, activation, element-wise
 // multiply, residual: the reference's order, internal/blas/gemm.go:276-347);
-// GeGLU (the gate and up weights interleaved in 32-row groups, so each wave's
-// two column blocks hold gate and up of the same 32 features and the lane
+// GeGLU (gate and up weights interleaved in 32-row groups, so a wave's column
+// blocks 2p and 2p+1 hold gate and up of the same 32 features and the lane
 // writes gelu_tanh(gate) * up, models/gemma/embed.go:226-227).
+
+#include <cstdlib>
+#include <algorithm>
+#include <cstring>
 
 #include "fa_internal.h"
 #include "device_math.h"
@@ -33,9 +48,25 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int LDSK = BK + 4;  // padded LDS row stride (floats): rows start 4 banks apart
-constexpr int NTHREADS = 256;
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN;
+  static constexpr int FM = TM / 32, FN = TN / 32;
+  static constexpr int LDSK = BK + 4;  // padded LDS row stride (floats): rows start 4 banks apart
+  static constexpr int S = BK / 8;     // MFMA steps (of 4 MFMA k-pairs) per slab
+  static constexpr int ACC = FM * FN * 16;  // accumulators per lane
+  static_assert(TM % 32 == 0 && TN % 32 == 0 && BK % 8 == 0, "tile shape");
+  static_assert((BM * BK / 4) % NT == 0 && (BN * BK / 8) % NT == 0 && (BN * BK / 4) % NT == 0, "loader shape");
+  static_assert((BM * BK) % NT == 0 && (BN * BK) % NT == 0, "checked loader shape");
+};
+
+// Tile shapes compiled into the library.
+using T128x128 = Tile<128, 128, 32, 2, 2>;  // 4 waves of 64x64
+using T64x64 = Tile<64, 64, 32, 2, 2>;      // 4 waves of 32x32
+using T128x64v = Tile<128, 64, 32, 4, 1>;   // 4 waves of 32x64 (column-block pairs for GeGLU)
+using T64x128 = Tile<64, 128, 32, 2, 2>;    // 4 waves of 32x64
 
 struct GemmParams {
   int64_t m, n, k;
@@ -53,86 +84,87 @@ struct GemmParams {
   int64_t ldr;
   int act;
   int tiles_m, tiles_n;
+  int nk;  // K slabs per tile
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-template <bool BBF16, bool BNK, bool FAST, Epi EPI>
-__global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmParams p) {
+template <class TL, bool BBF16, bool BNK, bool FAST, Epi EPI>
+__global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmParams p) {
+  constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, NT = TL::NT, LDSK = TL::LDSK;
+  constexpr int FM = TL::FM, FN = TL::FN, S = TL::S;
   __shared__ __attribute__((aligned(16))) float As[2][BM * LDSK];
   __shared__ __attribute__((aligned(16))) float Bs[2][BN * LDSK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const int total = p.tiles_m * p.tiles_n;
-  int tile = blockIdx.x;
-  {
-    // XCD-aware: give each XCD a contiguous run of tiles (row-major over n).
-    constexpr int kXcd = 8;
-    int per = total / kXcd;
-    if (per > 0 && tile < per * kXcd) tile = (tile % kXcd) * per + tile / kXcd;
-  }
-  const int tm = tile / p.tiles_n, tn = tile % p.tiles_n;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
   const int64_t M = p.m, N = p.n, K = p.k;
   const float* __restrict__ A = p.a;
 
+  int64_t m0 = 0, n0 = 0;  // current tile origin
+
   // ---- global -> register staging ----
-  f32x4 ra[4];
-  uint32_t rbh[2][4];  // bf16 pairs (FAST bf16 path)
-  f32x4 rbf[4];        // fp32 B (FAST f32 path)
-  float rs_a[16], rs_b[16];  // checked path
+  constexpr int NA = BM * BK / 4 / NT;   // float4 of A per thread
+  constexpr int NBH = BN * BK / 8 / NT;  // 8 x bf16 of B per thread
+  constexpr int NBF = BN * BK / 4 / NT;  // float4 of fp32 B per thread
+  constexpr int NCA = BM * BK / NT;      // checked path: elements per thread
+  constexpr int NCB = BN * BK / NT;
+  f32x4 ra[FAST ? NA : 1];
+  uint4 rbh[(FAST && BBF16) ? NBH : 1];
+  f32x4 rbf[(FAST && !BBF16) ? NBF : 1];
+  float rs_a[FAST ? 1 : NCA], rs_b[FAST ? 1 : NCB];
 
   auto load_global = [&](int64_t k0) {
     if constexpr (FAST) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        int row = (tid >> 3) + 32 * i, col = (tid & 7) * 4;
-        int64_t gr = min(m0 + row, M - 1);
+      for (int i = 0; i < NA; i++) {
+        const int idx = tid + NT * i;
+        const int row = idx / (BK / 4), col = (idx % (BK / 4)) * 4;
+        const int64_t gr = min(m0 + row, M - 1);
         ra[i] = *reinterpret_cast<const f32x4*>(A + gr * p.lda + k0 + col);
       }
       if constexpr (BBF16) {
         const uint16_t* B = static_cast<const uint16_t*>(p.b);
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-          int row = (tid >> 2) + 64 * i, col = (tid & 3) * 8;
-          int64_t gn = min(n0 + row, N - 1);
-          uint4 v = *reinterpret_cast<const uint4*>(B + gn * p.ldb + k0 + col);
-          rbh[i][0] = v.x; rbh[i][1] = v.y; rbh[i][2] = v.z; rbh[i][3] = v.w;
+        for (int i = 0; i < NBH; i++) {
+          const int idx = tid + NT * i;
+          const int row = idx / (BK / 8), col = (idx % (BK / 8)) * 8;
+          const int64_t gn = min(n0 + row, N - 1);
+          rbh[i] = *reinterpret_cast<const uint4*>(B + gn * p.ldb + k0 + col);
         }
       } else {
         const float* B = static_cast<const float*>(p.b);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          int row = (tid >> 3) + 32 * i, col = (tid & 7) * 4;
-          int64_t gn = min(n0 + row, N - 1);
+        for (int i = 0; i < NBF; i++) {
+          const int idx = tid + NT * i;
+          const int row = idx / (BK / 4), col = (idx % (BK / 4)) * 4;
+          const int64_t gn = min(n0 + row, N - 1);
           rbf[i] = *reinterpret_cast<const f32x4*>(B + gn * p.ldb + k0 + col);
         }
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        int idx = tid + NTHREADS * i;
-        int row = idx >> 5, col = idx & 31;
-        int64_t gr = m0 + row, gk = k0 + col;
+      for (int i = 0; i < NCA; i++) {
+        const int idx = tid + NT * i;
+        const int row = idx / BK, col = idx % BK;
+        const int64_t gr = m0 + row, gk = k0 + col;
         rs_a[i] = (gr < M && gk < K) ? A[gr * p.lda + gk] : 0.f;
       }
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        int idx = tid + NTHREADS * i;
+      for (int i = 0; i < NCB; i++) {
+        const int idx = tid + NT * i;
         int nn, kk;
         if constexpr (BNK) {
-          nn = idx >> 5; kk = idx & 31;
+          nn = idx / BK; kk = idx % BK;
         } else {
-          nn = idx & 127; kk = idx >> 7;
+          nn = idx % BN; kk = idx / BN;
         }
-        int64_t gn = n0 + nn, gk = k0 + kk;
+        const int64_t gn = n0 + nn, gk = k0 + kk;
         float v = 0.f;
         if (gn < N && gk < K) {
-          int64_t off = BNK ? gn * p.ldb + gk : gk * p.ldb + gn;
+          const int64_t off = BNK ? gn * p.ldb + gk : gk * p.ldb + gn;
           if constexpr (BBF16) v = bf16_to_f32(static_cast<const uint16_t*>(p.b)[off]);
           else v = static_cast<const float*>(p.b)[off];
         }
@@ -144,141 +176,239 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmParams p) {
   auto store_lds = [&](int buf) {
     if constexpr (FAST) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        int row = (tid >> 3) + 32 * i, col = (tid & 7) * 4;
+      for (int i = 0; i < NA; i++) {
+        const int idx = tid + NT * i;
+        const int row = idx / (BK / 4), col = (idx % (BK / 4)) * 4;
         *reinterpret_cast<f32x4*>(&As[buf][row * LDSK + col]) = ra[i];
       }
       if constexpr (BBF16) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-          int row = (tid >> 2) + 64 * i, col = (tid & 3) * 8;
+        for (int i = 0; i < NBH; i++) {
+          const int idx = tid + NT * i;
+          const int row = idx / (BK / 8), col = (idx % (BK / 8)) * 8;
           f32x4 lo, hi;
-          lo.x = __uint_as_float(rbh[i][0] << 16); lo.y = __uint_as_float(rbh[i][0] & 0xFFFF0000u);
-          lo.z = __uint_as_float(rbh[i][1] << 16); lo.w = __uint_as_float(rbh[i][1] & 0xFFFF0000u);
-          hi.x = __uint_as_float(rbh[i][2] << 16); hi.y = __uint_as_float(rbh[i][2] & 0xFFFF0000u);
-          hi.z = __uint_as_float(rbh[i][3] << 16); hi.w = __uint_as_float(rbh[i][3] & 0xFFFF0000u);
+          lo.x = __uint_as_float(rbh[i].x << 16); lo.y = __uint_as_float(rbh[i].x & 0xFFFF0000u);
+          lo.z = __uint_as_float(rbh[i].y << 16); lo.w = __uint_as_float(rbh[i].y & 0xFFFF0000u);
+          hi.x = __uint_as_float(rbh[i].z << 16); hi.y = __uint_as_float(rbh[i].z & 0xFFFF0000u);
+          hi.z = __uint_as_float(rbh[i].w << 16); hi.w = __uint_as_float(rbh[i].w & 0xFFFF0000u);
           *reinterpret_cast<f32x4*>(&Bs[buf][row * LDSK + col]) = lo;
           *reinterpret_cast<f32x4*>(&Bs[buf][row * LDSK + col + 4]) = hi;
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          int row = (tid >> 3) + 32 * i, col = (tid & 7) * 4;
+        for (int i = 0; i < NBF; i++) {
+          const int idx = tid + NT * i;
+          const int row = idx / (BK / 4), col = (idx % (BK / 4)) * 4;
           *reinterpret_cast<f32x4*>(&Bs[buf][row * LDSK + col]) = rbf[i];
         }
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        int idx = tid + NTHREADS * i;
-        As[buf][(idx >> 5) * LDSK + (idx & 31)] = rs_a[i];
+      for (int i = 0; i < NCA; i++) {
+        const int idx = tid + NT * i;
+        As[buf][(idx / BK) * LDSK + (idx % BK)] = rs_a[i];
       }
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        int idx = tid + NTHREADS * i;
+      for (int i = 0; i < NCB; i++) {
+        const int idx = tid + NT * i;
         int nn, kk;
         if constexpr (BNK) {
-          nn = idx >> 5; kk = idx & 31;
+          nn = idx / BK; kk = idx % BK;
         } else {
-          nn = idx & 127; kk = idx >> 7;
+          nn = idx % BN; kk = idx / BN;
         }
         Bs[buf][nn * LDSK + kk] = rs_b[i];
       }
     }
   };
 
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-  const int nk = (int)((K + BK - 1) / BK);
-  load_global(0);
-  store_lds(0);
-  __syncthreads();
-
-  const int arow = wm * 64 + (lane & 31);
-  const int brow = wn * 64 + (lane & 31);
+  const int arow = wm * TL::TM + (lane & 31);
+  const int brow = wn * TL::TN + (lane & 31);
   const int kofs = (lane >> 5) * 4;
+  auto read_ops = [&](int buf, int s, f32x4 (&oa)[FM], f32x4 (&ob)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+      oa[i] = *reinterpret_cast<const f32x4*>(&As[buf][(arow + 32 * i) * LDSK + s * 8 + kofs]);
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+      ob[j] = *reinterpret_cast<const f32x4*>(&Bs[buf][(brow + 32 * j) * LDSK + s * 8 + kofs]);
+  };
 
-  for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_global((int64_t)(kt + 1) * BK);
-    const float* as = As[buf];
-    const float* bs = Bs[buf];
+  f32x16 acc[FM][FN];
+
+  // acc = A[m0:m0+BM, slabs kb..ke) . B[slabs kb..ke), n0:n0+BN]
+  auto mainloop = [&](int kb, int ke) {
 #pragma unroll
-    for (int s = 0; s < BK / 8; s++) {
-      f32x4 a0 = *reinterpret_cast<const f32x4*>(&as[arow * LDSK + s * 8 + kofs]);
-      f32x4 a1 = *reinterpret_cast<const f32x4*>(&as[(arow + 32) * LDSK + s * 8 + kofs]);
-      f32x4 b0 = *reinterpret_cast<const f32x4*>(&bs[brow * LDSK + s * 8 + kofs]);
-      f32x4 b1 = *reinterpret_cast<const f32x4*>(&bs[(brow + 32) * LDSK + s * 8 + kofs]);
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[c], b0[c], acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[c], b1[c], acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[c], b0[c], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[c], b1[c], acc[1][1], 0, 0, 0);
-      }
-    }
-    if (kt + 1 < nk) store_lds(buf ^ 1);
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+    if (ke <= kb) return;
+    f32x4 ca[FM], cb[FN];  // operands of the current step
+    __syncthreads();       // the LDS buffers may still be read by a previous tile
+    load_global((int64_t)kb * BK);
+    store_lds(0);
     __syncthreads();
-  }
-
-  // ---- epilogue ----
-  const int lcol = lane & 31;
-  const int lrow4 = (lane >> 5) * 4;
-  if constexpr (EPI == Epi::GeGLU) {
-    // wave's block 0 = gate features, block 1 = up features (same 32 features)
-    const int64_t fcol = n0 / 2 + wn * 32 + lcol;
-    const int64_t F = N / 2;
+    read_ops(0, 0, ca, cb);
+    for (int kt = kb; kt < ke; kt++) {
+      const int buf = (kt - kb) & 1;
+      const bool more = kt + 1 < ke;
+      if (more) load_global((int64_t)(kt + 1) * BK);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+      for (int s = 0; s < S; s++) {
+        f32x4 na[FM], nb[FN];
+        if (s + 1 < S) {
+          read_ops(buf, s + 1, na, nb);
+        } else if (more) {
+          store_lds(buf ^ 1);
+          __syncthreads();
+          read_ops(buf ^ 1, 0, na, nb);
+        }
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
-        if (row < M && fcol < F) {
-          float g = acc[i][0][r], u = acc[i][1][r];
-          p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+          for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[i][c], cb[j][c], acc[i][j], 0, 0, 0);
+        if (s + 1 < S || more) {
+#pragma unroll
+          for (int i = 0; i < FM; i++) ca[i] = na[i];
+#pragma unroll
+          for (int j = 0; j < FN; j++) cb[j] = nb[j];
         }
       }
     }
-  } else {
+  };
+
+  const int lcol = lane & 31;
+  const int lrow4 = (lane >> 5) * 4;
+  auto store_tile = [&]() {
+    if constexpr (EPI == Epi::GeGLU) {
+      static_assert(FN % 2 == 0, "GeGLU pairs column blocks");
+      const int64_t F = N / 2;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+      for (int pj = 0; pj < FN / 2; pj++) {
+        const int64_t fcol = (n0 + wn * TL::TN) / 2 + pj * 32 + lcol;
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int64_t col = n0 + wn * 64 + j * 32 + lcol;
+        for (int i = 0; i < FM; i++) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
-          if (row < M && col < N) {
-            float v = acc[i][j][r];
-            if constexpr (EPI == Epi::Generic) {
-              if (p.bias) v = v + p.bias[col];
-              if (p.row_scale) v = v * p.row_scale[row];
-              if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
-              else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
-              if (p.mul) v = v * p.mul[row * p.ldm + col];
-              if (p.residual) v = v + p.residual[row * p.ldr + col];
+          for (int r = 0; r < 16; r++) {
+            const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
+            if (row < M && fcol < F) {
+              const float g = acc[i][2 * pj][r], u = acc[i][2 * pj + 1][r];
+              p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
             }
-            p.c[row * p.ldc + col] = v;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const int64_t col = n0 + wn * TL::TN + j * 32 + lcol;
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
+            if (row < M && col < N) {
+              float v = acc[i][j][r];
+              if constexpr (EPI == Epi::Generic) {
+                if (p.bias) v = v + p.bias[col];
+                if (p.row_scale) v = v * p.row_scale[row];
+                if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
+                else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
+                if (p.mul) v = v * p.mul[row * p.ldm + col];
+                if (p.residual) v = v + p.residual[row * p.ldr + col];
+              }
+              p.c[row * p.ldc + col] = v;
+            }
           }
         }
       }
     }
+  };
+
+  auto set_tile = [&](int tile) {
+    const int tm = tile / p.tiles_n, tn = tile % p.tiles_n;
+    m0 = (int64_t)tm * BM;
+    n0 = (int64_t)tn * BN;
+  };
+
+  const int total = p.tiles_m * p.tiles_n;
+  int tile = blockIdx.x;
+  {
+    // XCD-aware: workgroup ids are dealt to the 8 XCDs round-robin; give each
+    // XCD a contiguous run of tiles (row-major over n) so the tiles sharing A
+    // rows and B columns share that XCD's L2.
+    constexpr int kXcd = 8;
+    const int per = total / kXcd;
+    if (per > 0 && tile < per * kXcd) tile = (tile % kXcd) * per + tile / kXcd;
   }
+  set_tile(tile);
+  mainloop(0, p.nk);
+  store_tile();
 }
 
-template <bool BBF16, bool BNK, bool FAST, Epi EPI>
-void launch_t(const GemmParams& p, hipStream_t s) {
-  dim3 grid(p.tiles_m * p.tiles_n), block(NTHREADS);
-  hipLaunchKernelGGL((gemm_kernel<BBF16, BNK, FAST, EPI>), grid, block, 0, s, p);
+template <class TL, bool BBF16, bool BNK, bool FAST, Epi EPI>
+void launch_dp(GemmParams p, hipStream_t s) {
+  p.tiles_m = (int)((p.m + TL::BM - 1) / TL::BM);
+  p.tiles_n = (int)((p.n + TL::BN - 1) / TL::BN);
+  p.nk = (int)((p.k + TL::BK - 1) / TL::BK);
+  dim3 grid(p.tiles_m * p.tiles_n), block(TL::NT);
+  hipLaunchKernelGGL((gemm_kernel<TL, BBF16, BNK, FAST, EPI>), grid, block, 0, s, p);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+enum class TileId { k128x128 = 0, k64x64, k128x64v, k64x128, kCount };
+const char* const kTileNames[] = {"128x128", "64x64", "128x64v", "64x128"};
+
+// FA_GEMM_TILE=<name> forces a tile shape on the fast path (tuning).
+int forced_tile() {
+  static int v = [] {
+    const char* e = std::getenv("FA_GEMM_TILE");
+    if (!e) return -1;
+    for (int i = 0; i < (int)TileId::kCount; i++)
+      if (std::strcmp(e, kTileNames[i]) == 0) return i;
+    return -1;
+  }();
+  return v;
+}
+
+// Tile choice, from measurements on MI355X (M in 128..32768, N in
+// 768..3072, K in 768..3072): while the 128x128 tiles would give fewer than
+// six per CU, smaller tiles win (more resident workgroups per CU and a finer
+// split over the CUs; 1.5x on the N=768 products at M=5517, 3x at M=128);
+// beyond that the 128x128 tile's operand reuse wins. GeGLU needs an even
+// number of 32-column blocks per wave: 128x64 with four waves stacked in M.
+TileId pick_tile(int64_t m, int64_t n, Epi epi, int cus) {
+  const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128);
+  if (tiles128 >= 6LL * cus) return TileId::k128x128;
+  return epi == Epi::GeGLU ? TileId::k128x64v : TileId::k64x64;
+}
+
+template <class TL, bool BBF16>
+void dispatch_fast(const GemmParams& p, Epi epi, hipStream_t s) {
+  switch (epi) {
+    case Epi::None: launch_dp<TL, BBF16, true, true, Epi::None>(p, s); break;
+    case Epi::Generic: launch_dp<TL, BBF16, true, true, Epi::Generic>(p, s); break;
+    case Epi::GeGLU:
+      if constexpr (TL::FN % 2 == 0) launch_dp<TL, BBF16, true, true, Epi::GeGLU>(p, s);
+      break;
+  }
+}
+
+template <bool BBF16>
+void dispatch_tile(TileId t, const GemmParams& p, Epi epi, hipStream_t s) {
+  switch (t) {
+    case TileId::k64x64: dispatch_fast<T64x64, BBF16>(p, epi, s); break;
+    case TileId::k128x64v: dispatch_fast<T128x64v, BBF16>(p, epi, s); break;
+    case TileId::k64x128: dispatch_fast<T64x128, BBF16>(p, epi, s); break;
+    default: dispatch_fast<T128x128, BBF16>(p, epi, s); break;
+  }
+}
 
 }  // namespace
 
@@ -290,41 +420,41 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.epi == Epi::GeGLU && (g.n % 64 != 0))
     return set_error(ctx, FA_ERR_ARG, "GeGLU product needs n (2F) divisible by 64, got %lld", (long long)g.n);
   GemmParams p;
+  std::memset(&p, 0, sizeof p);
   p.m = g.m; p.n = g.n; p.k = g.k;
   p.a = g.a; p.lda = g.lda; p.b = g.b; p.ldb = g.ldb; p.c = g.c; p.ldc = g.ldc;
   p.bias = g.bias; p.row_scale = g.row_scale; p.mul = g.mul; p.ldm = g.ldm;
   p.residual = g.residual; p.ldr = g.ldr; p.act = g.act;
-  int64_t tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
-  if (tm * tn > INT32_MAX) return set_error(ctx, FA_ERR_ARG, "MatMul: too many tiles");
-  p.tiles_m = (int)tm; p.tiles_n = (int)tn;
+  if (((g.m + 63) / 64) * ((g.n + 63) / 64) > INT32_MAX / 4) return set_error(ctx, FA_ERR_ARG, "MatMul: too many tiles");
   const bool bf16 = g.b_dtype == FA_DT_BF16;
   const bool nk = g.b_layout == FA_B_NK;
   // The fast loaders read 16-byte vectors: every row start must be 16-byte
-  // aligned and k a whole number of slabs.
-  const bool fast = nk && g.k > 0 && g.k % BK == 0 && aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 &&
+  // aligned and k a whole number of 32-wide slabs.
+  const bool fast = nk && g.k > 0 && g.k % 32 == 0 && aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 &&
                     (bf16 ? g.ldb % 8 == 0 : g.ldb % 4 == 0);
-  if (g.k == 0) {
-    // empty inner dimension: the product is zero; the epilogue still applies
-  }
-#define FA_DISPATCH_EPI(BB, NK, FT)                                            \
-  switch (g.epi) {                                                           \
-    case Epi::None: launch_t<BB, NK, FT, Epi::None>(p, s); break;            \
-    case Epi::Generic: launch_t<BB, NK, FT, Epi::Generic>(p, s); break;      \
-    case Epi::GeGLU: launch_t<BB, NK, FT, Epi::GeGLU>(p, s); break;          \
-  }
   if (fast) {
-    if (bf16) { FA_DISPATCH_EPI(true, true, true) }
-    else { FA_DISPATCH_EPI(false, true, true) }
+    TileId t = (TileId)forced_tile();
+    if ((int)t < 0 || (g.epi == Epi::GeGLU && t == TileId::k64x64))
+      t = pick_tile(g.m, g.n, g.epi, ctx->cu_count > 0 ? ctx->cu_count : 256);
+    if (bf16) dispatch_tile<true>(t, p, g.epi, s);
+    else dispatch_tile<false>(t, p, g.epi, s);
   } else {
-    if (bf16) {
-      if (nk) { FA_DISPATCH_EPI(true, true, false) }
-      else { FA_DISPATCH_EPI(true, false, false) }
-    } else {
-      if (nk) { FA_DISPATCH_EPI(false, true, false) }
-      else { FA_DISPATCH_EPI(false, false, false) }
-    }
+    using TC = T128x128;
+#define FA_DISPATCH_EPI(BB, NK)                                                      \
+  switch (g.epi) {                                                                   \
+    case Epi::None: launch_dp<TC, BB, NK, false, Epi::None>(p, s); break;           \
+    case Epi::Generic: launch_dp<TC, BB, NK, false, Epi::Generic>(p, s); break;     \
+    case Epi::GeGLU: launch_dp<TC, BB, NK, false, Epi::GeGLU>(p, s); break;         \
   }
+    if (bf16) {
+      if (nk) { FA_DISPATCH_EPI(true, true) }
+      else { FA_DISPATCH_EPI(true, false) }
+    } else {
+      if (nk) { FA_DISPATCH_EPI(false, true) }
+      else { FA_DISPATCH_EPI(false, false) }
+    }
 #undef FA_DISPATCH_EPI
+  }
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

@@ -101,6 +101,11 @@ typedef struct fa_epilogue {
 int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
                     int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc);
 
+/* Device-pointer variant of fa_matmul_fused: a, b, c and the epilogue's
+ * arrays are device pointers; enqueues on fa_stream(ctx) and returns. */
+int fa_matmul_fused_dev(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
+                        int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc);
+
 /* out[i] = sum_j x[i,j]^2 for row-major x [m x n].
  * Replaces (*Tensor).RowSumSquares (tensor/matmul_fused.go:125-143). */
 int fa_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out);
