@@ -13,21 +13,25 @@
 // 97-107; models/gemma/embed.go:168-186).
 //
 // MFMA formulation (v_mfma_f32_16x16x4_f32; lane l of a 16x16 result holds
-// column l%16 and rows 4*(l/16)+r, r=0..3): each wave owns 16 queries of one
-// head and computes the TRANSPOSED products
-//     S^T[key, query] = K . Q^T        (A = K tile from LDS, B = Q in VGPRs)
-//     O^T[d, query]  += V^T . P^T      (A = V^T tile from LDS, B = P in VGPRs)
-// so that every lane's accumulators belong to a single query (column l%16):
-// the probabilities computed from S^T are already in the B-operand layout of
-// the second product, and the online-softmax rescale of O^T is a per-lane
-// scalar. Within a 16-wide k step each lane group g = l/16 takes 4
-// consecutive k values (one 16-byte LDS read); MFMA c (0..3) pairs them, which
-// is a permutation of the k sum.
+// column l%16 and rows 4*(l/16)+r, r=0..3). A workgroup is two waves; each
+// wave owns 16 queries of one head. Per tile of 16 keys it computes
+//     S^T[key, query] = K . Q^T   (A = K rows from LDS, B = Q in VGPRs)
+// so lane l holds the scores of query l%16 against keys 4*(l/16)+r: the
+// online-softmax statistics of a query are lane-local plus two shuffles, and
+// the probabilities are already the A operand of
+//     O[query, d] += P . V        (B = V rows from LDS, row-major)
+// when the k index of MFMA c in lane group g is taken as key 4g+c (a
+// permutation of the k sum). O's rows are queries 4*(l/16)+r, so the rescale
+// factors reach them with one shuffle each. The next tile's K and V rows are
+// loaded into registers while the current tile is computed; with 33 KB of LDS
+// per workgroup four workgroups fit on a CU.
 //
 // attention_generic_kernel (the tensor.AttentionScaled drop-in): arbitrary
 // B, H, T, S, D <= 512, strides and an additive mask tensor, one wavefront
 // per query row, the reference's algebra: raw scores, + mask/scale, max,
 // exp(scale*row - scale*max) with the flush, P.V, times 1/sum.
+
+#include <cstdlib>
 
 #include "fa_internal.h"
 #include "device_math.h"
@@ -37,38 +41,40 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int AD = 256;        // head_dim
-constexpr int QW = 16;         // queries per wave
-constexpr int NWAVE = 4;       // waves per workgroup
-constexpr int QBLK = QW * NWAVE;
-constexpr int KT = 32;         // keys per LDS tile
-constexpr int KLD = AD + 4;    // padded K row stride (floats)
-constexpr int VLD = KT + 4;    // padded V^T row stride (floats)
+constexpr int AD = 256;                  // head_dim
+constexpr int QW = 16;                   // queries per wave
+constexpr int NWAVE = 2;                 // waves per workgroup
+constexpr int QBLK = QW * NWAVE;         // queries per work item
+constexpr int NTA = NWAVE * 64;          // threads per workgroup
+constexpr int KT = 16;                   // keys per tile
+constexpr int KLD = AD + 4;              // padded LDS row stride (floats)
+constexpr int NLD = KT * AD / 4 / NTA;   // float4 of K (and of V) per thread per tile
 constexpr float kNegBig = -1e30f;
 
 struct VarlenParams {
   const float* qkv;
   float* out;
   const int32_t* cu;
-  const int32_t* items;  // pairs (seq, q0)
+  const int32_t* items;  // triples (seq, q0, head)
   int32_t H, Hkv;
   int32_t window;
   float scale;
 };
 
-__global__ __launch_bounds__(256, 2) void attention_varlen_kernel(VarlenParams p) {
+template <bool PREFETCH>
+__global__ __launch_bounds__(NTA) void attention_varlen_kernel(VarlenParams p) {
   __shared__ __attribute__((aligned(16))) float Ks[KT * KLD];
-  __shared__ __attribute__((aligned(16))) float Vt[AD * VLD];
+  __shared__ __attribute__((aligned(16))) float Vs[KT * KLD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int g = lane >> 4;   // lane group: k sub-range / result row group
-  const int lq = lane & 15;  // the lane's query column
+  const int g = lane >> 4;   // lane group
+  const int lq = lane & 15;  // the lane's query column in S^T
 
-  const int seq = p.items[2 * blockIdx.x];
-  const int q0 = p.items[2 * blockIdx.x + 1];
-  const int h = blockIdx.y;
+  const int seq = p.items[3 * blockIdx.x];
+  const int q0 = p.items[3 * blockIdx.x + 1];
+  const int h = p.items[3 * blockIdx.x + 2];
   const int hk = h / (p.H / p.Hkv);
   const int start = p.cu[seq];
   const int L = p.cu[seq + 1] - start;
@@ -77,7 +83,8 @@ __global__ __launch_bounds__(256, 2) void attention_varlen_kernel(VarlenParams p
   const float* kbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + hk) * AD;
   const float* vbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + p.Hkv + hk) * AD;
 
-  const int qi = q0 + wave * QW + lq;  // this lane's query
+  const int qw0 = q0 + wave * QW;  // the wave's first query
+  const int qi = qw0 + lq;         // this lane's query in S^T
   const bool qvalid = qi < L;
 
   // Q in VGPRs, B-operand layout: qreg[sg] = Q[qi][16*sg + 4*g .. +4]
@@ -91,13 +98,13 @@ __global__ __launch_bounds__(256, 2) void attention_varlen_kernel(VarlenParams p
     }
   }
 
-  f32x4 oacc[AD / 16];
+  f32x4 oacc[AD / 16];  // O[query qw0 + 4g + r][d = 16*db + lq]
 #pragma unroll
   for (int db = 0; db < AD / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegBig;  // running max of scaled scores of this lane's query
-  float l_part = 0.f;     // this lane's share of the running sum
+  float m_run = kNegBig;  // running max of scaled scores of query qi
+  float l_part = 0.f;     // this lane's share of query qi's running sum
 
-  // keys this workgroup needs
+  // keys this work item needs
   const int qlast = min(q0 + QBLK, L) - 1;
   int kbeg = 0, kend = L;
   if (p.window > 0) {
@@ -105,61 +112,59 @@ __global__ __launch_bounds__(256, 2) void attention_varlen_kernel(VarlenParams p
     kend = min(L, qlast + p.window);
   }
 
-  for (int k0 = kbeg; k0 < kend; k0 += KT) {
-    __syncthreads();  // previous tile fully consumed
-    // K tile: rows k0..k0+31 -> Ks[row][d]
+  f32x4 kr[NLD], vr[NLD];  // next tile (in flight while the current one is computed, with PREFETCH)
+  auto load_tile = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < (KT * AD / 4) / 256; i++) {
-      const int idx = tid + 256 * i;
-      const int row = idx >> 6, c4 = idx & 63;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k0 + row < kend) v = *reinterpret_cast<const f32x4*>(kbase + (int64_t)(k0 + row) * W + c4 * 4);
-      *reinterpret_cast<f32x4*>(&Ks[row * KLD + c4 * 4]) = v;
+    for (int i = 0; i < NLD; i++) {
+      const int idx = tid + NTA * i;
+      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
+      const bool ok = k0 + row < kend;
+      const int64_t off = (int64_t)(ok ? k0 + row : 0) * W + c4 * 4;
+      const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off);
+      const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off);
+      kr[i] = ok ? kv : f32x4{0.f, 0.f, 0.f, 0.f};
+      vr[i] = ok ? vv : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    // V tile transposed: Vt[d][key]
+  };
+  if (PREFETCH && kbeg < kend) load_tile(kbeg);
+
+  for (int k0 = kbeg; k0 < kend; k0 += KT) {
+    if (!PREFETCH) load_tile(k0);
+    __syncthreads();  // the previous tile is consumed
 #pragma unroll
-    for (int i = 0; i < (KT * AD / 4) / 256; i++) {
-      const int idx = tid + 256 * i;
-      const int row = idx & (KT - 1), c4 = idx / KT;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (k0 + row < kend) v = *reinterpret_cast<const f32x4*>(vbase + (int64_t)(k0 + row) * W + c4 * 4);
-      Vt[(c4 * 4 + 0) * VLD + row] = v.x;
-      Vt[(c4 * 4 + 1) * VLD + row] = v.y;
-      Vt[(c4 * 4 + 2) * VLD + row] = v.z;
-      Vt[(c4 * 4 + 3) * VLD + row] = v.w;
+    for (int i = 0; i < NLD; i++) {
+      const int idx = tid + NTA * i;
+      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
+      *reinterpret_cast<f32x4*>(&Ks[row * KLD + c4 * 4]) = kr[i];
+      *reinterpret_cast<f32x4*>(&Vs[row * KLD + c4 * 4]) = vr[i];
     }
     __syncthreads();
+    if (PREFETCH && k0 + KT < kend) load_tile(k0 + KT);
 
-    // S^T for two 16-key sub-blocks
-    f32x4 sacc[KT / 16];
-#pragma unroll
-    for (int kb = 0; kb < KT / 16; kb++) {
-      sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const float* krow = &Ks[(kb * 16 + lq) * KLD + g * 4];
+    // S^T for 16 keys
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      const float* krow = &Ks[lq * KLD + g * 4];
 #pragma unroll
       for (int sg = 0; sg < AD / 16; sg++) {
-        f32x4 a = *reinterpret_cast<const f32x4*>(krow + sg * 16);
+        const f32x4 a = *reinterpret_cast<const f32x4*>(krow + sg * 16);
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-          sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc[kb], 0, 0, 0);
+        for (int c = 0; c < 4; c++) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc, 0, 0, 0);
       }
     }
 
-    // mask, scale, tile max over this query's keys (spread over the 4 lane groups)
+    // mask, scale, tile max over query qi's keys (spread over the 4 lane groups)
     float tmax = kNegBig;
-    bool valid[KT / 16][4];
+    bool valid[4];
 #pragma unroll
-    for (int kb = 0; kb < KT / 16; kb++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int j = k0 + kb * 16 + g * 4 + r;
-        bool ok = qvalid && j < kend;
-        if (p.window > 0) ok = ok && (qi - j < p.window) && (j - qi < p.window);
-        valid[kb][r] = ok;
-        const float t = sacc[kb][r] * p.scale;
-        sacc[kb][r] = t;
-        if (ok) tmax = fmaxf(tmax, t);
-      }
+    for (int r = 0; r < 4; r++) {
+      const int j = k0 + g * 4 + r;
+      bool ok = qvalid && j < kend;
+      if (p.window > 0) ok = ok && (qi - j < p.window) && (j - qi < p.window);
+      valid[r] = ok;
+      const float t = sacc[r] * p.scale;
+      sacc[r] = t;
+      if (ok) tmax = fmaxf(tmax, t);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
@@ -168,40 +173,45 @@ __global__ __launch_bounds__(256, 2) void attention_varlen_kernel(VarlenParams p
     m_run = m_new;
     float psum = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < KT / 16; kb++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float pv = valid[kb][r] ? exp_flush(sacc[kb][r] - m_new) : 0.f;
-        sacc[kb][r] = pv;
-        psum += pv;
-      }
+    for (int r = 0; r < 4; r++) {
+      const float pv = valid[r] ? exp_flush(sacc[r] - m_new) : 0.f;
+      sacc[r] = pv;
+      psum += pv;
     }
     l_part = l_part * alpha + psum;
-#pragma unroll
-    for (int db = 0; db < AD / 16; db++) oacc[db] *= alpha;
 
-    // O^T += V^T . P^T
+    // rescale O's rows (queries qw0 + 4g + r) by their queries' alpha
 #pragma unroll
-    for (int kb = 0; kb < KT / 16; kb++) {
+    for (int r = 0; r < 4; r++) {
+      const float ar = __shfl(alpha, 4 * g + r, 64);
 #pragma unroll
-      for (int db = 0; db < AD / 16; db++) {
-        f32x4 a = *reinterpret_cast<const f32x4*>(&Vt[(db * 16 + lq) * VLD + kb * 16 + g * 4]);
+      for (int db = 0; db < AD / 16; db++) oacc[db][r] *= ar;
+    }
+
+    // O += P . V
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], sacc[kb][c], oacc[db], 0, 0, 0);
-      }
+    for (int db = 0; db < AD / 16; db++) {
+      f32x4 b;
+#pragma unroll
+      for (int c = 0; c < 4; c++) b[c] = Vs[(4 * g + c) * KLD + db * 16 + lq];
+#pragma unroll
+      for (int c = 0; c < 4; c++) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sacc[c], b[c], oacc[db], 0, 0, 0);
     }
   }
 
   float l_tot = l_part + __shfl_xor(l_part, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
-  if (!qvalid) return;
-  const float inv = 1.f / l_tot;
-  float* orow = p.out + (int64_t)(start + qi) * (p.H * AD) + (int64_t)h * AD;
+  float* obase = p.out + (int64_t)h * AD;
+  const int OW = p.H * AD;
 #pragma unroll
-  for (int db = 0; db < AD / 16; db++) {
-    f32x4 o = oacc[db] * inv;
-    *reinterpret_cast<f32x4*>(orow + db * 16 + g * 4) = o;
+  for (int r = 0; r < 4; r++) {
+    const int qr = qw0 + 4 * g + r;
+    const float inv = 1.f / __shfl(l_tot, 4 * g + r, 64);
+    if (qr < L) {
+      float* orow = obase + (int64_t)(start + qr) * OW;
+#pragma unroll
+      for (int db = 0; db < AD / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
+    }
   }
 }
 
@@ -281,8 +291,14 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   VarlenParams p;
   p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
-  dim3 grid((unsigned)n_items, (unsigned)a.H), block(256);
-  hipLaunchKernelGGL(attention_varlen_kernel, grid, block, 0, s, p);
+  static const int prefetch = [] {
+    const char* e = std::getenv("FA_ATTN_PREFETCH");  // tuning switch
+    return e ? std::atoi(e) : 1;
+  }();
+  if (prefetch)
+    hipLaunchKernelGGL(attention_varlen_kernel<true>, dim3((unsigned)n_items), dim3(NTA), 0, s, p);
+  else
+    hipLaunchKernelGGL(attention_varlen_kernel<false>, dim3((unsigned)n_items), dim3(NTA), 0, s, p);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

@@ -156,7 +156,8 @@ struct AttnVarlenArgs {
   int32_t window;
   float scale;
 };
-// d_items holds n_items pairs (sequence, first query) of 64-query blocks.
+// d_items holds n_items triples (sequence, first query, head): one work item
+// per query block of attention_varlen_qblock() queries and head.
 int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const int32_t* d_items, int32_t n_items,
                                   hipStream_t s);
 // Queries per workgroup of the varlen kernel (the item granularity).

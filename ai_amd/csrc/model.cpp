@@ -82,6 +82,7 @@ struct fa_model {
   size_t plan_host_ints = 0;
   hipEvent_t plan_done = nullptr;
   bool plan_pending = false;
+  std::vector<int> seq_order;
   fa::DevBuf ids_dev, out_dev;
   // profiling
   bool profiling = false;
@@ -428,10 +429,10 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     if (lengths[b] < 1 || lengths[b] > T)
       return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
     M += lengths[b];
-    n_items += (lengths[b] + qblk - 1) / qblk;
+    n_items += (int64_t)((lengths[b] + qblk - 1) / qblk) * H;
   }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
-  const size_t plan_ints = (size_t)(B + 1) + 2 * (size_t)n_items;
+  const size_t plan_ints = (size_t)(B + 1) + 3 * (size_t)n_items;
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
     m->plan_pending = false;
@@ -446,13 +447,23 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   int32_t* cu_h = m->plan_host;
   int32_t* items_h = m->plan_host + (B + 1);
   cu_h[0] = 0;
+  for (int b = 0; b < B; b++) cu_h[b + 1] = cu_h[b] + lengths[b];
+  // Work items (sequence, query block, head), longest sequences first: an
+  // item's work grows with its sequence's length, and dispatching the long
+  // ones first shortens the tail.
+  std::vector<int>& order = m->seq_order;
+  order.resize(B);
+  for (int b = 0; b < B; b++) order[b] = b;
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
   int64_t it = 0;
-  for (int b = 0; b < B; b++) {
-    cu_h[b + 1] = cu_h[b] + lengths[b];
+  for (int b : order) {
     for (int q0 = 0; q0 < lengths[b]; q0 += qblk) {
-      items_h[2 * it] = b;
-      items_h[2 * it + 1] = q0;
-      it++;
+      for (int h = 0; h < H; h++) {
+        items_h[3 * it] = b;
+        items_h[3 * it + 1] = q0;
+        items_h[3 * it + 2] = h;
+        it++;
+      }
     }
   }
   int rc;
