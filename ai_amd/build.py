@@ -2,6 +2,10 @@
 
   ai_amd/_lib/libfa_rocm.so   HIP kernels + C ABI (include/fa_rocm.h), gfx950
   ai_amd/_lib/libfa_synth.so  seeded synthetic inputs (include/fa_synth.h), host only
+  ai_amd/_lib/libfiber_host.so  C++ mirror of the reference's tensor/gemma API
+                                (ai_amd/host/fiber.hpp) over libfa_rocm.so
+  _build/cpp_tests/*          C++ tests of that mirror (tests/cpp), run by
+                              tests/test_cpp_host.py on a GPU
 
 Compiles every source on every call (the driver's "does it build" check).
 Usage: python -m ai_amd.build [-v]
@@ -78,6 +82,35 @@ def build_synth(verbose: bool = False) -> str:
     return out
 
 
+HOST = os.path.join(PKG, "host")
+CPP_TESTS = ["test_tensor", "test_gemma"]
+CPP_TEST_BIN = os.path.join(BUILD, "cpp_tests")
+
+
+def build_host(verbose: bool = False) -> str:
+    """libfiber_host.so (host C++ only; the device work is in libfa_rocm.so)."""
+    cxx = shutil.which("g++") or "g++"
+    out = os.path.join(LIB, "libfiber_host.so")
+    tmp = out + ".tmp"
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", INCLUDE, "-I", HOST,
+          os.path.join(HOST, "fiber.cpp"), "-o", tmp, "-L", LIB, "-lfa_rocm",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, out)
+    os.makedirs(CPP_TEST_BIN, exist_ok=True)
+    tdir = os.path.join(ROOT, "tests", "cpp")
+    # rpath relative to the binary, so the tree can be moved to another host
+    rpath = "-Wl,-rpath,$ORIGIN/" + os.path.relpath(LIB, CPP_TEST_BIN)
+    jobs = []
+    for t in CPP_TESTS:
+        jobs.append([cxx, "-O2", "-std=c++17", "-Wall", "-I", INCLUDE, "-I", HOST, "-I", tdir,
+                     os.path.join(tdir, t + ".cpp"), "-o", os.path.join(CPP_TEST_BIN, t),
+                     "-L", LIB, "-lfiber_host", "-lfa_rocm", "-lfa_synth", rpath])
+    with cf.ThreadPoolExecutor(len(jobs)) as ex:
+        for f in [ex.submit(_run, j, verbose) for j in jobs]:
+            f.result()
+    return out
+
+
 def build_oracle(verbose: bool = False) -> None:
     """The CPU oracle is test infrastructure; it is built beside the product."""
     _run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle"), "-j2"], verbose)
@@ -86,6 +119,7 @@ def build_oracle(verbose: bool = False) -> None:
 def build_all(verbose: bool = False) -> None:
     build_synth(verbose)
     build_rocm(verbose)
+    build_host(verbose)
     build_oracle(verbose)
 
 

@@ -200,18 +200,27 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   *reinterpret_cast<f32x4*>(p + lane * 4) = r;
 }
 
-// pooled[b, c] = (sum over the sequence's rows of h[., c]) * (1/L_b), each
-// thread summing one column in row order.
+// pooled[b, c] = (sum over the sequence's rows of h[., c]) * (1/L_b). A
+// block covers 64 columns of one sequence: its 4 waves take every 4th row
+// (coalesced 256-byte row segments) and the 4 partial sums are added in wave
+// order, so the result does not depend on scheduling.
 __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ cu,
                                                    int d, float* __restrict__ pooled) {
+  __shared__ float part[4][64];
   const int b = blockIdx.x;
-  const int c = blockIdx.y * 256 + threadIdx.x;
-  if (c >= d) return;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = blockIdx.y * 64 + tx;
   const int r0 = cu[b], r1 = cu[b + 1];
   float s = 0.f;
-  for (int r = r0; r < r1; r++) s += h[(int64_t)r * d + c];
-  const int n = r1 - r0 > 0 ? r1 - r0 : 1;
-  pooled[(int64_t)b * d + c] = s * (1.f / (float)n);
+  if (c < d)
+    for (int r = r0 + ty; r < r1; r += 4) s += h[(int64_t)r * d + c];
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && c < d) {
+    const float tot = ((part[0][tx] + part[1][tx]) + part[2][tx]) + part[3][tx];
+    const int n = r1 - r0 > 0 ? r1 - r0 : 1;
+    pooled[(int64_t)b * d + c] = tot * (1.f / (float)n);
+  }
 }
 
 // out[b, :dim] = y[b, :dim] / sqrt(sum(y[b, :dim]^2) + 1e-12); one wave per row.
@@ -324,7 +333,7 @@ int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t
 int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t nseq, int32_t d, float* pooled,
                 hipStream_t s) {
   if (nseq == 0) return FA_OK;
-  dim3 grid(nseq, (d + 255) / 256), block(256);
+  dim3 grid(nseq, (d + 63) / 64), block(256);
   hipLaunchKernelGGL(pool_kernel, grid, block, 0, s, h, cu_seqlens, d, pooled);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;

@@ -1,0 +1,402 @@
+// C++ host mirror of fiber/ai's tensor and gemma API on top of the C ABI.
+// See fiber.hpp for the mapping to the reference.
+#include "fiber.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <numeric>
+#include <sstream>
+
+namespace fiber {
+
+namespace {
+
+fa_ctx* g_ctx = nullptr;
+std::once_flag g_once;
+std::string g_err;
+
+std::string shape_str(const tensor::Shape& s) {
+  std::ostringstream o;
+  o << "[";
+  for (size_t i = 0; i < s.size(); i++) o << (i ? " " : "") << s[i];
+  o << "]";
+  return o.str();
+}
+
+tensor::Shape contiguous_strides(const tensor::Shape& s) {
+  tensor::Shape st(s.size());
+  int64_t acc = 1;
+  for (int i = (int)s.size() - 1; i >= 0; i--) {
+    st[i] = acc;
+    acc *= s[i];
+  }
+  return st;
+}
+
+int64_t prod(const tensor::Shape& s) {
+  int64_t n = 1;
+  for (int64_t v : s) n *= v;
+  return n;
+}
+
+// Calls fn and maps a non-OK status to tensor::Error{op, message}.
+void call(const char* op, int rc) {
+  if (rc == FA_OK) return;
+  std::string msg = fa_last_error(device());
+  if (rc == FA_ERR_ARG) throw tensor::Error(op, msg);
+  throw std::runtime_error(std::string("fa_rocm: ") + op + ": " + msg);
+}
+
+}  // namespace
+
+fa_ctx* device() {
+  std::call_once(g_once, [] {
+    if (fa_create(0, &g_ctx) != FA_OK) g_err = fa_last_error(nullptr);
+  });
+  if (!g_ctx) throw std::runtime_error("fa_rocm: no GPU context: " + g_err);
+  return g_ctx;
+}
+
+namespace tensor {
+
+[[noreturn]] static void fail(const std::string& op, const std::string& msg) { throw Error(op, msg); }
+
+Tensor Tensor::New(std::vector<float> data, Shape shape) {
+  for (int64_t d : shape)
+    if (d < 0) fail("New", "negative dimension in " + shape_str(shape));
+  if ((int64_t)data.size() != prod(shape))
+    fail("New", std::to_string(data.size()) + " values for shape " + shape_str(shape));
+  Tensor t;
+  t.store_ = std::make_shared<std::vector<float>>(std::move(data));
+  t.shape_ = shape;
+  t.strides_ = contiguous_strides(shape);
+  return t;
+}
+
+Tensor Tensor::Zeros(Shape shape) { return New(std::vector<float>(prod(shape), 0.f), shape); }
+
+int64_t Tensor::Size() const { return prod(shape_); }
+
+bool Tensor::IsContiguous() const { return strides_ == contiguous_strides(shape_); }
+
+float Tensor::At(std::initializer_list<int64_t> idx) const {
+  if (idx.size() != shape_.size()) fail("At", "index rank does not match " + shape_str(shape_));
+  int64_t off = offset_;
+  int i = 0;
+  for (int64_t v : idx) {
+    if (v < 0 || v >= shape_[i]) fail("At", "index out of range for " + shape_str(shape_));
+    off += v * strides_[i++];
+  }
+  return (*store_)[off];
+}
+
+std::vector<float> Tensor::Float32s() const {
+  const int64_t n = Size();
+  std::vector<float> out(n);
+  if (n == 0) return out;
+  if (IsContiguous()) {
+    std::memcpy(out.data(), store_->data() + offset_, n * sizeof(float));
+    return out;
+  }
+  std::vector<int64_t> idx(shape_.size(), 0);
+  for (int64_t k = 0; k < n; k++) {
+    int64_t off = offset_;
+    for (size_t d = 0; d < shape_.size(); d++) off += idx[d] * strides_[d];
+    out[k] = (*store_)[off];
+    for (int d = (int)shape_.size() - 1; d >= 0; d--) {
+      if (++idx[d] < shape_[d]) break;
+      idx[d] = 0;
+    }
+  }
+  return out;
+}
+
+Tensor Tensor::Contiguous() const {
+  if (IsContiguous()) return *this;
+  return New(Float32s(), shape_);
+}
+
+Tensor Tensor::Reshape(Shape shape) const {
+  if (prod(shape) != Size()) fail("Reshape", "cannot reshape " + shape_str(shape_) + " to " + shape_str(shape));
+  Tensor t = Contiguous();
+  t.shape_ = shape;
+  t.strides_ = contiguous_strides(shape);
+  return t;
+}
+
+Tensor Tensor::Expand(Shape shape) const {
+  if (shape.size() < shape_.size()) fail("Expand", "cannot expand " + shape_str(shape_) + " to " + shape_str(shape));
+  Tensor t = *this;
+  const size_t lead = shape.size() - shape_.size();
+  Shape st(shape.size(), 0);
+  for (size_t i = 0; i < shape.size(); i++) {
+    if (i < lead) continue;  // new leading dimension: stride 0
+    const int64_t have = shape_[i - lead];
+    if (have == shape[i]) st[i] = strides_[i - lead];
+    else if (have == 1) st[i] = 0;
+    else fail("Expand", "cannot expand " + shape_str(shape_) + " to " + shape_str(shape));
+  }
+  t.shape_ = shape;
+  t.strides_ = st;
+  return t;
+}
+
+Tensor Tensor::T() const {
+  if (shape_.size() != 2) fail("T", "expected a 2-D tensor, got " + shape_str(shape_));
+  Tensor t = *this;
+  std::swap(t.shape_[0], t.shape_[1]);
+  std::swap(t.strides_[0], t.strides_[1]);
+  return t;
+}
+
+std::vector<float> Tensor::RowSumSquares() const {
+  if (shape_.size() != 2) fail("RowSumSquares", "expected a 2-D tensor, got " + shape_str(shape_));
+  Tensor x = Contiguous();
+  std::vector<float> out(shape_[0]);
+  if (shape_[0] == 0) return out;
+  call("RowSumSquares", fa_row_sum_squares(device(), x.base(), shape_[0], shape_[1], out.data()));
+  return out;
+}
+
+Tensor MatMulFused(const Tensor& x, const Tensor& w, const Fused& f) {
+  if (x.Dims() != 2 || w.Dims() != 2)
+    fail("MatMulFused", "expected 2-D operands, got " + shape_str(x.shape()) + " and " + shape_str(w.shape()));
+  const int64_t m = x.Dim(0), k = x.Dim(1), n = w.Dim(1);
+  if (k != w.Dim(0)) fail("MatMulFused", "shape mismatch " + shape_str(x.shape()) + " · " + shape_str(w.shape()));
+  if (f.Bias && f.Bias->Size() != n)
+    fail("MatMulFused", "bias has " + std::to_string(f.Bias->Size()) + " elements for " + std::to_string(n) + " columns");
+  if (!f.RowScale.empty() && (int64_t)f.RowScale.size() != m)
+    fail("MatMulFused", "row scale has " + std::to_string(f.RowScale.size()) + " elements for " + std::to_string(m) + " rows");
+  for (const Tensor* t : {f.Mul, f.Residual})
+    if (t && !(t->Dims() == 2 && t->Dim(0) == m && t->Dim(1) == n))
+      fail("MatMulFused", "Mul/Residual must be [" + std::to_string(m) + "×" + std::to_string(n) + "], got " +
+                              shape_str(t->shape()));
+  Tensor out = Tensor::Zeros({m, n});
+  if (m == 0 || n == 0) return out;
+  const Tensor xc = x.Contiguous();
+  // A transposed view of a contiguous [n, k] operand is consumed in place
+  // (the reference reads strided views without a copy, matmul.go:10-36).
+  int layout = FA_B_KN;
+  Tensor wc;
+  int64_t ldb = n;
+  if (!w.IsContiguous() && w.strides()[0] == 1 && w.strides()[1] == k) {
+    wc = w;
+    layout = FA_B_NK;
+    ldb = k;
+  } else {
+    wc = w.Contiguous();
+  }
+  fa_epilogue e{};
+  Tensor bias, mul, res;
+  if (f.Bias) { bias = f.Bias->Contiguous(); e.bias = bias.base(); }
+  if (!f.RowScale.empty()) e.row_scale = f.RowScale.data();
+  e.act = f.Act;
+  if (f.Mul) { mul = f.Mul->Contiguous(); e.mul = mul.base(); e.ldm = n; }
+  if (f.Residual) { res = f.Residual->Contiguous(); e.residual = res.base(); e.ldr = n; }
+  call("MatMulFused", fa_matmul_fused(device(), m, n, k, xc.base(), k, wc.base(), ldb, FA_DT_F32, layout, &e,
+                                      const_cast<float*>(out.base()), n));
+  return out;
+}
+
+Tensor MatMul(const Tensor& x, const Tensor& w) {
+  if (x.Dims() != 2 || w.Dims() != 2)
+    fail("MatMul", "this mirror covers the 2-D product, got " + shape_str(x.shape()) + " and " + shape_str(w.shape()));
+  if (x.Dim(1) != w.Dim(0)) fail("MatMul", "shape mismatch " + shape_str(x.shape()) + " · " + shape_str(w.shape()));
+  return MatMulFused(x, w, Fused{});
+}
+
+Tensor RMSNorm(const Tensor& x, const Tensor& g, float eps) {
+  if (x.Dims() == 0) fail("RMSNorm", "expected at least a 1-D input");
+  const int64_t n = x.Dim(-1);
+  if (g.Size() != n)
+    fail("RMSNorm", "g must have " + std::to_string(n) + " elements, got " + std::to_string(g.Size()));
+  const Tensor xc = x.Contiguous(), gc = g.Contiguous();
+  Tensor out = Tensor::Zeros(x.shape());
+  const int64_t rows = n ? x.Size() / n : 0;
+  if (rows == 0) return out;
+  call("RMSNorm", fa_rmsnorm(device(), xc.base(), gc.base(), eps, rows, n, const_cast<float*>(out.base())));
+  return out;
+}
+
+Tensor RoPE(const Tensor& x, double base, const std::vector<int>& positions) {
+  const int nd = x.Dims();
+  if (nd < 2) fail("RoPE", "expected at least a 2-D input, got " + shape_str(x.shape()));
+  const int64_t T = x.Dim(-2), D = x.Dim(-1);
+  if (D % 2 != 0) fail("RoPE", "head dimension " + std::to_string(D) + " must be even");
+  if ((int64_t)positions.size() != T)
+    fail("RoPE", "got " + std::to_string(positions.size()) + " positions for " + std::to_string(T) + " slots");
+  const Tensor xc = x.Contiguous();
+  Tensor out = Tensor::Zeros(x.shape());
+  const int64_t rows = D ? x.Size() / D : 0;
+  if (rows == 0) return out;
+  std::vector<int32_t> pos(positions.begin(), positions.end());
+  call("RoPE", fa_rope(device(), xc.base(), base, pos.data(), rows, (int32_t)T, (int32_t)D,
+                       const_cast<float*>(out.base())));
+  return out;
+}
+
+Tensor AttentionScaled(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* mask, float scale) {
+  const int nd = q.Dims();
+  if (nd < 2 || k.Dims() != nd || v.Dims() != nd)
+    fail("Attention", "q, k, v must have the same rank ≥ 2, got " + shape_str(q.shape()) + " " + shape_str(k.shape()) +
+                          " " + shape_str(v.shape()));
+  const int64_t D = q.Dim(-1);
+  if (k.Dim(-1) != D || v.Dim(-2) != k.Dim(-2))
+    fail("Attention", "shapes do not match: q " + shape_str(q.shape()) + ", k " + shape_str(k.shape()) + ", v " +
+                          shape_str(v.shape()));
+  if (nd > 4) fail("Attention", "this mirror covers up to two leading dimensions, got " + shape_str(q.shape()));
+  for (int i = 0; i < nd - 2; i++)
+    if (k.Dim(i) != q.Dim(i) || v.Dim(i) != q.Dim(i))
+      fail("Attention", "leading dimensions of q, k, v differ");
+  const int64_t T = q.Dim(-2), S = k.Dim(-2);
+  // lead dims as (B, H) with element strides; rows of D must be contiguous
+  auto rows_ok = [&](const Tensor& t, int64_t R) {
+    return t.strides()[nd - 1] == 1 && (R <= 1 || t.strides()[nd - 2] == D);
+  };
+  const Tensor qc = rows_ok(q, T) ? q : q.Contiguous();
+  const Tensor kc = rows_ok(k, S) ? k : k.Contiguous();
+  const Tensor vc = rows_ok(v, S) ? v : v.Contiguous();
+  auto lead = [&](const Tensor& t, int64_t& sb, int64_t& sh) {
+    sb = sh = 0;
+    if (nd == 4) { sb = t.strides()[0]; sh = t.strides()[1]; }
+    else if (nd == 3) { sh = t.strides()[0]; }
+  };
+  const int64_t B = nd == 4 ? q.Dim(0) : 1, H = nd >= 3 ? q.Dim(nd - 3) : 1;
+  int64_t qsb, qsh, ksb, ksh, vsb, vsh;
+  lead(qc, qsb, qsh);
+  lead(kc, ksb, ksh);
+  lead(vc, vsb, vsh);
+  // mask: broadcast strides over [B, H, T, S]
+  Tensor mc;
+  int64_t ms[4] = {0, 0, 0, 0};
+  const float* mp = nullptr;
+  if (mask) {
+    if (mask->Dims() > 4) fail("Attention", "mask rank " + std::to_string(mask->Dims()) + " > 4");
+    mc = mask->Contiguous();
+    const Shape full = {B, H, T, S};
+    const int off = 4 - mc.Dims();
+    for (int i = 0; i < 4; i++) {
+      if (i < off) continue;
+      const int64_t have = mc.shape()[i - off];
+      if (have == full[i]) ms[i] = mc.strides()[i - off];
+      else if (have == 1) ms[i] = 0;
+      else fail("Attention", "mask " + shape_str(mask->shape()) + " does not broadcast to " + shape_str(full));
+    }
+    mp = mc.base();
+  }
+  Tensor out = Tensor::Zeros(q.shape());
+  if (B * H * T == 0 || D == 0) return out;
+  call("Attention", fa_attention(device(), qc.base(), kc.base(), vc.base(), (int32_t)B, (int32_t)H, (int32_t)T,
+                                 (int32_t)S, (int32_t)D, qsb, qsh, ksb, ksh, vsb, vsh, mp, ms[0], ms[1], ms[2], ms[3],
+                                 scale, const_cast<float*>(out.base())));
+  return out;
+}
+
+Tensor Attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* mask) {
+  const double d = (double)q.Dim(-1);
+  return AttentionScaled(q, k, v, mask, (float)(1.0 / std::sqrt(d)));
+}
+
+Tensor PaddingMask(const std::vector<int>& lengths, int64_t n) {
+  const int64_t b = (int64_t)lengths.size();
+  std::vector<float> m(b * n, 0.f);
+  for (int64_t i = 0; i < b; i++)
+    for (int64_t j = std::max<int64_t>(0, lengths[i]); j < n; j++) m[i * n + j] = kMaskNeg;
+  return Tensor::New(std::move(m), {b, 1, 1, n});
+}
+
+Tensor WindowMask(int64_t n, int64_t w) {
+  std::vector<float> m(n * n, 0.f);
+  for (int64_t i = 0; i < n; i++)
+    for (int64_t j = 0; j < n; j++)
+      if (j - i >= w || i - j >= w) m[i * n + j] = kMaskNeg;
+  return Tensor::New(std::move(m), {n, n});
+}
+
+Tensor CausalMask(int64_t n) {
+  std::vector<float> m(n * n, 0.f);
+  for (int64_t i = 0; i < n; i++)
+    for (int64_t j = i + 1; j < n; j++) m[i * n + j] = kMaskNeg;
+  return Tensor::New(std::move(m), {n, n});
+}
+
+}  // namespace tensor
+
+namespace gemma {
+
+namespace {
+void gcheck(fa_ctx* ctx, int rc) {
+  if (rc != FA_OK) throw Error(fa_last_error(ctx));
+}
+}  // namespace
+
+Model::Model(const Config& cfg) : cfg_(cfg) {
+  fa_gemma_config c{};
+  c.hidden_size = cfg.HiddenSize;
+  c.num_hidden_layers = cfg.NumHiddenLayers;
+  c.num_attention_heads = cfg.NumAttentionHeads;
+  c.num_key_value_heads = cfg.NumKeyValueHeads;
+  c.head_dim = cfg.HeadDim;
+  c.intermediate_size = cfg.IntermediateSize;
+  c.vocab_size = cfg.VocabSize;
+  c.sliding_window = cfg.SlidingWindow;
+  c.use_bidirectional = cfg.UseBidirectional ? 1 : 0;
+  c.sliding_window_pattern = cfg.SlidingWindowPattern;
+  c.rope_local_base_freq = cfg.RopeLocalBaseFreq;
+  c.rope_theta = cfg.RopeTheta;
+  c.query_pre_attn_scalar = cfg.QueryPreAttnScalar;
+  c.rms_norm_eps = cfg.RMSNormEps;
+  c.max_tokens = cfg.MaxTokens;
+  if (cfg.Dense.size() > 4) throw Error("gemma: at most 4 Dense layers");
+  c.n_dense = (int32_t)cfg.Dense.size();
+  for (size_t i = 0; i < cfg.Dense.size(); i++) c.dense_out[i] = cfg.Dense[i];
+  gcheck(device(), fa_gemma_create(device(), &c, &m_));
+}
+
+Model::~Model() { Close(); }
+
+void Model::Close() {
+  if (m_) fa_gemma_destroy(m_);
+  m_ = nullptr;
+}
+
+void Model::SetWeightBF16(const std::string& name, const std::vector<int64_t>& shape, const uint16_t* data) {
+  gcheck(device(), fa_gemma_set_weight(m_, name.c_str(), FA_DT_BF16, shape.data(), (int32_t)shape.size(), data));
+}
+
+void Model::SetWeightF32(const std::string& name, const std::vector<int64_t>& shape, const float* data) {
+  gcheck(device(), fa_gemma_set_weight(m_, name.c_str(), FA_DT_F32, shape.data(), (int32_t)shape.size(), data));
+}
+
+void Model::Finalize() { gcheck(device(), fa_gemma_finalize(m_)); }
+
+int Model::Dim() const { return cfg_.Dense.empty() ? cfg_.HiddenSize : cfg_.Dense.back(); }
+
+std::vector<std::vector<float>> Model::EmbedIDs(const std::vector<std::vector<int32_t>>& ids, EmbedOpts o) const {
+  if (!m_) throw Error("gemma: model is closed");
+  int dim = Dim();
+  if (o.Dim != 0) {
+    if (o.Dim < 1 || o.Dim > dim) throw Error("gemma: Dim(" + std::to_string(o.Dim) + ") outside 1.." + std::to_string(dim));
+    dim = o.Dim;
+  }
+  const int32_t B = (int32_t)ids.size();
+  if (B == 0) return {};
+  int32_t T = 0;
+  std::vector<int32_t> lengths(B);
+  for (int32_t b = 0; b < B; b++) {
+    lengths[b] = (int32_t)std::min<size_t>(ids[b].size(), (size_t)cfg_.MaxTokens);  // embed.go:40-42
+    T = std::max(T, lengths[b]);
+  }
+  std::vector<int32_t> flat((size_t)B * T, 0);  // pad id 0 (embed.go:128-138)
+  for (int32_t b = 0; b < B; b++) std::copy(ids[b].begin(), ids[b].begin() + lengths[b], flat.begin() + (size_t)b * T);
+  std::vector<float> out((size_t)B * dim);
+  gcheck(device(), fa_gemma_embed_ids(m_, flat.data(), lengths.data(), B, T, dim, out.data()));
+  std::vector<std::vector<float>> res(B);
+  for (int32_t b = 0; b < B; b++) res[b].assign(out.begin() + (size_t)b * dim, out.begin() + (size_t)(b + 1) * dim);
+  return res;
+}
+
+}  // namespace gemma
+}  // namespace fiber

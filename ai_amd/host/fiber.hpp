@@ -1,0 +1,156 @@
+// fiber.hpp — C++ host mirror of fiber/ai's Go API on the EmbeddingGemma
+// path, computed on the GPU through the C ABI (include/fa_rocm.h).
+//
+// The names, argument meaning and error behaviour follow the reference:
+//   tensor.MatMul / MatMulFused / Fused        tensor/matmul.go:19, matmul_fused.go:17-96
+//   (*Tensor).RowSumSquares                    tensor/matmul_fused.go:125-143
+//   tensor.RMSNorm                             tensor/attention.go:292-337
+//   tensor.RoPE                                tensor/rope.go:20-61
+//   tensor.Attention / AttentionScaled         tensor/attention.go:56-83
+//   tensor.PaddingMask / WindowMask / CausalMask   tensor/attention.go:21-42,97-107
+//   (*Tensor).Expand (stride-0 views)          tensor/view.go
+//   gemma.Model: Embed at the ids level, Dim, Close   models/gemma/model.go:40-71,336-343; embed.go:15-157
+// Shape errors throw fiber::tensor::Error{Op, Msg}, where the reference
+// panics with *tensor.Error (tensor/errors.go:5-31); gemma's functions throw
+// fiber::gemma::Error where the reference returns error.
+//
+// Tensors here are host arrays (float32, row-major, with strides so that
+// Expand views exist); every operator copies its operands to the device,
+// computes there and returns a new contiguous tensor, like the reference's
+// operators return fresh tensors.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "fa_rocm.h"
+
+namespace fiber {
+
+// The process-wide GPU context (device 0), created on first use.
+fa_ctx* device();
+
+namespace tensor {
+
+struct Error : std::runtime_error {
+  std::string Op, Msg;
+  Error(std::string op, std::string msg)
+      : std::runtime_error("tensor: " + op + ": " + msg), Op(std::move(op)), Msg(std::move(msg)) {}
+};
+
+using Shape = std::vector<int64_t>;
+
+class Tensor {
+ public:
+  Tensor() = default;
+  // New copies data into a fresh tensor of the given shape (tensor.New).
+  static Tensor New(std::vector<float> data, Shape shape);
+  static Tensor Zeros(Shape shape);
+
+  const Shape& shape() const { return shape_; }
+  const Shape& strides() const { return strides_; }
+  int64_t Dim(int i) const { return shape_[i < 0 ? i + (int)shape_.size() : i]; }
+  int Dims() const { return (int)shape_.size(); }
+  int64_t Size() const;
+  bool IsContiguous() const;
+  // Element access by full index (views included).
+  float At(std::initializer_list<int64_t> idx) const;
+  // Contiguous copy of the values in row-major order (Float32s).
+  std::vector<float> Float32s() const;
+  Tensor Contiguous() const;
+  Tensor Reshape(Shape shape) const;
+  // View broadcasting dimensions of size 1 to shape (stride 0), tensor.Expand.
+  Tensor Expand(Shape shape) const;
+  // Transposed view of a 2-D tensor (T).
+  Tensor T() const;
+
+  // (*Tensor).RowSumSquares: sum of squares of each row of a 2-D tensor.
+  std::vector<float> RowSumSquares() const;
+
+  const float* base() const { return store_ ? store_->data() + offset_ : nullptr; }
+
+ private:
+  std::shared_ptr<std::vector<float>> store_;
+  int64_t offset_ = 0;
+  Shape shape_, strides_;
+  friend Tensor AttentionScaled(const Tensor&, const Tensor&, const Tensor&, const Tensor*, float);
+};
+
+enum Activation { NoAct = FA_ACT_NONE, ReLUAct = FA_ACT_RELU, GELUAct = FA_ACT_GELU };
+
+// Epilogue of MatMulFused, applied in the order Bias, RowScale, Act, Mul,
+// Residual (tensor/matmul_fused.go:11-23). Null pointers / empty RowScale
+// are skipped.
+struct Fused {
+  const Tensor* Bias = nullptr;
+  Activation Act = NoAct;
+  const Tensor* Mul = nullptr;
+  std::vector<float> RowScale;
+  const Tensor* Residual = nullptr;
+};
+
+Tensor MatMul(const Tensor& x, const Tensor& w);
+Tensor MatMulFused(const Tensor& x, const Tensor& w, const Fused& f);
+Tensor RMSNorm(const Tensor& x, const Tensor& g, float eps);
+Tensor RoPE(const Tensor& x, double base, const std::vector<int>& positions);
+Tensor Attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* mask);
+Tensor AttentionScaled(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* mask, float scale);
+Tensor PaddingMask(const std::vector<int>& lengths, int64_t n);
+Tensor WindowMask(int64_t n, int64_t w);
+Tensor CausalMask(int64_t n);
+
+constexpr float kMaskNeg = -1e9f;  // tensor/attention.go:17
+
+}  // namespace tensor
+
+namespace gemma {
+
+struct Error : std::runtime_error {
+  explicit Error(const std::string& m) : std::runtime_error(m) {}
+};
+
+// Hyper-parameters of config.json (models/gemma/config.go:19-58), Variant 0,
+// and the sentence-transformers Dense head; defaults are EmbeddingGemma-300M.
+struct Config {
+  int HiddenSize = 768, NumHiddenLayers = 24, NumAttentionHeads = 3, NumKeyValueHeads = 1, HeadDim = 256;
+  int IntermediateSize = 1152, VocabSize = 262144, SlidingWindow = 512, SlidingWindowPattern = 6;
+  bool UseBidirectional = true;
+  double RopeLocalBaseFreq = 1e4, RopeTheta = 1e6, QueryPreAttnScalar = 256;
+  float RMSNormEps = 1e-6f;
+  int MaxTokens = 2048;
+  std::vector<int> Dense = {3072, 768};
+};
+
+// Option of Embed (embed.go:24-30): Dim truncates before L2 (Matryoshka).
+struct EmbedOpts {
+  int Dim = 0;
+};
+
+class Model {
+ public:
+  explicit Model(const Config& cfg);
+  ~Model();
+  Model(const Model&) = delete;
+  Model& operator=(const Model&) = delete;
+  // One checkpoint tensor by its Hugging Face name (gemma.Load's names,
+  // model.go:142-191); bf16 bits or float32, shape [out, in] for matrices.
+  void SetWeightBF16(const std::string& name, const std::vector<int64_t>& shape, const uint16_t* data);
+  void SetWeightF32(const std::string& name, const std::vector<int64_t>& shape, const float* data);
+  void Finalize();
+  // Embeddings of token-id sequences (each already tokenised with BOS),
+  // batched in one forward pass; sequences longer than MaxTokens are
+  // truncated (embed.go:40-42). Returns one row per sequence.
+  std::vector<std::vector<float>> EmbedIDs(const std::vector<std::vector<int32_t>>& ids, EmbedOpts o = {}) const;
+  int Dim() const;
+  void Close();
+
+ private:
+  Config cfg_;
+  fa_model* m_ = nullptr;
+};
+
+}  // namespace gemma
+}  // namespace fiber
