@@ -89,6 +89,73 @@ struct GemmParams {
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// Tile index of this workgroup. Workgroup ids are dealt to the 8 XCDs
+// round-robin; each XCD gets a contiguous run of tiles (row-major over n) so
+// the tiles sharing A rows and B columns share that XCD's L2.
+__device__ __forceinline__ int xcd_tile(const GemmParams& p) {
+  constexpr int kXcd = 8;
+  const int total = p.tiles_m * p.tiles_n;
+  int tile = blockIdx.x;
+  const int per = total / kXcd;
+  if (per > 0 && tile < per * kXcd) tile = (tile % kXcd) * per + tile / kXcd;
+  return tile;
+}
+
+// Writes a wave's accumulators (FM x FN blocks of 32x32 in the MFMA C
+// layout) through the epilogue. Shared by the fp32 and split-bf16 kernels,
+// whose 32x32 MFMAs have the same C layout.
+template <class TL, Epi EPI>
+__device__ __forceinline__ void store_c(const GemmParams& p, const f32x16 (&acc)[TL::FM][TL::FN], int64_t m0,
+                                        int64_t n0, int wm, int wn, int lane) {
+  constexpr int FM = TL::FM, FN = TL::FN;
+  const int64_t M = p.m, N = p.n;
+  const int lcol = lane & 31;
+  const int lrow4 = (lane >> 5) * 4;
+  if constexpr (EPI == Epi::GeGLU) {
+    static_assert(FN % 2 == 0, "GeGLU pairs column blocks");
+    const int64_t F = N / 2;
+#pragma unroll
+    for (int pj = 0; pj < FN / 2; pj++) {
+      const int64_t fcol = (n0 + wn * TL::TN) / 2 + pj * 32 + lcol;
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
+          if (row < M && fcol < F) {
+            const float g = acc[i][2 * pj][r], u = acc[i][2 * pj + 1][r];
+            p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int64_t col = n0 + wn * TL::TN + j * 32 + lcol;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
+          if (row < M && col < N) {
+            float v = acc[i][j][r];
+            if constexpr (EPI == Epi::Generic) {
+              if (p.bias) v = v + p.bias[col];
+              if (p.row_scale) v = v * p.row_scale[row];
+              if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
+              else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
+              if (p.mul) v = v * p.mul[row * p.ldm + col];
+              if (p.residual) v = v + p.residual[row * p.ldr + col];
+            }
+            p.c[row * p.ldc + col] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
 template <class TL, bool BBF16, bool BNK, bool FAST, Epi EPI>
 __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmParams p) {
   constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, NT = TL::NT, LDSK = TL::LDSK;
@@ -282,73 +349,11 @@ __global__ __launch_bounds__(TL::NT) void gemm_kernel(GemmParams p) {
     }
   };
 
-  const int lcol = lane & 31;
-  const int lrow4 = (lane >> 5) * 4;
-  auto store_tile = [&]() {
-    if constexpr (EPI == Epi::GeGLU) {
-      static_assert(FN % 2 == 0, "GeGLU pairs column blocks");
-      const int64_t F = N / 2;
-#pragma unroll
-      for (int pj = 0; pj < FN / 2; pj++) {
-        const int64_t fcol = (n0 + wn * TL::TN) / 2 + pj * 32 + lcol;
-#pragma unroll
-        for (int i = 0; i < FM; i++) {
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
-            if (row < M && fcol < F) {
-              const float g = acc[i][2 * pj][r], u = acc[i][2 * pj + 1][r];
-              p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
-            }
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < FM; i++) {
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-          const int64_t col = n0 + wn * TL::TN + j * 32 + lcol;
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
-            if (row < M && col < N) {
-              float v = acc[i][j][r];
-              if constexpr (EPI == Epi::Generic) {
-                if (p.bias) v = v + p.bias[col];
-                if (p.row_scale) v = v * p.row_scale[row];
-                if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
-                else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
-                if (p.mul) v = v * p.mul[row * p.ldm + col];
-                if (p.residual) v = v + p.residual[row * p.ldr + col];
-              }
-              p.c[row * p.ldc + col] = v;
-            }
-          }
-        }
-      }
-    }
-  };
-
-  auto set_tile = [&](int tile) {
-    const int tm = tile / p.tiles_n, tn = tile % p.tiles_n;
-    m0 = (int64_t)tm * BM;
-    n0 = (int64_t)tn * BN;
-  };
-
-  const int total = p.tiles_m * p.tiles_n;
-  int tile = blockIdx.x;
-  {
-    // XCD-aware: workgroup ids are dealt to the 8 XCDs round-robin; give each
-    // XCD a contiguous run of tiles (row-major over n) so the tiles sharing A
-    // rows and B columns share that XCD's L2.
-    constexpr int kXcd = 8;
-    const int per = total / kXcd;
-    if (per > 0 && tile < per * kXcd) tile = (tile % kXcd) * per + tile / kXcd;
-  }
-  set_tile(tile);
+  const int tile = xcd_tile(p);
+  m0 = (int64_t)(tile / p.tiles_n) * BM;
+  n0 = (int64_t)(tile % p.tiles_n) * BN;
   mainloop(0, p.nk);
-  store_tile();
+  store_c<TL, EPI>(p, acc, m0, n0, wm, wn, lane);
 }
 
 template <class TL, bool BBF16, bool BNK, bool FAST, Epi EPI>
@@ -358,6 +363,225 @@ void launch_dp(GemmParams p, hipStream_t s) {
   p.nk = (int)((p.k + TL::BK - 1) / TL::BK);
   dim3 grid(p.tiles_m * p.tiles_n), block(TL::NT);
   hipLaunchKernelGGL((gemm_kernel<TL, BBF16, BNK, FAST, EPI>), grid, block, 0, s, p);
+}
+
+// ---------------------------------------------------------------------------
+// Split-bf16 kernel for bf16 weights: C = A . B with A fp32, B bf16 [n x k].
+//
+// Each fp32 value a of A is written to LDS as three bf16 terms with
+// a = hi + mid + lo exactly: hi keeps the top 8 significant bits of a
+// (truncation), mid the top 8 of the remainder a - hi (exact in fp32), lo
+// the rest (at most 8 significant bits, so exact in bf16). Products of a
+// bf16 term and a bf16 weight are exact in fp32, and the three
+// v_mfma_f32_32x32x16_bf16 per operand pair accumulate them in fp32, so C
+// carries the same information as an fp32 product of A and the
+// (bf16-exact) weights; only the summation order differs. Non-finite A
+// values give NaN (inf - inf in the split).
+//
+// Operand layout (32x32x16): lane l supplies A[row l%32][8 k values] and
+// B[8 k values][col l%32]; the k assignment is any bijection shared by both
+// operands, here k = 8*(l/32) .. +7 of each 16-wide step, one 16-byte LDS
+// read per operand. C has the 32x32x2 layout (store_c).
+//
+// Pipeline: slab kt is in LDS buffer kt&1 while registers hold the global
+// values of slab kt+1 (split and written to the other buffer during slab kt's
+// MFMAs) and receive slab kt+2; one barrier per slab. The loop body has no
+// branches (the last loads are clamped, redundant), so the compiler
+// interleaves the split's VALU work and the LDS traffic with the MFMAs.
+template <int BM_, int BN_, int WM_, int WN_>
+struct XTile {
+  static constexpr int BM = BM_, BN = BN_, BK = 32, WM = WM_, WN = WN_;
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN;
+  static constexpr int FM = TM / 32, FN = TN / 32;
+  static constexpr int S = BK / 16;   // MFMA k-steps per slab
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "tile shape");
+};
+
+using X128x128 = XTile<128, 128, 2, 2>;  // 4 waves of 64x64
+using X128x64 = XTile<128, 64, 2, 2>;    // 4 waves of 64x32
+using X128x64v = XTile<128, 64, 4, 1>;   // 4 waves of 32x64 (column-block pairs for GeGLU)
+using X64x128 = XTile<64, 128, 2, 2>;    // 4 waves of 32x64
+using X64x64 = XTile<64, 64, 2, 2>;      // 4 waves of 32x32
+using X256x128 = XTile<256, 128, 4, 2>;  // 8 waves of 64x64
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// LDS rows of the split kernel are 32 bf16 (64 bytes, four 16-byte chunks)
+// without padding; chunk c of row r is stored at position c ^ lds_swz(r).
+// With this swizzle the 16-byte operand reads (32 consecutive rows, one chunk
+// each) and the 16-byte staging writes (four chunks of a row per four lanes)
+// touch distinct banks in every group of 8 lanes over 128 bytes and of 16
+// lanes over 256 bytes.
+__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t lo_elem, uint32_t hi_elem) {
+  return (lo_elem >> 16) | (hi_elem & 0xFFFF0000u);
+}
+
+template <class TL, Epi EPI>
+__global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
+  constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, NT = TL::NT;
+  constexpr int FM = TL::FM, FN = TL::FN;
+  static_assert(TL::S == 2 && BK == 32, "two MFMA k-steps per 32-wide slab");
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][3][BM * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * BK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / TL::WN, wn = wave % TL::WN;
+  const int64_t M = p.m, N = p.n;
+  const float* __restrict__ A = p.a;
+  const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.b);
+
+  const int tile = xcd_tile(p);
+  const int64_t m0 = (int64_t)(tile / p.tiles_n) * BM;
+  const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
+
+  // Staging chunks: 8 consecutive k of one row (two float4 of A, one 16-byte
+  // vector of B). A slab row is 4 chunks.
+  constexpr int NA = BM * 4 / NT;  // A chunks per thread
+  constexpr int NB = BN * 4 / NT;  // B chunks per thread
+  static_assert(NA * NT == BM * 4 && NB * NT == BN * 4, "loader shape");
+
+  const float* ga[NA];
+  const uint16_t* gb[NB];
+  int la[NA], lb[NB];  // LDS element offsets of the chunks
+#pragma unroll
+  for (int i = 0; i < NA; i++) {
+    const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
+    ga[i] = A + min(m0 + row, M - 1) * p.lda + c * 8;
+    la[i] = row * BK + ((c ^ lds_swz(row)) << 3);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
+    gb[i] = B + min(n0 + row, N - 1) * p.ldb + c * 8;
+    lb[i] = row * BK + ((c ^ lds_swz(row)) << 3);
+  }
+  auto load_global = [&](f32x4 (&ra)[2 * NA], uint4 (&rb)[NB], int kt) {
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+      ra[2 * i] = *reinterpret_cast<const f32x4*>(ga[i] + (int64_t)kt * BK);
+      ra[2 * i + 1] = *reinterpret_cast<const f32x4*>(ga[i] + (int64_t)kt * BK + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; i++) rb[i] = *reinterpret_cast<const uint4*>(gb[i] + (int64_t)kt * BK);
+  };
+
+  // hi + mid + lo = a exactly, packed two bf16 per dword.
+  auto split_store = [&](const f32x4 (&ra)[2 * NA], const uint4 (&rb)[NB], int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+      uint32_t h[8], m[8], l[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float a = ra[2 * i + (e >> 2)][e & 3];
+        h[e] = __float_as_uint(a) & 0xFFFF0000u;
+        const float r1 = a - __uint_as_float(h[e]);
+        m[e] = __float_as_uint(r1) & 0xFFFF0000u;
+        l[e] = __float_as_uint(r1 - __uint_as_float(m[e]));
+      }
+      *reinterpret_cast<uint4*>(&As[buf][0][la[i]]) =
+          make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
+      *reinterpret_cast<uint4*>(&As[buf][1][la[i]]) =
+          make_uint4(pack_hi16(m[0], m[1]), pack_hi16(m[2], m[3]), pack_hi16(m[4], m[5]), pack_hi16(m[6], m[7]));
+      *reinterpret_cast<uint4*>(&As[buf][2][la[i]]) =
+          make_uint4(pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7]));
+    }
+#pragma unroll
+    for (int i = 0; i < NB; i++) *reinterpret_cast<uint4*>(&Bs[buf][lb[i]]) = rb[i];
+  };
+
+  // Operand reads: lane half h takes chunk 2s+h of its row; every row read by
+  // a lane is (32-aligned base) + lane%32, so its swizzle is lds_swz(lane%32).
+  const int arow = wm * TL::TM + (lane & 31);
+  const int brow = wn * TL::TN + (lane & 31);
+  const int sw = lds_swz(lane & 31);
+  const int h = lane >> 5;
+  auto read_ops = [&](int buf, int s, bf16x8 (&oa)[3][FM], bf16x8 (&ob)[FN]) {
+    const int co = ((2 * s + h) ^ sw) << 3;
+#pragma unroll
+    for (int t = 0; t < 3; t++)
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+        oa[t][i] = *reinterpret_cast<const bf16x8*>(&As[buf][t][(arow + 32 * i) * BK + co]);
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+      ob[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(brow + 32 * j) * BK + co]);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  auto mfma_step = [&](const bf16x8 (&oa)[3][FM], const bf16x8 (&ob)[FN]) {
+    // smallest terms first
+#pragma unroll
+    for (int t = 2; t >= 0; t--)
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t][i], ob[j], acc[i][j], 0, 0, 0);
+  };
+
+  // Slab kt is in LDS buffer kt&1; `use` holds the global values of slab
+  // kt+1 and `fill` receives slab kt+2 (clamped to the last slab: a
+  // redundant load keeps the body free of branches, so the split's VALU work
+  // and the LDS traffic interleave with the MFMAs).
+  const int nk = p.nk;
+  auto body = [&](int kt, const f32x4 (&ra_use)[2 * NA], const uint4 (&rb_use)[NB], f32x4 (&ra_fill)[2 * NA],
+                  uint4 (&rb_fill)[NB]) {
+    const int buf = kt & 1;
+    load_global(ra_fill, rb_fill, min(kt + 2, nk - 1));
+    bf16x8 a0[3][FM], b0[FN], a1[3][FM], b1[FN];
+    read_ops(buf, 0, a0, b0);
+    read_ops(buf, 1, a1, b1);
+    mfma_step(a0, b0);
+    split_store(ra_use, rb_use, buf ^ 1);
+    mfma_step(a1, b1);
+    __syncthreads();
+  };
+
+  f32x4 raA[2 * NA], raB[2 * NA];
+  uint4 rbA[NB], rbB[NB];
+  load_global(raA, rbA, 0);
+  split_store(raA, rbA, 0);
+  load_global(raA, rbA, min(1, nk - 1));
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    body(kt, raA, rbA, raB, rbB);
+    body(kt + 1, raB, rbB, raA, rbA);
+  }
+  if (kt + 1 < nk) {
+    body(kt, raA, rbA, raB, rbB);
+    kt++;
+  }
+  {
+    const int buf = kt & 1;
+    bf16x8 a0[3][FM], b0[FN], a1[3][FM], b1[FN];
+    read_ops(buf, 0, a0, b0);
+    read_ops(buf, 1, a1, b1);
+    mfma_step(a0, b0);
+    mfma_step(a1, b1);
+  }
+  store_c<TL, EPI>(p, acc, m0, n0, wm, wn, lane);
+}
+
+template <class TL, Epi EPI>
+void launch_x3(GemmParams p, hipStream_t s) {
+  p.tiles_m = (int)((p.m + TL::BM - 1) / TL::BM);
+  p.tiles_n = (int)((p.n + TL::BN - 1) / TL::BN);
+  p.nk = (int)(p.k / TL::BK);
+  dim3 grid(p.tiles_m * p.tiles_n), block(TL::NT);
+  hipLaunchKernelGGL((gemm_x3_kernel<TL, EPI>), grid, block, 0, s, p);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -410,6 +634,70 @@ void dispatch_tile(TileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   }
 }
 
+enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, kCount };
+const char* const kXTileNames[] = {"128x128", "128x64", "128x64v", "64x128", "64x64", "256x128"};
+
+// FA_GEMM_XTILE=<name> forces a split-bf16 tile shape; FA_GEMM_MFMA=f32 runs
+// bf16 weights through the fp32 MFMA kernel instead (tuning, comparison).
+int forced_xtile() {
+  static int v = [] {
+    const char* e = std::getenv("FA_GEMM_XTILE");
+    if (!e) return -1;
+    for (int i = 0; i < (int)XTileId::kCount; i++)
+      if (std::strcmp(e, kXTileNames[i]) == 0) return i;
+    return -1;
+  }();
+  return v;
+}
+
+bool use_f32_mfma() {
+  static bool v = [] {
+    const char* e = std::getenv("FA_GEMM_MFMA");
+    return e && std::strcmp(e, "f32") == 0;
+  }();
+  return v;
+}
+
+// Split-bf16 tile choice, from measurements on MI355X (M 5517 and 32768,
+// N 768..2304, K 768 and 1152): the 256x128 tile (eight waves of 64x64) wins
+// once it gives most CUs a tile; below that 64x64 tiles (128x64 for GeGLU,
+// which needs column-block pairs) spread the work over all CUs.
+XTileId pick_xtile(int64_t m, int64_t n, Epi epi, int cus) {
+  const int64_t tiles256 = ((m + 255) / 256) * ((n + 127) / 128);
+  if (5 * tiles256 >= 4LL * cus) return XTileId::x256x128;
+  return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
+}
+
+template <class TL>
+void dispatch_x3_epi(const GemmParams& p, Epi epi, hipStream_t s) {
+  switch (epi) {
+    case Epi::None: launch_x3<TL, Epi::None>(p, s); break;
+    case Epi::Generic: launch_x3<TL, Epi::Generic>(p, s); break;
+    case Epi::GeGLU:
+      if constexpr (TL::FN % 2 == 0) launch_x3<TL, Epi::GeGLU>(p, s);
+      break;
+  }
+}
+
+void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
+  switch (t) {
+    case XTileId::x128x64: dispatch_x3_epi<X128x64>(p, epi, s); break;
+    case XTileId::x128x64v: dispatch_x3_epi<X128x64v>(p, epi, s); break;
+    case XTileId::x64x128: dispatch_x3_epi<X64x128>(p, epi, s); break;
+    case XTileId::x64x64: dispatch_x3_epi<X64x64>(p, epi, s); break;
+    case XTileId::x256x128: dispatch_x3_epi<X256x128>(p, epi, s); break;
+    default: dispatch_x3_epi<X128x128>(p, epi, s); break;
+  }
+}
+
+bool x3_has_geglu(XTileId t) {
+  switch (t) {
+    case XTileId::x128x64: return X128x64::FN % 2 == 0;
+    case XTileId::x64x64: return X64x64::FN % 2 == 0;
+    default: return true;
+  }
+}
+
 }  // namespace
 
 int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
@@ -432,7 +720,12 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   // aligned and k a whole number of 32-wide slabs.
   const bool fast = nk && g.k > 0 && g.k % 32 == 0 && aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 &&
                     (bf16 ? g.ldb % 8 == 0 : g.ldb % 4 == 0);
-  if (fast) {
+  if (fast && bf16 && !use_f32_mfma()) {
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    XTileId t = (XTileId)forced_xtile();
+    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.epi, cus);
+    dispatch_x3(t, p, g.epi, s);
+  } else if (fast) {
     TileId t = (TileId)forced_tile();
     if ((int)t < 0 || (g.epi == Epi::GeGLU && t == TileId::k64x64))
       t = pick_tile(g.m, g.n, g.epi, ctx->cu_count > 0 ? ctx->cu_count : 256);

@@ -99,3 +99,76 @@ def test_bad_inputs(models):
         gm.embed_ids(np.full((1, 4), 262144, np.int32), np.array([4], np.int32))  # id out of range
     with pytest.raises(G.GemmaError):
         gm.embed_ids(ids, np.array([0], np.int32))
+
+
+def test_c3_sliding_band(models):
+    """C3 (64 x 512, all full length): T = 512 > 257, so the 20 sliding layers
+    mask |i-j| >= 257 (embed.go:169-172,183-186) and differ from the global
+    ones. All 64 on the GPU, the first 4 through the oracle."""
+    gm, om = models
+    b = S.make_batch("C3")
+    got = gm.embed_ids(b.ids, b.lengths)
+    assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
+    ref = om.embed(b.ids[:4], b.lengths[:4])
+    compare(got[:4], ref, "C3[0:4]")
+
+
+def test_c4_long_sequences(models):
+    """C4 (8 x 2048, lengths 1024..2048): the GPU batch against the oracle for
+    the shortest sequence (band active, far beyond one attention tile)."""
+    gm, om = models
+    b = S.make_batch("C4")
+    got = gm.embed_ids(b.ids, b.lengths)
+    i = int(np.argmin(b.lengths))
+    L = int(b.lengths[i])
+    ref = om.embed(b.ids[i:i + 1, :L], b.lengths[i:i + 1])
+    compare(got[i:i + 1], ref, f"C4[{i}] L={L}")
+    # the other sequences: unit norm and batch invariance against a single-sequence run
+    j = int(np.argmax(b.lengths))
+    alone = gm.embed_ids(b.ids[j:j + 1, :int(b.lengths[j])], b.lengths[j:j + 1])
+    assert cos_rows(alone, got[j:j + 1]).min() >= 0.9999
+
+
+def _topk_agree(q, docs, gi, oi, k, what):
+    """Top-k index lists agree wherever the float64 scores leave no near-tie
+    (gap > 1e-5 among the k+1 best); elsewhere the GPU's list must still be a
+    valid top-k within that tolerance. Ties order by lower index
+    (reduce.go:286-289)."""
+    s = q.astype(np.float64) @ docs.astype(np.float64).T
+    srt = -np.sort(-s, axis=1)[:, :k + 1]
+    gaps = np.diff(-srt, axis=1).min(1)
+    clear = gaps > 1e-5
+    assert np.array_equal(gi[clear], oi[clear]), what
+    kth = srt[:, k - 1]
+    got_scores = np.take_along_axis(s, gi.astype(np.int64), 1)
+    assert (got_scores.min(1) >= kth - 1e-5).all(), what
+    print(f"{what}: {int(clear.sum())}/{len(clear)} rows without near-ties, all identical", flush=True)
+    return clear
+
+
+def test_c5_scoring_top10(models, ctx):
+    """C5 (256 x 128 ragged) + scoring against 100 000 unit docs: embeddings
+    vs the oracle on 8 queries; GPU top-10 (fa_similarities_topk) vs the
+    oracle's top-10 on the same queries, and end to end from the oracle's own
+    embeddings of those 8."""
+    from ai_amd import _native as N
+    gm, om = models
+    b = S.make_batch("C5")
+    q = gm.embed_ids(b.ids, b.lengths)
+    sub = slice(0, 8)
+    Tm = int(b.lengths[sub].max())
+    ref = om.embed(b.ids[sub, :Tm], b.lengths[sub])
+    compare(q[sub], ref, "C5[0:8]")
+    docs = b.corpus
+    k = 10
+    idx = np.empty((q.shape[0], k), np.int32)
+    val = np.empty((q.shape[0], k), np.float32)
+    N.check(ctx.h, N.lib().fa_similarities_topk(ctx.h, N.ptr(q), q.shape[0], N.ptr(docs), docs.shape[0], 768, k,
+                                                N.ptr(idx), N.ptr(val)))
+    nq = 64
+    oi, ov = O.similarities_topk(q[:nq], docs, k)
+    clear = _topk_agree(q[:nq], docs, idx[:nq], oi, k, "C5 scoring, same queries")
+    assert clear.mean() >= 0.9
+    assert np.allclose(val[:nq], ov, atol=1e-5)
+    oi2, _ = O.similarities_topk(ref, docs, k)
+    _topk_agree(ref, docs, idx[sub], oi2, k, "C5 scoring, oracle embeddings end to end")
