@@ -1,17 +1,28 @@
-// fp32-accumulate MFMA GEMM for gfx950: C = epilogue(A . B).
+// MFMA GEMMs for gfx950 with fp32 results: C = epilogue(A . B).
 //
 // A: fp32 [m x k] row-major. B: logical [k x n], stored bf16 or fp32, either
-// as [n x k] rows (checkpoint [out,in] weights, docs) or [k x n] rows. A
-// workgroup computes a BM x BN tile of C with WM x WN waves; each wave owns a
-// (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks of v_mfma_f32_32x32x2_f32
-// (16 accumulators per lane per block). K advances in slabs of BK through two
-// LDS buffers: the next slab's global loads are issued at the top of a slab,
-// written to the other buffer before the slab's last MFMA step, and one
-// barrier per slab separates the buffers. The first operand reads of the next
-// slab are issued right after that barrier, so their latency overlaps the
-// current slab's last MFMAs; within a slab the operands of step s+1 are read
-// while the MFMAs of step s run. bf16 weights are widened to fp32 (exact) when
-// written to LDS, so the MFMA operands are always fp32.
+// as [n x k] rows (checkpoint [out,in] weights, docs) or [k x n] rows.
+//
+// Two kernels:
+//  - gemm_x3_kernel (bf16 [n x k] weights, the encoder's path): each fp32 A
+//    value is split exactly into three bf16 terms and multiplied by the bf16
+//    weight with v_mfma_f32_32x32x16_bf16, accumulating in fp32 (the products
+//    are exact, so the result carries fp32 information at the bf16 MFMA rate
+//    divided by three). Described at the kernel.
+//  - gemm_kernel (every other operand combination, and fp32 weights): fp32
+//    operands on v_mfma_f32_32x32x2_f32, described below.
+//
+// gemm_kernel: a workgroup computes a BM x BN tile of C with WM x WN waves;
+// each wave owns a (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks of
+// v_mfma_f32_32x32x2_f32 (16 accumulators per lane per block). K advances in
+// slabs of BK through two LDS buffers: the next slab's global loads are
+// issued at the top of a slab, written to the other buffer before the slab's
+// last MFMA step, and one barrier per slab separates the buffers. The first
+// operand reads of the next slab are issued right after that barrier, so
+// their latency overlaps the current slab's last MFMAs; within a slab the
+// operands of step s+1 are read while the MFMAs of step s run. bf16 weights
+// are widened to fp32 (exact) when written to LDS, so the MFMA operands are
+// always fp32.
 //
 // MFMA operand layout (32x32x2, one block): lane l supplies A[row l%32][k]
 // and B[k][col l%32] with k = l/32; the 16 results of lane l are C[row][col]
@@ -21,11 +32,9 @@
 // k = 8s..8s+3 and lanes 32-63 take k = 8s+4..8s+7, and MFMA number c (0..3)
 // pairs k = 8s+c with 8s+4+c on both operands.
 //
-// Work distribution: one workgroup per tile, XCD-aware tile order. The tile
-// shape is chosen per call from the output's tile count: 64x64 tiles (four
-// or more resident workgroups per CU, fine-grained balance over the 256 CUs)
-// until the 128x128 tiles fill several rounds of the CUs, 128x128 beyond.
-// A stream-K distribution (equal shares of (tile, K-slab) units plus a fixup
+// Work distribution (both kernels): one workgroup per tile, XCD-aware tile
+// order, tile shape chosen per call from the output's tile count. A
+// stream-K distribution (equal shares of (tile, K-slab) units plus a fixup
 // pass over split tiles) measured slower at these sizes: the fixup pass alone
 // costs 45-60 us at the C2 shapes.
 //
