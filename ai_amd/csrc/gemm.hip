@@ -413,6 +413,7 @@ using X128x64v = XTile<128, 64, 4, 1>;   // 4 waves of 32x64 (column-block pairs
 using X64x128 = XTile<64, 128, 2, 2>;    // 4 waves of 32x64
 using X64x64 = XTile<64, 64, 2, 2>;      // 4 waves of 32x32
 using X256x128 = XTile<256, 128, 4, 2>;  // 8 waves of 64x64
+using X128x128w8 = XTile<128, 128, 4, 2>;  // 8 waves of 32x64
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -643,8 +644,8 @@ void dispatch_tile(TileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   }
 }
 
-enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, kCount };
-const char* const kXTileNames[] = {"128x128", "128x64", "128x64v", "64x128", "64x64", "256x128"};
+enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, x128x128w8, kCount };
+const char* const kXTileNames[] = {"128x128", "128x64", "128x64v", "64x128", "64x64", "256x128", "128x128w8"};
 
 // FA_GEMM_XTILE=<name> forces a split-bf16 tile shape; FA_GEMM_MFMA=f32 runs
 // bf16 weights through the fp32 MFMA kernel instead (tuning, comparison).
@@ -668,12 +669,13 @@ bool use_f32_mfma() {
 }
 
 // Split-bf16 tile choice, from measurements on MI355X (M 5517 and 32768,
-// N 768..2304, K 768 and 1152): the 256x128 tile (eight waves of 64x64) wins
-// once it gives most CUs a tile; below that 64x64 tiles (128x64 for GeGLU,
-// which needs column-block pairs) spread the work over all CUs.
+// N 768..2304, K 768 and 1152): the 128x128 tile of eight 32x64 waves (two
+// workgroups per CU) is the fastest or within 4 % of the fastest at every
+// measured shape once it gives the CUs half a tile each; below that, 64x64
+// tiles (128x64 for GeGLU, which needs column-block pairs) spread the work.
 XTileId pick_xtile(int64_t m, int64_t n, Epi epi, int cus) {
-  const int64_t tiles256 = ((m + 255) / 256) * ((n + 127) / 128);
-  if (5 * tiles256 >= 4LL * cus) return XTileId::x256x128;
+  const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128);
+  if (2 * tiles128 >= cus) return XTileId::x128x128w8;
   return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
 }
 
@@ -695,6 +697,7 @@ void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
     case XTileId::x64x128: dispatch_x3_epi<X64x128>(p, epi, s); break;
     case XTileId::x64x64: dispatch_x3_epi<X64x64>(p, epi, s); break;
     case XTileId::x256x128: dispatch_x3_epi<X256x128>(p, epi, s); break;
+    case XTileId::x128x128w8: dispatch_x3_epi<X128x128w8>(p, epi, s); break;
     default: dispatch_x3_epi<X128x128>(p, epi, s); break;
   }
 }
