@@ -66,4 +66,26 @@ __device__ __forceinline__ float rms_inv(float ss, int n, float eps) {
   return (float)(1.0 / sqrt((double)t));
 }
 
+// Exact three-way bf16 split of an fp32 value: a = hi + mid + lo, hi is a
+// with its low 16 bits cleared, mid the same of a - hi (exact in fp32),
+// lo = a - hi - mid (at most 8 significant bits, so exact in bf16). The
+// split-bf16 GEMM multiplies each term by a bf16 weight exactly and
+// accumulates in fp32. Non-finite values do not survive the split
+// (inf - inf).
+struct Split3 {
+  uint32_t h, m, l;  // fp32 bit patterns; the bf16 terms are the high halves
+};
+
+__device__ __forceinline__ Split3 split3(float a) {
+  Split3 r;
+  r.h = __float_as_uint(a) & 0xFFFF0000u;
+  const float r1 = a - __uint_as_float(r.h);
+  r.m = __float_as_uint(r1) & 0xFFFF0000u;
+  r.l = __float_as_uint(r1 - __uint_as_float(r.m));
+  return r;
+}
+
+// Two bf16 high halves packed as one dword, element `lo` first in memory.
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t lo, uint32_t hi) { return (lo >> 16) | (hi & 0xFFFF0000u); }
+
 }  // namespace fa

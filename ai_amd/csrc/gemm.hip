@@ -425,9 +425,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // lanes over 256 bytes.
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-__device__ __forceinline__ uint32_t pack_hi16(uint32_t lo_elem, uint32_t hi_elem) {
-  return (lo_elem >> 16) | (hi_elem & 0xFFFF0000u);
-}
+
+// Staging registers hold vector types (HIP's struct uint4 in an array was
+// placed in scratch memory by the compiler).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <class TL, Epi EPI>
 __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
@@ -455,13 +456,13 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
   constexpr int NB = BN * 4 / NT;  // B chunks per thread
   static_assert(NA * NT == BM * 4 && NB * NT == BN * 4, "loader shape");
 
-  const float* ga[NA];
+  int64_t ga[NA];  // element offsets of the A chunks (slab 0)
   const uint16_t* gb[NB];
   int la[NA], lb[NB];  // LDS element offsets of the chunks
 #pragma unroll
   for (int i = 0; i < NA; i++) {
     const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
-    ga[i] = A + min(m0 + row, M - 1) * p.lda + c * 8;
+    ga[i] = min(m0 + row, M - 1) * p.lda + c * 8;
     la[i] = row * BK + ((c ^ lds_swz(row)) << 3);
   }
 #pragma unroll
@@ -470,28 +471,28 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
     gb[i] = B + min(n0 + row, N - 1) * p.ldb + c * 8;
     lb[i] = row * BK + ((c ^ lds_swz(row)) << 3);
   }
-  auto load_global = [&](f32x4 (&ra)[2 * NA], uint4 (&rb)[NB], int kt) {
+  auto load_global = [&](f32x4 (&ra)[2 * NA], u32x4 (&rb)[NB], int kt) {
 #pragma unroll
     for (int i = 0; i < NA; i++) {
-      ra[2 * i] = *reinterpret_cast<const f32x4*>(ga[i] + (int64_t)kt * BK);
-      ra[2 * i + 1] = *reinterpret_cast<const f32x4*>(ga[i] + (int64_t)kt * BK + 4);
+      const int64_t off = ga[i] + (int64_t)kt * BK;
+      ra[2 * i] = *reinterpret_cast<const f32x4*>(A + off);
+      ra[2 * i + 1] = *reinterpret_cast<const f32x4*>(A + off + 4);
     }
 #pragma unroll
-    for (int i = 0; i < NB; i++) rb[i] = *reinterpret_cast<const uint4*>(gb[i] + (int64_t)kt * BK);
+    for (int i = 0; i < NB; i++) rb[i] = *reinterpret_cast<const u32x4*>(gb[i] + (int64_t)kt * BK);
   };
 
-  // hi + mid + lo = a exactly, packed two bf16 per dword.
-  auto split_store = [&](const f32x4 (&ra)[2 * NA], const uint4 (&rb)[NB], int buf) {
+  // hi + mid + lo = a exactly (split3, device_math.h), two bf16 per dword.
+  auto split_store = [&](const f32x4 (&ra)[2 * NA], const u32x4 (&rb)[NB], int buf) {
 #pragma unroll
     for (int i = 0; i < NA; i++) {
       uint32_t h[8], m[8], l[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const float a = ra[2 * i + (e >> 2)][e & 3];
-        h[e] = __float_as_uint(a) & 0xFFFF0000u;
-        const float r1 = a - __uint_as_float(h[e]);
-        m[e] = __float_as_uint(r1) & 0xFFFF0000u;
-        l[e] = __float_as_uint(r1 - __uint_as_float(m[e]));
+        const Split3 sp = split3(ra[2 * i + (e >> 2)][e & 3]);
+        h[e] = sp.h;
+        m[e] = sp.m;
+        l[e] = sp.l;
       }
       *reinterpret_cast<uint4*>(&As[buf][0][la[i]]) =
           make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
@@ -501,7 +502,7 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
           make_uint4(pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7]));
     }
 #pragma unroll
-    for (int i = 0; i < NB; i++) *reinterpret_cast<uint4*>(&Bs[buf][lb[i]]) = rb[i];
+    for (int i = 0; i < NB; i++) *reinterpret_cast<u32x4*>(&Bs[buf][lb[i]]) = rb[i];
   };
 
   // Operand reads: lane half h takes chunk 2s+h of its row; every row read by
@@ -546,8 +547,8 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
   // redundant load keeps the body free of branches, so the split's VALU work
   // and the LDS traffic interleave with the MFMAs).
   const int nk = p.nk;
-  auto body = [&](int kt, const f32x4 (&ra_use)[2 * NA], const uint4 (&rb_use)[NB], f32x4 (&ra_fill)[2 * NA],
-                  uint4 (&rb_fill)[NB]) {
+  auto body = [&](int kt, const f32x4 (&ra_use)[2 * NA], const u32x4 (&rb_use)[NB], f32x4 (&ra_fill)[2 * NA],
+                  u32x4 (&rb_fill)[NB]) {
     const int buf = kt & 1;
     load_global(ra_fill, rb_fill, min(kt + 2, nk - 1));
     bf16x8 a0[3][FM], b0[FN], a1[3][FM], b1[FN];
@@ -560,7 +561,7 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
   };
 
   f32x4 raA[2 * NA], raB[2 * NA];
-  uint4 rbA[NB], rbB[NB];
+  u32x4 rbA[NB], rbB[NB];
   load_global(raA, rbA, 0);
   split_store(raA, rbA, 0);
   load_global(raA, rbA, min(1, nk - 1));

@@ -339,7 +339,7 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
     char* end = nullptr;
     long i = std::strtol(s.c_str() + 6, &end, 10);
     if (i < 0 || i >= c.n_dense || std::string(end) != ".linear.weight")
-      return set_error(ctx, FA_ERR_ARG, "gemma: weight %q not found", name);
+      return set_error(ctx, FA_ERR_ARG, "gemma: weight \"%s\" not found", name);
     if (!shape_is({m->dense_out[i], m->dense_in[i]}))
       return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
     rc = put_matrix(m->dense[i], m->dense_out[i], m->dense_in[i], identity);
