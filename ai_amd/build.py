@@ -83,7 +83,9 @@ def build_synth(verbose: bool = False) -> str:
 
 
 HOST = os.path.join(PKG, "host")
-CPP_TESTS = ["test_tensor", "test_gemma"]
+HOST_SOURCES = ["fiber.cpp", "json.cpp", "tokenizer.cpp"]
+CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer"]
+CPP_CPU_TESTS = ["test_tokenizer"]  # need no GPU
 CPP_TEST_BIN = os.path.join(BUILD, "cpp_tests")
 
 
@@ -93,7 +95,7 @@ def build_host(verbose: bool = False) -> str:
     out = os.path.join(LIB, "libfiber_host.so")
     tmp = out + ".tmp"
     _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", INCLUDE, "-I", HOST,
-          os.path.join(HOST, "fiber.cpp"), "-o", tmp, "-L", LIB, "-lfa_rocm",
+          *[os.path.join(HOST, f) for f in HOST_SOURCES], "-o", tmp, "-L", LIB, "-lfa_rocm",
           "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(tmp, out)
     os.makedirs(CPP_TEST_BIN, exist_ok=True)
