@@ -83,9 +83,10 @@ def build_synth(verbose: bool = False) -> str:
 
 
 HOST = os.path.join(PKG, "host")
-HOST_SOURCES = ["fiber.cpp", "json.cpp", "tokenizer.cpp"]
+HOST_SOURCES = ["fiber.cpp", "json.cpp", "tokenizer.cpp", "safetensors.cpp"]
 CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer"]
 CPP_CPU_TESTS = ["test_tokenizer"]  # need no GPU
+CPP_DRIVERS = ["st_dump", "embed_dir"]  # programs the Python tests drive
 CPP_TEST_BIN = os.path.join(BUILD, "cpp_tests")
 
 
@@ -103,7 +104,7 @@ def build_host(verbose: bool = False) -> str:
     # rpath relative to the binary, so the tree can be moved to another host
     rpath = "-Wl,-rpath,$ORIGIN/" + os.path.relpath(LIB, CPP_TEST_BIN)
     jobs = []
-    for t in CPP_TESTS:
+    for t in CPP_TESTS + CPP_DRIVERS:
         jobs.append([cxx, "-O2", "-std=c++17", "-Wall", "-I", INCLUDE, "-I", HOST, "-I", tdir,
                      os.path.join(tdir, t + ".cpp"), "-o", os.path.join(CPP_TEST_BIN, t),
                      "-L", LIB, "-lfiber_host", "-lfa_rocm", "-lfa_synth", rpath])

@@ -2,12 +2,17 @@
 // See fiber.hpp for the mapping to the reference.
 #include "fiber.hpp"
 
+#include <sys/stat.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
 #include <numeric>
 #include <sstream>
+
+#include "json.hpp"
+#include "safetensors.hpp"
 
 namespace fiber {
 
@@ -396,6 +401,261 @@ std::vector<std::vector<float>> Model::EmbedIDs(const std::vector<std::vector<in
   std::vector<std::vector<float>> res(B);
   for (int32_t b = 0; b < B; b++) res[b].assign(out.begin() + (size_t)b * dim, out.begin() + (size_t)(b + 1) * dim);
   return res;
+}
+
+namespace {
+
+bool exists(const std::string& path) {
+  struct stat st;
+  return stat(path.c_str(), &st) == 0;
+}
+
+json::Value read_json(const std::string& path, const char* what) {
+  try {
+    return json::parse_file(path);
+  } catch (const json::Error& e) {
+    throw Error(std::string("gemma: ") + what + ": " + e.what());
+  }
+}
+
+}  // namespace
+
+Config LoadConfig(const std::string& dir) {
+  const json::Value v = read_json(dir + "/config.json", "config.json");
+  Config c;
+  try {
+    if (v.get_string("model_type") == "embedding_gemma2")
+      throw Error("gemma: EmbeddingGemma 2 checkpoints are not supported by this build");
+    c.HiddenSize = (int)v.get_int("hidden_size");
+    c.IntermediateSize = (int)v.get_int("intermediate_size");
+    c.NumHiddenLayers = (int)v.get_int("num_hidden_layers");
+    c.NumAttentionHeads = (int)v.get_int("num_attention_heads");
+    c.NumKeyValueHeads = (int)v.get_int("num_key_value_heads");
+    c.HeadDim = (int)v.get_int("head_dim");
+    c.VocabSize = (int)v.get_int("vocab_size");
+    c.SlidingWindow = (int)v.get_int("sliding_window");
+    c.UseBidirectional = v.get_bool("use_bidirectional_attention");
+    c.RopeTheta = v.get_number("rope_theta");
+    c.RopeLocalBaseFreq = v.get_number("rope_local_base_freq");
+    c.QueryPreAttnScalar = v.get_number("query_pre_attn_scalar");
+    c.RMSNormEps = (float)v.get_number("rms_norm_eps");
+    const int64_t maxpos = v.get_int("max_position_embeddings");
+    c.MaxTokens = (maxpos == 0 || maxpos > 2048) ? 2048 : (int)maxpos;  // model.go:100-104
+    c.SlidingWindowPattern = (int)v.get_int("sliding_window_pattern", 6);  // config.go:211-213
+    if (c.SlidingWindowPattern == 0) c.SlidingWindowPattern = 6;
+    // layer_types must be the periodic pattern the GPU encoder runs:
+    // full attention iff (l+1) % pattern == 0 (config.go:214-225)
+    if (const json::Value* lt = v.find("layer_types"); lt && lt->is_array() && !lt->items().empty()) {
+      const auto& t = lt->items();
+      int first_full = -1;
+      for (size_t i = 0; i < t.size(); i++)
+        if (t[i].as_string() == "full_attention") {
+          first_full = (int)i;
+          break;
+        }
+      const int pat = first_full >= 0 ? first_full + 1 : (int)t.size() + 1;
+      for (size_t i = 0; i < t.size(); i++) {
+        const bool full = (int)((i + 1) % pat) == 0;
+        if (t[i].as_string() != (full ? "full_attention" : "sliding_attention"))
+          throw Error("gemma: layer_types is not a periodic sliding/full pattern");
+      }
+      c.SlidingWindowPattern = pat;
+    }
+    const std::string act = v.get_string("hidden_activation");
+    if (!act.empty() && act != "gelu_pytorch_tanh")
+      throw Error("gemma: activation \"" + act + "\" not supported (want gelu_pytorch_tanh)");
+    if (const json::Value* rs = v.find("rope_scaling"); rs && !rs->is_null())
+      throw Error("gemma: rope_scaling is set; not supported");
+  } catch (const json::Error& e) {
+    throw Error(std::string("gemma: config.json: ") + e.what());
+  }
+  if (c.HiddenSize == 0 || c.NumHiddenLayers == 0) throw Error("gemma: config is missing hidden_size or num_hidden_layers");
+  if (c.HeadDim % 2 != 0) throw Error("gemma: head_dim " + std::to_string(c.HeadDim) + " must be even for RoPE");
+  if (c.NumKeyValueHeads <= 0 || c.NumAttentionHeads % c.NumKeyValueHeads != 0)
+    throw Error("gemma: " + std::to_string(c.NumAttentionHeads) + " query heads not a multiple of " +
+                std::to_string(c.NumKeyValueHeads) + " key/value heads");
+  c.Dense.clear();
+  return c;
+}
+
+std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
+  std::string stage = "config.json";  // names the file in JSON type errors
+  try {
+    Config cfg = LoadConfig(dir);
+    if (o.MaxTokens > 0) cfg.MaxTokens = std::min(o.MaxTokens, 2048);
+    if (o.BatchTokens <= 0) throw Error("gemma: BatchTokens must be positive");
+    // sentence-transformers head (model.go:236-310): mean pooling, Dense
+    // layers without bias or activation, Normalize
+    struct DenseMod {
+      std::string path;
+      int in, out;
+    };
+    std::vector<DenseMod> dense;
+    stage = "modules.json";
+    if (exists(dir + "/modules.json")) {
+      const json::Value mods = read_json(dir + "/modules.json", "modules.json");
+      for (const json::Value& mod : mods.items()) {
+        const std::string type = mod.get_string("type"), path = mod.get_string("path");
+        const std::string mdir = dir + "/" + path;
+        stage = mdir + "/config.json";
+        if (type == "sentence_transformers.models.Pooling" ||
+            type == "sentence_transformers.sentence_transformer.modules.pooling.Pooling") {
+          const json::Value pc = read_json(mdir + "/config.json", "pooling config");
+          const std::string mode = pc.get_string("pooling_mode");
+          if ((!mode.empty() && mode != "mean") || pc.get_bool("pooling_mode_cls_token") ||
+              pc.get_bool("pooling_mode_lasttoken") ||
+              (mode.empty() && !pc.get_bool("pooling_mode_mean_tokens", true)))
+            throw Error("gemma: only mean pooling is supported");
+        } else if (type == "sentence_transformers.models.Dense") {
+          const json::Value dc = read_json(mdir + "/config.json", "Dense config");
+          if (dc.get_bool("bias")) throw Error("gemma: Dense layers with bias are not supported");
+          const std::string act = dc.get_string("activation_function");
+          if (!(act.empty() || act == "torch.nn.modules.linear.Identity"))
+            throw Error("gemma: Dense activation \"" + act + "\" not supported");
+          dense.push_back({mdir, (int)dc.get_int("in_features"), (int)dc.get_int("out_features")});
+        }
+      }
+    }
+    if (dense.size() > 4) throw Error("gemma: at most 4 Dense layers");
+    int width = cfg.HiddenSize;
+    for (const auto& d : dense) {
+      if (d.in != width)
+        throw Error("gemma: Dense in_features " + std::to_string(d.in) + " after width " + std::to_string(width));
+      cfg.Dense.push_back(d.out);
+      width = d.out;
+    }
+    // every file is read and checked before the GPU is touched
+    stage = "tokenizer.json";
+    std::unique_ptr<tokenizer::Tokenizer> tok;
+    try {
+      tok = std::make_unique<tokenizer::Tokenizer>(tokenizer::Tokenizer::Load(dir + "/tokenizer.json"));
+    } catch (const tokenizer::Error& e) {
+      throw Error(e.what());
+    }
+    stage = "config_sentence_transformers.json";
+    std::map<std::string, std::string> prompts;
+    if (exists(dir + "/config_sentence_transformers.json")) {
+      const json::Value sc = read_json(dir + "/config_sentence_transformers.json", "config_sentence_transformers.json");
+      if (const json::Value* pr = sc.find("prompts"); pr && pr->is_object())
+        for (const auto& kv : pr->members()) prompts[kv.first] = kv.second.as_string();
+    }
+    stage = "safetensors";
+    auto open_dir = [](const std::string& d) {
+      try {
+        return safetensors::File::OpenDir(d);
+      } catch (const safetensors::Error& e) {
+        throw Error(e.what());
+      }
+    };
+    safetensors::File f = open_dir(dir);
+    std::vector<safetensors::File> dense_files;
+    for (const auto& d : dense) {
+      dense_files.push_back(open_dir(d.path));
+      if (!dense_files.back().Find("linear.weight")) throw Error("gemma: " + d.path + ": no linear.weight");
+    }
+    // weights (model.go:104-191): names with or without a model./language_model. prefix
+    std::vector<std::pair<std::string, std::string>> names;  // (stored, ours)
+    auto want = [&](const std::string& name) {
+      for (const char* prefix : {"", "model.", "language_model."})
+        if (f.Find(prefix + name)) {
+          names.emplace_back(prefix + name, name);
+          return;
+        }
+      throw Error("gemma: weight \"" + name + "\" not found");
+    };
+    want("embed_tokens.weight");
+    for (int l = 0; l < cfg.NumHiddenLayers; l++) {
+      const std::string p = "layers." + std::to_string(l) + ".";
+      for (const char* n : {"input_layernorm.weight", "post_attention_layernorm.weight",
+                            "pre_feedforward_layernorm.weight", "post_feedforward_layernorm.weight",
+                            "self_attn.q_norm.weight", "self_attn.k_norm.weight", "self_attn.q_proj.weight",
+                            "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                            "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight"})
+        want(p + n);
+    }
+    want("norm.weight");
+
+    stage = "weights";
+    auto m = std::make_unique<Model>(cfg);
+    m->batch_tokens_ = o.BatchTokens;
+    m->tok_ = std::move(tok);
+    m->prompts_ = std::move(prompts);
+    auto put = [&](const safetensors::File& file, const std::string& stored, const std::string& name) {
+      const safetensors::Info* info = file.Find(stored);
+      if (info->dtype == "BF16") {
+        size_t nb;
+        const uint8_t* raw = file.Raw(stored, &nb);
+        std::vector<uint16_t> bits(nb / 2);
+        std::memcpy(bits.data(), raw, nb);  // the data section need not be 2-byte aligned
+        m->SetWeightBF16(name, info->shape, bits.data());
+      } else {
+        std::vector<float> v;
+        try {
+          v = file.Float32s(stored);
+        } catch (const safetensors::Error& e) {
+          throw Error(e.what());
+        }
+        m->SetWeightF32(name, info->shape, v.data());
+      }
+    };
+    for (const auto& n : names) put(f, n.first, n.second);
+    for (size_t i = 0; i < dense.size(); i++)
+      put(dense_files[i], "linear.weight", "dense." + std::to_string(i) + ".linear.weight");
+    m->Finalize();
+    return m;
+  } catch (const json::Error& e) {
+    throw Error("gemma: " + stage + ": " + e.what());
+  }
+}
+
+std::vector<std::vector<float>> Model::Embed(const std::vector<std::string>& texts, const EmbedOpts& o) const {
+  if (!tok_) throw Error("gemma: Embed needs a model from Load (it has no tokenizer)");
+  std::string prefix;  // embed.go:99-114
+  if (o.has_prompt_text) {
+    prefix = o.PromptText;
+  } else if (!o.Prompt.empty()) {
+    auto it = prompts_.find(o.Prompt);
+    if (it == prompts_.end()) throw Error("gemma: no prompt named \"" + o.Prompt + "\"");
+    prefix = it->second;
+  }
+  const int dim = Dim();
+  if (o.Dim != 0 && (o.Dim < 1 || o.Dim > dim))
+    throw Error("gemma: Dim(" + std::to_string(o.Dim) + ") outside 1.." + std::to_string(dim));
+  const size_t n = texts.size();
+  std::vector<std::vector<int32_t>> ids(n);
+  for (size_t i = 0; i < n; i++) {
+    const std::vector<int> seq = tok_->Encode(prefix + texts[i]);
+    const size_t L = std::min(seq.size(), (size_t)cfg_.MaxTokens);
+    ids[i].assign(seq.begin(), seq.begin() + L);
+  }
+  // shortest first, stable (model.go:412-423); greedy batches whose longest
+  // sequence times their size stays within the token budget (embed.go:45-74)
+  std::vector<size_t> order(n);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return ids[a].size() < ids[b].size(); });
+  std::vector<std::vector<float>> out(n);
+  std::vector<size_t> batch;
+  size_t max_len = 0;
+  EmbedOpts eo;
+  eo.Dim = o.Dim;
+  auto flush = [&]() {
+    if (batch.empty()) return;
+    std::vector<std::vector<int32_t>> b;
+    for (size_t i : batch) b.push_back(ids[i]);
+    auto e = EmbedIDs(b, eo);
+    for (size_t k = 0; k < batch.size(); k++) out[batch[k]] = std::move(e[k]);
+    batch.clear();
+    max_len = 0;
+  };
+  for (size_t i : order) {
+    const size_t l = ids[i].size();
+    const size_t nm = std::max(max_len, l);
+    if (!batch.empty() && nm * (batch.size() + 1) > (size_t)batch_tokens_) flush();
+    batch.push_back(i);
+    max_len = std::max(max_len, l);
+  }
+  flush();
+  return out;
 }
 
 }  // namespace gemma

@@ -9,7 +9,11 @@
 //   tensor.Attention / AttentionScaled         tensor/attention.go:56-83
 //   tensor.PaddingMask / WindowMask / CausalMask   tensor/attention.go:21-42,97-107
 //   (*Tensor).Expand (stride-0 views)          tensor/view.go
-//   gemma.Model: Embed at the ids level, Dim, Close   models/gemma/model.go:40-71,336-343; embed.go:15-157
+//   gemma.Load / LoadConfig / Model.Embed (texts, prompts, Dim), Dim, Close
+//                                              models/gemma/model.go:76-330,336-382; config.go:153-240;
+//                                              embed.go:15-114 (EmbedIDs: the ids-level core, embed.go:118-157)
+//   tokenizer.Tokenizer                        tokenizer/tokenizer.go (tokenizer.hpp)
+//   safetensors.File                           safetensors/safetensors.go (safetensors.hpp)
 // Shape errors throw fiber::tensor::Error{Op, Msg}, where the reference
 // panics with *tensor.Error (tensor/errors.go:5-31); gemma's functions throw
 // fiber::gemma::Error where the reference returns error.
@@ -21,12 +25,14 @@
 #pragma once
 
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "fa_rocm.h"
+#include "tokenizer.hpp"
 
 namespace fiber {
 
@@ -124,13 +130,36 @@ struct Config {
   std::vector<int> Dense = {3072, 768};
 };
 
-// Option of Embed (embed.go:24-30): Dim truncates before L2 (Matryoshka).
+// Options of Embed (model.go:372-379): Dim truncates before L2
+// (Matryoshka); Prompt names a prompt of config_sentence_transformers.json,
+// PromptText gives the prefix itself (has_prompt_text marks it as set).
 struct EmbedOpts {
   int Dim = 0;
+  std::string Prompt;
+  std::string PromptText;
+  bool has_prompt_text = false;
 };
+
+// Options of Load (model.go:352-359): MaxTokens truncates sequences (0: the
+// config's max_position_embeddings, at most 2048); BatchTokens bounds
+// batch size x longest length per forward pass.
+struct LoadOpts {
+  int MaxTokens = 0;
+  int BatchTokens = 8192;
+};
+
+// config.json of a Gemma 3 text model (config.go:153-240): the fields the
+// encoder uses, validated as the reference validates them; EmbeddingGemma 2
+// checkpoints are refused.
+Config LoadConfig(const std::string& dir);
 
 class Model {
  public:
+  // Reads a model directory in the Hugging Face / sentence-transformers
+  // layout: config.json, tokenizer.json, *.safetensors (+ index), and the
+  // modules.json Pooling (mean), Dense (no bias, identity) and Normalize
+  // modules with config_sentence_transformers.json prompts (model.go:76-330).
+  static std::unique_ptr<Model> Load(const std::string& dir, const LoadOpts& o = {});
   explicit Model(const Config& cfg);
   ~Model();
   Model(const Model&) = delete;
@@ -144,12 +173,21 @@ class Model {
   // batched in one forward pass; sequences longer than MaxTokens are
   // truncated (embed.go:40-42). Returns one row per sequence.
   std::vector<std::vector<float>> EmbedIDs(const std::vector<std::vector<int32_t>>& ids, EmbedOpts o = {}) const;
+  // Embeddings of texts (embed.go:15-80): prompt prefix, tokenizer with its
+  // BOS/EOS template, truncation to MaxTokens, batches of similar length
+  // under BatchTokens, input order restored. Needs a model from Load.
+  std::vector<std::vector<float>> Embed(const std::vector<std::string>& texts, const EmbedOpts& o = {}) const;
   int Dim() const;
+  const Config& GetConfig() const { return cfg_; }
+  const tokenizer::Tokenizer* GetTokenizer() const { return tok_.get(); }
   void Close();
 
  private:
   Config cfg_;
   fa_model* m_ = nullptr;
+  std::unique_ptr<tokenizer::Tokenizer> tok_;
+  std::map<std::string, std::string> prompts_;
+  int batch_tokens_ = 8192;
 };
 
 }  // namespace gemma
