@@ -215,6 +215,175 @@ __global__ __launch_bounds__(NTA) void attention_varlen_kernel(VarlenParams p) {
   }
 }
 
+// ---- d-split variant -------------------------------------------------------
+// Four waves per workgroup: waves 2b and 2b+1 own the same 16 queries
+// (query block b of the item) and the two halves of the head dimension. Each
+// computes the partial scores over its 128 dimensions, the pair exchanges
+// them through LDS and adds them in the same order (half 0 + half 1, so both
+// waves hold identical scores and softmax statistics), and each accumulates
+// its half of O. Against one wave per 16 queries this halves the Q and O
+// registers and the K/V staging per thread, so two workgroups fit per SIMD
+// pair, and doubles the waves over a batch.
+constexpr int DS_NWAVE = 4;
+constexpr int DS_NT = DS_NWAVE * 64;
+constexpr int DS_HALF = AD / 2;
+constexpr int DS_NLD = KT * AD / 4 / DS_NT;  // float4 of K (and of V) per thread per tile
+
+__global__ __launch_bounds__(DS_NT) void attention_dsplit_kernel(VarlenParams p) {
+  __shared__ __attribute__((aligned(16))) float Ks[KT * KLD];
+  __shared__ __attribute__((aligned(16))) float Vs[KT * KLD];
+  __shared__ __attribute__((aligned(16))) float Sx[DS_NWAVE][64 * 4];  // partial scores per wave
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qb = wave >> 1, half = wave & 1;
+  const int g = lane >> 4;
+  const int lq = lane & 15;
+
+  const int seq = p.items[3 * blockIdx.x];
+  const int q0 = p.items[3 * blockIdx.x + 1];
+  const int h = p.items[3 * blockIdx.x + 2];
+  const int hk = h / (p.H / p.Hkv);
+  const int start = p.cu[seq];
+  const int L = p.cu[seq + 1] - start;
+  const int W = (p.H + 2 * p.Hkv) * AD;
+  const int dofs = half * DS_HALF;
+  const float* qbase = p.qkv + (int64_t)start * W + (int64_t)h * AD + dofs;
+  const float* kbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + hk) * AD;
+  const float* vbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + p.Hkv + hk) * AD;
+
+  const int qw0 = q0 + qb * QW;
+  const int qi = qw0 + lq;
+  const bool qvalid = qi < L;
+
+  // Q half in VGPRs, B-operand layout: qreg[sg] = Q[qi][dofs + 16*sg + 4*g .. +4]
+  f32x4 qreg[DS_HALF / 16];
+  {
+    const float* qr = qbase + (int64_t)(qvalid ? qi : 0) * W;
+#pragma unroll
+    for (int sg = 0; sg < DS_HALF / 16; sg++) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(qr + sg * 16 + g * 4);
+      qreg[sg] = qvalid ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  f32x4 oacc[DS_HALF / 16];  // O[query qw0 + 4g + r][dofs + 16*db + lq]
+#pragma unroll
+  for (int db = 0; db < DS_HALF / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig;
+  float l_part = 0.f;
+
+  const int qlast = min(q0 + QBLK, L) - 1;
+  int kbeg = 0, kend = L;
+  if (p.window > 0) {
+    kbeg = max(0, q0 - p.window + 1);
+    kend = min(L, qlast + p.window);
+  }
+
+  f32x4 kr[DS_NLD], vr[DS_NLD];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < DS_NLD; i++) {
+      const int idx = tid + DS_NT * i;
+      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
+      const bool ok = k0 + row < kend;
+      const int64_t off = (int64_t)(ok ? k0 + row : 0) * W + c4 * 4;
+      const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off);
+      const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off);
+      kr[i] = ok ? kv : f32x4{0.f, 0.f, 0.f, 0.f};
+      vr[i] = ok ? vv : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  if (kbeg < kend) load_tile(kbeg);
+
+  for (int k0 = kbeg; k0 < kend; k0 += KT) {
+    __syncthreads();  // the previous tile's K, V and scores are consumed
+#pragma unroll
+    for (int i = 0; i < DS_NLD; i++) {
+      const int idx = tid + DS_NT * i;
+      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
+      *reinterpret_cast<f32x4*>(&Ks[row * KLD + c4 * 4]) = kr[i];
+      *reinterpret_cast<f32x4*>(&Vs[row * KLD + c4 * 4]) = vr[i];
+    }
+    __syncthreads();
+    if (k0 + KT < kend) load_tile(k0 + KT);
+
+    // partial S^T over this wave's half of the head dimension
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      const float* krow = &Ks[lq * KLD + dofs + g * 4];
+#pragma unroll
+      for (int sg = 0; sg < DS_HALF / 16; sg++) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(krow + sg * 16);
+#pragma unroll
+        for (int c = 0; c < 4; c++) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc, 0, 0, 0);
+      }
+    }
+    *reinterpret_cast<f32x4*>(&Sx[wave][lane * 4]) = sacc;
+    __syncthreads();
+    {
+      const f32x4 other = *reinterpret_cast<const f32x4*>(&Sx[wave ^ 1][lane * 4]);
+      const f32x4 lo = half == 0 ? sacc : other, hi = half == 0 ? other : sacc;
+#pragma unroll
+      for (int r = 0; r < 4; r++) sacc[r] = lo[r] + hi[r];
+    }
+
+    float tmax = kNegBig;
+    bool valid[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int j = k0 + g * 4 + r;
+      bool ok = qvalid && j < kend;
+      if (p.window > 0) ok = ok && (qi - j < p.window) && (j - qi < p.window);
+      valid[r] = ok;
+      const float t = sacc[r] * p.scale;
+      sacc[r] = t;
+      if (ok) tmax = fmaxf(tmax, t);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = exp_flush(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float pv = valid[r] ? exp_flush(sacc[r] - m_new) : 0.f;
+      sacc[r] = pv;
+      psum += pv;
+    }
+    l_part = l_part * alpha + psum;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+      for (int db = 0; db < DS_HALF / 16; db++) oacc[db][r] *= ar;
+    }
+#pragma unroll
+    for (int db = 0; db < DS_HALF / 16; db++) {
+      f32x4 b;
+#pragma unroll
+      for (int c = 0; c < 4; c++) b[c] = Vs[(4 * g + c) * KLD + dofs + db * 16 + lq];
+#pragma unroll
+      for (int c = 0; c < 4; c++) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sacc[c], b[c], oacc[db], 0, 0, 0);
+    }
+  }
+
+  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  const int OW = p.H * AD;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int qr = qw0 + 4 * g + r;
+    const float inv = 1.f / __shfl(l_tot, 4 * g + r, 64);
+    if (qr < L) {
+      float* orow = p.out + (int64_t)(start + qr) * OW + (int64_t)h * AD + dofs;
+#pragma unroll
+      for (int db = 0; db < DS_HALF / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
+    }
+  }
+}
+
 // ---- generic attention (per-op drop-in) ------------------------------------------
 constexpr int GMAXD = 512;
 
@@ -291,14 +460,14 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   VarlenParams p;
   p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
-  static const int prefetch = [] {
-    const char* e = std::getenv("FA_ATTN_PREFETCH");  // tuning switch
+  static const int kernel = [] {
+    const char* e = std::getenv("FA_ATTN_KERNEL");  // tuning switch: 0 = two waves of 16 queries, 1 = d-split
     return e ? std::atoi(e) : 1;
   }();
-  if (prefetch)
-    hipLaunchKernelGGL(attention_varlen_kernel<true>, dim3((unsigned)n_items), dim3(NTA), 0, s, p);
+  if (kernel == 1)
+    hipLaunchKernelGGL(attention_dsplit_kernel, dim3((unsigned)n_items), dim3(DS_NT), 0, s, p);
   else
-    hipLaunchKernelGGL(attention_varlen_kernel<false>, dim3((unsigned)n_items), dim3(NTA), 0, s, p);
+    hipLaunchKernelGGL(attention_varlen_kernel<true>, dim3((unsigned)n_items), dim3(NTA), 0, s, p);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

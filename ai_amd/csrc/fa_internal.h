@@ -96,12 +96,21 @@ struct GemmArgs {
   const float* residual = nullptr;
   int64_t ldr = 0;
   Epi epi = Epi::None;
+  // ksplit > 1: the K range is split in ksplit equal parts computed by
+  // separate workgroups; part s writes its partial product (no epilogue) to
+  // c + s * c_split, and the consumer adds the parts in order s = 0, 1, ...
+  int ksplit = 1;
+  int64_t c_split = 0;
 };
 
 // Launches C = epi(A . B) on stream. For Epi::GeGLU, B is the interleaved
 // gate/up weight [2F x K] (32-row groups alternating gate, up) and C is
 // [m x F] = gelu(gate) * up.
 int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t stream);
+
+// K-split factor the encoder uses for its N = hidden products (o, down):
+// FA_GEMM_KSPLIT=1 or 2 (default 2).
+int gemm_ksplit();
 
 int launch_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out, hipStream_t s);
 int launch_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64_t rows, int64_t n, float* out,
@@ -142,8 +151,10 @@ int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t
 
 // x += RMSNorm(o; g_post); then xn = RMSNorm(x; g_next) (g_next may be null:
 // then xn is not written).
+// o2 (optional): second partial product of a K-split GEMM, added to o.
 int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
-                         const float* g_post, const float* g_next, float eps, hipStream_t s);
+                         const float* g_post, const float* g_next, float eps, hipStream_t s,
+                         const float* o2 = nullptr);
 
 // Fused varlen attention over packed tokens. qkv [rows x (H+2Hkv)*D]; out
 // [rows x H*D]; cu_seqlens [nseq+1]; window: keys with |i-j| >= window are

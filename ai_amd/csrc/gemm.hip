@@ -94,6 +94,10 @@ struct GemmParams {
   int act;
   int tiles_m, tiles_n;
   int nk;  // K slabs per tile
+  // split-bf16 kernel: K split into ksplit equal ranges (grid.y); range s
+  // writes its partial product to c + s * c_split (epilogue None)
+  int ksplit;
+  int64_t c_split;
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -449,6 +453,8 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
   const int tile = xcd_tile(p);
   const int64_t m0 = (int64_t)(tile / p.tiles_n) * BM;
   const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
+  const int nk = p.nk / p.ksplit;                      // slabs of this K range
+  const int64_t k_off = (int64_t)blockIdx.y * nk * BK;  // its first k
 
   // Staging chunks: 8 consecutive k of one row (two float4 of A, one 16-byte
   // vector of B). A slab row is 4 chunks.
@@ -462,13 +468,13 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
 #pragma unroll
   for (int i = 0; i < NA; i++) {
     const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
-    ga[i] = min(m0 + row, M - 1) * p.lda + c * 8;
+    ga[i] = min(m0 + row, M - 1) * p.lda + k_off + c * 8;
     la[i] = row * BK + ((c ^ lds_swz(row)) << 3);
   }
 #pragma unroll
   for (int i = 0; i < NB; i++) {
     const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
-    gb[i] = B + min(n0 + row, N - 1) * p.ldb + c * 8;
+    gb[i] = B + min(n0 + row, N - 1) * p.ldb + k_off + c * 8;
     lb[i] = row * BK + ((c ^ lds_swz(row)) << 3);
   }
   auto load_global = [&](f32x4 (&ra)[2 * NA], u32x4 (&rb)[NB], int kt) {
@@ -546,7 +552,6 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
   // kt+1 and `fill` receives slab kt+2 (clamped to the last slab: a
   // redundant load keeps the body free of branches, so the split's VALU work
   // and the LDS traffic interleave with the MFMAs).
-  const int nk = p.nk;
   auto body = [&](int kt, const f32x4 (&ra_use)[2 * NA], const u32x4 (&rb_use)[NB], f32x4 (&ra_fill)[2 * NA],
                   u32x4 (&rb_fill)[NB]) {
     const int buf = kt & 1;
@@ -583,7 +588,13 @@ __global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
     mfma_step(a0, b0);
     mfma_step(a1, b1);
   }
-  store_c<TL, EPI>(p, acc, m0, n0, wm, wn, lane);
+  if (p.ksplit > 1) {  // this K range's partial product, no epilogue
+    GemmParams q = p;
+    q.c = p.c + blockIdx.y * p.c_split;
+    store_c<TL, Epi::None>(q, acc, m0, n0, wm, wn, lane);
+  } else {
+    store_c<TL, EPI>(p, acc, m0, n0, wm, wn, lane);
+  }
 }
 
 template <class TL, Epi EPI>
@@ -591,7 +602,8 @@ void launch_x3(GemmParams p, hipStream_t s) {
   p.tiles_m = (int)((p.m + TL::BM - 1) / TL::BM);
   p.tiles_n = (int)((p.n + TL::BN - 1) / TL::BN);
   p.nk = (int)(p.k / TL::BK);
-  dim3 grid(p.tiles_m * p.tiles_n), block(TL::NT);
+  if (p.ksplit < 1) p.ksplit = 1;
+  dim3 grid(p.tiles_m * p.tiles_n, p.ksplit), block(TL::NT);
   hipLaunchKernelGGL((gemm_x3_kernel<TL, EPI>), grid, block, 0, s, p);
 }
 
@@ -713,6 +725,14 @@ bool x3_has_geglu(XTileId t) {
 
 }  // namespace
 
+int gemm_ksplit() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_GEMM_KSPLIT");
+    return (e && std::strcmp(e, "1") == 0) ? 1 : 2;
+  }();
+  return v;
+}
+
 int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.m < 0 || g.n < 0 || g.k < 0)
     return set_error(ctx, FA_ERR_ARG, "MatMul: negative size m=%lld n=%lld k=%lld", (long long)g.m,
@@ -726,13 +746,24 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   p.a = g.a; p.lda = g.lda; p.b = g.b; p.ldb = g.ldb; p.c = g.c; p.ldc = g.ldc;
   p.bias = g.bias; p.row_scale = g.row_scale; p.mul = g.mul; p.ldm = g.ldm;
   p.residual = g.residual; p.ldr = g.ldr; p.act = g.act;
+  p.ksplit = 1;
   if (((g.m + 63) / 64) * ((g.n + 63) / 64) > INT32_MAX / 4) return set_error(ctx, FA_ERR_ARG, "MatMul: too many tiles");
   const bool bf16 = g.b_dtype == FA_DT_BF16;
   const bool nk = g.b_layout == FA_B_NK;
+  if (g.ksplit > 1) {
+    // K split into equal ranges of whole slabs, partial products to c + s*c_split
+    if (!(bf16 && nk && g.epi == Epi::None && g.k % (32 * g.ksplit) == 0 && g.c_split >= g.m * g.ldc &&
+          !use_f32_mfma()))
+      return set_error(ctx, FA_ERR_ARG, "MatMul: K split needs bf16 [n x k] weights, no epilogue, k %% (32*%d) == 0 "
+                       "and disjoint partial outputs", g.ksplit);
+    p.ksplit = g.ksplit;
+    p.c_split = g.c_split;
+  }
   // The fast loaders read 16-byte vectors: every row start must be 16-byte
   // aligned and k a whole number of 32-wide slabs.
   const bool fast = nk && g.k > 0 && g.k % 32 == 0 && aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 &&
                     (bf16 ? g.ldb % 8 == 0 : g.ldb % 4 == 0);
+  if (p.ksplit > 1 && !fast) return set_error(ctx, FA_ERR_ARG, "MatMul: K split needs 16-byte aligned rows");
   if (fast && bf16 && !use_f32_mfma()) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     XTileId t = (XTileId)forced_xtile();

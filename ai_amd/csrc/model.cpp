@@ -476,7 +476,9 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   FA_HIP_CHECK(ctx, hipEventRecord(m->plan_done, ctx->stream));
   m->plan_pending = true;
   // ---- workspace ----
-  const int64_t ncols = 2LL * d + m->width_qkv + (int64_t)H * D + d + F;
+  // o has room for two partial products of the K-split o/down GEMMs
+  const int ksplit = fa::gemm_ksplit();
+  const int64_t ncols = 2LL * d + m->width_qkv + (int64_t)H * D + (int64_t)ksplit * d + F;
   const int maxw = std::max(d, std::max(full, c.n_dense > 0 ? *std::max_element(m->dense_out.begin(), m->dense_out.end()) : d));
   const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw)) * 4 + 4096;
   if ((rc = m->ws.ensure(ctx, ws_bytes))) return rc;
@@ -485,7 +487,11 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   float* qkv = xn + M * d;
   float* att = qkv + M * m->width_qkv;
   float* o = att + M * H * D;
-  float* gu = o + M * d;
+  float* gu = o + (int64_t)ksplit * M * d;
+  // per product: split only when K divides into whole 32-wide slabs
+  const int ks_o = (H * D) % (32 * ksplit) == 0 ? ksplit : 1, ks_down = F % (32 * ksplit) == 0 ? ksplit : 1;
+  const float* o2_o = ks_o > 1 ? o + M * d : nullptr;
+  const float* o2_down = ks_down > 1 ? o + M * d : nullptr;
   float* pooled = gu + M * F;
   float* hbuf0 = pooled + (size_t)B * d;
   float* hbuf1 = hbuf0 + (size_t)B * maxw;
@@ -543,13 +549,14 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     {
       fa::GemmArgs g;
       g.m = M; g.n = d; g.k = H * D; g.a = att; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = o; g.ldc = d;
+      g.ksplit = ks_o; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_O, 2.0 * M * d * H * D, 0);
       if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
       pr.done();
     }
     {
       fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
-      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_attn, L.g_pre_ffn, eps, s))) return rc;
+      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_attn, L.g_pre_ffn, eps, s, o2_o))) return rc;
       pr.done();
     }
     {
@@ -563,6 +570,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     {
       fa::GemmArgs g;
       g.m = M; g.n = d; g.k = F; g.a = gu; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = o; g.ldc = d;
+      g.ksplit = ks_down; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * M * d * F, 0);
       if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
       pr.done();
@@ -571,7 +579,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       // the last layer's "next norm" is the final RMSNorm (embed.go:237): xn = h
       const float* g_next = (l + 1 < c.num_hidden_layers) ? m->layers[l + 1].g_in : m->g_final;
       fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
-      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_ffn, g_next, eps, s))) return rc;
+      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_ffn, g_next, eps, s, o2_down))) return rc;
       pr.done();
     }
   }

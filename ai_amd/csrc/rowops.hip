@@ -121,10 +121,12 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* __rest
 }
 
 // x += RMSNorm(o; g_post); xn = RMSNorm(x; g_next) when g_next != null.
+// With o2 != null, o is the sum of two partial products o + o2 (in that
+// order) of a K-split GEMM.
 template <int NC>
-__global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ o, float* __restrict__ x,
-                                                            float* __restrict__ xn, int64_t rows,
-                                                            const float* __restrict__ g_post,
+__global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ o, const float* __restrict__ o2,
+                                                            float* __restrict__ x, float* __restrict__ xn,
+                                                            int64_t rows, const float* __restrict__ g_post,
                                                             const float* __restrict__ g_next, float eps) {
   constexpr int d = NC * 256;
   int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -136,6 +138,13 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
     const int col = c * 256 + lane * 4;
     ov[c] = *reinterpret_cast<const f32x4*>(o + row * d + col);
     xv[c] = *reinterpret_cast<const f32x4*>(x + row * d + col);
+  }
+  if (o2) {
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + row * d + c * 256 + lane * 4);
+      ov[c].x = ov[c].x + p2.x; ov[c].y = ov[c].y + p2.y; ov[c].z = ov[c].z + p2.z; ov[c].w = ov[c].w + p2.w;
+    }
   }
   const float inv = rms_inv(sumsq<NC>(ov), d, eps);
 #pragma unroll
@@ -305,14 +314,14 @@ int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_
 }
 
 int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
-                         const float* g_post, const float* g_next, float eps, hipStream_t s) {
+                         const float* g_post, const float* g_next, float eps, hipStream_t s, const float* o2) {
   if (rows == 0) return FA_OK;
   dim3 grid(blocks_for(rows, 4)), block(256);
   switch (d) {
-    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
-    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
-    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
-    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, x, xn, rows, g_post, g_next, eps); break;
+    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
+    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
+    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
+    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
     default: return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden size %d not in {256,512,768,1024}", d);
   }
   FA_CHECK_LAUNCH(ctx);
