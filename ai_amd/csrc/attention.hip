@@ -12,19 +12,28 @@
 // attention.go:61-136) with PaddingMask + WindowMask (attention.go:33-42,
 // 97-107; models/gemma/embed.go:168-186).
 //
-// MFMA formulation (v_mfma_f32_16x16x4_f32; lane l of a 16x16 result holds
-// column l%16 and rows 4*(l/16)+r, r=0..3). A workgroup is two waves; each
-// wave owns 16 queries of one head. Per tile of 16 keys it computes
-//     S^T[key, query] = K . Q^T   (A = K rows from LDS, B = Q in VGPRs)
-// so lane l holds the scores of query l%16 against keys 4*(l/16)+r: the
-// online-softmax statistics of a query are lane-local plus two shuffles, and
-// the probabilities are already the A operand of
-//     O[query, d] += P . V        (B = V rows from LDS, row-major)
-// when the k index of MFMA c in lane group g is taken as key 4g+c (a
-// permutation of the k sum). O's rows are queries 4*(l/16)+r, so the rescale
-// factors reach them with one shuffle each. The next tile's K and V rows are
-// loaded into registers while the current tile is computed; with 33 KB of LDS
-// per workgroup four workgroups fit on a CU.
+// Formulation (v_mfma_f32_16x16x4_f32; lane l of a 16x16 result holds
+// column l%16 and rows 4*(l/16)+r, r=0..3). A work item is (sequence, block
+// of 32 queries, head); its workgroup is four waves: waves 2b and 2b+1 own
+// the same 16 queries (block b) and the two halves of the head dimension.
+// Per tile of 16 keys each wave computes the partial scores over its 128
+// dimensions as S^T[key, query] = K . Q^T (A = K rows from LDS, B = Q in
+// VGPRs), so lane l holds the scores of query l%16 against keys
+// 4*(l/16)+r; the pair exchanges partial scores through LDS and adds them
+// in one order (half 0 + half 1), so both hold the same scores and softmax
+// statistics (lane-local plus two shuffles). The probabilities are already
+// the A operand of O[query, d] += P . V (B = V rows from LDS) when the k
+// index of MFMA c in lane group g is taken as key 4g+c, and each wave
+// accumulates its half of O. Splitting the head dimension halves the Q and
+// O registers per wave (two waves per SIMD) and doubles the waves over a
+// batch.
+//
+// K and V tiles reach LDS by direct global->LDS loads (global_load_lds,
+// one 1 KB row per wave instruction) into two buffers, the next tile
+// loading while the current one is computed; a row's 16-byte chunks are
+// XOR-swizzled by row so the operand reads hit distinct banks. The
+// barriers use explicit counter waits so the exchange barrier does not wait
+// for the next tile's loads.
 //
 // attention_generic_kernel (the tensor.AttentionScaled drop-in): arbitrary
 // B, H, T, S, D <= 512, strides and an additive mask tensor, one wavefront
@@ -42,13 +51,9 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int AD = 256;                  // head_dim
-constexpr int QW = 16;                   // queries per wave
-constexpr int NWAVE = 2;                 // waves per workgroup
-constexpr int QBLK = QW * NWAVE;         // queries per work item
-constexpr int NTA = NWAVE * 64;          // threads per workgroup
+constexpr int QW = 16;                   // queries per wave pair
+constexpr int QBLK = 2 * QW;             // queries per work item (two pairs)
 constexpr int KT = 16;                   // keys per tile
-constexpr int KLD = AD + 4;              // padded LDS row stride (floats)
-constexpr int NLD = KT * AD / 4 / NTA;   // float4 of K (and of V) per thread per tile
 constexpr float kNegBig = -1e30f;
 
 struct VarlenParams {
@@ -61,178 +66,41 @@ struct VarlenParams {
   float scale;
 };
 
-template <bool PREFETCH>
-__global__ __launch_bounds__(NTA) void attention_varlen_kernel(VarlenParams p) {
-  __shared__ __attribute__((aligned(16))) float Ks[KT * KLD];
-  __shared__ __attribute__((aligned(16))) float Vs[KT * KLD];
+// ---- the model path's kernel ------------------------------------------------
+constexpr int DS_HALF = AD / 2;  // head dimensions per wave
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int g = lane >> 4;   // lane group
-  const int lq = lane & 15;  // the lane's query column in S^T
+// Direct-to-LDS tile loads: each K or V row of a tile (256
+// floats, 1 KB) is one global_load_lds_dwordx4 of a wave (64 lanes x 16
+// bytes, LDS address = row base + 16 * lane), into two LDS buffers. A row's
+// 16-byte chunk c is stored at position c ^ (row & 15) (lane i loads global
+// chunk i ^ (row & 15)), so the score reads (16 rows, one chunk each) and
+// the V reads (4 rows x 4 chunks) hit distinct banks. Keys past the range
+// load the last valid row (finite values; their weights are 0).
+constexpr int DL_NT = 256;
+constexpr int DL_ROWF = AD;  // floats per LDS row (unpadded)
 
-  const int seq = p.items[3 * blockIdx.x];
-  const int q0 = p.items[3 * blockIdx.x + 1];
-  const int h = p.items[3 * blockIdx.x + 2];
-  const int hk = h / (p.H / p.Hkv);
-  const int start = p.cu[seq];
-  const int L = p.cu[seq + 1] - start;
-  const int W = (p.H + 2 * p.Hkv) * AD;
-  const float* qbase = p.qkv + (int64_t)start * W + (int64_t)h * AD;
-  const float* kbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + hk) * AD;
-  const float* vbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + p.Hkv + hk) * AD;
+__device__ __forceinline__ int dl_pos(int row, int chunk) { return chunk ^ (row & 15); }
 
-  const int qw0 = q0 + wave * QW;  // the wave's first query
-  const int qi = qw0 + lq;         // this lane's query in S^T
-  const bool qvalid = qi < L;
-
-  // Q in VGPRs, B-operand layout: qreg[sg] = Q[qi][16*sg + 4*g .. +4]
-  f32x4 qreg[AD / 16];
-  {
-    const float* qr = qbase + (int64_t)(qvalid ? qi : 0) * W;
-#pragma unroll
-    for (int sg = 0; sg < AD / 16; sg++) {
-      f32x4 v = *reinterpret_cast<const f32x4*>(qr + sg * 16 + g * 4);
-      qreg[sg] = qvalid ? v : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
-
-  f32x4 oacc[AD / 16];  // O[query qw0 + 4g + r][d = 16*db + lq]
-#pragma unroll
-  for (int db = 0; db < AD / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegBig;  // running max of scaled scores of query qi
-  float l_part = 0.f;     // this lane's share of query qi's running sum
-
-  // keys this work item needs
-  const int qlast = min(q0 + QBLK, L) - 1;
-  int kbeg = 0, kend = L;
-  if (p.window > 0) {
-    kbeg = max(0, q0 - p.window + 1);
-    kend = min(L, qlast + p.window);
-  }
-
-  f32x4 kr[NLD], vr[NLD];  // next tile (in flight while the current one is computed, with PREFETCH)
-  auto load_tile = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < NLD; i++) {
-      const int idx = tid + NTA * i;
-      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
-      const bool ok = k0 + row < kend;
-      const int64_t off = (int64_t)(ok ? k0 + row : 0) * W + c4 * 4;
-      const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off);
-      const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off);
-      kr[i] = ok ? kv : f32x4{0.f, 0.f, 0.f, 0.f};
-      vr[i] = ok ? vv : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  if (PREFETCH && kbeg < kend) load_tile(kbeg);
-
-  for (int k0 = kbeg; k0 < kend; k0 += KT) {
-    if (!PREFETCH) load_tile(k0);
-    __syncthreads();  // the previous tile is consumed
-#pragma unroll
-    for (int i = 0; i < NLD; i++) {
-      const int idx = tid + NTA * i;
-      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
-      *reinterpret_cast<f32x4*>(&Ks[row * KLD + c4 * 4]) = kr[i];
-      *reinterpret_cast<f32x4*>(&Vs[row * KLD + c4 * 4]) = vr[i];
-    }
-    __syncthreads();
-    if (PREFETCH && k0 + KT < kend) load_tile(k0 + KT);
-
-    // S^T for 16 keys
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-    {
-      const float* krow = &Ks[lq * KLD + g * 4];
-#pragma unroll
-      for (int sg = 0; sg < AD / 16; sg++) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(krow + sg * 16);
-#pragma unroll
-        for (int c = 0; c < 4; c++) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc, 0, 0, 0);
-      }
-    }
-
-    // mask, scale, tile max over query qi's keys (spread over the 4 lane groups)
-    float tmax = kNegBig;
-    bool valid[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int j = k0 + g * 4 + r;
-      bool ok = qvalid && j < kend;
-      if (p.window > 0) ok = ok && (qi - j < p.window) && (j - qi < p.window);
-      valid[r] = ok;
-      const float t = sacc[r] * p.scale;
-      sacc[r] = t;
-      if (ok) tmax = fmaxf(tmax, t);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp_flush(m_run - m_new);  // 0 when m_run is the sentinel
-    m_run = m_new;
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float pv = valid[r] ? exp_flush(sacc[r] - m_new) : 0.f;
-      sacc[r] = pv;
-      psum += pv;
-    }
-    l_part = l_part * alpha + psum;
-
-    // rescale O's rows (queries qw0 + 4g + r) by their queries' alpha
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float ar = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-      for (int db = 0; db < AD / 16; db++) oacc[db][r] *= ar;
-    }
-
-    // O += P . V
-#pragma unroll
-    for (int db = 0; db < AD / 16; db++) {
-      f32x4 b;
-#pragma unroll
-      for (int c = 0; c < 4; c++) b[c] = Vs[(4 * g + c) * KLD + db * 16 + lq];
-#pragma unroll
-      for (int c = 0; c < 4; c++) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sacc[c], b[c], oacc[db], 0, 0, 0);
-    }
-  }
-
-  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  float* obase = p.out + (int64_t)h * AD;
-  const int OW = p.H * AD;
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int qr = qw0 + 4 * g + r;
-    const float inv = 1.f / __shfl(l_tot, 4 * g + r, 64);
-    if (qr < L) {
-      float* orow = obase + (int64_t)(start + qr) * OW;
-#pragma unroll
-      for (int db = 0; db < AD / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
-    }
-  }
+// Workgroup barrier with an explicit counter wait (s_waitcnt encoding WAIT)
+// instead of __syncthreads()'s release fence, which would also wait for the
+// next tile's loads to LDS. The signal fences keep the compiler from moving
+// LDS accesses across it.
+template <int WAIT>
+__device__ __forceinline__ void dl_barrier() {
+  __builtin_amdgcn_s_waitcnt(WAIT);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// ---- d-split variant -------------------------------------------------------
-// Four waves per workgroup: waves 2b and 2b+1 own the same 16 queries
-// (query block b of the item) and the two halves of the head dimension. Each
-// computes the partial scores over its 128 dimensions, the pair exchanges
-// them through LDS and adds them in the same order (half 0 + half 1, so both
-// waves hold identical scores and softmax statistics), and each accumulates
-// its half of O. Against one wave per 16 queries this halves the Q and O
-// registers and the K/V staging per thread, so two workgroups fit per SIMD
-// pair, and doubles the waves over a batch.
-constexpr int DS_NWAVE = 4;
-constexpr int DS_NT = DS_NWAVE * 64;
-constexpr int DS_HALF = AD / 2;
-constexpr int DS_NLD = KT * AD / 4 / DS_NT;  // float4 of K (and of V) per thread per tile
-
-__global__ __launch_bounds__(DS_NT) void attention_dsplit_kernel(VarlenParams p) {
-  __shared__ __attribute__((aligned(16))) float Ks[KT * KLD];
-  __shared__ __attribute__((aligned(16))) float Vs[KT * KLD];
-  __shared__ __attribute__((aligned(16))) float Sx[DS_NWAVE][64 * 4];  // partial scores per wave
+__global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p) {
+  // separate objects per buffer, so the compiler can tell the tile being
+  // read from the one being loaded and need not wait for the loads
+  __shared__ __attribute__((aligned(16))) float K0[KT * DL_ROWF];
+  __shared__ __attribute__((aligned(16))) float V0[KT * DL_ROWF];
+  __shared__ __attribute__((aligned(16))) float K1[KT * DL_ROWF];
+  __shared__ __attribute__((aligned(16))) float V1[KT * DL_ROWF];
+  __shared__ __attribute__((aligned(16))) float Sx[4][64 * 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -256,8 +124,6 @@ __global__ __launch_bounds__(DS_NT) void attention_dsplit_kernel(VarlenParams p)
   const int qw0 = q0 + qb * QW;
   const int qi = qw0 + lq;
   const bool qvalid = qi < L;
-
-  // Q half in VGPRs, B-operand layout: qreg[sg] = Q[qi][dofs + 16*sg + 4*g .. +4]
   f32x4 qreg[DS_HALF / 16];
   {
     const float* qr = qbase + (int64_t)(qvalid ? qi : 0) * W;
@@ -267,7 +133,7 @@ __global__ __launch_bounds__(DS_NT) void attention_dsplit_kernel(VarlenParams p)
       qreg[sg] = qvalid ? v : f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  f32x4 oacc[DS_HALF / 16];  // O[query qw0 + 4g + r][dofs + 16*db + lq]
+  f32x4 oacc[DS_HALF / 16];
 #pragma unroll
   for (int db = 0; db < DS_HALF / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig;
@@ -280,47 +146,44 @@ __global__ __launch_bounds__(DS_NT) void attention_dsplit_kernel(VarlenParams p)
     kend = min(L, qlast + p.window);
   }
 
-  f32x4 kr[DS_NLD], vr[DS_NLD];
-  auto load_tile = [&](int k0) {
+  // wave w loads rows w, w+4, w+8, w+12 of K and of V
+  auto issue_tile = [&](int k0, float* Kb, float* Vb) {
 #pragma unroll
-    for (int i = 0; i < DS_NLD; i++) {
-      const int idx = tid + DS_NT * i;
-      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
-      const bool ok = k0 + row < kend;
-      const int64_t off = (int64_t)(ok ? k0 + row : 0) * W + c4 * 4;
-      const f32x4 kv = *reinterpret_cast<const f32x4*>(kbase + off);
-      const f32x4 vv = *reinterpret_cast<const f32x4*>(vbase + off);
-      kr[i] = ok ? kv : f32x4{0.f, 0.f, 0.f, 0.f};
-      vr[i] = ok ? vv : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < KT / 4; j++) {
+      const int r = wave + 4 * j;
+      const int64_t key = min(k0 + r, kend - 1);
+      const int chunk = dl_pos(r, lane);  // the global chunk that lands at position `lane`
+      __builtin_amdgcn_global_load_lds(kbase + key * W + chunk * 4,
+                                       (__attribute__((address_space(3))) void*)&Kb[r * DL_ROWF], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + key * W + chunk * 4,
+                                       (__attribute__((address_space(3))) void*)&Vb[r * DL_ROWF], 16, 0, 0);
     }
   };
-  if (kbeg < kend) load_tile(kbeg);
+  if (kbeg < kend) issue_tile(kbeg, K0, V0);
 
-  for (int k0 = kbeg; k0 < kend; k0 += KT) {
-    __syncthreads();  // the previous tile's K, V and scores are consumed
-#pragma unroll
-    for (int i = 0; i < DS_NLD; i++) {
-      const int idx = tid + DS_NT * i;
-      const int row = idx / (AD / 4), c4 = idx % (AD / 4);
-      *reinterpret_cast<f32x4*>(&Ks[row * KLD + c4 * 4]) = kr[i];
-      *reinterpret_cast<f32x4*>(&Vs[row * KLD + c4 * 4]) = vr[i];
-    }
-    __syncthreads();
-    if (k0 + KT < kend) load_tile(k0 + KT);
+  auto step = [&](int k0, const float* Kc, const float* Vc, float* Kn, float* Vn) {
+    // this wave's loads of the tile have landed; after the barrier, every
+    // wave's have, and the other buffer is free (its tile was consumed)
+    dl_barrier<0x0070>();  // vmcnt(0) lgkmcnt(0): the tile landed, the scores were read
+    if (k0 + KT < kend) issue_tile(k0 + KT, Kn, Vn);
 
-    // partial S^T over this wave's half of the head dimension
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
     {
-      const float* krow = &Ks[lq * KLD + dofs + g * 4];
+      const float* krow = &Kc[lq * DL_ROWF];
+      auto kfrag = [&](int sg) {
+        return *reinterpret_cast<const f32x4*>(krow + dl_pos(lq, (dofs + sg * 16 + g * 4) >> 2) * 4);
+      };
+      f32x4 a = kfrag(0);  // operands of step sg+1 are read while step sg computes
 #pragma unroll
       for (int sg = 0; sg < DS_HALF / 16; sg++) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(krow + sg * 16);
+        const f32x4 an = sg + 1 < DS_HALF / 16 ? kfrag(sg + 1) : a;
 #pragma unroll
         for (int c = 0; c < 4; c++) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc, 0, 0, 0);
+        a = an;
       }
     }
     *reinterpret_cast<f32x4*>(&Sx[wave][lane * 4]) = sacc;
-    __syncthreads();
+    dl_barrier<0xC07F>();  // lgkmcnt(0) only: the next tile's loads stay in flight
     {
       const f32x4 other = *reinterpret_cast<const f32x4*>(&Sx[wave ^ 1][lane * 4]);
       const f32x4 lo = half == 0 ? sacc : other, hi = half == 0 ? other : sacc;
@@ -361,12 +224,20 @@ __global__ __launch_bounds__(DS_NT) void attention_dsplit_kernel(VarlenParams p)
     }
 #pragma unroll
     for (int db = 0; db < DS_HALF / 16; db++) {
+      const int f = dofs + db * 16 + lq;
       f32x4 b;
 #pragma unroll
-      for (int c = 0; c < 4; c++) b[c] = Vs[(4 * g + c) * KLD + dofs + db * 16 + lq];
+      for (int c = 0; c < 4; c++) {
+        const int row = 4 * g + c;
+        b[c] = Vc[row * DL_ROWF + dl_pos(row, f >> 2) * 4 + (f & 3)];
+      }
 #pragma unroll
       for (int c = 0; c < 4; c++) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sacc[c], b[c], oacc[db], 0, 0, 0);
     }
+  };
+  for (int k0 = kbeg; k0 < kend; k0 += 2 * KT) {
+    step(k0, K0, V0, K1, V1);
+    if (k0 + KT < kend) step(k0 + KT, K1, V1, K0, V0);
   }
 
   float l_tot = l_part + __shfl_xor(l_part, 16, 64);
@@ -460,14 +331,7 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   VarlenParams p;
   p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
-  static const int kernel = [] {
-    const char* e = std::getenv("FA_ATTN_KERNEL");  // tuning switch: 0 = two waves of 16 queries, 1 = d-split
-    return e ? std::atoi(e) : 1;
-  }();
-  if (kernel == 1)
-    hipLaunchKernelGGL(attention_dsplit_kernel, dim3((unsigned)n_items), dim3(DS_NT), 0, s, p);
-  else
-    hipLaunchKernelGGL(attention_varlen_kernel<true>, dim3((unsigned)n_items), dim3(NTA), 0, s, p);
+  hipLaunchKernelGGL(attention_varlen_kernel, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
