@@ -74,6 +74,12 @@ _SIGS = {
                                i64, i64, f32, vp]),
     "fa_similarities_topk": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
     "fa_similarities_topk_dev": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
+    "fa_cluster_normalize": (C.c_int, [vp, vp, i64, i32, vp]),
+    "fa_cluster_normalize_dev": (C.c_int, [vp, vp, i64, i32, vp]),
+    "fa_cluster_nearest": (C.c_int, [vp, vp, i64, vp, i64, i32, vp, vp]),
+    "fa_cluster_nearest_dev": (C.c_int, [vp, vp, i64, vp, i64, i32, vp, vp]),
+    "fa_cluster_kmeans": (C.c_int, [vp, vp, i64, i32, i32, i32, C.c_uint64, vp, vp, vp, vp, C.POINTER(i32)]),
+    "fa_cluster_kmeans_dev": (C.c_int, [vp, vp, i64, i32, i32, i32, C.c_uint64, vp, vp, vp, vp, C.POINTER(i32)]),
     "fa_gemma_create": (C.c_int, [vp, C.POINTER(GemmaConfig), C.POINTER(vp)]),
     "fa_gemma_destroy": (None, [vp]),
     "fa_gemma_set_weight": (C.c_int, [vp, C.c_char_p, C.c_int, P_i64, i32, vp]),

@@ -36,7 +36,7 @@ HIP_FLAGS = [
     "-I", INCLUDE, "-I", CSRC,
 ]
 
-ROCM_SOURCES = ["context.cpp", "model.cpp", "gemm.hip", "rowops.hip", "attention.hip", "score.hip"]
+ROCM_SOURCES = ["context.cpp", "model.cpp", "gemm.hip", "rowops.hip", "attention.hip", "score.hip", "cluster.hip"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -83,8 +83,8 @@ def build_synth(verbose: bool = False) -> str:
 
 
 HOST = os.path.join(PKG, "host")
-HOST_SOURCES = ["fiber.cpp", "json.cpp", "tokenizer.cpp", "safetensors.cpp"]
-CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer"]
+HOST_SOURCES = ["fiber.cpp", "json.cpp", "tokenizer.cpp", "safetensors.cpp", "cluster.cpp"]
+CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer", "test_cluster"]
 CPP_CPU_TESTS = ["test_tokenizer"]  # need no GPU
 CPP_DRIVERS = ["st_dump", "embed_dir"]  # programs the Python tests drive
 CPP_TEST_BIN = os.path.join(BUILD, "cpp_tests")

@@ -81,8 +81,7 @@ void rope_tables_host(double base, const int32_t* positions, int T, int D, std::
 
 using fa::set_error;
 
-// Scratch slots used by the host-pointer entry points.
-enum { S_A = 0, S_B, S_C, S_BIAS, S_ROWSCALE, S_MUL, S_RES, S_X, S_G, S_OUT, S_COS, S_SIN, S_Q, S_K, S_V, S_MASK };
+using namespace fa::slots;
 
 extern "C" {
 

@@ -65,6 +65,14 @@ struct fa_ctx {
 
 namespace fa {
 
+// Scratch slots of fa_ctx (per-call device buffers of the entry points).
+namespace slots {
+enum : size_t {
+  S_A = 0, S_B, S_C, S_BIAS, S_ROWSCALE, S_MUL, S_RES, S_X, S_G, S_OUT, S_COS, S_SIN, S_Q, S_K, S_V, S_MASK,
+  S_CL_WORK, S_CL_X, S_CL_C, S_CL_OUT  // cluster entry points
+};
+}  // namespace slots
+
 // Copies host data into scratch slot `slot` (grown as needed) and returns
 // the device pointer via *out.
 int stage_h2d(fa_ctx* ctx, size_t slot, const void* src, size_t bytes, void** out);

@@ -14,6 +14,8 @@
 //                                              embed.go:15-114 (EmbedIDs: the ids-level core, embed.go:118-157)
 //   tokenizer.Tokenizer                        tokenizer/tokenizer.go (tokenizer.hpp)
 //   safetensors.File                           safetensors/safetensors.go (safetensors.hpp)
+//   cluster.Normalize / KMeans / Nearest / Cosine / Similarities
+//                                              cluster/cluster.go (cluster.hpp)
 // Shape errors throw fiber::tensor::Error{Op, Msg}, where the reference
 // panics with *tensor.Error (tensor/errors.go:5-31); gemma's functions throw
 // fiber::gemma::Error where the reference returns error.

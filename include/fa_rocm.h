@@ -148,6 +148,46 @@ int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const fl
 int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
                              int32_t topk, int32_t* idx, float* val);
 
+/* ---- cluster (cluster/cluster.go) ------------------------------------ */
+
+/* out = x with every row scaled to unit length (x / sqrt(sum x^2)); rows of
+ * length zero stay zero. x, out: [n x d] row-major; out may equal x.
+ * Replaces cluster.Normalize (cluster/cluster.go:17-28). */
+int fa_cluster_normalize(fa_ctx* ctx, const float* x, int64_t n, int32_t d, float* out);
+/* Device-pointer variant (enqueue only). */
+int fa_cluster_normalize_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, float* out);
+
+/* For every row of x [n x d], the index of the most similar of the k
+ * centres [k x d] by dot product (the first index on equal scores, the
+ * rule of (*Tensor).Argmax, tensor/reduce.go:269-297) and that
+ * similarity. k >= 1. Replaces cluster.Nearest (cluster/cluster.go:134-146). */
+int fa_cluster_nearest(fa_ctx* ctx, const float* x, int64_t n, const float* centres, int64_t k, int32_t d,
+                       int32_t* index, float* similarity);
+/* Device-pointer variant (enqueue only). */
+int fa_cluster_nearest_dev(fa_ctx* ctx, const float* x, int64_t n, const float* centres, int64_t k, int32_t d,
+                           int32_t* index, float* similarity);
+
+/* k-means of the unit-length rows of x [n x d] into k groups by cosine
+ * similarity, as cluster.KMeans (cluster/cluster.go:39-131): k-means++
+ * seeding driven by Go's math/rand/v2 PCG seeded (seed, seed ^
+ * 0x9e3779b97f4a7c15), then up to iters rounds of assignment and centre
+ * update (an empty centre restarts on the worst-fitting row), stopping
+ * when no row changed centre in a round after the first. Outputs the
+ * fields of cluster.Result: centres [k x d] (unit length), assignment [n],
+ * similarity [n] (each row's similarity to its centre at the last
+ * assignment), sizes [k] and *iterations. 1 <= k <= n, else FA_ERR_ARG
+ * ("cluster: k must be between 1 and the number of rows", the reference's
+ * panic). n < 2^31. */
+int fa_cluster_kmeans(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int32_t k, int32_t iters, uint64_t seed,
+                      float* centres, int32_t* assignment, float* similarity, int32_t* sizes, int32_t* iterations);
+/* Device-pointer variant: x, centres, assignment, similarity and sizes in
+ * device memory, *iterations on the host. Synchronises the context's stream
+ * once per round (the early stop and the empty-centre restarts read the
+ * round's change count and sizes). */
+int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int32_t k, int32_t iters,
+                          uint64_t seed, float* centres, int32_t* assignment, float* similarity, int32_t* sizes,
+                          int32_t* iterations);
+
 /* ---- the EmbeddingGemma model (models/gemma) ------------------------- */
 
 /* Hyper-parameters as read from config.json by gemma.LoadConfig

@@ -782,3 +782,194 @@ ORC_API int orc_model_embed(void* p, const int32_t* ids, const int32_t* lengths,
 }
 
 ORC_API int orc_num_threads(void) { return omp_get_max_threads(); }
+
+// ---------------------------------------------------------------------------
+// cluster (cluster/cluster.go): Normalize, Nearest, KMeans with k-means++
+// seeding from Go's math/rand/v2 PCG generator.
+// ---------------------------------------------------------------------------
+
+// Go standard library math/rand/v2 (Go >= 1.22; not part of the reference
+// tree): PCG is O'Neill's 128-bit LCG with the pcg-cpp default multiplier
+// and increment, state (hi, lo) = (seed1, seed2) as NewPCG sets it; Uint64
+// advances the state and returns the DXSM ("double xorshift multiply")
+// output of the new state.
+struct OrcPCG {
+  uint64_t hi, lo;
+};
+
+static uint64_t orc_pcg_next(OrcPCG& p) {
+  typedef unsigned __int128 u128;
+  const u128 mul = ((u128)2549297995355413924ULL << 64) | 4865540595714422341ULL;
+  const u128 inc = ((u128)6364136223846793005ULL << 64) | 1442695040888963407ULL;
+  const u128 s = (((u128)p.hi << 64) | p.lo) * mul + inc;
+  p.hi = (uint64_t)(s >> 64);
+  p.lo = (uint64_t)s;
+  uint64_t h = p.hi;
+  h ^= h >> 32;
+  h *= 0xda942042e4dd58b5ULL;
+  h ^= h >> 48;
+  h *= (p.lo | 1);
+  return h;
+}
+
+// Rand.IntN (uint64n on 64-bit hosts): a mask for powers of two, else
+// Lemire's multiply-shift with rejection of the biased low products.
+static uint64_t orc_pcg_uint64n(OrcPCG& p, uint64_t n) {
+  typedef unsigned __int128 u128;
+  if ((n & (n - 1)) == 0) return orc_pcg_next(p) & (n - 1);
+  u128 m = (u128)orc_pcg_next(p) * n;
+  if ((uint64_t)m < n) {
+    const uint64_t thresh = (0 - n) % n;
+    while ((uint64_t)m < thresh) m = (u128)orc_pcg_next(p) * n;
+  }
+  return (uint64_t)(m >> 64);
+}
+
+// Rand.Float64: 53 random bits / 2^53.
+static double orc_pcg_float64(OrcPCG& p) { return (double)(orc_pcg_next(p) << 11 >> 11) / 9007199254740992.0; }
+
+// state[2] = {hi, lo}; the draws advance it.
+ORC_API void orc_pcg_uint64s(uint64_t* state, int64_t count, uint64_t* out) {
+  OrcPCG p{state[0], state[1]};
+  for (int64_t i = 0; i < count; i++) out[i] = orc_pcg_next(p);
+  state[0] = p.hi;
+  state[1] = p.lo;
+}
+ORC_API void orc_pcg_intns(uint64_t* state, uint64_t n, int64_t count, uint64_t* out) {
+  OrcPCG p{state[0], state[1]};
+  for (int64_t i = 0; i < count; i++) out[i] = orc_pcg_uint64n(p, n);
+  state[0] = p.hi;
+  state[1] = p.lo;
+}
+ORC_API void orc_pcg_float64s(uint64_t* state, int64_t count, double* out) {
+  OrcPCG p{state[0], state[1]};
+  for (int64_t i = 0; i < count; i++) out[i] = orc_pcg_float64(p);
+  state[0] = p.hi;
+  state[1] = p.lo;
+}
+
+// cluster.Normalize (cluster.go:17-28): row / sqrt(sum of squares), a zero
+// norm replaced by 1 so zero rows stay zero. Sum(1) is one horizontal
+// kernel.Sum per row (tensor/reduce.go:131-141).
+static void orc_normalize_rows(const float* x, i64 n, int d, float* out) {
+#pragma omp parallel for schedule(static)
+  for (i64 i = 0; i < n; i++) {
+    const float* r = x + i * d;
+    std::vector<float> sq(d);
+    for (int j = 0; j < d; j++) sq[j] = r[j] * r[j];
+    float nrm = std::sqrt(orc_sumf(sq.data(), d));
+    if (nrm == 0) nrm = 1;
+    for (int j = 0; j < d; j++) out[i * d + j] = r[j] / nrm;
+  }
+}
+
+ORC_API void orc_cluster_normalize(const float* x, i64 n, int d, float* out) { orc_normalize_rows(x, n, d, out); }
+
+// sim[n x k] = x . c^T, then the first-max argmax of each row
+// (tensor/reduce.go:269-297): the first index holding the row's maximum.
+static void orc_sim_argmax(const float* x, i64 n, const float* c, i64 k, int d, float* sim, int32_t* idx) {
+#pragma omp parallel for schedule(static)
+  for (i64 i = 0; i < n; i++) {
+    float* sr = sim + i * k;
+    for (i64 j = 0; j < k; j++) sr[j] = orc_dotf(x + i * d, c + j * d, d);
+    float best = sr[0];
+    int32_t bi = 0;
+    for (i64 j = 1; j < k; j++)
+      if (sr[j] > best) {
+        best = sr[j];
+        bi = (int32_t)j;
+      }
+    idx[i] = bi;
+  }
+}
+
+// cluster.Nearest (cluster.go:134-146).
+ORC_API int orc_cluster_nearest(const float* x, i64 n, const float* c, i64 k, int d, int32_t* idx, float* sim_out) {
+  if (k <= 0) return -1;
+  std::vector<float> sim((size_t)(n * k));
+  orc_sim_argmax(x, n, c, k, d, sim.data(), idx);
+  for (i64 i = 0; i < n; i++) sim_out[i] = sim[(size_t)(i * k + idx[i])];
+  return 0;
+}
+
+// cluster.KMeans (cluster.go:39-131). chosen[k] receives the seeding's row
+// indices (test visibility).
+ORC_API int orc_cluster_kmeans(const float* x, i64 n, int d, int k, int iters, uint64_t seed, float* centres_out,
+                               int32_t* assign, float* similarity, int32_t* sizes, int* iterations,
+                               int32_t* chosen) {
+  if (k <= 0 || k > n) return -1;
+  OrcPCG rng{seed, seed ^ 0x9e3779b97f4a7c15ULL};
+  // k-means++ (cluster.go:51-85)
+  std::vector<float> centres;
+  centres.reserve((size_t)k * d);
+  const i64 first = (i64)orc_pcg_uint64n(rng, (uint64_t)n);
+  chosen[0] = (int32_t)first;
+  centres.insert(centres.end(), x + first * d, x + (first + 1) * d);
+  std::vector<float> best((size_t)n, -1.0f), sim1((size_t)n);
+  std::vector<double> weights((size_t)n);
+  for (int r = 1; r < k; r++) {
+    const float* c = centres.data() + (size_t)(r - 1) * d;
+#pragma omp parallel for schedule(static)
+    for (i64 i = 0; i < n; i++) sim1[i] = orc_dotf(x + i * d, c, d);
+    double total = 0;
+    for (i64 i = 0; i < n; i++) {
+      if (sim1[i] > best[i]) best[i] = sim1[i];
+      const double w = (double)(1 - best[i]);
+      weights[i] = w * w;
+      total += weights[i];
+    }
+    double pick = orc_pcg_float64(rng) * total;
+    i64 idx = n - 1;
+    for (i64 i = 0; i < n; i++) {
+      pick -= weights[i];
+      if (pick <= 0) {
+        idx = i;
+        break;
+      }
+    }
+    chosen[r] = (int32_t)idx;
+    centres.insert(centres.end(), x + idx * d, x + (idx + 1) * d);
+  }
+  std::vector<float> cs((size_t)k * d);
+  orc_normalize_rows(centres.data(), k, d, cs.data());
+
+  // Lloyd rounds (cluster.go:86-129)
+  for (i64 i = 0; i < n; i++) {
+    assign[i] = 0;
+    similarity[i] = 0;
+  }
+  for (int c = 0; c < k; c++) sizes[c] = 0;
+  *iterations = 0;
+  std::vector<float> sim((size_t)(n * k)), sums((size_t)k * d);
+  std::vector<int32_t> na((size_t)n);
+  for (int it = 1; it <= iters; it++) {
+    *iterations = it;
+    orc_sim_argmax(x, n, cs.data(), k, d, sim.data(), na.data());
+    i64 changed = 0;
+    for (i64 i = 0; i < n; i++) {
+      similarity[i] = sim[(size_t)(i * k + na[i])];
+      if (na[i] != assign[i]) changed++;
+      assign[i] = na[i];
+    }
+    std::fill(sums.begin(), sums.end(), 0.0f);
+    for (int c = 0; c < k; c++) sizes[c] = 0;
+    for (i64 i = 0; i < n; i++) {
+      const int a = assign[i];
+      sizes[a]++;
+      float* acc = sums.data() + (size_t)a * d;
+      for (int j = 0; j < d; j++) acc[j] += x[i * d + j];
+    }
+    for (int c = 0; c < k; c++) {
+      if (sizes[c] != 0) continue;
+      i64 worst = 0;  // empty centre: restart on the worst-fitting row
+      for (i64 i = 0; i < n; i++)
+        if (similarity[i] < similarity[worst]) worst = i;
+      std::memcpy(sums.data() + (size_t)c * d, x + worst * d, sizeof(float) * d);
+      similarity[worst] = 1;
+    }
+    orc_normalize_rows(sums.data(), k, d, cs.data());
+    if (changed == 0 && it > 1) break;
+  }
+  std::memcpy(centres_out, cs.data(), sizeof(float) * cs.size());
+  return 0;
+}

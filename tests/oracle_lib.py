@@ -36,6 +36,12 @@ _SIGS = {
     "orc_model_finalize": (C.c_int, [vp]),
     "orc_model_embed": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
     "orc_num_threads": (C.c_int, []),
+    "orc_pcg_uint64s": (None, [vp, i64, vp]),
+    "orc_pcg_intns": (None, [vp, C.c_uint64, i64, vp]),
+    "orc_pcg_float64s": (None, [vp, i64, vp]),
+    "orc_cluster_normalize": (None, [vp, i64, C.c_int, vp]),
+    "orc_cluster_nearest": (C.c_int, [vp, i64, vp, i64, C.c_int, vp, vp]),
+    "orc_cluster_kmeans": (C.c_int, [vp, i64, C.c_int, C.c_int, C.c_int, C.c_uint64, vp, vp, vp, vp, vp, vp]),
 }
 
 _lib = None
@@ -172,6 +178,63 @@ def similarities_topk(q, docs, k):
     rc = lib().orc_similarities_topk(P(q), q.shape[0], P(docs), docs.shape[0], q.shape[1], k, P(idx), P(val))
     assert rc == 0
     return idx, val
+
+
+def pcg_uint64s(seed1, seed2, count):
+    """Go math/rand/v2 NewPCG(seed1, seed2).Uint64() x count."""
+    st = np.array([seed1, seed2], np.uint64)
+    out = np.empty(count, np.uint64)
+    lib().orc_pcg_uint64s(P(st), count, P(out))
+    return out
+
+
+def pcg_intns(seed1, seed2, n, count):
+    st = np.array([seed1, seed2], np.uint64)
+    out = np.empty(count, np.uint64)
+    lib().orc_pcg_intns(P(st), n, count, P(out))
+    return out
+
+
+def pcg_float64s(seed1, seed2, count):
+    st = np.array([seed1, seed2], np.uint64)
+    out = np.empty(count, np.float64)
+    lib().orc_pcg_float64s(P(st), count, P(out))
+    return out
+
+
+def cluster_normalize(x):
+    x = f32c(x)
+    out = np.empty_like(x)
+    lib().orc_cluster_normalize(P(x), x.shape[0], x.shape[1], P(out))
+    return out
+
+
+def cluster_nearest(x, centres):
+    x, c = f32c(x), f32c(centres)
+    n = x.shape[0]
+    idx = np.empty(n, np.int32)
+    sim = np.empty(n, np.float32)
+    if lib().orc_cluster_nearest(P(x), n, P(c), c.shape[0], x.shape[1], P(idx), P(sim)) != 0:
+        raise ValueError("oracle nearest: no centres")
+    return idx, sim
+
+
+def cluster_kmeans(x, k, iters, seed):
+    """cluster.KMeans: dict of centres, assignment, similarity, sizes,
+    iterations and the seeding's chosen rows."""
+    x = f32c(x)
+    n, d = x.shape
+    centres = np.empty((k, d), np.float32)
+    assign = np.empty(n, np.int32)
+    sim = np.empty(n, np.float32)
+    sizes = np.empty(k, np.int32)
+    chosen = np.empty(k, np.int32)
+    it = C.c_int(0)
+    rc = lib().orc_cluster_kmeans(P(x), n, d, k, iters, C.c_uint64(seed), P(centres), P(assign), P(sim), P(sizes),
+                                  C.byref(it), P(chosen))
+    if rc != 0:
+        raise ValueError("cluster: k must be between 1 and the number of rows")
+    return dict(centres=centres, assignment=assign, similarity=sim, sizes=sizes, iterations=it.value, chosen=chosen)
 
 
 class OracleModel:
