@@ -10,19 +10,21 @@
 // and centre sizes for the early stop and the empty-centre restarts.
 //   k-means++ (cluster.go:51-85): per new centre, kpp_weights_kernel scores
 //     every row against the newest centre, keeps the best similarity and
-//     writes the float64 weight (1 - best)^2; kpp_pick_kernel (one
-//     workgroup) sums the weights, scales the uniform draw by the total and
-//     finds the row where the running subtraction crosses zero, then copies
+//     writes the float64 weight (1 - best)^2; block_sums_kernel sums the
+//     weights in blocks of 256; kpp_pick_kernel (one workgroup) scans the
+//     block sums, scales the uniform draw by the total, finds the block and
+//     then the row where the running subtraction crosses zero, and copies
 //     that row into the centre list.
 //   Lloyd rounds (cluster.go:86-129): sim product, argmax_rows_kernel
-//     (assignment, similarity, change count, per-chunk centre counts), a
-//     stable counting sort of the row indices by centre (chunk_scan_kernel,
-//     offsets_kernel, scatter_kernel), then colsum_kernel adds each centre's
-//     rows in increasing row order, one thread per (centre, column): the
-//     same float32 additions in the same order as the reference's loop, so
-//     the centre sums are bit-identical given the same assignment. Empty
-//     centres restart on the worst-fitting row (worst_kernel, in increasing
-//     centre order), and normalize_rows_kernel renormalises.
+//     (assignment, similarity), count_kernel (per-chunk centre counts and
+//     change counts), a stable counting sort of the row indices by centre
+//     (chunk_scan_kernel, offsets_kernel, scatter_kernel), then
+//     colsum_kernel adds each centre's rows in increasing row order, one
+//     lane per (centre, column): the same float32 additions in the same
+//     order as the reference's loop, so the centre sums are bit-identical
+//     given the same assignment. Empty centres restart on the worst-fitting
+//     row (worst_kernel, in increasing centre order), and
+//     normalize_rows_kernel renormalises.
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -34,9 +36,11 @@ namespace fa {
 namespace {
 
 constexpr int kRowWG = 256;        // one wave per row, 4 rows per workgroup
-constexpr int kChunk = 1024;       // rows per counting-sort chunk
-constexpr int kCntWindow = 8192;   // centres per LDS counter window of scatter_kernel
+constexpr int kChunk = 256;        // rows per counting-sort chunk (one per thread of count_kernel)
+constexpr int kCntWindow = 8192;   // centres per LDS counter window
 constexpr int kPickThreads = 1024;
+constexpr int kSumBlock = 256;     // weights per partial sum of the k-means++ pick
+constexpr int kColTile = 32;       // rows loaded ahead by colsum_kernel
 
 inline unsigned row_blocks(int64_t n) { return (unsigned)((n + 3) / 4); }
 
@@ -60,11 +64,10 @@ __global__ __launch_bounds__(kRowWG) void normalize_rows_kernel(const float* x, 
 
 // First-max argmax of each row of sim [n x k] with the sequential rule of
 // (*Tensor).Argmax: the first index holding the maximum; NaN never wins
-// except at index 0, where the sequential scan starts. Optional outputs:
-// change count against the previous assignment, per-chunk centre counts.
+// except at index 0, where the sequential scan starts.
 __global__ __launch_bounds__(kRowWG) void argmax_rows_kernel(const float* __restrict__ sim, int64_t n, int k,
-                                                             int32_t* assign, float* __restrict__ simil,
-                                                             int32_t* changed, int32_t* chunk_cnt) {
+                                                             int32_t* __restrict__ assign,
+                                                             float* __restrict__ simil) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= n) return;
@@ -89,10 +92,36 @@ __global__ __launch_bounds__(kRowWG) void argmax_rows_kernel(const float* __rest
   }
   if (lane != 0) return;
   if (bi == INT32_MAX || isnan(sr[0])) bi = 0;
-  if (changed && assign[row] != bi) atomicAdd(changed, 1);
   assign[row] = bi;
   simil[row] = sr[bi];
-  if (chunk_cnt) atomicAdd(&chunk_cnt[(row / kChunk) * k + bi], 1);
+}
+
+// Per chunk of kChunk rows: rows per centre (chunk_cnt[c][ch], centre-major)
+// and rows whose centre differs from the previous round's
+// (chunk_changed[ch]); then the previous assignment is brought up to date.
+__global__ __launch_bounds__(kChunk) void count_kernel(const int32_t* __restrict__ cur, int32_t* __restrict__ prev,
+                                                       int64_t n, int k, int nchunks, int32_t* __restrict__ chunk_cnt,
+                                                       int32_t* __restrict__ chunk_changed) {
+  __shared__ int32_t cnt[kCntWindow];
+  __shared__ int32_t nchanged;
+  const int t = threadIdx.x;
+  const int64_t ch = blockIdx.x;
+  const int64_t row = ch * kChunk + t;
+  const int a = row < n ? cur[row] : -1;
+  if (t == 0) nchanged = 0;
+  __syncthreads();
+  if (row < n && prev[row] != a) atomicAdd(&nchanged, 1);
+  for (int w0 = 0; w0 < k; w0 += kCntWindow) {
+    const int w1 = min(k, w0 + kCntWindow);
+    for (int c = t; c < w1 - w0; c += kChunk) cnt[c] = 0;
+    __syncthreads();
+    if (a >= w0 && a < w1) atomicAdd(&cnt[a - w0], 1);
+    __syncthreads();
+    for (int c = t; c < w1 - w0; c += kChunk) chunk_cnt[(int64_t)(w0 + c) * nchunks + ch] = cnt[c];
+    __syncthreads();
+  }
+  if (row < n) prev[row] = a;
+  if (t == 0) chunk_changed[ch] = nchanged;
 }
 
 // k-means++ step over all rows: s = x[i] . c, best[i] = max(best[i], s),
@@ -104,7 +133,17 @@ __global__ __launch_bounds__(kRowWG) void kpp_weights_kernel(const float* __rest
   if (row >= n) return;
   const float* xr = x + row * d;
   float s = 0.f;
-  for (int j = lane; j < d; j += 64) s += xr[j] * c[j];
+  if ((d & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(c)) & 15) == 0) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4* xv = reinterpret_cast<const f4*>(xr);
+    const f4* cv = reinterpret_cast<const f4*>(c);
+    for (int j = lane; j < d / 4; j += 64) {
+      const f4 a = xv[j], b = cv[j];
+      s += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    }
+  } else {
+    for (int j = lane; j < d; j += 64) s += xr[j] * c[j];
+  }
   s = wave_sum(s);
   if (lane != 0) return;
   float b = best[row];
@@ -114,44 +153,104 @@ __global__ __launch_bounds__(kRowWG) void kpp_weights_kernel(const float* __rest
   w[row] = om * om;
 }
 
-// k-means++ pick (cluster.go:73-82): total = sum w; pick = u * total; the
-// chosen row is the first i where pick - w[0] - ... - w[i] <= 0 (n-1 when
-// rounding leaves it positive). Thread t sums a contiguous segment; the
-// segment sums locate the crossing and the crossing segment is walked
-// element by element. The row is copied to centre_out.
-__global__ __launch_bounds__(kPickThreads) void kpp_pick_kernel(const double* __restrict__ w, int64_t n, double u,
+// part[b] = sum of w[b*kSumBlock ...] in a fixed tree order.
+__global__ __launch_bounds__(kSumBlock) void block_sums_kernel(const double* __restrict__ w, int64_t n,
+                                                               double* __restrict__ part) {
+  __shared__ double buf[kSumBlock];
+  const int t = threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * kSumBlock + t;
+  buf[t] = i < n ? w[i] : 0.0;
+  __syncthreads();
+  for (int o = kSumBlock / 2; o > 0; o >>= 1) {
+    if (t < o) buf[t] += buf[t + o];
+    __syncthreads();
+  }
+  if (t == 0) part[blockIdx.x] = buf[0];
+}
+
+// k-means++ pick (cluster.go:73-82): pick = u * total; the chosen row is
+// the first i where pick - w[0] - ... - w[i] <= 0 (n-1 when rounding leaves
+// it positive). The block partial sums' inclusive prefix locates the
+// crossing block, whose weights are then walked one by one. The row is
+// copied to centre_out.
+__global__ __launch_bounds__(kPickThreads) void kpp_pick_kernel(const double* __restrict__ w, int64_t n,
+                                                                const double* __restrict__ part, int nparts, double u,
                                                                 const float* __restrict__ x, int d,
                                                                 float* __restrict__ centre_out, int32_t* chosen) {
-  __shared__ double part[kPickThreads];
+  __shared__ double scan[kPickThreads];
+  __shared__ double wblk[kSumBlock];
+  __shared__ double carry, total_s;
+  __shared__ int first_blk;
   __shared__ int64_t pick_idx;
   const int t = threadIdx.x;
-  const int64_t seg = (n + kPickThreads - 1) / kPickThreads;
-  const int64_t b0 = (int64_t)t * seg, b1 = min(n, b0 + seg);
-  double s = 0;
-  for (int64_t i = b0; i < b1; i++) s += w[i];
-  part[t] = s;
+  if (t == 0) {
+    carry = 0;
+    first_blk = INT32_MAX;
+  }
+  __syncthreads();
+  // total: inclusive scan of the partials in tiles of kPickThreads (pass 1)
+  for (int base = 0; base < nparts; base += kPickThreads) {
+    scan[t] = base + t < nparts ? part[base + t] : 0.0;
+    __syncthreads();
+    for (int o = 1; o < kPickThreads; o <<= 1) {
+      const double add = t >= o ? scan[t - o] : 0.0;
+      __syncthreads();
+      scan[t] += add;
+      __syncthreads();
+    }
+    if (t == 0) carry += scan[kPickThreads - 1];
+    __syncthreads();
+  }
+  if (t == 0) total_s = carry;
+  __syncthreads();
+  const double pick = u * total_s;
+  // pass 2: the first block whose inclusive prefix reaches pick (one tile of
+  // partials: the scan of pass 1 is still in LDS)
+  const bool one_tile = nparts <= kPickThreads;
+  if (t == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < nparts; base += kPickThreads) {
+    if (!one_tile) {
+      scan[t] = base + t < nparts ? part[base + t] : 0.0;
+      __syncthreads();
+      for (int o = 1; o < kPickThreads; o <<= 1) {
+        const double add = t >= o ? scan[t - o] : 0.0;
+        __syncthreads();
+        scan[t] += add;
+        __syncthreads();
+      }
+    }
+    if (base + t < nparts && pick - (carry + scan[t]) <= 0) atomicMin(&first_blk, base + t);
+    __syncthreads();
+    if (first_blk != INT32_MAX) break;
+    if (t == 0) carry += scan[kPickThreads - 1];
+    __syncthreads();
+  }
+  __syncthreads();
+  const int fb = first_blk;
+  // the prefix before block fb, in the order pass 2 formed it
+  if (fb != INT32_MAX && t == 0) {
+    const int tile = fb / kPickThreads * kPickThreads;
+    total_s = carry + (fb > tile ? scan[fb - tile - 1] : 0.0);
+  }
+  const int64_t b0 = fb != INT32_MAX ? (int64_t)fb * kSumBlock : n;
+  if (t < kSumBlock) wblk[t] = b0 + t < n ? w[b0 + t] : 0.0;
   __syncthreads();
   if (t == 0) {
-    double total = 0;
-    for (int i = 0; i < kPickThreads; i++) total += part[i];
-    double p = u * total;
     int64_t idx = n - 1;
-    int64_t start = n;
-    for (int i = 0; i < kPickThreads; i++) {
-      const int64_t s0 = (int64_t)i * seg;
-      if (s0 >= n) break;
-      if (p - part[i] <= 0) {
-        start = s0;
-        break;
+    if (fb != INT32_MAX) {
+      double p = pick - total_s;
+      int64_t i = b0;
+      for (; i < min(n, b0 + kSumBlock); i++) {
+        p -= wblk[i - b0];
+        if (p <= 0) break;
       }
-      p -= part[i];
-    }
-    for (int64_t i = start; i < n; i++) {
-      p -= w[i];
-      if (p <= 0) {
-        idx = i;
-        break;
-      }
+      if (i >= min(n, b0 + kSumBlock))  // rounding: keep walking
+        for (; i < n; i++) {
+          p -= w[i];
+          if (p <= 0) break;
+        }
+      if (i < n) idx = i;
     }
     pick_idx = idx;
     *chosen = (int32_t)idx;
@@ -161,22 +260,37 @@ __global__ __launch_bounds__(kPickThreads) void kpp_pick_kernel(const double* __
   for (int j = t; j < d; j += kPickThreads) centre_out[j] = src[j];
 }
 
-// chunk_cnt[ch][c] (rows of chunk ch assigned to c) -> exclusive prefix over
-// chunks; sizes[c] = total. One thread per centre.
-__global__ __launch_bounds__(256) void chunk_scan_kernel(int32_t* chunk_cnt, int nchunks, int k, int32_t* sizes) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= k) return;
-  int32_t run = 0;
-  for (int ch = 0; ch < nchunks; ch++) {
-    const int32_t v = chunk_cnt[(int64_t)ch * k + c];
-    chunk_cnt[(int64_t)ch * k + c] = run;
-    run += v;
+// chunk_cnt[c][ch] (rows of chunk ch assigned to c) -> exclusive prefix over
+// chunks; sizes[c] = total. One workgroup per centre.
+__global__ __launch_bounds__(256) void chunk_scan_kernel(int32_t* chunk_cnt, int nchunks, int32_t* sizes) {
+  __shared__ int32_t buf[256];
+  __shared__ int32_t carry;
+  const int t = threadIdx.x;
+  int32_t* row = chunk_cnt + (int64_t)blockIdx.x * nchunks;
+  if (t == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < nchunks; base += 256) {
+    const int32_t v = base + t < nchunks ? row[base + t] : 0;
+    buf[t] = v;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const int32_t add = t >= o ? buf[t - o] : 0;
+      __syncthreads();
+      buf[t] += add;
+      __syncthreads();
+    }
+    if (base + t < nchunks) row[base + t] = carry + buf[t] - v;
+    __syncthreads();
+    if (t == 0) carry += buf[255];
+    __syncthreads();
   }
-  sizes[c] = run;
+  if (t == 0) sizes[blockIdx.x] = carry;
 }
 
-// offsets[c] = sizes[0] + ... + sizes[c-1]. One workgroup.
-__global__ __launch_bounds__(1024) void offsets_kernel(const int32_t* sizes, int k, int32_t* offsets) {
+// offsets[c] = sizes[0] + ... + sizes[c-1]; *changed = sum of the chunks'
+// change counts. One workgroup.
+__global__ __launch_bounds__(1024) void offsets_kernel(const int32_t* sizes, int k, int32_t* offsets,
+                                                       const int32_t* chunk_changed, int nchunks, int32_t* changed) {
   __shared__ int32_t buf[1024];
   __shared__ int32_t carry;
   const int t = threadIdx.x;
@@ -197,6 +311,15 @@ __global__ __launch_bounds__(1024) void offsets_kernel(const int32_t* sizes, int
     if (t == 0) carry += buf[1023];
     __syncthreads();
   }
+  int32_t s = 0;
+  for (int ch = t; ch < nchunks; ch += 1024) s += chunk_changed[ch];
+  buf[t] = s;
+  __syncthreads();
+  for (int o = 512; o > 0; o >>= 1) {
+    if (t < o) buf[t] += buf[t + o];
+    __syncthreads();
+  }
+  if (t == 0) *changed = buf[0];
 }
 
 // Stable scatter of row indices by centre: list[offsets[a] + (rows of a in
@@ -205,7 +328,7 @@ __global__ __launch_bounds__(1024) void offsets_kernel(const int32_t* sizes, int
 // comes from shuffles, the running count per centre from LDS (centre
 // windows of kCntWindow).
 __global__ __launch_bounds__(64) void scatter_kernel(const int32_t* __restrict__ assign, int64_t n, int k,
-                                                     const int32_t* __restrict__ offsets,
+                                                     int nchunks, const int32_t* __restrict__ offsets,
                                                      const int32_t* __restrict__ chunk_pre, int32_t* __restrict__ list) {
   __shared__ int32_t cnt[kCntWindow];
   const int lane = threadIdx.x;
@@ -227,7 +350,7 @@ __global__ __launch_bounds__(64) void scatter_kernel(const int32_t* __restrict__
           later += j > lane;
         }
       }
-      if (a >= 0) list[offsets[a] + chunk_pre[ch * k + a] + cnt[a - w0] + rank] = (int32_t)row;
+      if (a >= 0) list[offsets[a] + chunk_pre[(int64_t)a * nchunks + ch] + cnt[a - w0] + rank] = (int32_t)row;
       __syncthreads();
       if (a >= 0 && later == 0) cnt[a - w0] += rank + 1;
       __syncthreads();
@@ -236,27 +359,25 @@ __global__ __launch_bounds__(64) void scatter_kernel(const int32_t* __restrict__
 }
 
 // sums[c][j] = sum over c's rows in increasing row order of x[row][j],
-// accumulated in float32 from 0 (cluster.go:100-112).
-__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ x, int d,
-                                                     const int32_t* __restrict__ list,
-                                                     const int32_t* __restrict__ offsets,
-                                                     const int32_t* __restrict__ sizes, float* __restrict__ sums) {
+// accumulated in float32 from 0 (cluster.go:100-112). One wave per (centre,
+// 64 columns); kColTile rows are loaded ahead of their additions.
+__global__ __launch_bounds__(64) void colsum_kernel(const float* __restrict__ x, int d,
+                                                    const int32_t* __restrict__ list,
+                                                    const int32_t* __restrict__ offsets,
+                                                    const int32_t* __restrict__ sizes, float* __restrict__ sums) {
   const int c = blockIdx.x;
-  const int j = blockIdx.y * 256 + threadIdx.x;
+  const int j = blockIdx.y * 64 + threadIdx.x;
   if (j >= d) return;
   const int32_t* rows = list + offsets[c];
   const int m = sizes[c];
   float acc = 0.f;
   int p = 0;
-  for (; p + 4 <= m; p += 4) {  // four loads in flight, additions in order
-    const float v0 = x[(int64_t)rows[p] * d + j];
-    const float v1 = x[(int64_t)rows[p + 1] * d + j];
-    const float v2 = x[(int64_t)rows[p + 2] * d + j];
-    const float v3 = x[(int64_t)rows[p + 3] * d + j];
-    acc += v0;
-    acc += v1;
-    acc += v2;
-    acc += v3;
+  for (; p + kColTile <= m; p += kColTile) {
+    float v[kColTile];
+#pragma unroll
+    for (int u = 0; u < kColTile; u++) v[u] = x[(int64_t)rows[p + u] * d + j];
+#pragma unroll
+    for (int u = 0; u < kColTile; u++) acc += v[u];
   }
   for (; p < m; p++) acc += x[(int64_t)rows[p] * d + j];
   sums[(int64_t)c * d + j] = acc;
@@ -427,7 +548,7 @@ int fa_cluster_nearest_dev(fa_ctx* ctx, const float* x, int64_t n, const float* 
   float* sim = ws.as<float>();
   if ((rc = fa::launch_sim(ctx, x, n, centres, k, d, sim))) return rc;
   hipLaunchKernelGGL(fa::argmax_rows_kernel, dim3(fa::row_blocks(n)), dim3(fa::kRowWG), 0, ctx->stream, sim, n,
-                     (int)k, index, similarity, (int32_t*)nullptr, (int32_t*)nullptr);
+                     (int)k, index, similarity);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
@@ -470,29 +591,21 @@ int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int
   hipStream_t st = ctx->stream;
   const int nchunks = (int)((n + fa::kChunk - 1) / fa::kChunk);
 
-  // workspace: raw centres, sums [k x d]; best [n]; w [n] f64; sim [n x k];
-  // chunk counts [nchunks x k]; offsets [k]; list [n]; changed; chosen [k]
+  // workspace: raw centres, sums [k x d]; best [n]; w [n] f64; partial
+  // sums of w; sim [n x k]; chunk counts [nchunks x k]; chunk change counts;
+  // offsets [k]; list [n]; previous assignment [n]; changed; chosen [k]
+  const int nparts = (int)((n + fa::kSumBlock - 1) / fa::kSumBlock);
   size_t off = 0;
-  const size_t o_raw = off;
-  off += fa::align256((size_t)k * d * 4);
-  const size_t o_sums = off;
-  off += fa::align256((size_t)k * d * 4);
-  const size_t o_best = off;
-  off += fa::align256((size_t)n * 4);
-  const size_t o_w = off;
-  off += fa::align256((size_t)n * 8);
-  const size_t o_sim = off;
-  off += fa::align256((size_t)n * k * 4);
-  const size_t o_cnt = off;
-  off += fa::align256((size_t)nchunks * k * 4);
-  const size_t o_offs = off;
-  off += fa::align256((size_t)k * 4);
-  const size_t o_list = off;
-  off += fa::align256((size_t)n * 4);
-  const size_t o_changed = off;
-  off += 256;
-  const size_t o_chosen = off;
-  off += fa::align256((size_t)k * 4);
+  auto take = [&off](size_t bytes) {
+    const size_t o = off;
+    off += fa::align256(bytes);
+    return o;
+  };
+  const size_t o_raw = take((size_t)k * d * 4), o_sums = take((size_t)k * d * 4), o_best = take((size_t)n * 4),
+               o_w = take((size_t)n * 8), o_part = take((size_t)nparts * 8), o_sim = take((size_t)n * k * 4),
+               o_cnt = take((size_t)nchunks * k * 4), o_chg = take((size_t)nchunks * 4), o_offs = take((size_t)k * 4),
+               o_list = take((size_t)n * 4), o_prev = take((size_t)n * 4), o_changed = take(4),
+               o_chosen = take((size_t)k * 4);
   fa::DevBuf& ws = ctx->slot(S_CL_WORK);
   if ((rc = ws.ensure(ctx, off))) return rc;
   char* base = ws.as<char>();
@@ -500,10 +613,13 @@ int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int
   float* sums = (float*)(base + o_sums);
   float* best = (float*)(base + o_best);
   double* w = (double*)(base + o_w);
+  double* part = (double*)(base + o_part);
   float* sim = (float*)(base + o_sim);
   int32_t* cnt = (int32_t*)(base + o_cnt);
+  int32_t* chg = (int32_t*)(base + o_chg);
   int32_t* offs = (int32_t*)(base + o_offs);
   int32_t* list = (int32_t*)(base + o_list);
+  int32_t* prev = (int32_t*)(base + o_prev);
   int32_t* changed = (int32_t*)(base + o_changed);
   int32_t* chosen = (int32_t*)(base + o_chosen);
 
@@ -519,14 +635,18 @@ int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int
     hipLaunchKernelGGL(fa::kpp_weights_kernel, dim3(fa::row_blocks(n)), dim3(fa::kRowWG), 0, st, x, n, (int)d,
                        (const float*)(raw + (size_t)(r - 1) * d), best, w);
     FA_CHECK_LAUNCH(ctx);
-    hipLaunchKernelGGL(fa::kpp_pick_kernel, dim3(1), dim3(fa::kPickThreads), 0, st, (const double*)w, n, u[r], x,
-                       (int)d, raw + (size_t)r * d, chosen + r);
+    hipLaunchKernelGGL(fa::block_sums_kernel, dim3((unsigned)nparts), dim3(fa::kSumBlock), 0, st, (const double*)w,
+                       n, part);
+    FA_CHECK_LAUNCH(ctx);
+    hipLaunchKernelGGL(fa::kpp_pick_kernel, dim3(1), dim3(fa::kPickThreads), 0, st, (const double*)w, n,
+                       (const double*)part, nparts, u[r], x, (int)d, raw + (size_t)r * d, chosen + r);
     FA_CHECK_LAUNCH(ctx);
   }
   if ((rc = fa::launch_normalize(ctx, raw, k, d, centres))) return rc;
 
   // Lloyd rounds (cluster.go:86-129)
   FA_HIP_CHECK(ctx, hipMemsetAsync(assignment, 0, (size_t)n * 4, st));
+  FA_HIP_CHECK(ctx, hipMemsetAsync(prev, 0, (size_t)n * 4, st));
   FA_HIP_CHECK(ctx, hipMemsetAsync(similarity, 0, (size_t)n * 4, st));
   FA_HIP_CHECK(ctx, hipMemsetAsync(sizes, 0, (size_t)k * 4, st));
   std::vector<int32_t> host((size_t)k + 1);
@@ -534,21 +654,22 @@ int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int
   for (int it = 1; it <= iters; it++) {
     it_done = it;
     if ((rc = fa::launch_sim(ctx, x, n, centres, k, d, sim))) return rc;
-    FA_HIP_CHECK(ctx, hipMemsetAsync(changed, 0, 4, st));
-    FA_HIP_CHECK(ctx, hipMemsetAsync(cnt, 0, (size_t)nchunks * k * 4, st));
     hipLaunchKernelGGL(fa::argmax_rows_kernel, dim3(fa::row_blocks(n)), dim3(fa::kRowWG), 0, st,
-                       (const float*)sim, n, (int)k, assignment, similarity, changed, cnt);
+                       (const float*)sim, n, (int)k, assignment, similarity);
     FA_CHECK_LAUNCH(ctx);
-    hipLaunchKernelGGL(fa::chunk_scan_kernel, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, st, cnt, nchunks,
-                       (int)k, sizes);
+    hipLaunchKernelGGL(fa::count_kernel, dim3((unsigned)nchunks), dim3(fa::kChunk), 0, st,
+                       (const int32_t*)assignment, prev, n, (int)k, nchunks, cnt, chg);
     FA_CHECK_LAUNCH(ctx);
-    hipLaunchKernelGGL(fa::offsets_kernel, dim3(1), dim3(1024), 0, st, (const int32_t*)sizes, (int)k, offs);
+    hipLaunchKernelGGL(fa::chunk_scan_kernel, dim3((unsigned)k), dim3(256), 0, st, cnt, nchunks, sizes);
+    FA_CHECK_LAUNCH(ctx);
+    hipLaunchKernelGGL(fa::offsets_kernel, dim3(1), dim3(1024), 0, st, (const int32_t*)sizes, (int)k, offs,
+                       (const int32_t*)chg, nchunks, changed);
     FA_CHECK_LAUNCH(ctx);
     hipLaunchKernelGGL(fa::scatter_kernel, dim3((unsigned)nchunks), dim3(64), 0, st, (const int32_t*)assignment, n,
-                       (int)k, (const int32_t*)offs, (const int32_t*)cnt, list);
+                       (int)k, nchunks, (const int32_t*)offs, (const int32_t*)cnt, list);
     FA_CHECK_LAUNCH(ctx);
-    hipLaunchKernelGGL(fa::colsum_kernel, dim3((unsigned)k, (unsigned)((d + 255) / 256)), dim3(256), 0, st, x,
-                       (int)d, (const int32_t*)list, (const int32_t*)offs, (const int32_t*)sizes, sums);
+    hipLaunchKernelGGL(fa::colsum_kernel, dim3((unsigned)k, (unsigned)((d + 63) / 64)), dim3(64), 0, st, x, (int)d,
+                       (const int32_t*)list, (const int32_t*)offs, (const int32_t*)sizes, sums);
     FA_CHECK_LAUNCH(ctx);
     FA_HIP_CHECK(ctx, hipMemcpyAsync(host.data(), sizes, (size_t)k * 4, hipMemcpyDeviceToHost, st));
     FA_HIP_CHECK(ctx, hipMemcpyAsync(host.data() + k, changed, 4, hipMemcpyDeviceToHost, st));

@@ -107,7 +107,8 @@ def test_kmeans_recovers_planted_clusters():
     assert r.Inertia() <= 0.1
 
 
-@pytest.mark.parametrize("n,d,k,iters,seed", [(20000, 768, 40, 10, 3), (5000, 128, 200, 8, 11), (3000, 33, 7, 30, 5)])
+@pytest.mark.parametrize("n,d,k,iters,seed", [(20000, 768, 40, 10, 3), (5000, 128, 200, 8, 11), (3000, 33, 7, 30, 5),
+                                               (300000, 8, 4, 5, 21)])
 def test_kmeans_matches_oracle(n, d, k, iters, seed):
     rng = np.random.default_rng(seed)
     x, _ = planted(rng, n, d, k, 0.3 / np.sqrt(d) * 8)
