@@ -127,11 +127,94 @@ def weight_specs(s: ModelShape):
     return specs
 
 
-def make_weight(name: str, shape, kind: str, seed: int = WEIGHT_SEED) -> np.ndarray:
-    """bf16 bits (uint16) for matrices, float32 for norm vectors."""
+@dataclass
+class ModelShape2:
+    """EmbeddingGemma 2 text tower hyper-parameters (models/gemma/config.go:
+    247-297; the values of the reference's TestConfig2, gemma2_test.go:44-95):
+    layer l is full attention iff (l+1) % 6 == 0, with head_dim
+    global_head_dim and global_kv_heads key/value heads; sliding layers use
+    head_dim and num_key_value_heads and attend within an inclusive radius of
+    sliding_window."""
+    hidden_size: int = 512
+    num_hidden_layers: int = 12
+    num_attention_heads: int = 4
+    num_key_value_heads: int = 2
+    head_dim: int = 256
+    global_head_dim: int = 512
+    global_kv_heads: int = 1
+    intermediate_size: int = 2048
+    vocab_size: int = 262144
+    sliding_window: int = 512
+    hidden_size_per_layer_input: int = 512
+    embedding_dim: int = 768
+    rope_local_base_freq: float = 1e4
+    rope_theta: float = 1e6
+    rms_norm_eps: float = 1e-6
+    max_tokens: int = 8192
+    dense_out: list = field(default_factory=list)
+
+    def sliding(self, l: int) -> bool:
+        return (l + 1) % 6 != 0
+
+    def layer_head_dim(self, l: int) -> int:
+        return self.head_dim if self.sliding(l) else self.global_head_dim
+
+    def layer_kv_heads(self, l: int) -> int:
+        return self.num_key_value_heads if self.sliding(l) else self.global_kv_heads
+
+
+def weight_specs2(s: ModelShape2):
+    """(name, shape, kind) of every EmbeddingGemma 2 tensor (names without
+    the checkpoint's "language_model." prefix, as models/gemma/model.go:
+    142-205 reads them); kinds: 'm' matrix, 'g' RMSNorm gain (multiplies the
+    normalised value directly), 's' the per-layer scalar."""
+    d, H, F, P = s.hidden_size, s.num_attention_heads, s.intermediate_size, s.hidden_size_per_layer_input
+    specs = [("embed_tokens.weight", (s.vocab_size, d), "m")]
+    for l in range(s.num_hidden_layers):
+        D, Hkv = s.layer_head_dim(l), s.layer_kv_heads(l)
+        p = f"layers.{l}."
+        specs += [
+            (p + "input_layernorm.weight", (d,), "g"),
+            (p + "post_attention_layernorm.weight", (d,), "g"),
+            (p + "pre_feedforward_layernorm.weight", (d,), "g"),
+            (p + "post_feedforward_layernorm.weight", (d,), "g"),
+            (p + "self_attn.q_norm.weight", (D,), "g"),
+            (p + "self_attn.k_norm.weight", (D,), "g"),
+            (p + "self_attn.q_proj.weight", (H * D, d), "m"),
+            (p + "self_attn.k_proj.weight", (Hkv * D, d), "m"),
+            (p + "self_attn.v_proj.weight", (Hkv * D, d), "m"),
+            (p + "self_attn.o_proj.weight", (d, H * D), "m"),
+            (p + "mlp.gate_proj.weight", (F, d), "m"),
+            (p + "mlp.up_proj.weight", (F, d), "m"),
+            (p + "mlp.down_proj.weight", (d, F), "m"),
+            (p + "ple_block.per_layer_input_gate.weight", (P, d), "m"),
+            (p + "ple_block.per_layer_projection.weight", (d, P), "m"),
+            (p + "ple_block.post_per_layer_input_norm.weight", (d,), "g"),
+            (p + "layer_scalar", (1,), "s"),
+        ]
+    specs += [("norm.weight", (d,), "g"),
+              ("ple.per_layer_model_projection.weight", (s.num_hidden_layers * P, d), "m"),
+              ("ple.per_layer_projection_norm.weight", (P,), "g"),
+              ("embedding_projection.weight", (s.embedding_dim, d), "m")]
+    din = s.embedding_dim
+    for i, o in enumerate(s.dense_out):
+        specs.append((f"dense.{i}.linear.weight", (o, din), "m"))
+        din = o
+    return specs
+
+
+def make_weight(name: str, shape, kind: str, seed: int = WEIGHT_SEED, mat_std: float = 0.02,
+                norm_std: float = 0.1) -> np.ndarray:
+    """bf16 bits (uint16) for matrices ('m', N(0, mat_std)); float32 for norm
+    vectors ('n': N(0, norm_std), applied as 1+w), gains ('g': 1 + N(0,
+    norm_std), applied as is) and layer scalars ('s': 1 + N(0, 0.1))."""
     if kind == "m":
-        return normal_bf16(seed, name, 0.02, shape)
-    return normal_f32(seed, name, 0.1, shape)
+        return normal_bf16(seed, name, mat_std, shape)
+    if kind == "g":
+        return (normal_f32(seed, name, norm_std, shape) + np.float32(1)).astype(np.float32)
+    if kind == "s":
+        return (normal_f32(seed, name, 0.1, shape) + np.float32(1)).astype(np.float32)
+    return normal_f32(seed, name, norm_std, shape)
 
 
 # ---- inputs ---------------------------------------------------------------------

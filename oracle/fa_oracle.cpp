@@ -973,3 +973,311 @@ ORC_API int orc_cluster_kmeans(const float* x, i64 n, int d, int k, int iters, u
   std::memcpy(centres_out, cs.data(), sizeof(float) * cs.size());
   return 0;
 }
+
+// ---------------------------------------------------------------------------
+// EmbeddingGemma 2 text tower (models/gemma: config.go:247-362, model.go:
+// 105-205, embed.go:247-377, 408-429).
+// ---------------------------------------------------------------------------
+struct Orc2Layer {
+  int D = 0, Hkv = 0;
+  bool sliding = true;
+  float scalar = 1;
+  std::vector<float> wq, wk, wv, wo, wgate, wup, wdown, pleGate, pleProj;  // [in, out]
+  std::vector<float> inputNorm, postAttnNorm, preFFNNorm, postFFNNorm, qNorm, kNorm, plePostNorm;  // gains as is
+  std::vector<float> raw_wq, raw_wk, raw_wv, raw_wgate, raw_wup;
+};
+
+struct OrcModel2 {
+  int hidden = 0, layers = 0, heads = 0, ffn = 0, vocab = 0, radius = 0, P = 0, E = 0, n_dense = 0;
+  double rope_local = 1e4, rope_theta = 1e6;
+  float eps = 1e-6f;
+  std::vector<Orc2Layer> L;
+  std::vector<float> embed, norm, pleProj, pleNorm, embProj;  // pleProj [hidden, layers*P], embProj [hidden, E]
+  std::vector<std::vector<float>> dense;
+  std::vector<int> dense_in, dense_out;
+  std::map<std::string, int> seen;
+  bool finalized = false;
+};
+
+ORC_API void* orc_model2_create(int hidden, int layers, int heads, int ffn, int vocab, int radius, int ple_dim,
+                                int embedding_dim, double rope_local, double rope_theta, float eps,
+                                const int* layer_head_dim, const int* layer_kv_heads, const int* layer_sliding,
+                                int n_dense, const int* dense_out) {
+  if (n_dense < 0 || n_dense > 4 || layers <= 0) return nullptr;
+  OrcModel2* m = new OrcModel2();
+  m->hidden = hidden; m->layers = layers; m->heads = heads; m->ffn = ffn; m->vocab = vocab; m->radius = radius;
+  m->P = ple_dim; m->E = embedding_dim; m->rope_local = rope_local; m->rope_theta = rope_theta; m->eps = eps;
+  m->n_dense = n_dense;
+  m->L.resize(layers);
+  for (int l = 0; l < layers; l++) {
+    m->L[l].D = layer_head_dim[l];
+    m->L[l].Hkv = layer_kv_heads[l];
+    m->L[l].sliding = layer_sliding[l] != 0;
+  }
+  int in = embedding_dim;
+  m->dense.resize(n_dense);
+  for (int i = 0; i < n_dense; i++) {
+    m->dense_in.push_back(in);
+    m->dense_out.push_back(dense_out[i]);
+    in = dense_out[i];
+  }
+  return m;
+}
+
+ORC_API void orc_model2_destroy(void* p) { delete (OrcModel2*)p; }
+
+// model.go:142-205 with Variant 2's loaders: norms keep their gains
+// (model.go:128-140), per-layer geometry from the layer's head_dim and
+// key/value heads, "layer_scalar" one value (model.go:183-190).
+ORC_API int orc_model2_set(void* p, const char* name, const float* data, i64 numel) {
+  OrcModel2* m = (OrcModel2*)p;
+  const std::string s(name);
+  const int d = m->hidden, H = m->heads, F = m->ffn, P = m->P;
+  auto gain = [&](std::vector<float>& dst, i64 n) {
+    if (numel != n) return -2;
+    dst.assign(data, data + n);
+    return 0;
+  };
+  auto mat = [&](std::vector<float>& dst, int out, int in) {
+    if (numel != (i64)out * in) return -2;
+    dst = transpose_w(data, out, in);
+    return 0;
+  };
+  int rc = 0;
+  if (s == "embed_tokens.weight") {
+    if (numel != (i64)m->vocab * d) return -2;
+    m->embed.assign(data, data + numel);
+  } else if (s == "norm.weight") {
+    rc = gain(m->norm, d);
+  } else if (s == "ple.per_layer_model_projection.weight") {
+    rc = mat(m->pleProj, m->layers * P, d);
+  } else if (s == "ple.per_layer_projection_norm.weight") {
+    rc = gain(m->pleNorm, P);
+  } else if (s == "embedding_projection.weight") {
+    rc = mat(m->embProj, m->E, d);
+  } else if (s.rfind("dense.", 0) == 0) {
+    int i = std::atoi(s.c_str() + 6);
+    if (i < 0 || i >= m->n_dense) return -3;
+    rc = mat(m->dense[i], m->dense_out[i], m->dense_in[i]);
+  } else if (s.rfind("layers.", 0) == 0) {
+    int l = std::atoi(s.c_str() + 7);
+    if (l < 0 || l >= m->layers) return -3;
+    const std::string rest = s.substr(s.find('.', 7) + 1);
+    Orc2Layer& Y = m->L[l];
+    const int D = Y.D, Hkv = Y.Hkv;
+    if (rest == "input_layernorm.weight") rc = gain(Y.inputNorm, d);
+    else if (rest == "post_attention_layernorm.weight") rc = gain(Y.postAttnNorm, d);
+    else if (rest == "pre_feedforward_layernorm.weight") rc = gain(Y.preFFNNorm, d);
+    else if (rest == "post_feedforward_layernorm.weight") rc = gain(Y.postFFNNorm, d);
+    else if (rest == "self_attn.q_norm.weight") rc = gain(Y.qNorm, D);
+    else if (rest == "self_attn.k_norm.weight") rc = gain(Y.kNorm, D);
+    else if (rest == "self_attn.q_proj.weight") rc = mat(Y.raw_wq, H * D, d);
+    else if (rest == "self_attn.k_proj.weight") rc = mat(Y.raw_wk, Hkv * D, d);
+    else if (rest == "self_attn.v_proj.weight") rc = mat(Y.raw_wv, Hkv * D, d);
+    else if (rest == "self_attn.o_proj.weight") rc = mat(Y.wo, d, H * D);
+    else if (rest == "mlp.gate_proj.weight") rc = mat(Y.raw_wgate, F, d);
+    else if (rest == "mlp.up_proj.weight") rc = mat(Y.raw_wup, F, d);
+    else if (rest == "mlp.down_proj.weight") rc = mat(Y.wdown, d, F);
+    else if (rest == "ple_block.per_layer_input_gate.weight") rc = mat(Y.pleGate, P, d);
+    else if (rest == "ple_block.per_layer_projection.weight") rc = mat(Y.pleProj, d, P);
+    else if (rest == "ple_block.post_per_layer_input_norm.weight") rc = gain(Y.plePostNorm, d);
+    else if (rest == "layer_scalar") {
+      if (numel != 1) return -2;
+      Y.scalar = data[0];
+    } else return -3;
+  } else {
+    return -3;
+  }
+  if (rc) return rc;
+  m->seen[s]++;
+  return 0;
+}
+
+// Pre-norm gains folded into the weights they feed (model.go:206-222).
+ORC_API int orc_model2_finalize(void* p) {
+  OrcModel2* m = (OrcModel2*)p;
+  const int expected = 5 + m->n_dense + 17 * m->layers;
+  if ((int)m->seen.size() != expected) return -4;
+  const int d = m->hidden, H = m->heads, F = m->ffn;
+  for (auto& Y : m->L) {
+    Y.wq = fold(Y.raw_wq, Y.inputNorm, d, H * Y.D);
+    Y.wk = fold(Y.raw_wk, Y.inputNorm, d, Y.Hkv * Y.D);
+    Y.wv = fold(Y.raw_wv, Y.inputNorm, d, Y.Hkv * Y.D);
+    Y.wgate = fold(Y.raw_wgate, Y.preFFNNorm, d, F);
+    Y.wup = fold(Y.raw_wup, Y.preFFNNorm, d, F);
+    std::vector<float>().swap(Y.raw_wq);
+    std::vector<float>().swap(Y.raw_wk);
+    std::vector<float>().swap(Y.raw_wv);
+    std::vector<float>().swap(Y.raw_wgate);
+    std::vector<float>().swap(Y.raw_wup);
+  }
+  m->finalized = true;
+  return 0;
+}
+
+// encode2 + encode2From (embed.go:247-377), pool (embed.go:381-404) and
+// applyHead with the embedding projection (embed.go:408-429). hidden_out
+// (optional) receives the final normed hidden states [B, T, hidden].
+ORC_API int orc_model2_embed(void* p, const int32_t* ids, const int32_t* lengths, int B, int T, int dim, float* out,
+                             float* hidden_out) {
+  OrcModel2* m = (OrcModel2*)p;
+  if (!m->finalized) return -5;
+  const int d = m->hidden, H = m->heads, F = m->ffn, P = m->P, NL = m->layers;
+  const i64 M = (i64)B * T;
+  const float eps = m->eps;
+  int full = m->E;
+  if (m->n_dense > 0) full = m->dense_out[m->n_dense - 1];
+  if (dim <= 0) dim = full;
+  if (dim > full) return -6;
+  for (i64 i = 0; i < M; i++)
+    if (ids[i] < 0 || ids[i] >= m->vocab) return -7;
+  std::vector<int32_t> positions(T);
+  for (int t = 0; t < T; t++) positions[t] = t;
+  const int w = m->radius + 1;                       // config.go:331-335
+  const bool use_window = m->radius > 0 && T > w;    // embed.go:268-271
+
+  const float sq = (float)std::sqrt((double)d);
+  std::vector<float> x((size_t)M * d);
+#pragma omp parallel for schedule(static)
+  for (i64 r = 0; r < M; r++) {
+    const float* e = &m->embed[(size_t)ids[r] * d];
+    for (int i = 0; i < d; i++) x[(size_t)r * d + i] = e[i] * sq;
+  }
+  // per-layer inputs (embed.go:274-279)
+  std::vector<float> pl((size_t)M * NL * P), ple((size_t)M * NL * P);
+  orc_gemm(M, NL * P, d, x.data(), d, m->pleProj.data(), NL * P, pl.data(), NL * P, nullptr, nullptr, 0, nullptr, 0,
+           nullptr, 0);
+  const float inv_sqrt_d = (float)(1 / std::sqrt((double)d));
+#pragma omp parallel for schedule(static)
+  for (i64 i = 0; i < M * NL * P; i++) pl[i] = pl[i] * inv_sqrt_d;
+  orc_rmsnorm(pl.data(), m->pleNorm.data(), eps, M * NL, P, ple.data());
+
+  std::vector<float> padm((size_t)B * T), winm, mask_sl;
+  orc_padding_mask(lengths, B, T, padm.data());
+  if (use_window) {
+    winm.resize((size_t)T * T);
+    orc_window_mask(T, w, winm.data());
+    mask_sl.resize((size_t)B * T * T);
+    for (int b = 0; b < B; b++)
+      for (int i = 0; i < T; i++)
+        for (int j = 0; j < T; j++)
+          mask_sl[((size_t)b * T + i) * T + j] = padm[(size_t)b * T + j] + winm[(size_t)i * T + j];
+  }
+  std::vector<float> ss(M), sc(M), o0((size_t)M * d), o((size_t)M * d), up((size_t)M * F), gu((size_t)M * F);
+  std::vector<float> pleL((size_t)M * P), g((size_t)M * P), cs, sn, tmp;
+  for (int l = 0; l < NL; l++) {
+    const Orc2Layer& Y = m->L[l];
+    const int D = Y.D, Hkv = Y.Hkv, half = D / 2;
+    std::vector<float> q0((size_t)M * H * D), k0((size_t)M * Hkv * D), v0((size_t)M * Hkv * D);
+    std::vector<float> q((size_t)M * H * D), k((size_t)M * Hkv * D), v((size_t)M * Hkv * D);
+    std::vector<float> qr((size_t)M * H * D), kr((size_t)M * Hkv * D), vc((size_t)M * Hkv * D);
+    std::vector<float> att((size_t)M * H * D), attc((size_t)M * H * D), ones(D, 1.0f);
+    orc_row_sum_squares(x.data(), M, d, d, ss.data());
+    orc_rms_scale(ss.data(), M, d, eps, sc.data());
+    orc_gemm(M, H * D, d, x.data(), d, Y.wq.data(), H * D, q0.data(), H * D, nullptr, sc.data(), 0, nullptr, 0, nullptr, 0);
+    orc_gemm(M, Hkv * D, d, x.data(), d, Y.wk.data(), Hkv * D, k0.data(), Hkv * D, nullptr, sc.data(), 0, nullptr, 0, nullptr, 0);
+    orc_gemm(M, Hkv * D, d, x.data(), d, Y.wv.data(), Hkv * D, v0.data(), Hkv * D, nullptr, sc.data(), 0, nullptr, 0, nullptr, 0);
+    orc_rmsnorm(q0.data(), Y.qNorm.data(), eps, M * H, D, q.data());
+    orc_rmsnorm(k0.data(), Y.kNorm.data(), eps, M * Hkv, D, k.data());
+    orc_rmsnorm(v0.data(), ones.data(), eps, M * Hkv, D, v.data());  // v_norm: no weight (model.go:189)
+    const double base = Y.sliding ? (m->rope_local != 0 ? m->rope_local : 10000.0)
+                                  : (m->rope_theta != 0 ? m->rope_theta : 10000.0);  // config.go:346-351
+    rope_tables(base, positions.data(), T, D, cs, sn);
+#pragma omp parallel for schedule(static)
+    for (i64 r = 0; r < M; r++) {
+      const int b = (int)(r / T), t = (int)(r % T);
+      for (int h = 0; h < H; h++)
+        rope_row(&q[((size_t)r * H + h) * D], &qr[(((size_t)b * H + h) * T + t) * D], &cs[(size_t)t * half],
+                 &sn[(size_t)t * half], D);
+      for (int h = 0; h < Hkv; h++) {
+        rope_row(&k[((size_t)r * Hkv + h) * D], &kr[(((size_t)b * Hkv + h) * T + t) * D], &cs[(size_t)t * half],
+                 &sn[(size_t)t * half], D);
+        std::memcpy(&vc[(((size_t)b * Hkv + h) * T + t) * D], &v[((size_t)r * Hkv + h) * D], sizeof(float) * D);
+      }
+    }
+    // grouped-query attention, query head h reads key/value head h/rep,
+    // score scale 1 (model.go:105-110)
+    const bool sl = use_window && Y.sliding;
+    const int grp = H / Hkv;
+    const float* mk = sl ? mask_sl.data() : padm.data();
+    const i64 msb = sl ? (i64)T * T : T, msr = sl ? T : 0;
+    tmp.resize((size_t)B * grp * T * D);
+    for (int hk = 0; hk < Hkv; hk++) {
+      orc_attention(&qr[(size_t)hk * grp * T * D], &kr[(size_t)hk * T * D], &vc[(size_t)hk * T * D], B, grp, T, T, D,
+                    (i64)H * T * D, (i64)T * D, (i64)Hkv * T * D, 0, (i64)Hkv * T * D, 0, mk, msb, 0, msr, 1, 1.0f,
+                    tmp.data());
+      for (int b = 0; b < B; b++)
+        for (int gg = 0; gg < grp; gg++)
+          std::memcpy(&att[(((size_t)b * H + hk * grp + gg) * T) * D], &tmp[(((size_t)b * grp + gg) * T) * D],
+                      sizeof(float) * T * D);
+    }
+#pragma omp parallel for schedule(static)
+    for (i64 r = 0; r < M; r++) {
+      const int b = (int)(r / T), t = (int)(r % T);
+      for (int h = 0; h < H; h++)
+        std::memcpy(&attc[((size_t)r * H + h) * D], &att[(((size_t)b * H + h) * T + t) * D], sizeof(float) * D);
+    }
+    orc_gemm(M, d, H * D, attc.data(), H * D, Y.wo.data(), d, o0.data(), d, nullptr, nullptr, 0, nullptr, 0, nullptr, 0);
+    orc_rmsnorm(o0.data(), Y.postAttnNorm.data(), eps, M, d, o.data());
+#pragma omp parallel for schedule(static)
+    for (i64 i = 0; i < M * d; i++) x[i] = x[i] + o[i];
+    // feed-forward (embed.go:344-357)
+    orc_row_sum_squares(x.data(), M, d, d, ss.data());
+    orc_rms_scale(ss.data(), M, d, eps, sc.data());
+    orc_gemm(M, F, d, x.data(), d, Y.wup.data(), F, up.data(), F, nullptr, sc.data(), 0, nullptr, 0, nullptr, 0);
+    orc_gemm(M, F, d, x.data(), d, Y.wgate.data(), F, gu.data(), F, nullptr, sc.data(), ORC_ACT_GELU, up.data(), F,
+             nullptr, 0);
+    orc_gemm(M, d, F, gu.data(), F, Y.wdown.data(), d, o0.data(), d, nullptr, nullptr, 0, nullptr, 0, nullptr, 0);
+    orc_rmsnorm(o0.data(), Y.postFFNNorm.data(), eps, M, d, o.data());
+#pragma omp parallel for schedule(static)
+    for (i64 i = 0; i < M * d; i++) x[i] = x[i] + o[i];
+    // per-layer-input block and layer scalar (embed.go:359-371)
+#pragma omp parallel for schedule(static)
+    for (i64 r = 0; r < M; r++) std::memcpy(&pleL[(size_t)r * P], &ple[((size_t)r * NL + l) * P], sizeof(float) * P);
+    orc_gemm(M, P, d, x.data(), d, Y.pleGate.data(), P, g.data(), P, nullptr, nullptr, ORC_ACT_GELU, pleL.data(), P,
+             nullptr, 0);
+    orc_gemm(M, d, P, g.data(), P, Y.pleProj.data(), d, o0.data(), d, nullptr, nullptr, 0, nullptr, 0, nullptr, 0);
+    orc_rmsnorm(o0.data(), Y.plePostNorm.data(), eps, M, d, o.data());
+#pragma omp parallel for schedule(static)
+    for (i64 i = 0; i < M * d; i++) {
+      const float x4 = x[i] + o[i];
+      x[i] = x4 * Y.scalar;
+    }
+  }
+  std::vector<float> h((size_t)M * d);
+  orc_rmsnorm(x.data(), m->norm.data(), eps, M, d, h.data());
+  if (hidden_out) std::memcpy(hidden_out, h.data(), sizeof(float) * h.size());
+  std::vector<float> pooled((size_t)B * d, 0.f);
+  for (int b = 0; b < B; b++) {
+    int n = lengths[b];
+    if (n == 0) n = 1;
+    float* dst = &pooled[(size_t)b * d];
+    for (int t = 0; t < n; t++) {
+      const float* row = &h[((size_t)b * T + t) * d];
+      for (int i = 0; i < d; i++) dst[i] += row[i];
+    }
+    const float inv = 1.f / (float)n;
+    for (int i = 0; i < d; i++) dst[i] *= inv;
+  }
+  std::vector<float> y((size_t)B * m->E), y2;
+  orc_gemm(B, m->E, d, pooled.data(), d, m->embProj.data(), m->E, y.data(), m->E, nullptr, nullptr, 0, nullptr, 0,
+           nullptr, 0);
+  int cur = m->E;
+  for (int i = 0; i < m->n_dense; i++) {
+    const int no = m->dense_out[i];
+    y2.assign((size_t)B * no, 0.f);
+    orc_gemm(B, no, cur, y.data(), cur, m->dense[i].data(), no, y2.data(), no, nullptr, nullptr, 0, nullptr, 0, nullptr,
+             0);
+    y.swap(y2);
+    cur = no;
+  }
+  for (int b = 0; b < B; b++) {
+    const float* yr = &y[(size_t)b * cur];
+    std::vector<float> sq2(dim);
+    for (int i = 0; i < dim; i++) sq2[i] = yr[i] * yr[i];
+    const float s = orc_sumf(sq2.data(), dim);
+    const float nrm = std::sqrt(s + 1e-12f);
+    for (int i = 0; i < dim; i++) out[(size_t)b * dim + i] = yr[i] / nrm;
+  }
+  return 0;
+}

@@ -36,6 +36,11 @@ _SIGS = {
     "orc_model_finalize": (C.c_int, [vp]),
     "orc_model_embed": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
     "orc_num_threads": (C.c_int, []),
+    "orc_model2_create": (vp, [C.c_int] * 8 + [f64, f64, f32, vp, vp, vp, C.c_int, vp]),
+    "orc_model2_destroy": (None, [vp]),
+    "orc_model2_set": (C.c_int, [vp, C.c_char_p, vp, i64]),
+    "orc_model2_finalize": (C.c_int, [vp]),
+    "orc_model2_embed": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
     "orc_pcg_uint64s": (None, [vp, i64, vp]),
     "orc_pcg_intns": (None, [vp, C.c_uint64, i64, vp]),
     "orc_pcg_float64s": (None, [vp, i64, vp]),
@@ -285,6 +290,59 @@ class OracleModel:
     def close(self):
         if self.h:
             lib().orc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class OracleModel2:
+    """The oracle's EmbeddingGemma 2 text tower (fp32 weights; pre-norm gains
+    folded as the reference does)."""
+
+    def __init__(self, shape):
+        s = shape
+        L = s.num_hidden_layers
+        self._hd = np.array([s.layer_head_dim(l) for l in range(L)], np.int32)
+        self._kv = np.array([s.layer_kv_heads(l) for l in range(L)], np.int32)
+        self._sl = np.array([1 if s.sliding(l) else 0 for l in range(L)], np.int32)
+        self._do = np.array(list(s.dense_out) + [0] * (4 - len(s.dense_out)), np.int32)
+        self.h = lib().orc_model2_create(s.hidden_size, L, s.num_attention_heads, s.intermediate_size, s.vocab_size,
+                                         s.sliding_window, s.hidden_size_per_layer_input, s.embedding_dim,
+                                         s.rope_local_base_freq, s.rope_theta, s.rms_norm_eps, P(self._hd),
+                                         P(self._kv), P(self._sl), len(s.dense_out), P(self._do))
+        assert self.h
+        self.shape = shape
+
+    def set(self, name, data):
+        a = f32c(data)
+        rc = lib().orc_model2_set(self.h, name.encode(), P(a), a.size)
+        if rc != 0:
+            raise ValueError(f"oracle set {name}: {rc}")
+
+    def finalize(self):
+        rc = lib().orc_model2_finalize(self.h)
+        if rc != 0:
+            raise ValueError(f"oracle finalize: {rc}")
+
+    def embed(self, ids, lengths, dim=0, hidden=False):
+        ids = np.ascontiguousarray(ids, np.int32); lengths = np.ascontiguousarray(lengths, np.int32)
+        B, T = ids.shape
+        full = self.shape.dense_out[-1] if self.shape.dense_out else self.shape.embedding_dim
+        d = full if dim == 0 else dim
+        out = np.empty((B, d), np.float32)
+        hid = np.empty((B, T, self.shape.hidden_size), np.float32) if hidden else None
+        rc = lib().orc_model2_embed(self.h, P(ids), P(lengths), B, T, d, P(out), P(hid))
+        if rc != 0:
+            raise ValueError(f"oracle embed: {rc}")
+        return (out, hid) if hidden else out
+
+    def close(self):
+        if self.h:
+            lib().orc_model2_destroy(self.h)
             self.h = None
 
     def __del__(self):
