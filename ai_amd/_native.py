@@ -22,7 +22,7 @@ FA_DT_F32, FA_DT_BF16 = 0, 1
 FA_ACT_NONE, FA_ACT_RELU, FA_ACT_GELU = 0, 1, 2
 FA_B_KN, FA_B_NK = 0, 1
 KERNEL_KINDS = ["gemm_qkv", "gemm_o", "gemm_gateup", "gemm_down", "gemm_head", "attention", "qknorm_rope",
-                "residual_norm", "gather", "pool_l2"]
+                "residual_norm", "gather", "pool_l2", "gemm_ple", "ple_norm"]
 
 i32, i64, f32, f64, vp = C.c_int32, C.c_int64, C.c_float, C.c_double, C.c_void_p
 P_f32 = C.POINTER(C.c_float)
@@ -49,7 +49,9 @@ class GemmaConfig(C.Structure):
                 ("num_key_value_heads", i32), ("head_dim", i32), ("intermediate_size", i32), ("vocab_size", i32),
                 ("sliding_window", i32), ("use_bidirectional", i32), ("sliding_window_pattern", i32),
                 ("rope_local_base_freq", f64), ("rope_theta", f64), ("query_pre_attn_scalar", f64),
-                ("rms_norm_eps", f32), ("max_tokens", i32), ("n_dense", i32), ("dense_out", i32 * 4)]
+                ("rms_norm_eps", f32), ("max_tokens", i32), ("n_dense", i32), ("dense_out", i32 * 4),
+                ("variant", i32), ("hidden_size_per_layer_input", i32), ("embedding_dim", i32),
+                ("layer_head_dim", i32 * 64), ("layer_kv_heads", i32 * 64), ("layer_sliding", i32 * 64)]
 
 
 _SIGS = {

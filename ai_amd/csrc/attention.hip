@@ -2,7 +2,7 @@
 //
 // attention_varlen_kernel (the model path): packed variable-length
 // sequences, grouped-query heads (every query head h reads key/value head
-// h / (H/Hkv)), head_dim 256, optional sliding window |i-j| < window, padding
+// h / (H/Hkv)), head_dim 256 or 512, optional sliding window |i-j| < window, padding
 // implied by the packing (a sequence's keys are exactly its valid tokens).
 // Computes softmax(scale * q.k^T) . v with an online softmax over key tiles,
 // never materialising scores or masks. Masked keys get weight exactly 0, and
@@ -50,7 +50,6 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int AD = 256;                  // head_dim
 constexpr int QW = 16;                   // queries per wave pair
 constexpr int QBLK = 2 * QW;             // queries per work item (two pairs)
 constexpr int KT = 16;                   // keys per tile
@@ -67,17 +66,15 @@ struct VarlenParams {
 };
 
 // ---- the model path's kernel ------------------------------------------------
-constexpr int DS_HALF = AD / 2;  // head dimensions per wave
-
-// Direct-to-LDS tile loads: each K or V row of a tile (256
-// floats, 1 KB) is one global_load_lds_dwordx4 of a wave (64 lanes x 16
-// bytes, LDS address = row base + 16 * lane), into two LDS buffers. A row's
-// 16-byte chunk c is stored at position c ^ (row & 15) (lane i loads global
-// chunk i ^ (row & 15)), so the score reads (16 rows, one chunk each) and
-// the V reads (4 rows x 4 chunks) hit distinct banks. Keys past the range
-// load the last valid row (finite values; their weights are 0).
+// Direct-to-LDS tile loads: each 1 KB of a K or V row of a tile (256
+// floats; a row is 1 KB at head_dim 256, 2 KB at 512) is one
+// global_load_lds_dwordx4 of a wave (64 lanes x 16 bytes, LDS address =
+// base + 16 * lane), into two LDS buffers. A row's 16-byte chunk c is stored
+// at position c ^ (row & 15) (the XOR stays within each 1 KB part), so the
+// score reads (16 rows, one chunk each) and the V reads (4 rows x 4 chunks)
+// hit distinct banks. Keys past the range load the last valid row (finite
+// values; their weights are 0).
 constexpr int DL_NT = 256;
-constexpr int DL_ROWF = AD;  // floats per LDS row (unpadded)
 
 __device__ __forceinline__ int dl_pos(int row, int chunk) { return chunk ^ (row & 15); }
 
@@ -93,13 +90,16 @@ __device__ __forceinline__ void dl_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+template <int HD>
 __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p) {
+  constexpr int HALF = HD / 2;  // head dimensions per wave
+  constexpr int ROWF = HD;      // floats per LDS row (unpadded)
   // separate objects per buffer, so the compiler can tell the tile being
   // read from the one being loaded and need not wait for the loads
-  __shared__ __attribute__((aligned(16))) float K0[KT * DL_ROWF];
-  __shared__ __attribute__((aligned(16))) float V0[KT * DL_ROWF];
-  __shared__ __attribute__((aligned(16))) float K1[KT * DL_ROWF];
-  __shared__ __attribute__((aligned(16))) float V1[KT * DL_ROWF];
+  __shared__ __attribute__((aligned(16))) float K0[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float V0[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float K1[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float V1[KT * ROWF];
   __shared__ __attribute__((aligned(16))) float Sx[4][64 * 4];
 
   const int tid = threadIdx.x;
@@ -115,27 +115,27 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   const int hk = h / (p.H / p.Hkv);
   const int start = p.cu[seq];
   const int L = p.cu[seq + 1] - start;
-  const int W = (p.H + 2 * p.Hkv) * AD;
-  const int dofs = half * DS_HALF;
-  const float* qbase = p.qkv + (int64_t)start * W + (int64_t)h * AD + dofs;
-  const float* kbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + hk) * AD;
-  const float* vbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + p.Hkv + hk) * AD;
+  const int W = (p.H + 2 * p.Hkv) * HD;
+  const int dofs = half * HALF;
+  const float* qbase = p.qkv + (int64_t)start * W + (int64_t)h * HD + dofs;
+  const float* kbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + hk) * HD;
+  const float* vbase = p.qkv + (int64_t)start * W + (int64_t)(p.H + p.Hkv + hk) * HD;
 
   const int qw0 = q0 + qb * QW;
   const int qi = qw0 + lq;
   const bool qvalid = qi < L;
-  f32x4 qreg[DS_HALF / 16];
+  f32x4 qreg[HALF / 16];
   {
     const float* qr = qbase + (int64_t)(qvalid ? qi : 0) * W;
 #pragma unroll
-    for (int sg = 0; sg < DS_HALF / 16; sg++) {
+    for (int sg = 0; sg < HALF / 16; sg++) {
       f32x4 v = *reinterpret_cast<const f32x4*>(qr + sg * 16 + g * 4);
       qreg[sg] = qvalid ? v : f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  f32x4 oacc[DS_HALF / 16];
+  f32x4 oacc[HALF / 16];
 #pragma unroll
-  for (int db = 0; db < DS_HALF / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < HALF / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig;
   float l_part = 0.f;
 
@@ -146,17 +146,23 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
     kend = min(L, qlast + p.window);
   }
 
-  // wave w loads rows w, w+4, w+8, w+12 of K and of V
+  // wave w loads rows w, w+4, w+8, w+12 of K and of V, 1 KB (64 lanes x 16
+  // bytes) per instruction
   auto issue_tile = [&](int k0, float* Kb, float* Vb) {
 #pragma unroll
     for (int j = 0; j < KT / 4; j++) {
       const int r = wave + 4 * j;
       const int64_t key = min(k0 + r, kend - 1);
-      const int chunk = dl_pos(r, lane);  // the global chunk that lands at position `lane`
-      __builtin_amdgcn_global_load_lds(kbase + key * W + chunk * 4,
-                                       (__attribute__((address_space(3))) void*)&Kb[r * DL_ROWF], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + key * W + chunk * 4,
-                                       (__attribute__((address_space(3))) void*)&Vb[r * DL_ROWF], 16, 0, 0);
+#pragma unroll
+      for (int part = 0; part < HD / 256; part++) {
+        const int chunk = dl_pos(r, part * 64 + lane);  // the global chunk that lands at this position
+        __builtin_amdgcn_global_load_lds(kbase + key * W + chunk * 4,
+                                         (__attribute__((address_space(3))) void*)&Kb[r * ROWF + part * 256], 16, 0,
+                                         0);
+        __builtin_amdgcn_global_load_lds(vbase + key * W + chunk * 4,
+                                         (__attribute__((address_space(3))) void*)&Vb[r * ROWF + part * 256], 16, 0,
+                                         0);
+      }
     }
   };
   if (kbeg < kend) issue_tile(kbeg, K0, V0);
@@ -169,14 +175,14 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
 
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
     {
-      const float* krow = &Kc[lq * DL_ROWF];
+      const float* krow = &Kc[lq * ROWF];
       auto kfrag = [&](int sg) {
         return *reinterpret_cast<const f32x4*>(krow + dl_pos(lq, (dofs + sg * 16 + g * 4) >> 2) * 4);
       };
       f32x4 a = kfrag(0);  // operands of step sg+1 are read while step sg computes
 #pragma unroll
-      for (int sg = 0; sg < DS_HALF / 16; sg++) {
-        const f32x4 an = sg + 1 < DS_HALF / 16 ? kfrag(sg + 1) : a;
+      for (int sg = 0; sg < HALF / 16; sg++) {
+        const f32x4 an = sg + 1 < HALF / 16 ? kfrag(sg + 1) : a;
 #pragma unroll
         for (int c = 0; c < 4; c++) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc, 0, 0, 0);
         a = an;
@@ -220,16 +226,16 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
     for (int r = 0; r < 4; r++) {
       const float ar = __shfl(alpha, 4 * g + r, 64);
 #pragma unroll
-      for (int db = 0; db < DS_HALF / 16; db++) oacc[db][r] *= ar;
+      for (int db = 0; db < HALF / 16; db++) oacc[db][r] *= ar;
     }
 #pragma unroll
-    for (int db = 0; db < DS_HALF / 16; db++) {
+    for (int db = 0; db < HALF / 16; db++) {
       const int f = dofs + db * 16 + lq;
       f32x4 b;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const int row = 4 * g + c;
-        b[c] = Vc[row * DL_ROWF + dl_pos(row, f >> 2) * 4 + (f & 3)];
+        b[c] = Vc[row * ROWF + dl_pos(row, f >> 2) * 4 + (f & 3)];
       }
 #pragma unroll
       for (int c = 0; c < 4; c++) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sacc[c], b[c], oacc[db], 0, 0, 0);
@@ -242,15 +248,15 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
 
   float l_tot = l_part + __shfl_xor(l_part, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
-  const int OW = p.H * AD;
+  const int OW = p.H * HD;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int qr = qw0 + 4 * g + r;
     const float inv = 1.f / __shfl(l_tot, 4 * g + r, 64);
     if (qr < L) {
-      float* orow = p.out + (int64_t)(start + qr) * OW + (int64_t)h * AD + dofs;
+      float* orow = p.out + (int64_t)(start + qr) * OW + (int64_t)h * HD + dofs;
 #pragma unroll
-      for (int db = 0; db < DS_HALF / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
+      for (int db = 0; db < HALF / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
     }
   }
 }
@@ -324,14 +330,18 @@ __global__ __launch_bounds__(256) void attention_generic_kernel(AttnGenericArgs 
 
 int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const int32_t* d_items, int32_t n_items,
                                   hipStream_t s) {
-  if (a.D != AD) return set_error(ctx, FA_ERR_UNSUPPORTED, "attention: head_dim %d != 256", a.D);
+  if (a.D != 256 && a.D != 512)
+    return set_error(ctx, FA_ERR_UNSUPPORTED, "attention: head_dim %d not 256 or 512", a.D);
   if (a.Hkv <= 0 || a.H % a.Hkv != 0)
     return set_error(ctx, FA_ERR_ARG, "attention: %d query heads not a multiple of %d kv heads", a.H, a.Hkv);
   if (n_items == 0) return FA_OK;
   VarlenParams p;
   p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
-  hipLaunchKernelGGL(attention_varlen_kernel, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
+  if (a.D == 256)
+    hipLaunchKernelGGL(attention_varlen_kernel<256>, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
+  else
+    hipLaunchKernelGGL(attention_varlen_kernel<512>, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

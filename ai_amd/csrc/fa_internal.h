@@ -153,16 +153,22 @@ int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_
 
 // q/k RMSNorm with (1+g) and RoPE on the packed qkv buffer [rows x (H+2*Hkv)*D],
 // in place; positions from d_pos.
+// With norm_v, the Hkv value heads are RMS-normalised too (unit gain, no
+// rotation). D is 256 or 512.
 int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t Hkv, int32_t D, const float* gq,
                        const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
-                       hipStream_t s);
+                       hipStream_t s, bool norm_v = false);
 
-// x += RMSNorm(o; g_post); then xn = RMSNorm(x; g_next) (g_next may be null:
-// then xn is not written).
+// pl [rows, nl*P] in place: each P-wide piece becomes RMSNorm(pl * scale; g).
+int launch_ple_norm(fa_ctx* ctx, float* pl, int64_t rows, int32_t nl, int32_t P, float scale, const float* g,
+                    float eps, hipStream_t s);
+
+// x = (x + RMSNorm(o; g_post)) * scale; then xn = RMSNorm(x; g_next)
+// (g_next may be null: then xn is not written).
 // o2 (optional): second partial product of a K-split GEMM, added to o.
 int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
                          const float* g_post, const float* g_next, float eps, hipStream_t s,
-                         const float* o2 = nullptr);
+                         const float* o2 = nullptr, float scale = 1.f);
 
 // Fused varlen attention over packed tokens. qkv [rows x (H+2Hkv)*D]; out
 // [rows x H*D]; cu_seqlens [nseq+1]; window: keys with |i-j| >= window are

@@ -5,6 +5,12 @@
 //   down GEMM, post-norm+residual(+next pre-norm)] -> mean pool -> Dense head
 //   -> L2
 // following models/gemma/embed.go:160-240,381-475 and model.go:76-232.
+// Variant 2 (EmbeddingGemma 2, embed.go:247-377) adds per-layer head dims
+// and key/value heads, the v norm, the per-layer inputs (one projection of
+// the scaled embeddings, normalised per layer), each layer's
+// per-layer-input block (gate GEMM with GELU and the layer's input in the
+// epilogue, projection GEMM, post-norm + residual, times the layer scalar)
+// and the embedding projection of the pooled vector.
 //
 // Layout in HBM (M = sum of valid lengths; padding rows are never stored):
 //   x   [M, d] fp32   residual stream
@@ -40,12 +46,20 @@ bool bf16_exact(float f, uint16_t* out) {
 }
 
 struct Layer {
+  int D = 0, Hkv = 0, width = 0;  // head dim, key/value heads, q|k|v width (H+2Hkv)*D
+  bool sliding = true;
+  const float *cos_t = nullptr, *sin_t = nullptr;  // RoPE tables of this layer's base and D
   uint16_t* wqkv = nullptr;   // [(H+2Hkv)*D, d]
   uint16_t* wo = nullptr;     // [d, H*D]
   uint16_t* wgu = nullptr;    // [2F, d], 32-row groups gate/up alternating
   uint16_t* wdown = nullptr;  // [d, F]
   float *g_in = nullptr, *g_post_attn = nullptr, *g_pre_ffn = nullptr, *g_post_ffn = nullptr;
   float *g_q = nullptr, *g_k = nullptr;
+  // variant 2: per-layer-input block and layer scalar
+  uint16_t* wple_gate = nullptr;  // [P, d]
+  uint16_t* wple_proj = nullptr;  // [d, P]
+  float* g_ple_post = nullptr;
+  float scalar = 1.f;
 };
 
 struct KernelStat {
@@ -65,7 +79,12 @@ struct PendingEvent {
 struct fa_model {
   fa_ctx* ctx = nullptr;
   fa_gemma_config cfg{};
-  int width_qkv = 0;
+  int variant = 0;
+  int max_width = 0, max_hd = 0;  // widest q|k|v row, widest attention output H*D
+  int P = 0, E = 0;               // variant 2: per-layer input width, embedding projection width
+  uint16_t* wple_model = nullptr; // variant 2: [layers*P, d]
+  float* g_ple_norm = nullptr;    // variant 2: [P]
+  uint16_t* wemb_proj = nullptr;  // variant 2: [E, d]
   std::vector<void*> allocations;
   uint16_t* embed = nullptr;
   std::vector<fa::Layer> layers;
@@ -73,6 +92,7 @@ struct fa_model {
   std::vector<uint16_t*> dense;
   std::vector<int> dense_in, dense_out;
   float *cos_local = nullptr, *sin_local = nullptr, *cos_global = nullptr, *sin_global = nullptr;
+  int d_local = 0, d_global = 0;  // head dims of the sliding and the full layers
   std::set<std::string> seen;
   bool finalized = false;
   // workspace
@@ -179,26 +199,55 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
   if (c.hidden_size <= 0 || c.num_hidden_layers <= 0 || c.num_attention_heads <= 0 || c.num_key_value_heads <= 0 ||
       c.head_dim <= 0 || c.intermediate_size <= 0 || c.vocab_size <= 0)
     return set_error(ctx, FA_ERR_ARG, "gemma: config sizes must be positive");
+  if (c.variant != 0 && c.variant != 2) return set_error(ctx, FA_ERR_ARG, "gemma: variant %d not 0 or 2", c.variant);
+  const bool v2 = c.variant == 2;
   if (c.hidden_size % 256 != 0 || c.hidden_size > 1024)
     return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden_size %d not in {256,512,768,1024}", c.hidden_size);
-  if (c.head_dim != 256) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d != 256", c.head_dim);
-  if (c.num_attention_heads % c.num_key_value_heads != 0)
-    return set_error(ctx, FA_ERR_ARG, "gemma: %d heads not a multiple of %d kv heads", c.num_attention_heads,
-                     c.num_key_value_heads);
+  if (c.num_hidden_layers > FA_GEMMA_MAX_LAYERS)
+    return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: %d layers, at most %d", c.num_hidden_layers, FA_GEMMA_MAX_LAYERS);
+  if (!v2 && c.head_dim != 256) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d != 256", c.head_dim);
   if (c.intermediate_size % 32 != 0)
     return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: intermediate_size %d not a multiple of 32", c.intermediate_size);
   if (c.n_dense < 0 || c.n_dense > 4) return set_error(ctx, FA_ERR_ARG, "gemma: n_dense %d outside 0..4", c.n_dense);
   if (c.max_tokens <= 0) return set_error(ctx, FA_ERR_ARG, "gemma: max_tokens must be positive");
-  if (c.query_pre_attn_scalar <= 0) return set_error(ctx, FA_ERR_ARG, "gemma: query_pre_attn_scalar must be > 0");
+  if (!v2 && c.query_pre_attn_scalar <= 0) return set_error(ctx, FA_ERR_ARG, "gemma: query_pre_attn_scalar must be > 0");
+  if (v2 && (c.hidden_size_per_layer_input <= 0 || c.hidden_size_per_layer_input % 32 != 0))
+    return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden_size_per_layer_input %d not a positive multiple of 32",
+                     c.hidden_size_per_layer_input);
+  if (v2 && c.embedding_dim <= 0) return set_error(ctx, FA_ERR_ARG, "gemma: embedding_dim must be positive");
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   fa_model* m = new fa_model();
   m->ctx = ctx;
   m->cfg = c;
+  m->variant = c.variant;
   if (m->cfg.sliding_window_pattern <= 0) m->cfg.sliding_window_pattern = 6;
-  const int d = c.hidden_size, H = c.num_attention_heads, Hkv = c.num_key_value_heads, D = c.head_dim,
-            F = c.intermediate_size;
-  m->width_qkv = (H + 2 * Hkv) * D;
+  const int d = c.hidden_size, H = c.num_attention_heads, F = c.intermediate_size, NL = c.num_hidden_layers;
+  m->layers.resize(NL);
   int rc = FA_OK;
+  for (int l = 0; l < NL && !rc; l++) {
+    fa::Layer& L = m->layers[l];
+    L.D = v2 && c.layer_head_dim[l] > 0 ? c.layer_head_dim[l] : c.head_dim;
+    L.Hkv = v2 && c.layer_kv_heads[l] > 0 ? c.layer_kv_heads[l] : c.num_key_value_heads;
+    L.sliding = v2 ? c.layer_sliding[l] != 0 : (l + 1) % m->cfg.sliding_window_pattern != 0;  // config.go:213-225
+    L.width = (H + 2 * L.Hkv) * L.D;
+    int& dt = L.sliding ? m->d_local : m->d_global;
+    if (L.D != 256 && L.D != 512)
+      rc = set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: layer %d head_dim %d not 256 or 512", l, L.D);
+    else if (H % L.Hkv != 0)
+      rc = set_error(ctx, FA_ERR_ARG, "gemma: layer %d: %d heads not a multiple of %d kv heads", l, H, L.Hkv);
+    else if (dt != 0 && dt != L.D)
+      rc = set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: layer %d head_dim %d differs from other %s layers' %d", l, L.D,
+                     L.sliding ? "sliding" : "full-attention", dt);
+    dt = L.D;
+    m->max_width = std::max(m->max_width, L.width);
+    m->max_hd = std::max(m->max_hd, H * L.D);
+  }
+  if (rc) {
+    delete m;
+    return rc;
+  }
+  m->P = v2 ? c.hidden_size_per_layer_input : 0;
+  m->E = v2 ? c.embedding_dim : 0;
   void* p;
   auto A = [&](size_t bytes) -> void* {
     if (rc) return nullptr;
@@ -206,21 +255,30 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     return rc ? nullptr : p;
   };
   m->embed = (uint16_t*)A((size_t)c.vocab_size * d * 2);
-  m->layers.resize(c.num_hidden_layers);
   for (auto& L : m->layers) {
-    L.wqkv = (uint16_t*)A((size_t)m->width_qkv * d * 2);
-    L.wo = (uint16_t*)A((size_t)d * H * D * 2);
+    L.wqkv = (uint16_t*)A((size_t)L.width * d * 2);
+    L.wo = (uint16_t*)A((size_t)d * H * L.D * 2);
     L.wgu = (uint16_t*)A((size_t)2 * F * d * 2);
     L.wdown = (uint16_t*)A((size_t)d * F * 2);
     L.g_in = (float*)A(d * 4);
     L.g_post_attn = (float*)A(d * 4);
     L.g_pre_ffn = (float*)A(d * 4);
     L.g_post_ffn = (float*)A(d * 4);
-    L.g_q = (float*)A(D * 4);
-    L.g_k = (float*)A(D * 4);
+    L.g_q = (float*)A(L.D * 4);
+    L.g_k = (float*)A(L.D * 4);
+    if (v2) {
+      L.wple_gate = (uint16_t*)A((size_t)m->P * d * 2);
+      L.wple_proj = (uint16_t*)A((size_t)d * m->P * 2);
+      L.g_ple_post = (float*)A(d * 4);
+    }
   }
   m->g_final = (float*)A(d * 4);
-  int in = d;
+  if (v2) {
+    m->wple_model = (uint16_t*)A((size_t)NL * m->P * d * 2);
+    m->g_ple_norm = (float*)A(m->P * 4);
+    m->wemb_proj = (uint16_t*)A((size_t)m->E * d * 2);
+  }
+  int in = v2 ? m->E : d;
   for (int i = 0; i < c.n_dense; i++) {
     if (c.dense_out[i] <= 0) rc = set_error(ctx, FA_ERR_ARG, "gemma: dense_out[%d] = %d", i, c.dense_out[i]);
     m->dense_in.push_back(in);
@@ -228,11 +286,20 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     m->dense.push_back((uint16_t*)A((size_t)in * c.dense_out[i] * 2));
     in = c.dense_out[i];
   }
-  const size_t tab = (size_t)c.max_tokens * (D / 2) * 4;
-  m->cos_local = (float*)A(tab);
-  m->sin_local = (float*)A(tab);
-  m->cos_global = (float*)A(tab);
-  m->sin_global = (float*)A(tab);
+  if (m->d_local) {
+    const size_t tab = (size_t)c.max_tokens * (m->d_local / 2) * 4;
+    m->cos_local = (float*)A(tab);
+    m->sin_local = (float*)A(tab);
+  }
+  if (m->d_global) {
+    const size_t tab = (size_t)c.max_tokens * (m->d_global / 2) * 4;
+    m->cos_global = (float*)A(tab);
+    m->sin_global = (float*)A(tab);
+  }
+  for (auto& L : m->layers) {
+    L.cos_t = L.sliding ? m->cos_local : m->cos_global;
+    L.sin_t = L.sliding ? m->sin_local : m->sin_global;
+  }
   if (!rc && hipEventCreateWithFlags(&m->plan_done, hipEventDisableTiming) != hipSuccess)
     rc = set_error(ctx, FA_ERR_HIP, "hipEventCreate failed");
   if (rc) {
@@ -269,8 +336,8 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
   if (dtype != FA_DT_F32 && dtype != FA_DT_BF16) return set_error(ctx, FA_ERR_ARG, "gemma: weight %s: dtype %d", name, dtype);
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   const fa_gemma_config& c = m->cfg;
-  const int d = c.hidden_size, H = c.num_attention_heads, Hkv = c.num_key_value_heads, D = c.head_dim,
-            F = c.intermediate_size;
+  const bool v2 = m->variant == 2;
+  const int d = c.hidden_size, H = c.num_attention_heads, F = c.intermediate_size, P = m->P;
   const std::string s(name);
   auto shape_is = [&](std::initializer_list<int64_t> want) {
     if ((size_t)ndim != want.size()) return false;
@@ -321,7 +388,7 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
       } else {
         w = ((const float*)data)[i];
       }
-      v[i] = w + 1.0f;  // Gemma's (1 + w) (model.go:131-140)
+      v[i] = v2 ? w : w + 1.0f;  // Gemma 3's (1 + w); EmbeddingGemma 2 uses w itself (model.go:128-140)
     }
     FA_HIP_CHECK(ctx, hipMemcpy(dst, v.data(), n * 4, hipMemcpyHostToDevice));
     return FA_OK;
@@ -335,6 +402,16 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
   } else if (s == "norm.weight") {
     if (!shape_is({d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
     rc = put_norm(m->g_final, d);
+  } else if (v2 && s == "ple.per_layer_model_projection.weight") {
+    if (!shape_is({(int64_t)c.num_hidden_layers * P, d}))
+      return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+    rc = put_matrix(m->wple_model, (int64_t)c.num_hidden_layers * P, d, identity);
+  } else if (v2 && s == "ple.per_layer_projection_norm.weight") {
+    if (!shape_is({P})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+    rc = put_norm(m->g_ple_norm, P);
+  } else if (v2 && s == "embedding_projection.weight") {
+    if (!shape_is({m->E, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+    rc = put_matrix(m->wemb_proj, m->E, d, identity);
   } else if (s.rfind("dense.", 0) == 0 && s.size() > 6) {
     char* end = nullptr;
     long i = std::strtol(s.c_str() + 6, &end, 10);
@@ -345,6 +422,7 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
     rc = put_matrix(m->dense[i], m->dense_out[i], m->dense_in[i], identity);
   } else if (fa::parse_layer(s, c.num_hidden_layers, &l, &rest) == 0) {
     fa::Layer& L = m->layers[l];
+    const int D = L.D, Hkv = L.Hkv;
     if (rest == "input_layernorm.weight" || rest == "post_attention_layernorm.weight" ||
         rest == "pre_feedforward_layernorm.weight" || rest == "post_feedforward_layernorm.weight") {
       if (!shape_is({d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
@@ -372,6 +450,24 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
     } else if (rest == "mlp.down_proj.weight") {
       if (!shape_is({d, F})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
       rc = put_matrix(L.wdown, d, F, identity);
+    } else if (v2 && rest == "ple_block.per_layer_input_gate.weight") {
+      if (!shape_is({P, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wple_gate, P, d, identity);
+    } else if (v2 && rest == "ple_block.per_layer_projection.weight") {
+      if (!shape_is({d, P})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_matrix(L.wple_proj, d, P, identity);
+    } else if (v2 && rest == "ple_block.post_per_layer_input_norm.weight") {
+      if (!shape_is({d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      rc = put_norm(L.g_ple_post, d);
+    } else if (v2 && rest == "layer_scalar") {
+      // one value (model.go:183-188); the checkpoint stores it with shape [1]
+      if (!(shape_is({1}) || ndim == 0)) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
+      if (dtype == FA_DT_BF16) {
+        const uint32_t u = (uint32_t)((const uint16_t*)data)[0] << 16;
+        std::memcpy(&L.scalar, &u, 4);
+      } else {
+        L.scalar = ((const float*)data)[0];
+      }
     } else {
       return set_error(ctx, FA_ERR_ARG, "gemma: weight \"%s\" not found", name);
     }
@@ -388,7 +484,8 @@ int fa_gemma_finalize(fa_model* m) {
   if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
   fa_ctx* ctx = m->ctx;
   const fa_gemma_config& c = m->cfg;
-  const size_t expected = 2 + (size_t)c.n_dense + 13 * (size_t)c.num_hidden_layers;
+  const size_t expected = m->variant == 2 ? 5 + (size_t)c.n_dense + 17 * (size_t)c.num_hidden_layers
+                                          : 2 + (size_t)c.n_dense + 13 * (size_t)c.num_hidden_layers;
   if (m->seen.size() != expected)
     return set_error(ctx, FA_ERR_STATE, "gemma: %zu of %zu weights set", m->seen.size(), expected);
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
@@ -397,12 +494,16 @@ int fa_gemma_finalize(fa_model* m) {
   std::vector<float> cs, sn;
   const double local = c.rope_local_base_freq != 0 ? c.rope_local_base_freq : 10000.0;
   const double global = c.rope_theta != 0 ? c.rope_theta : 10000.0;
-  fa::rope_tables_host(local, pos.data(), c.max_tokens, c.head_dim, cs, sn);
-  FA_HIP_CHECK(ctx, hipMemcpy(m->cos_local, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-  FA_HIP_CHECK(ctx, hipMemcpy(m->sin_local, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-  fa::rope_tables_host(global, pos.data(), c.max_tokens, c.head_dim, cs, sn);
-  FA_HIP_CHECK(ctx, hipMemcpy(m->cos_global, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-  FA_HIP_CHECK(ctx, hipMemcpy(m->sin_global, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  if (m->d_local) {
+    fa::rope_tables_host(local, pos.data(), c.max_tokens, m->d_local, cs, sn);
+    FA_HIP_CHECK(ctx, hipMemcpy(m->cos_local, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    FA_HIP_CHECK(ctx, hipMemcpy(m->sin_local, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  }
+  if (m->d_global) {
+    fa::rope_tables_host(global, pos.data(), c.max_tokens, m->d_global, cs, sn);
+    FA_HIP_CHECK(ctx, hipMemcpy(m->cos_global, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    FA_HIP_CHECK(ctx, hipMemcpy(m->sin_global, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  }
   m->finalized = true;
   return FA_OK;
 }
@@ -417,9 +518,10 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   if (B == 0) return FA_OK;
   if (!d_ids || !lengths || !d_out) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
   if (T > c.max_tokens) return set_error(ctx, FA_ERR_ARG, "gemma: T=%d exceeds max_tokens %d", T, c.max_tokens);
-  const int d = c.hidden_size, H = c.num_attention_heads, Hkv = c.num_key_value_heads, D = c.head_dim,
-            F = c.intermediate_size;
-  const int full = c.n_dense > 0 ? m->dense_out.back() : d;
+  const bool v2 = m->variant == 2;
+  const int d = c.hidden_size, H = c.num_attention_heads, F = c.intermediate_size, NL = c.num_hidden_layers,
+            P = m->P;
+  const int full = c.n_dense > 0 ? m->dense_out.back() : (v2 ? m->E : d);
   if (dim <= 0) dim = full;
   if (dim > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
   // ---- plan (host): cu_seqlens and attention work items ----
@@ -477,22 +579,27 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   m->plan_pending = true;
   // ---- workspace ----
   // o has room for two partial products of the K-split o/down GEMMs
+  // variant 2 adds the per-layer inputs [M, layers*P]; its [M, P] gate
+  // output reuses gu (free after the down product)
   const int ksplit = fa::gemm_ksplit();
-  const int64_t ncols = 2LL * d + m->width_qkv + (int64_t)H * D + (int64_t)ksplit * d + F;
-  const int maxw = std::max(d, std::max(full, c.n_dense > 0 ? *std::max_element(m->dense_out.begin(), m->dense_out.end()) : d));
+  const int64_t ncols = 2LL * d + m->max_width + m->max_hd + (int64_t)ksplit * d + std::max(F, P) +
+                        (v2 ? (int64_t)NL * P : 0);
+  int maxw = std::max(d, std::max(full, v2 ? m->E : d));
+  for (int o : m->dense_out) maxw = std::max(maxw, o);
   const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw)) * 4 + 4096;
   if ((rc = m->ws.ensure(ctx, ws_bytes))) return rc;
   float* x = m->ws.as<float>();
   float* xn = x + M * d;
   float* qkv = xn + M * d;
-  float* att = qkv + M * m->width_qkv;
-  float* o = att + M * H * D;
+  float* att = qkv + M * m->max_width;
+  float* o = att + M * m->max_hd;
   float* gu = o + (int64_t)ksplit * M * d;
+  float* ple = gu + M * std::max(F, P);
   // per product: split only when K divides into whole 32-wide slabs
-  const int ks_o = (H * D) % (32 * ksplit) == 0 ? ksplit : 1, ks_down = F % (32 * ksplit) == 0 ? ksplit : 1;
-  const float* o2_o = ks_o > 1 ? o + M * d : nullptr;
+  const int ks_down = F % (32 * ksplit) == 0 ? ksplit : 1, ks_ple = P % (32 * ksplit) == 0 ? ksplit : 1;
   const float* o2_down = ks_down > 1 ? o + M * d : nullptr;
-  float* pooled = gu + M * F;
+  const float* o2_ple = ks_ple > 1 ? o + M * d : nullptr;
+  float* pooled = ple + (v2 ? M * NL * P : 0);
   float* hbuf0 = pooled + (size_t)B * d;
   float* hbuf1 = hbuf0 + (size_t)B * maxw;
   hipStream_t s = ctx->stream;
@@ -500,8 +607,10 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   if ((rc = fa::launch_row_plan(ctx, cu_d, B, T, M, row_src_d, pos_d, s))) return rc;
   const float eps = c.rms_norm_eps;
   const float emb_scale = (float)std::sqrt((double)d);  // embed.go:176
-  const float att_scale = (float)(1.0 / std::sqrt(c.query_pre_attn_scalar));  // model.go:100
-  const int wbound = c.use_bidirectional ? c.sliding_window / 2 + 1 : c.sliding_window;  // config.go:331-339
+  // model.go:100; variant 2 does not scale the scores (model.go:105-110)
+  const float att_scale = v2 ? 1.f : (float)(1.0 / std::sqrt(c.query_pre_attn_scalar));
+  // window bound (config.go:331-339): variant 2 reads an inclusive radius
+  const int wbound = v2 ? c.sliding_window + 1 : c.use_bidirectional ? c.sliding_window / 2 + 1 : c.sliding_window;
   {
     fa::Probe pr(m, FA_K_GATHER, 0, (double)M * (2.0 * d + 8.0 * d + 4));
     if ((rc = fa::launch_embed_gather(ctx, d_ids, row_src_d, m->embed, c.vocab_size, M, d, emb_scale,
@@ -509,21 +618,37 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       return rc;
     pr.done();
   }
-  for (int l = 0; l < c.num_hidden_layers; l++) {
-    const fa::Layer& L = m->layers[l];
-    const bool sliding = (l + 1) % m->cfg.sliding_window_pattern != 0;  // config.go:213-225
+  if (v2) {
+    // per-layer inputs: RMSNorm(x0 . W_ple^T * hidden^-1/2) per layer (embed.go:274-279)
     {
       fa::GemmArgs g;
-      g.m = M; g.n = m->width_qkv; g.k = d; g.a = xn; g.lda = d; g.b = L.wqkv; g.ldb = d; g.c = qkv; g.ldc = m->width_qkv;
-      fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * M * m->width_qkv * d, 0);
+      g.m = M; g.n = (int64_t)NL * P; g.k = d; g.a = x; g.lda = d; g.b = m->wple_model; g.ldb = d; g.c = ple;
+      g.ldc = (int64_t)NL * P;
+      fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * M * NL * P * d, 0);
+      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      pr.done();
+    }
+    fa::Probe pr(m, FA_K_PLE_NORM, 0, (double)M * NL * P * 8.0);
+    if ((rc = fa::launch_ple_norm(ctx, ple, M, NL, P, (float)(1 / std::sqrt((double)d)), m->g_ple_norm, eps, s)))
+      return rc;
+    pr.done();
+  }
+  for (int l = 0; l < NL; l++) {
+    const fa::Layer& L = m->layers[l];
+    const int D = L.D, Hkv = L.Hkv;
+    const bool sliding = L.sliding;
+    const int ks_o = (H * D) % (32 * ksplit) == 0 ? ksplit : 1;
+    const float* o2_o = ks_o > 1 ? o + M * d : nullptr;
+    {
+      fa::GemmArgs g;
+      g.m = M; g.n = L.width; g.k = d; g.a = xn; g.lda = d; g.b = L.wqkv; g.ldb = d; g.c = qkv; g.ldc = L.width;
+      fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * M * L.width * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
       pr.done();
     }
     {
-      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)M * (H + Hkv) * D * 8.0);
-      if ((rc = fa::launch_qknorm_rope(ctx, qkv, M, H, Hkv, D, L.g_q, L.g_k, eps, pos_d,
-                                       sliding ? m->cos_local : m->cos_global, sliding ? m->sin_local : m->sin_global,
-                                       s)))
+      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)M * (H + (v2 ? 2 : 1) * Hkv) * D * 8.0);
+      if ((rc = fa::launch_qknorm_rope(ctx, qkv, M, H, Hkv, D, L.g_q, L.g_k, eps, pos_d, L.cos_t, L.sin_t, s, v2)))
         return rc;
       pr.done();
     }
@@ -575,11 +700,36 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
       pr.done();
     }
+    // the last layer's "next norm" is the final RMSNorm (embed.go:237): xn = h
+    const float* g_next = (l + 1 < NL) ? m->layers[l + 1].g_in : m->g_final;
     {
-      // the last layer's "next norm" is the final RMSNorm (embed.go:237): xn = h
-      const float* g_next = (l + 1 < c.num_hidden_layers) ? m->layers[l + 1].g_in : m->g_final;
+      // variant 2: the per-layer-input block reads x itself, so no norm here
       fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
-      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_ffn, g_next, eps, s, o2_down))) return rc;
+      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_ffn, v2 ? nullptr : g_next, eps, s, o2_down)))
+        return rc;
+      pr.done();
+    }
+    if (v2) {
+      // x = (x + RMSNorm(gelu(x . Wg^T) * ple_l . Wp^T; g)) * scalar (embed.go:359-371)
+      {
+        fa::GemmArgs g;
+        g.m = M; g.n = P; g.k = d; g.a = x; g.lda = d; g.b = L.wple_gate; g.ldb = d; g.c = gu; g.ldc = P;
+        g.epi = fa::Epi::Generic; g.act = FA_ACT_GELU; g.mul = ple + (int64_t)l * P; g.ldm = (int64_t)NL * P;
+        fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * M * P * d, 0);
+        if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+        pr.done();
+      }
+      {
+        fa::GemmArgs g;
+        g.m = M; g.n = d; g.k = P; g.a = gu; g.lda = P; g.b = L.wple_proj; g.ldb = P; g.c = o; g.ldc = d;
+        g.ksplit = ks_ple; g.c_split = M * d;
+        fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * M * d * P, 0);
+        if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+        pr.done();
+      }
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
+      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_ple_post, g_next, eps, s, o2_ple, L.scalar)))
+        return rc;
       pr.done();
     }
   }
@@ -591,14 +741,25 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   const float* cur = pooled;
   int cur_w = d;
   float* bufs[2] = {hbuf0, hbuf1};
+  int nb = 0;
+  if (v2) {  // the embedding projection, applied to the pooled vector (embed.go:408-414)
+    fa::GemmArgs g;
+    g.m = B; g.n = m->E; g.k = d; g.a = pooled; g.lda = d; g.b = m->wemb_proj; g.ldb = d; g.c = bufs[0]; g.ldc = m->E;
+    fa::Probe pr(m, FA_K_GEMM_HEAD, 2.0 * B * m->E * d, 0);
+    if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+    pr.done();
+    cur = bufs[0];
+    cur_w = m->E;
+    nb = 1;
+  }
   for (int i = 0; i < c.n_dense; i++) {
     fa::GemmArgs g;
     g.m = B; g.n = m->dense_out[i]; g.k = cur_w; g.a = cur; g.lda = cur_w; g.b = m->dense[i]; g.ldb = cur_w;
-    g.c = bufs[i & 1]; g.ldc = m->dense_out[i];
+    g.c = bufs[(i + nb) & 1]; g.ldc = m->dense_out[i];
     fa::Probe pr(m, FA_K_GEMM_HEAD, 2.0 * B * m->dense_out[i] * cur_w, 0);
     if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
     pr.done();
-    cur = bufs[i & 1];
+    cur = bufs[(i + nb) & 1];
     cur_w = m->dense_out[i];
   }
   {
@@ -617,7 +778,7 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
   if (B == 0) return FA_OK;
   if (!ids || !lengths || !out) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
   const fa_gemma_config& c = m->cfg;
-  const int full = c.n_dense > 0 ? m->dense_out.back() : c.hidden_size;
+  const int full = c.n_dense > 0 ? m->dense_out.back() : (m->variant == 2 ? m->E : c.hidden_size);
   const int dd = dim <= 0 ? full : dim;
   // validate ids on the host: an out-of-range id would read outside the table
   for (int b = 0; b < B; b++) {

@@ -49,6 +49,25 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   for (int64_t i = lane; i < n; i += kWave) o[i] = r[i] * inv * g[i];
 }
 
+// EmbeddingGemma 2's per-layer inputs (embed.go:274-279): pl [rows, nl*P]
+// in place, each P-wide piece v = pl * s normalised as RMSNorm(v; g). One
+// wave per (row, layer).
+__global__ __launch_bounds__(256) void ple_norm_kernel(float* __restrict__ pl, int64_t pieces, int P, float sc,
+                                                       const float* __restrict__ g, float eps) {
+  const int64_t piece = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (piece >= pieces) return;
+  float* r = pl + piece * P;
+  float s = 0.f;
+  for (int i = lane; i < P; i += kWave) {
+    const float v = r[i] * sc;
+    s = fmaf(v, v, s);
+  }
+  s = wave_sum(s);
+  const float inv = rms_inv(s, P, eps);
+  for (int i = lane; i < P; i += kWave) r[i] = r[i] * sc * inv * g[i];
+}
+
 // ---- RoPE (generic) -------------------------------------------------------------
 // One thread per rotated pair (row, i < D/2); tables are [T, D/2].
 __global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, const float* __restrict__ cs,
@@ -120,14 +139,16 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* __rest
   }
 }
 
-// x += RMSNorm(o; g_post); xn = RMSNorm(x; g_next) when g_next != null.
-// With o2 != null, o is the sum of two partial products o + o2 (in that
-// order) of a K-split GEMM.
+// x = (x + RMSNorm(o; g_post)) * scale; xn = RMSNorm(x; g_next) when
+// g_next != null. With o2 != null, o is the sum of two partial products
+// o + o2 (in that order) of a K-split GEMM. scale is EmbeddingGemma 2's
+// layer scalar after its per-layer-input block (embed.go:367-370), else 1.
 template <int NC>
 __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ o, const float* __restrict__ o2,
                                                             float* __restrict__ x, float* __restrict__ xn,
                                                             int64_t rows, const float* __restrict__ g_post,
-                                                            const float* __restrict__ g_next, float eps) {
+                                                            const float* __restrict__ g_next, float eps,
+                                                            float scale) {
   constexpr int d = NC * 256;
   int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   int lane = threadIdx.x & 63;
@@ -155,6 +176,9 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
     xv[c].y = xv[c].y + ov[c].y * inv * gg.y;
     xv[c].z = xv[c].z + ov[c].z * inv * gg.z;
     xv[c].w = xv[c].w + ov[c].w * inv * gg.w;
+    if (scale != 1.f) {
+      xv[c].x = xv[c].x * scale; xv[c].y = xv[c].y * scale; xv[c].z = xv[c].z * scale; xv[c].w = xv[c].w * scale;
+    }
     *reinterpret_cast<f32x4*>(x + row * d + col) = xv[c];
   }
   if (g_next == nullptr) return;
@@ -169,44 +193,78 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
   }
 }
 
-// Per (token, head): RMSNorm over D=256 with (1+g), then rotate-half RoPE at
-// the token's position. One wavefront holds the head's 256 values (4 per
-// lane); the rotation partner of element i (< 128) is i+128, held by lane+32.
-// Block = one token: waves 0..H-1 are the query heads, H..H+Hkv-1 the keys.
+// Per (token, head): RMSNorm over D (256 or 512) with the head's gain vector
+// (the encoder's stored 1+w, or EmbeddingGemma 2's weight as is), then
+// rotate-half RoPE at the token's position; with norm_v, the value heads get
+// the same RMSNorm with a unit gain and no rotation (EmbeddingGemma 2's
+// v_norm, models/gemma/model.go:189). One wavefront holds a head's values,
+// 4 per lane per 256: at D=256 the rotation partner of element i (< 128) is
+// i+128, held by lane+32; at D=512 the partner of i (< 256) is i+256, held
+// by the same lane. Block = one token: waves 0..H-1 are the query heads,
+// H..H+Hkv-1 the keys, then the values.
+template <int D>
 __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qkv, int64_t rows, int H, int Hkv,
                                                           const float* __restrict__ gq, const float* __restrict__ gk,
                                                           float eps, const int32_t* __restrict__ pos,
-                                                          const float* __restrict__ cs, const float* __restrict__ sn) {
-  constexpr int D = 256, half = 128;
+                                                          const float* __restrict__ cs, const float* __restrict__ sn,
+                                                          int norm_v) {
+  constexpr int NQ = D / 256, half = D / 2;
   const int64_t row = blockIdx.x;
   const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= rows || head >= H + Hkv) return;
+  if (row >= rows || head >= H + Hkv + (norm_v ? Hkv : 0)) return;
   const int width = (H + 2 * Hkv) * D;
   float* p = qkv + row * width + (int64_t)head * D;
-  const float* g = head < H ? gq : gk;
-  f32x4 v = *reinterpret_cast<const f32x4*>(p + lane * 4);
-  float s = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
-  s = wave_sum(s);
-  const float inv = rms_inv(s, D, eps);
-  f32x4 gg = *reinterpret_cast<const f32x4*>(g + lane * 4);
-  v.x = v.x * inv * gg.x; v.y = v.y * inv * gg.y; v.z = v.z * inv * gg.z; v.w = v.w * inv * gg.w;
-  f32x4 w;
-  w.x = __shfl_xor(v.x, 32, 64); w.y = __shfl_xor(v.y, 32, 64);
-  w.z = __shfl_xor(v.z, 32, 64); w.w = __shfl_xor(v.w, 32, 64);
-  const int t = pos[row];
-  const int i0 = (lane & 31) * 4;
-  f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
-  f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
-  f32x4 r;
-  if (lane < 32) {  // y_i = x_i c - x_{i+h} s
-    r.x = v.x * c.x - w.x * sv.x; r.y = v.y * c.y - w.y * sv.y;
-    r.z = v.z * c.z - w.z * sv.z; r.w = v.w * c.w - w.w * sv.w;
-  } else {  // y_{i+h} = x_i s + x_{i+h} c
-    r.x = w.x * sv.x + v.x * c.x; r.y = w.y * sv.y + v.y * c.y;
-    r.z = w.z * sv.z + v.z * c.z; r.w = w.w * sv.w + v.w * c.w;
+  f32x4 v[NQ];
+#pragma unroll
+  for (int c = 0; c < NQ; c++) v[c] = *reinterpret_cast<const f32x4*>(p + c * 256 + lane * 4);
+  const float inv = rms_inv(sumsq<NQ>(v), D, eps);
+  if (head >= H + Hkv) {  // value head: unit gain, no rotation
+#pragma unroll
+    for (int c = 0; c < NQ; c++) {
+      f32x4 r;
+      r.x = v[c].x * inv; r.y = v[c].y * inv; r.z = v[c].z * inv; r.w = v[c].w * inv;
+      *reinterpret_cast<f32x4*>(p + c * 256 + lane * 4) = r;
+    }
+    return;
   }
-  *reinterpret_cast<f32x4*>(p + lane * 4) = r;
+  const float* g = head < H ? gq : gk;
+#pragma unroll
+  for (int c = 0; c < NQ; c++) {
+    const f32x4 gg = *reinterpret_cast<const f32x4*>(g + c * 256 + lane * 4);
+    v[c].x = v[c].x * inv * gg.x; v[c].y = v[c].y * inv * gg.y;
+    v[c].z = v[c].z * inv * gg.z; v[c].w = v[c].w * inv * gg.w;
+  }
+  const int t = pos[row];
+  if constexpr (D == 256) {
+    f32x4 w;
+    w.x = __shfl_xor(v[0].x, 32, 64); w.y = __shfl_xor(v[0].y, 32, 64);
+    w.z = __shfl_xor(v[0].z, 32, 64); w.w = __shfl_xor(v[0].w, 32, 64);
+    const int i0 = (lane & 31) * 4;
+    const f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
+    const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
+    f32x4 r;
+    if (lane < 32) {  // y_i = x_i c - x_{i+h} s
+      r.x = v[0].x * c.x - w.x * sv.x; r.y = v[0].y * c.y - w.y * sv.y;
+      r.z = v[0].z * c.z - w.z * sv.z; r.w = v[0].w * c.w - w.w * sv.w;
+    } else {  // y_{i+h} = x_i s + x_{i+h} c
+      r.x = w.x * sv.x + v[0].x * c.x; r.y = w.y * sv.y + v[0].y * c.y;
+      r.z = w.z * sv.z + v[0].z * c.z; r.w = w.w * sv.w + v[0].w * c.w;
+    }
+    *reinterpret_cast<f32x4*>(p + lane * 4) = r;
+  } else {
+    const int i0 = lane * 4;
+    const f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
+    const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
+    const f32x4 x0 = v[0], x1 = v[1];
+    f32x4 r0, r1;
+    r0.x = x0.x * c.x - x1.x * sv.x; r0.y = x0.y * c.y - x1.y * sv.y;
+    r0.z = x0.z * c.z - x1.z * sv.z; r0.w = x0.w * c.w - x1.w * sv.w;
+    r1.x = x0.x * sv.x + x1.x * c.x; r1.y = x0.y * sv.y + x1.y * c.y;
+    r1.z = x0.z * sv.z + x1.z * c.z; r1.w = x0.w * sv.w + x1.w * c.w;
+    *reinterpret_cast<f32x4*>(p + lane * 4) = r0;
+    *reinterpret_cast<f32x4*>(p + 256 + lane * 4) = r1;
+  }
 }
 
 // pooled[b, c] = (sum over the sequence's rows of h[., c]) * (1/L_b). A
@@ -288,6 +346,15 @@ int launch_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64
   return FA_OK;
 }
 
+int launch_ple_norm(fa_ctx* ctx, float* pl, int64_t rows, int32_t nl, int32_t P, float scale, const float* g,
+                    float eps, hipStream_t s) {
+  const int64_t pieces = rows * nl;
+  if (pieces == 0 || P == 0) return FA_OK;
+  hipLaunchKernelGGL(ple_norm_kernel, dim3(blocks_for(pieces, 4)), dim3(256), 0, s, pl, pieces, P, scale, g, eps);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
 int launch_rope(fa_ctx* ctx, const float* x, const float* cos_t, const float* sin_t, int64_t rows, int32_t T,
                 int32_t D, float* out, hipStream_t s) {
   int64_t work = rows * (D / 2);
@@ -314,14 +381,15 @@ int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_
 }
 
 int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
-                         const float* g_post, const float* g_next, float eps, hipStream_t s, const float* o2) {
+                         const float* g_post, const float* g_next, float eps, hipStream_t s, const float* o2,
+                         float scale) {
   if (rows == 0) return FA_OK;
   dim3 grid(blocks_for(rows, 4)), block(256);
   switch (d) {
-    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
-    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
-    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
-    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps); break;
+    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
     default: return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden size %d not in {256,512,768,1024}", d);
   }
   FA_CHECK_LAUNCH(ctx);
@@ -330,11 +398,17 @@ int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64
 
 int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t Hkv, int32_t D, const float* gq,
                        const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
-                       hipStream_t s) {
-  if (D != 256) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d != 256", D);
+                       hipStream_t s, bool norm_v) {
+  if (D != 256 && D != 512) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d not 256 or 512", D);
   if (rows == 0) return FA_OK;
-  dim3 grid((unsigned)rows, (unsigned)((H + Hkv + 3) / 4)), block(256);
-  hipLaunchKernelGGL(qknorm_rope_kernel, grid, block, 0, s, qkv, rows, H, Hkv, gq, gk, eps, d_pos, cos_t, sin_t);
+  const int heads = H + Hkv + (norm_v ? Hkv : 0);
+  dim3 grid((unsigned)rows, (unsigned)((heads + 3) / 4)), block(256);
+  if (D == 256)
+    hipLaunchKernelGGL(qknorm_rope_kernel<256>, grid, block, 0, s, qkv, rows, H, Hkv, gq, gk, eps, d_pos, cos_t,
+                       sin_t, norm_v ? 1 : 0);
+  else
+    hipLaunchKernelGGL(qknorm_rope_kernel<512>, grid, block, 0, s, qkv, rows, H, Hkv, gq, gk, eps, d_pos, cos_t,
+                       sin_t, norm_v ? 1 : 0);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

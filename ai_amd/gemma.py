@@ -21,7 +21,9 @@ class GemmaError(RuntimeError):
     """The error value gemma's functions return (the reference returns error)."""
 
 
-def _config_struct(shape: S.ModelShape) -> N.GemmaConfig:
+def _config_struct(shape) -> N.GemmaConfig:
+    if isinstance(shape, S.ModelShape2):
+        return _config_struct2(shape)
     c = N.GemmaConfig()
     for f in ("hidden_size", "num_hidden_layers", "num_attention_heads", "num_key_value_heads", "head_dim",
               "intermediate_size", "vocab_size", "sliding_window", "use_bidirectional", "sliding_window_pattern",
@@ -37,8 +39,30 @@ def _config_struct(shape: S.ModelShape) -> N.GemmaConfig:
     return c
 
 
+def _config_struct2(s: S.ModelShape2) -> N.GemmaConfig:
+    """EmbeddingGemma 2 (variant 2) geometry, per layer."""
+    c = N.GemmaConfig()
+    for f in ("hidden_size", "num_hidden_layers", "num_attention_heads", "num_key_value_heads", "head_dim",
+              "intermediate_size", "vocab_size", "sliding_window", "max_tokens", "hidden_size_per_layer_input",
+              "embedding_dim"):
+        setattr(c, f, int(getattr(s, f)))
+    c.variant = 2
+    c.rope_local_base_freq = float(s.rope_local_base_freq)
+    c.rope_theta = float(s.rope_theta)
+    c.query_pre_attn_scalar = 1.0
+    c.rms_norm_eps = float(s.rms_norm_eps)
+    c.n_dense = len(s.dense_out)
+    for i, o in enumerate(s.dense_out):
+        c.dense_out[i] = int(o)
+    for l in range(s.num_hidden_layers):
+        c.layer_head_dim[l] = s.layer_head_dim(l)
+        c.layer_kv_heads[l] = s.layer_kv_heads(l)
+        c.layer_sliding[l] = 1 if s.sliding(l) else 0
+    return c
+
+
 class Model:
-    def __init__(self, shape: S.ModelShape | None = None, ctx: N.Context | None = None):
+    def __init__(self, shape=None, ctx: N.Context | None = None):
         self.shape = shape or S.ModelShape()
         self.ctx = ctx or N.Context(0)
         self._cfg = _config_struct(self.shape)
@@ -63,7 +87,11 @@ class Model:
 
     def Dim(self) -> int:
         """Width of the embeddings (model.go:336-343)."""
-        return int(self.shape.dense_out[-1]) if self.shape.dense_out else int(self.shape.hidden_size)
+        if self.shape.dense_out:
+            return int(self.shape.dense_out[-1])
+        if isinstance(self.shape, S.ModelShape2):
+            return int(self.shape.embedding_dim)
+        return int(self.shape.hidden_size)
 
     def set_weight(self, name: str, data: np.ndarray) -> None:
         a = np.ascontiguousarray(data)
@@ -80,7 +108,8 @@ class Model:
 
     def load_synthetic(self, seed: int = S.WEIGHT_SEED) -> None:
         """Random-init weights of the benchmark configuration, tensor by tensor."""
-        for name, shp, kind in S.weight_specs(self.shape):
+        specs = S.weight_specs2(self.shape) if isinstance(self.shape, S.ModelShape2) else S.weight_specs(self.shape)
+        for name, shp, kind in specs:
             self.set_weight(name, S.make_weight(name, shp, kind, seed))
         self.finalize()
 

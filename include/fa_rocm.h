@@ -190,6 +190,8 @@ int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int
 
 /* ---- the EmbeddingGemma model (models/gemma) ------------------------- */
 
+#define FA_GEMMA_MAX_LAYERS 64
+
 /* Hyper-parameters as read from config.json by gemma.LoadConfig
  * (models/gemma/config.go:19-58,153-227), Variant 0 (Gemma 3 text encoder),
  * plus the sentence-transformers head (model.go:236-310). */
@@ -211,6 +213,20 @@ typedef struct fa_gemma_config {
   int32_t max_tokens;             /* 2048 (model.go:102-104) */
   int32_t n_dense;                /* head Dense layers (2: 768->3072->768), identity activation */
   int32_t dense_out[4];
+  /* EmbeddingGemma 2 text tower (variant 2; models/gemma/config.go:247-297,
+   * model.go:105-205, embed.go:247-377); all zero for the Gemma 3 encoder.
+   * Variant 2 reads sliding_window as an inclusive radius (a sliding layer
+   * attends while |i-j| <= sliding_window, config.go:331-335), scores are
+   * not scaled (query_pre_attn_scalar unused, model.go:105-110), RMSNorm
+   * weights multiply the normalised value as stored (no 1 + w,
+   * model.go:128-140), v is RMS-normalised without a weight, and sliding
+   * layers use rope_local_base_freq, full layers rope_theta. */
+  int32_t variant;                     /* 0: Gemma 3 encoder; 2: EmbeddingGemma 2 */
+  int32_t hidden_size_per_layer_input; /* P: width of each layer's per-layer input */
+  int32_t embedding_dim;               /* output of embedding_projection (the pooled vector's projection) */
+  int32_t layer_head_dim[FA_GEMMA_MAX_LAYERS];  /* per layer; 0 = head_dim */
+  int32_t layer_kv_heads[FA_GEMMA_MAX_LAYERS];  /* per layer; 0 = num_key_value_heads */
+  int32_t layer_sliding[FA_GEMMA_MAX_LAYERS];   /* variant 2: 1 sliding window, 0 full attention */
 } fa_gemma_config;
 
 /* Create an empty model on ctx (no weights yet). Replaces the allocation
@@ -266,7 +282,9 @@ enum {
   FA_K_RESIDUAL_NORM = 7,
   FA_K_GATHER = 8,
   FA_K_POOL_L2 = 9,
-  FA_K_COUNT = 10
+  FA_K_GEMM_PLE = 10,  /* EmbeddingGemma 2: per-layer input projection, gate and projection products */
+  FA_K_PLE_NORM = 11,  /* EmbeddingGemma 2: per-layer input RMSNorm */
+  FA_K_COUNT = 12
 };
 int fa_gemma_set_profiling(fa_model* m, int enabled);
 /* Accumulated launches, milliseconds, flops and bytes (algorithmic) for one

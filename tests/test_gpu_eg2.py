@@ -1,0 +1,115 @@
+"""EmbeddingGemma 2 text tower on the GPU (fa_gemma_* with variant 2).
+
+* Against the golden vectors of transformers' Gemma4TextModel
+  (tests/golden/eg2_tiny.npz; 6 layers, full layer 5 with head_dim 512 and
+  one key/value head, sliding radius 8 at T = 20): embeddings cosine >=
+  0.99999, max |d| <= 1e-4.
+* Against the CPU oracle (orc_model2_*, pinned by tests/test_eg2_golden.py)
+  at the reference's EmbeddingGemma 2 widths (TestConfig2: hidden 512, 4
+  heads, 2 key/value heads, head_dim 256 / 512 on full layers, per-layer
+  input 512, embedding 768) with sequences longer than a small sliding
+  radius, several batch shapes and Matryoshka Dim: cosine >= 0.9999.
+* Batch invariance: a sequence's embedding does not depend on its batch.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from ai_amd import gemma as G
+from ai_amd import synth as S
+from test_eg2_golden import load as load_golden
+
+pytestmark = pytest.mark.gpu
+
+
+def cos_rows(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+
+
+def gpu_model(shape, ws, ctx):
+    gm = G.Model(shape, ctx)
+    for name, shp, kind in S.weight_specs2(shape):
+        gm.set_weight(name, S.f32_to_bf16(ws[name]) if kind == "m" else ws[name])
+    gm.finalize()
+    return gm
+
+
+def test_gpu_matches_transformers_golden(ctx):
+    shape, ws, ids, lengths, hidden, emb, meta = load_golden()
+    gm = gpu_model(shape, ws, ctx)
+    got = gm.embed_ids(ids, lengths)
+    gm.close()
+    c = cos_rows(got, emb)
+    print(f"GPU vs {meta['source']}: cosine min {c.min():.9f}, max|d| {np.abs(got - emb).max():.3g}", flush=True)
+    assert c.min() >= 0.99999
+    assert np.abs(got - emb).max() <= 1e-4
+
+
+def eg2_shape(**kw):
+    base = dict(num_hidden_layers=6, vocab_size=4096, sliding_window=48, max_tokens=512)
+    base.update(kw)
+    return S.ModelShape2(**base)
+
+
+def weights(shape, seed):
+    ws = {}
+    for name, shp, kind in S.weight_specs2(shape):
+        w = S.make_weight(name, shp, kind, seed, 0.03, 0.2)
+        ws[name] = S.bf16_to_f32(w) if kind == "m" else w
+    return ws
+
+
+def batch(seed, B, T, lo, vocab):
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(lo, T + 1, B).astype(np.int32)
+    lengths[0] = T
+    ids = rng.integers(3, vocab, (B, T)).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(T)[None, :] >= lengths[:, None]] = 0
+    return ids, lengths
+
+
+@pytest.fixture(scope="module")
+def eg2(ctx):
+    shape = eg2_shape()
+    ws = weights(shape, 31)
+    om = O.OracleModel2(shape)
+    for k, v in ws.items():
+        om.set(k, v)
+    om.finalize()
+    gm = gpu_model(shape, ws, ctx)
+    yield shape, om, gm
+    gm.close()
+    om.close()
+
+
+@pytest.mark.parametrize("B,T,lo", [(4, 200, 20), (1, 97, 97), (9, 64, 1)])
+def test_gpu_matches_oracle(eg2, B, T, lo):
+    shape, om, gm = eg2
+    ids, lengths = batch(B * 1000 + T, B, T, lo, shape.vocab_size)
+    print(f"EG2 B={B} T={T} lengths {lengths.tolist()}", flush=True)
+    got = gm.embed_ids(ids, lengths)
+    want = om.embed(ids, lengths)
+    c = cos_rows(got, want)
+    print(f"cosine min {c.min():.8f}, max|d| {np.abs(got - want).max():.3g}", flush=True)
+    assert got.shape == (B, shape.embedding_dim)
+    assert c.min() >= 0.9999
+    assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
+
+
+def test_gpu_dim_and_batch_invariance(eg2):
+    shape, om, gm = eg2
+    ids, lengths = batch(5, 6, 120, 10, shape.vocab_size)
+    full = gm.embed_ids(ids, lengths)
+    d64 = gm.embed_ids(ids, lengths, dim=64)
+    want = full[:, :64].astype(np.float64)
+    want /= np.linalg.norm(want, axis=1, keepdims=True)
+    np.testing.assert_allclose(d64, want, atol=2e-6)
+    for b in (0, 3):
+        n = int(lengths[b])
+        one = gm.embed_ids(ids[b:b + 1, :n], lengths[b:b + 1])
+        assert cos_rows(one, full[b:b + 1])[0] >= 0.99999
