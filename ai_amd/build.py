@@ -84,8 +84,8 @@ def build_synth(verbose: bool = False) -> str:
 
 HOST = os.path.join(PKG, "host")
 HOST_SOURCES = ["fiber.cpp", "json.cpp", "tokenizer.cpp", "safetensors.cpp", "cluster.cpp"]
-CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer", "test_cluster"]
-CPP_CPU_TESTS = ["test_tokenizer"]  # need no GPU
+CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer", "test_cluster", "test_config"]
+CPP_CPU_TESTS = ["test_tokenizer", "test_config"]  # need no GPU
 CPP_DRIVERS = ["st_dump", "embed_dir"]  # programs the Python tests drive
 CPP_TEST_BIN = os.path.join(BUILD, "cpp_tests")
 

@@ -357,6 +357,21 @@ Model::Model(const Config& cfg) : cfg_(cfg) {
   if (cfg.Dense.size() > 4) throw Error("gemma: at most 4 Dense layers");
   c.n_dense = (int32_t)cfg.Dense.size();
   for (size_t i = 0; i < cfg.Dense.size(); i++) c.dense_out[i] = cfg.Dense[i];
+  if (cfg.Variant == 2) {
+    if (cfg.NumHiddenLayers > FA_GEMMA_MAX_LAYERS)
+      throw Error("gemma: " + std::to_string(cfg.NumHiddenLayers) + " layers; this build runs at most " +
+                  std::to_string(FA_GEMMA_MAX_LAYERS));
+    c.variant = 2;
+    c.hidden_size_per_layer_input = cfg.HiddenSizePerLayerInput;
+    c.embedding_dim = cfg.EmbeddingDim;
+    c.rope_local_base_freq = cfg.RopeBase(-1);
+    c.rope_theta = cfg.RopeBase(-2);
+    for (int l = 0; l < cfg.NumHiddenLayers; l++) {
+      c.layer_head_dim[l] = cfg.LayerHeadDim(l);
+      c.layer_kv_heads[l] = cfg.LayerKVHeads(l);
+      c.layer_sliding[l] = cfg.IsSliding(l) ? 1 : 0;
+    }
+  }
   gcheck(device(), fa_gemma_create(device(), &c, &m_));
 }
 
@@ -377,7 +392,12 @@ void Model::SetWeightF32(const std::string& name, const std::vector<int64_t>& sh
 
 void Model::Finalize() { gcheck(device(), fa_gemma_finalize(m_)); }
 
-int Model::Dim() const { return cfg_.Dense.empty() ? cfg_.HiddenSize : cfg_.Dense.back(); }
+// model.go:336-344: the embedding projection's width when there is one, else
+// the last Dense layer's, else the hidden size.
+int Model::Dim() const {
+  if (cfg_.Variant == 2) return cfg_.EmbeddingDim;
+  return cfg_.Dense.empty() ? cfg_.HiddenSize : cfg_.Dense.back();
+}
 
 std::vector<std::vector<float>> Model::EmbedIDs(const std::vector<std::vector<int32_t>>& ids, EmbedOpts o) const {
   if (!m_) throw Error("gemma: model is closed");
@@ -418,62 +438,195 @@ json::Value read_json(const std::string& path, const char* what) {
   }
 }
 
+std::string layer_key(int l) {
+  char b[16];
+  std::snprintf(b, sizeof b, "%02d", l);
+  return b;
+}
+
+const LayerOverride* override_of(const Config& c, int l) {
+  auto it = c.PerLayerConfig.find(layer_key(l));
+  if (it == c.PerLayerConfig.end()) it = c.PerLayerConfig.find(std::to_string(l));
+  return it == c.PerLayerConfig.end() ? nullptr : &it->second;
+}
+
+}  // namespace
+
+int Config::LayerHeadDim(int l) const {
+  const LayerOverride* o = override_of(*this, l);
+  return o && o->HeadDim != 0 ? o->HeadDim : HeadDim;
+}
+
+int Config::LayerKVHeads(int l) const {
+  const LayerOverride* o = override_of(*this, l);
+  return o && o->NumKeyValueHeads != 0 ? o->NumKeyValueHeads : NumKeyValueHeads;
+}
+
+bool Config::IsSliding(int l) const {
+  if (!LayerTypes.empty()) return LayerTypes[l] == "sliding_attention";
+  return (l + 1) % (SlidingWindowPattern > 0 ? SlidingWindowPattern : 6) != 0;
+}
+
+// l >= 0: that layer's base; -1 / -2: the sliding / full layers' base.
+double Config::RopeBase(int l) const {
+  const bool sliding = l == -1 || (l >= 0 && IsSliding(l));
+  if (Variant == 2) {
+    auto it = RopeThetaByType.find(sliding ? "sliding_attention" : "full_attention");
+    if (it != RopeThetaByType.end() && it->second != 0) return it->second;
+  }
+  if (sliding) return RopeLocalBaseFreq != 0 ? RopeLocalBaseFreq : 10000;
+  return RopeTheta != 0 ? RopeTheta : 10000;
+}
+
+int Config::Window() const {
+  if (Variant == 2) return SlidingWindow + 1;
+  return UseBidirectional ? SlidingWindow / 2 + 1 : SlidingWindow;
+}
+
+namespace {
+
+// The text-model fields shared by both variants (config.go:19-38).
+void read_text_fields(const json::Value& v, Config& c) {
+  c.HiddenSize = (int)v.get_int("hidden_size");
+  c.IntermediateSize = (int)v.get_int("intermediate_size");
+  c.NumHiddenLayers = (int)v.get_int("num_hidden_layers");
+  c.NumAttentionHeads = (int)v.get_int("num_attention_heads");
+  c.NumKeyValueHeads = (int)v.get_int("num_key_value_heads");
+  c.HeadDim = (int)v.get_int("head_dim");
+  c.VocabSize = (int)v.get_int("vocab_size");
+  c.SlidingWindow = (int)v.get_int("sliding_window");
+  c.UseBidirectional = v.get_bool("use_bidirectional_attention");
+  c.RopeTheta = v.get_number("rope_theta");
+  c.RopeLocalBaseFreq = v.get_number("rope_local_base_freq");
+  c.QueryPreAttnScalar = v.get_number("query_pre_attn_scalar");
+  c.RMSNormEps = (float)v.get_number("rms_norm_eps");
+  if (const json::Value* lt = v.find("layer_types"); lt && lt->is_array())
+    for (const auto& t : lt->items()) c.LayerTypes.push_back(t.as_string());
+  const std::string act = v.get_string("hidden_activation");
+  if (!act.empty() && act != "gelu_pytorch_tanh")
+    throw Error("gemma: activation \"" + act + "\" not supported (want gelu_pytorch_tanh)");
+  if (const json::Value* rs = v.find("rope_scaling"); rs && !rs->is_null())
+    throw Error("gemma: rope_scaling is set; not supported");
+}
+
+// fillVariant2 (config.go:247-297): EmbeddingGemma 2's defaults and checks.
+void fill_variant2(const json::Value& t, Config& c) {
+  c.HiddenSizePerLayerInput = (int)t.get_int("hidden_size_per_layer_input");
+  c.EmbeddingDim = (int)t.get_int("embedding_dim");
+  if (c.LayerTypes.empty())
+    for (int i = 0; i < c.NumHiddenLayers; i++)
+      c.LayerTypes.push_back((i + 1) % 6 == 0 ? "full_attention" : "sliding_attention");
+  if (const json::Value* pc = t.find("per_layer_config"); pc && pc->is_object()) {
+    for (const auto& kv : pc->members())
+      c.PerLayerConfig[kv.first] = LayerOverride{(int)kv.second.get_int("head_dim"),
+                                                 (int)kv.second.get_int("num_key_value_heads")};
+  } else {
+    for (int i = 0; i < (int)c.LayerTypes.size(); i++)
+      if (c.LayerTypes[i] == "full_attention") c.PerLayerConfig[layer_key(i)] = LayerOverride{512, 1};
+  }
+  if (const json::Value* rp = t.find("rope_parameters"); rp && rp->is_object()) {
+    for (const auto& kv : rp->members()) {
+      const std::string type = kv.second.get_string("rope_type");
+      if (!type.empty() && type != "default")
+        throw Error("gemma: rope_type \"" + type + "\" for " + kv.first + " not supported");
+      c.RopeThetaByType[kv.first] = kv.second.get_number("rope_theta");
+    }
+  } else {
+    c.RopeThetaByType = {{"sliding_attention", 10000.0}, {"full_attention", 1000000.0}};
+  }
+  if (c.EmbeddingDim == 0) c.EmbeddingDim = 768;
+  if (c.HiddenSizePerLayerInput == 0)
+    throw Error("gemma: embedding_gemma2 config without hidden_size_per_layer_input");
+}
+
 }  // namespace
 
 Config LoadConfig(const std::string& dir) {
   const json::Value v = read_json(dir + "/config.json", "config.json");
   Config c;
+  int64_t maxpos = 0;
   try {
-    if (v.get_string("model_type") == "embedding_gemma2")
-      throw Error("gemma: EmbeddingGemma 2 checkpoints are not supported by this build");
-    c.HiddenSize = (int)v.get_int("hidden_size");
-    c.IntermediateSize = (int)v.get_int("intermediate_size");
-    c.NumHiddenLayers = (int)v.get_int("num_hidden_layers");
-    c.NumAttentionHeads = (int)v.get_int("num_attention_heads");
-    c.NumKeyValueHeads = (int)v.get_int("num_key_value_heads");
-    c.HeadDim = (int)v.get_int("head_dim");
-    c.VocabSize = (int)v.get_int("vocab_size");
-    c.SlidingWindow = (int)v.get_int("sliding_window");
-    c.UseBidirectional = v.get_bool("use_bidirectional_attention");
-    c.RopeTheta = v.get_number("rope_theta");
-    c.RopeLocalBaseFreq = v.get_number("rope_local_base_freq");
-    c.QueryPreAttnScalar = v.get_number("query_pre_attn_scalar");
-    c.RMSNormEps = (float)v.get_number("rms_norm_eps");
-    const int64_t maxpos = v.get_int("max_position_embeddings");
-    c.MaxTokens = (maxpos == 0 || maxpos > 2048) ? 2048 : (int)maxpos;  // model.go:100-104
-    c.SlidingWindowPattern = (int)v.get_int("sliding_window_pattern", 6);  // config.go:211-213
-    if (c.SlidingWindowPattern == 0) c.SlidingWindowPattern = 6;
-    // layer_types must be the periodic pattern the GPU encoder runs:
-    // full attention iff (l+1) % pattern == 0 (config.go:214-225)
-    if (const json::Value* lt = v.find("layer_types"); lt && lt->is_array() && !lt->items().empty()) {
-      const auto& t = lt->items();
-      int first_full = -1;
-      for (size_t i = 0; i < t.size(); i++)
-        if (t[i].as_string() == "full_attention") {
-          first_full = (int)i;
-          break;
-        }
-      const int pat = first_full >= 0 ? first_full + 1 : (int)t.size() + 1;
-      for (size_t i = 0; i < t.size(); i++) {
-        const bool full = (int)((i + 1) % pat) == 0;
-        if (t[i].as_string() != (full ? "full_attention" : "sliding_attention"))
-          throw Error("gemma: layer_types is not a periodic sliding/full pattern");
+    if (v.get_string("model_type") == "embedding_gemma2") {
+      // the text tower's fields sit under text_config; the placeholder ids
+      // and the vision/audio configs beside it (config.go:157-208)
+      const json::Value* t = v.find("text_config");
+      if (!t || !t->is_object()) throw Error("gemma: config.json text_config: missing");
+      c.Variant = 2;
+      read_text_fields(*t, c);
+      maxpos = t->get_int("max_position_embeddings");
+      const struct {
+        const char* key;
+        const char* name;
+      } marks[] = {{"image_token_id", "image"},       {"audio_token_id", "audio"},
+                   {"video_token_id", "video"},       {"boi_token_id", "begin-of-image"},
+                   {"eoi_token_id", "end-of-image"},  {"boa_token_id", "begin-of-audio"},
+                   {"eoa_token_index", "end-of-audio"}};
+      for (const auto& mk : marks)
+        if (const json::Value* id = v.find(mk.key); id && !id->is_null())
+          c.MultimodalTokens[(int)id->as_int()] = mk.name;
+      auto has = [&](const char* k) {
+        const json::Value* x = v.find(k);
+        return x && !x->is_null();
+      };
+      if (has("image_token_id") && has("boi_token_id") && has("eoi_token_id") && has("vision_config")) {
+        c.ImageToken = (int)v.find("image_token_id")->as_int();
+        c.HasVision = true;
       }
-      c.SlidingWindowPattern = pat;
+      if (has("audio_token_id") && has("boa_token_id") && has("eoa_token_index") && has("audio_config")) {
+        c.AudioToken = (int)v.find("audio_token_id")->as_int();
+        c.HasAudio = true;
+      }
+      fill_variant2(*t, c);
+    } else {
+      read_text_fields(v, c);
+      maxpos = v.get_int("max_position_embeddings");
+      c.SlidingWindowPattern = (int)v.get_int("sliding_window_pattern", 6);  // config.go:211-213
+      if (c.SlidingWindowPattern == 0) c.SlidingWindowPattern = 6;
+      // layer_types must be the periodic pattern the GPU encoder runs:
+      // full attention iff (l+1) % pattern == 0 (config.go:214-225)
+      if (!c.LayerTypes.empty()) {
+        const auto& t = c.LayerTypes;
+        int first_full = -1;
+        for (size_t i = 0; i < t.size(); i++)
+          if (t[i] == "full_attention") {
+            first_full = (int)i;
+            break;
+          }
+        const int pat = first_full >= 0 ? first_full + 1 : (int)t.size() + 1;
+        for (size_t i = 0; i < t.size(); i++) {
+          const bool full = (int)((i + 1) % pat) == 0;
+          if (t[i] != (full ? "full_attention" : "sliding_attention"))
+            throw Error("gemma: layer_types is not a periodic sliding/full pattern");
+        }
+        c.SlidingWindowPattern = pat;
+        c.LayerTypes.clear();
+      }
     }
-    const std::string act = v.get_string("hidden_activation");
-    if (!act.empty() && act != "gelu_pytorch_tanh")
-      throw Error("gemma: activation \"" + act + "\" not supported (want gelu_pytorch_tanh)");
-    if (const json::Value* rs = v.find("rope_scaling"); rs && !rs->is_null())
-      throw Error("gemma: rope_scaling is set; not supported");
   } catch (const json::Error& e) {
     throw Error(std::string("gemma: config.json: ") + e.what());
   }
   if (c.HiddenSize == 0 || c.NumHiddenLayers == 0) throw Error("gemma: config is missing hidden_size or num_hidden_layers");
-  if (c.HeadDim % 2 != 0) throw Error("gemma: head_dim " + std::to_string(c.HeadDim) + " must be even for RoPE");
+  if (c.Variant == 2 && (int)c.LayerTypes.size() != c.NumHiddenLayers)
+    throw Error("gemma: " + std::to_string(c.LayerTypes.size()) + " layer types for " +
+                std::to_string(c.NumHiddenLayers) + " layers");
   if (c.NumKeyValueHeads <= 0 || c.NumAttentionHeads % c.NumKeyValueHeads != 0)
     throw Error("gemma: " + std::to_string(c.NumAttentionHeads) + " query heads not a multiple of " +
                 std::to_string(c.NumKeyValueHeads) + " key/value heads");
+  if (c.HeadDim % 2 != 0) throw Error("gemma: head_dim " + std::to_string(c.HeadDim) + " must be even for RoPE");
+  if (c.Variant == 2) {
+    for (int l = 0; l < c.NumHiddenLayers; l++) {
+      if (c.LayerHeadDim(l) % 2 != 0)
+        throw Error("gemma: layer " + std::to_string(l) + " head_dim " + std::to_string(c.LayerHeadDim(l)) +
+                    " must be even for RoPE");
+      if (c.LayerKVHeads(l) <= 0 || c.NumAttentionHeads % c.LayerKVHeads(l) != 0)
+        throw Error("gemma: layer " + std::to_string(l) + ": " + std::to_string(c.NumAttentionHeads) +
+                    " query heads not a multiple of " + std::to_string(c.LayerKVHeads(l)) + " key/value heads");
+    }
+    // model.go:102-110: the model card's 8192 tokens
+    c.MaxTokens = maxpos == 0 ? 8192 : (int)std::min<int64_t>(maxpos, 8192);
+  } else {
+    c.MaxTokens = (maxpos == 0 || maxpos > 2048) ? 2048 : (int)maxpos;  // model.go:100-104
+  }
   c.Dense.clear();
   return c;
 }
@@ -482,7 +635,7 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
   std::string stage = "config.json";  // names the file in JSON type errors
   try {
     Config cfg = LoadConfig(dir);
-    if (o.MaxTokens > 0) cfg.MaxTokens = std::min(o.MaxTokens, 2048);
+    if (o.MaxTokens > 0) cfg.MaxTokens = std::min(o.MaxTokens, cfg.Variant == 2 ? 8192 : 2048);
     if (o.BatchTokens <= 0) throw Error("gemma: BatchTokens must be positive");
     // sentence-transformers head (model.go:236-310): mean pooling, Dense
     // layers without bias or activation, Normalize
@@ -517,7 +670,7 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
       }
     }
     if (dense.size() > 4) throw Error("gemma: at most 4 Dense layers");
-    int width = cfg.HiddenSize;
+    int width = cfg.Variant == 2 ? cfg.EmbeddingDim : cfg.HiddenSize;  // after the embedding projection
     for (const auto& d : dense) {
       if (d.in != width)
         throw Error("gemma: Dense in_features " + std::to_string(d.in) + " after width " + std::to_string(width));
@@ -572,8 +725,16 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
                             "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
                             "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight"})
         want(p + n);
+      if (cfg.Variant == 2)
+        for (const char* n : {"ple_block.per_layer_input_gate.weight", "ple_block.per_layer_projection.weight",
+                              "ple_block.post_per_layer_input_norm.weight", "layer_scalar"})
+          want(p + n);
     }
     want("norm.weight");
+    if (cfg.Variant == 2)
+      for (const char* n : {"ple.per_layer_model_projection.weight", "ple.per_layer_projection_norm.weight",
+                            "embedding_projection.weight"})
+        want(n);
 
     stage = "weights";
     auto m = std::make_unique<Model>(cfg);
@@ -625,6 +786,18 @@ std::vector<std::vector<float>> Model::Embed(const std::vector<std::string>& tex
   std::vector<std::vector<int32_t>> ids(n);
   for (size_t i = 0; i < n; i++) {
     const std::vector<int> seq = tok_->Encode(prefix + texts[i]);
+    // checkTextOnly (embed.go:82-97): EmbeddingGemma 2's image, audio and
+    // video placeholders are refused, not embedded as ordinary tokens
+    for (int id : seq) {
+      auto mt = cfg_.MultimodalTokens.find(id);
+      if (mt == cfg_.MultimodalTokens.end()) continue;
+      const std::string& name = mt->second;
+      if ((id == cfg_.ImageToken && cfg_.HasVision) || (id == cfg_.AudioToken && cfg_.HasAudio))
+        throw Error("text " + std::to_string(i) + ": gemma: input contains the " + name +
+                    " placeholder token; pass the " + name + " with EmbedInputs");
+      throw Error("text " + std::to_string(i) + ": gemma: input contains the " + name +
+                  " placeholder token; EmbeddingGemma 2 video input is not supported");
+    }
     const size_t L = std::min(seq.size(), (size_t)cfg_.MaxTokens);
     ids[i].assign(seq.begin(), seq.begin() + L);
   }

@@ -120,8 +120,15 @@ struct Error : std::runtime_error {
   explicit Error(const std::string& m) : std::runtime_error(m) {}
 };
 
-// Hyper-parameters of config.json (models/gemma/config.go:19-58), Variant 0,
-// and the sentence-transformers Dense head; defaults are EmbeddingGemma-300M.
+// Per-layer geometry override of EmbeddingGemma 2 (config.go:141-144).
+struct LayerOverride {
+  int HeadDim = 0, NumKeyValueHeads = 0;
+};
+
+// Hyper-parameters of config.json (models/gemma/config.go:19-58) and the
+// sentence-transformers Dense head; defaults are EmbeddingGemma-300M
+// (Variant 0). Variant 2 is EmbeddingGemma 2's text tower, read from the
+// nested text_config with its defaults (config.go:247-297).
 struct Config {
   int HiddenSize = 768, NumHiddenLayers = 24, NumAttentionHeads = 3, NumKeyValueHeads = 1, HeadDim = 256;
   int IntermediateSize = 1152, VocabSize = 262144, SlidingWindow = 512, SlidingWindowPattern = 6;
@@ -130,6 +137,24 @@ struct Config {
   float RMSNormEps = 1e-6f;
   int MaxTokens = 2048;
   std::vector<int> Dense = {3072, 768};
+  // EmbeddingGemma 2 only (zero / empty for Variant 0)
+  int Variant = 0;
+  int HiddenSizePerLayerInput = 0, EmbeddingDim = 0;
+  std::vector<std::string> LayerTypes;              // "sliding_attention" / "full_attention" per layer
+  std::map<std::string, LayerOverride> PerLayerConfig;  // keyed by zero-padded layer index ("05")
+  std::map<std::string, double> RopeThetaByType;    // rope_parameters (config.go:147-150): type -> rope_theta
+  std::map<int, std::string> MultimodalTokens;      // placeholder ids -> name (embed.go:82-97)
+  int ImageToken = -1, AudioToken = -1;
+  bool HasVision = false, HasAudio = false;
+
+  // config.go:299-366: a layer's head dim and key/value heads (with the
+  // per-layer override), whether it uses the sliding window, its RoPE base,
+  // and the window bound (positions attend while |i-j| < Window()).
+  int LayerHeadDim(int l) const;
+  int LayerKVHeads(int l) const;
+  bool IsSliding(int l) const;
+  double RopeBase(int l) const;
+  int Window() const;
 };
 
 // Options of Embed (model.go:372-379): Dim truncates before L2
@@ -150,9 +175,9 @@ struct LoadOpts {
   int BatchTokens = 8192;
 };
 
-// config.json of a Gemma 3 text model (config.go:153-240): the fields the
-// encoder uses, validated as the reference validates them; EmbeddingGemma 2
-// checkpoints are refused.
+// config.json of a Gemma 3 text model or an EmbeddingGemma 2 checkpoint
+// (config.go:153-297): the fields the encoder uses, defaults filled and
+// validated as the reference does.
 Config LoadConfig(const std::string& dir);
 
 class Model {
@@ -161,6 +186,8 @@ class Model {
   // layout: config.json, tokenizer.json, *.safetensors (+ index), and the
   // modules.json Pooling (mean), Dense (no bias, identity) and Normalize
   // modules with config_sentence_transformers.json prompts (model.go:76-330).
+  // EmbeddingGemma 2 directories add the per-layer-input weights, the layer
+  // scalars and the embedding projection (model.go:163-205).
   static std::unique_ptr<Model> Load(const std::string& dir, const LoadOpts& o = {});
   explicit Model(const Config& cfg);
   ~Model();

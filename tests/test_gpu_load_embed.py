@@ -140,3 +140,84 @@ def test_load_errors(model_dir, tmp_path):
     assert r.returncode == 1 and "Dim(769) outside 1..768" in r.stdout
     r, _ = run(tmp_path, tmp_path, ["x"])  # no config.json
     assert r.returncode == 1 and "config.json" in r.stdout
+
+
+# ---- EmbeddingGemma 2 (model.go:76-330 with Variant 2; embed.go:82-97) ----
+
+IMAGE = "<|image|>"
+
+
+@pytest.fixture(scope="module")
+def eg2_dir(tmp_path_factory):
+    d = tmp_path_factory.mktemp("eg2_small")
+    tok = json.loads(json.load(open(GOLDEN, encoding="utf-8"))["files"]["learned"])
+    image_id = max(tok["model"]["vocab"].values()) + 1
+    tok.setdefault("added_tokens", []).append({"id": image_id, "content": IMAGE, "single_word": False,
+                                                "lstrip": False, "rstrip": False, "normalized": False,
+                                                "special": True})
+    (d / "tokenizer.json").write_text(json.dumps(tok), encoding="utf-8")
+    shape = S.ModelShape2(num_hidden_layers=6, vocab_size=(image_id + 1 + 63) // 64 * 64, sliding_window=24,
+                          hidden_size_per_layer_input=256, max_tokens=8192)
+    L = shape.num_hidden_layers
+    text = {"hidden_size": shape.hidden_size, "intermediate_size": shape.intermediate_size, "num_hidden_layers": L,
+            "num_attention_heads": shape.num_attention_heads, "num_key_value_heads": shape.num_key_value_heads,
+            "head_dim": shape.head_dim, "vocab_size": shape.vocab_size, "sliding_window": shape.sliding_window,
+            "rms_norm_eps": shape.rms_norm_eps, "hidden_activation": "gelu_pytorch_tanh",
+            "hidden_size_per_layer_input": shape.hidden_size_per_layer_input,
+            "embedding_dim": shape.embedding_dim, "max_position_embeddings": 262144,
+            "layer_types": ["sliding_attention" if shape.sliding(l) else "full_attention" for l in range(L)],
+            "per_layer_config": {f"{l:02d}": {"head_dim": shape.global_head_dim,
+                                             "num_key_value_heads": shape.global_kv_heads}
+                                 for l in range(L) if not shape.sliding(l)},
+            "rope_parameters": {"full_attention": {"rope_theta": 1e6, "rope_type": "default"},
+                                "sliding_attention": {"rope_theta": 1e4, "rope_type": "default"}}}
+    # the begin/end-of-image markers get ids this tokenizer never produces
+    cfg = {"model_type": "embedding_gemma2", "image_token_id": image_id, "boi_token_id": image_id + 1,
+           "eoi_token_id": image_id + 2,
+           "vision_config": {"hidden_size": 768}, "text_config": text}
+    (d / "config.json").write_text(json.dumps(cfg))
+    weights, main = {}, {}
+    for name, shp, kind in S.weight_specs2(shape):
+        w = S.make_weight(name, shp, kind, 77, 0.03, 0.2)
+        weights[name] = (w, kind)
+        main["language_model." + name] = bf16_tensor(w) if kind == "m" else torch.from_numpy(w)
+    save_file(main, str(d / "model.safetensors"))
+    mods = [{"idx": 0, "name": "0", "path": "", "type": "sentence_transformers.base.modules.transformer.Transformer"},
+            {"idx": 1, "name": "1", "path": "1_Pooling",
+             "type": "sentence_transformers.sentence_transformer.modules.pooling.Pooling"},
+            {"idx": 2, "name": "2", "path": "2_Normalize",
+             "type": "sentence_transformers.base.modules.normalize.Normalize"}]
+    (d / "1_Pooling").mkdir()
+    (d / "1_Pooling" / "config.json").write_text(json.dumps({"pooling_mode": "mean", "include_prompt": True}))
+    (d / "modules.json").write_text(json.dumps(mods))
+    (d / "config_sentence_transformers.json").write_text(json.dumps({"prompts": PROMPTS}))
+    om = O.OracleModel2(shape)
+    for name, (w, kind) in weights.items():
+        om.set(name, S.bf16_to_f32(w) if kind == "m" else w)
+    om.finalize()
+    yield d, om
+    om.close()
+
+
+@pytest.mark.parametrize("prompt,dim", [("-", 0), ("query", 0), ("document", 128)])
+def test_load_and_embed_texts_eg2(eg2_dir, tmp_path, prompt, dim):
+    d, om = eg2_dir
+    texts = TEXTS + ["long " * 70]  # longer than the sliding radius of 24
+    r, of = run(d, tmp_path, texts, prompt, dim)
+    assert r.returncode == 0, r.stdout
+    width = dim or 768
+    got = np.fromfile(of, np.float32).reshape(len(texts), width)
+    want = expected(om, d, texts, PROMPTS.get(prompt, ""), dim)
+    c = cos_rows(got, want)
+    print(f"EG2 prompt={prompt} dim={dim}: cosine min {c.min():.8f}, max|d| {np.abs(got - want).max():.3g}", flush=True)
+    assert c.min() >= 0.9999
+    assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
+
+
+def test_eg2_refuses_placeholders(eg2_dir, tmp_path):
+    """TestRejectsMultimodalPlaceholders2 (gemma2_test.go:319-335)."""
+    d, _ = eg2_dir
+    r, _ = run(d, tmp_path, ["fine", "look at this " + IMAGE + " picture"])
+    assert r.returncode == 1 and "text 1: gemma: input contains the image placeholder token" in r.stdout, r.stdout
+    r, _ = run(d, tmp_path, ["plain text mentioning an image"])
+    assert r.returncode == 0, r.stdout
