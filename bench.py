@@ -53,6 +53,9 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    p.add_argument("--model", default="eg300m", choices=["eg300m", "eg2"],
+                   help="eg300m: EmbeddingGemma-300M (the headline); eg2: the EmbeddingGemma 2 text tower at the "
+                        "reference's widths (hidden 512, 12 layers, head_dim 256/512, per-layer inputs 512)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -73,15 +76,23 @@ def calibrate_copy() -> None:
     print(json.dumps({"calibration": "device copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 3}))
 
 
-def cpu_baseline(batch, budget_s: float) -> dict:
+def cpu_baseline(batch, budget_s: float, model: str = "eg300m") -> dict:
     """The oracle on consecutive groups of 4 sequences of the workload (each
     padded to its own longest, as the reference's embedBatch pads), until the
     budget is spent. Test infrastructure used as the checker-side baseline."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     from ai_amd import synth as S
-    om = O.OracleModel(S.ModelShape())
-    om.load_synthetic()
+    if model == "eg2":
+        shape = S.ModelShape2()
+        om = O.OracleModel2(shape)
+        for name, shp, kind in S.weight_specs2(shape):
+            w = S.make_weight(name, shp, kind)
+            om.set(name, S.bf16_to_f32(w) if kind == "m" else w)
+        om.finalize()
+    else:
+        om = O.OracleModel(S.ModelShape())
+        om.load_synthetic()
     group = 4
     done = tokens = 0
     elapsed = 0.0
@@ -121,7 +132,7 @@ def main():
     from ai_amd import synth as S
 
     ctx = N.Context(0)
-    shape = S.ModelShape()
+    shape = S.ModelShape2() if a.model == "eg2" else S.ModelShape()
     model = G.Model(shape, ctx)
     model.load_synthetic()
     batch = S.make_batch(a.config, with_corpus=False)
@@ -180,10 +191,11 @@ def main():
 
     gs, g_ms, g_flops, _ = kstat("gemm_gateup")
     achieved = g_flops / (g_ms * 1e-3) if g_ms > 0 else 0.0
-    roofline = {"kernel": "gemm_x3_kernel split-bf16, GeGLU epilogue (gate|up, M=%d N=2304 K=768)" % batch.tokens,
+    roofline = {"kernel": "gemm_x3_kernel split-bf16, GeGLU epilogue (gate|up, M=%d N=%d K=%d)"
+                          % (batch.tokens, 2 * shape.intermediate_size, shape.hidden_size),
                 "bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": BF16_MFMA_PEAK / 1e12,
                 "unit": "TFLOP/s", "frac": round(achieved / BF16_MFMA_PEAK, 4),
-                "traffic": GATEUP_TRAFFIC_C2["bytes"] if a.config == "C2" else None,
+                "traffic": GATEUP_TRAFFIC_C2["bytes"] if a.config == "C2" and a.model == "eg300m" else None,
                 "launch_ms": round(g_ms, 4), "flops_per_launch": g_flops,
                 "mfma_flops_per_launch": SPLIT_TERMS * g_flops,
                 "mfma_frac": round(SPLIT_TERMS * achieved / BF16_MFMA_PEAK, 4),
@@ -211,7 +223,7 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline(batch, a.cpu_seconds)
+        cpu = cpu_baseline(batch, a.cpu_seconds, a.model)
 
     out = {
         "metric": METRIC,
@@ -226,7 +238,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (random-init bf16 weights N(0,0.02), Zipf(1.1) token ids; seeded)",
-        "config": {"workload": f"{a.config}: EmbeddingGemma-300M encoder forward, batch {B} x seq {T}, "
+        "config": {"workload": f"{a.config}: "
+                               + ("EmbeddingGemma 2 text tower" if a.model == "eg2" else "EmbeddingGemma-300M encoder")
+                               + f" forward, batch {B} x seq {T}, "
                                f"lengths {int(batch.lengths.min())}..{int(batch.lengths.max())}",
                    "batch": B, "seq_len": T, "valid_tokens": batch.tokens},
         "tokens_per_s": round(tok_s, 1),
