@@ -684,12 +684,18 @@ bool use_f32_mfma() {
 // Split-bf16 tile choice, from measurements on MI355X (M 5517 and 32768,
 // N 768..2304, K 768 and 1152): the 128x128 tile of eight 32x64 waves (two
 // workgroups per CU) is the fastest or within 4 % of the fastest at every
-// measured shape once it gives the CUs half a tile each; below that, 64x64
-// tiles (128x64 for GeGLU, which needs column-block pairs) spread the work.
-XTileId pick_xtile(int64_t m, int64_t n, Epi epi, int cus) {
-  const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128);
-  if (2 * tiles128 >= cus) return XTileId::x128x128w8;
-  return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
+// measured shape once it gives the CUs half a tile each, except where its
+// tiles (K-split parts included) fill just over one round of the CUs' two
+// slots: there the 64x128 tile of four 32x64 waves (four workgroups per CU)
+// halves the last round (the encoder's o and down products at 5 517 rows:
+// 0.79 -> 0.76 and 1.06 -> 1.01 ms per forward). Below half a tile per CU,
+// 64x64 tiles (128x64 for GeGLU, which needs column-block pairs) spread the
+// work.
+XTileId pick_xtile(int64_t m, int64_t n, int ksplit, Epi epi, int cus) {
+  const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128) * ksplit;
+  if (2 * tiles128 < cus) return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
+  if (tiles128 > 2 * cus && 4 * tiles128 <= 5 * 2 * cus) return XTileId::x64x128;
+  return XTileId::x128x128w8;
 }
 
 template <class TL>
@@ -767,7 +773,7 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (fast && bf16 && !use_f32_mfma()) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     XTileId t = (XTileId)forced_xtile();
-    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.epi, cus);
+    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, p.ksplit, g.epi, cus);
     dispatch_x3(t, p, g.epi, s);
   } else if (fast) {
     TileId t = (TileId)forced_tile();
