@@ -25,6 +25,7 @@
 // [2F, d] matrix (see gemm.hip), 1+w norm vectors in fp32.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <set>
@@ -36,6 +37,8 @@
 namespace fa {
 
 namespace {
+
+constexpr int kMaxMicrobatches = 4;  // streams a forward may use (micro-batches)
 
 bool bf16_exact(float f, uint16_t* out) {
   uint32_t u;
@@ -102,6 +105,10 @@ struct fa_model {
   size_t plan_host_ints = 0;
   hipEvent_t plan_done = nullptr;
   bool plan_pending = false;
+  // streams of micro-batches 1.. (micro-batch 0 runs on the context's
+  // stream), the fork event and one join event per extra stream
+  hipStream_t mb_stream[fa::kMaxMicrobatches] = {};
+  hipEvent_t ev_fork = nullptr, ev_join[fa::kMaxMicrobatches] = {};
   std::vector<int> seq_order;
   fa::DevBuf ids_dev, out_dev;
   // profiling
@@ -130,6 +137,31 @@ hipEvent_t take_event(fa_model* m) {
   hipEvent_t e = nullptr;
   if (hipEventCreate(&e) != hipSuccess) return nullptr;
   return e;
+}
+
+// Token count from which a batch runs as micro-batches on several streams;
+// FA_MICROBATCH=0 turns that off, FA_MICROBATCH=<rows> sets the threshold.
+int64_t microbatch_min_rows() {
+  static const int64_t v = [] {
+    const char* e = std::getenv("FA_MICROBATCH");
+    if (!e) return (int64_t)2048;
+    const long long n = std::atoll(e);
+    return n <= 0 ? INT64_MAX : (int64_t)n;
+  }();
+  return v;
+}
+
+// Number of micro-batches (2..kMaxMicrobatches; FA_MICROBATCH_GROUPS). Three
+// measured best on MI355X at 5 517, 11 550 and 32 768 tokens (C2: 6.41 ms
+// per forward on one stream, 5.49 with two groups, 5.43 with three, 5.92
+// with four) and within 3 % of best at 17 923.
+int microbatch_count() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_MICROBATCH_GROUPS");
+    const int n = e ? std::atoi(e) : 3;
+    return std::max(2, std::min(n, kMaxMicrobatches));
+  }();
+  return v;
 }
 
 // Brackets one launch with events when profiling.
@@ -300,8 +332,15 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     L.cos_t = L.sliding ? m->cos_local : m->cos_global;
     L.sin_t = L.sliding ? m->sin_local : m->sin_global;
   }
-  if (!rc && hipEventCreateWithFlags(&m->plan_done, hipEventDisableTiming) != hipSuccess)
+  if (!rc && (hipEventCreateWithFlags(&m->plan_done, hipEventDisableTiming) != hipSuccess ||
+              hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming) != hipSuccess))
     rc = set_error(ctx, FA_ERR_HIP, "hipEventCreate failed");
+  for (int i = 1; i < fa::kMaxMicrobatches && !rc; i++) {
+    if (hipEventCreateWithFlags(&m->ev_join[i], hipEventDisableTiming) != hipSuccess)
+      rc = set_error(ctx, FA_ERR_HIP, "hipEventCreate failed");
+    else if (hipStreamCreateWithFlags(&m->mb_stream[i], hipStreamNonBlocking) != hipSuccess)  // default priority
+      rc = set_error(ctx, FA_ERR_HIP, "hipStreamCreate failed");
+  }
   if (rc) {
     fa_gemma_destroy(m);
     return rc;
@@ -314,6 +353,8 @@ void fa_gemma_destroy(fa_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->ctx->device);
   (void)hipStreamSynchronize(m->ctx->stream);
+  for (hipStream_t st : m->mb_stream)
+    if (st) (void)hipStreamSynchronize(st);
   for (void* p : m->allocations) (void)hipFree(p);
   m->ws.release();
   m->plan_dev.release();
@@ -321,6 +362,11 @@ void fa_gemma_destroy(fa_model* m) {
   m->out_dev.release();
   if (m->plan_host) (void)hipHostFree(m->plan_host);
   if (m->plan_done) (void)hipEventDestroy(m->plan_done);
+  if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
+  for (int i = 0; i < fa::kMaxMicrobatches; i++) {
+    if (m->ev_join[i]) (void)hipEventDestroy(m->ev_join[i]);
+    if (m->mb_stream[i]) (void)hipStreamDestroy(m->mb_stream[i]);
+  }
   for (auto& p : m->pending) {
     m->event_pool.push_back(p.a);
     m->event_pool.push_back(p.b);
@@ -550,23 +596,49 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   int32_t* items_h = m->plan_host + (B + 1);
   cu_h[0] = 0;
   for (int b = 0; b < B; b++) cu_h[b + 1] = cu_h[b] + lengths[b];
-  // Work items (sequence, query block, head), longest sequences first: an
-  // item's work grows with its sequence's length, and dispatching the long
-  // ones first shortens the tail.
+  // Micro-batches: with enough tokens the sequences are cut into groups of
+  // about equal token count (contiguous rows) whose layers run on separate
+  // streams, so that one group's kernels occupy the CUs the others leave
+  // idle (the last round of GEMM tiles and attention items, the norms'
+  // low-occupancy phases). Not while profiling: the probes time one stream.
+  // Group g holds sequences [gb[g], gb[g+1]).
+  int groups = 1;
+  int gb[fa::kMaxMicrobatches + 1] = {0, B};
+  if (M >= fa::microbatch_min_rows() && !m->profiling) {
+    const int want = std::min(fa::microbatch_count(), B);
+    int b = 0;
+    int64_t cum = 0;
+    for (int g = 1; g < want; g++) {
+      // first cut at or past g/want of the tokens, leaving a sequence for each later group
+      while (b < B - (want - g) && (cum + lengths[b]) * want <= M * g) cum += lengths[b++];
+      if (b == gb[g - 1]) cum += lengths[b++];
+      gb[g] = b;
+    }
+    gb[want] = B;
+    groups = want;
+  }
+  // Work items (sequence, query block, head) of each group, longest
+  // sequences first: an item's work grows with its sequence's length, and
+  // dispatching the long ones first shortens the tail.
   std::vector<int>& order = m->seq_order;
-  order.resize(B);
-  for (int b = 0; b < B; b++) order[b] = b;
-  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
-  int64_t it = 0;
-  for (int b : order) {
-    for (int q0 = 0; q0 < lengths[b]; q0 += qblk) {
-      for (int h = 0; h < H; h++) {
-        items_h[3 * it] = b;
-        items_h[3 * it + 1] = q0;
-        items_h[3 * it + 2] = h;
-        it++;
+  int64_t it = 0, group_items[fa::kMaxMicrobatches] = {};
+  for (int gi = 0; gi < groups; gi++) {
+    const int b0 = gb[gi], b1 = gb[gi + 1];
+    order.resize(b1 - b0);
+    for (int b = b0; b < b1; b++) order[b - b0] = b;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
+    const int64_t first = it;
+    for (int b : order) {
+      for (int q0 = 0; q0 < lengths[b]; q0 += qblk) {
+        for (int h = 0; h < H; h++) {
+          items_h[3 * it] = b;
+          items_h[3 * it + 1] = q0;
+          items_h[3 * it + 2] = h;
+          it++;
+        }
       }
     }
+    group_items[gi] = it - first;
   }
   int rc;
   if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
@@ -633,22 +705,32 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       return rc;
     pr.done();
   }
-  for (int l = 0; l < NL; l++) {
+  // one layer over rows [r0, r0 + rows) (the sequences of one group, whose
+  // attention items are items[0, n_it)) on stream st
+  auto run_layer = [&](int l, int64_t r0, int64_t rows, const int32_t* items, int64_t n_it, hipStream_t st) -> int {
     const fa::Layer& L = m->layers[l];
     const int D = L.D, Hkv = L.Hkv;
     const bool sliding = L.sliding;
     const int ks_o = (H * D) % (32 * ksplit) == 0 ? ksplit : 1;
-    const float* o2_o = ks_o > 1 ? o + M * d : nullptr;
+    const float* o2_o = ks_o > 1 ? o + M * d + r0 * d : nullptr;
+    const float* o2_dn = o2_down ? o2_down + r0 * d : nullptr;
+    const float* o2_pl = o2_ple ? o2_ple + r0 * d : nullptr;
+    float* const xr = x + r0 * d;
+    float* const xnr = xn + r0 * d;
+    float* const qkvr = qkv + r0 * L.width;
+    float* const or_ = o + r0 * d;
+    int rc;
     {
       fa::GemmArgs g;
-      g.m = M; g.n = L.width; g.k = d; g.a = xn; g.lda = d; g.b = L.wqkv; g.ldb = d; g.c = qkv; g.ldc = L.width;
-      fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * M * L.width * d, 0);
-      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      g.m = rows; g.n = L.width; g.k = d; g.a = xnr; g.lda = d; g.b = L.wqkv; g.ldb = d; g.c = qkvr; g.ldc = L.width;
+      fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * rows * L.width * d, 0);
+      if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
     }
     {
-      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)M * (H + (v2 ? 2 : 1) * Hkv) * D * 8.0);
-      if ((rc = fa::launch_qknorm_rope(ctx, qkv, M, H, Hkv, D, L.g_q, L.g_k, eps, pos_d, L.cos_t, L.sin_t, s, v2)))
+      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * (H + (v2 ? 2 : 1) * Hkv) * D * 8.0);
+      if ((rc = fa::launch_qknorm_rope(ctx, qkvr, rows, H, Hkv, D, L.g_q, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t,
+                                       st, v2)))
         return rc;
       pr.done();
     }
@@ -658,54 +740,58 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
       a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
       double pairs = 0;
-      for (int b = 0; b < B; b++) {
-        const double Lb = lengths[b];
-        if (a.window > 0 && Lb > a.window) {
-          // sum over i of |{j : |i-j| < w}| = L(2w-1) - w(w-1)
-          pairs += Lb * (2.0 * a.window - 1) - (double)a.window * (a.window - 1);
-        } else {
-          pairs += Lb * Lb;
+      if (m->profiling) {
+        for (int b = 0; b < B; b++) {
+          const double Lb = lengths[b];
+          if (a.window > 0 && Lb > a.window) {
+            // sum over i of |{j : |i-j| < w}| = L(2w-1) - w(w-1)
+            pairs += Lb * (2.0 * a.window - 1) - (double)a.window * (a.window - 1);
+          } else {
+            pairs += Lb * Lb;
+          }
         }
       }
       fa::Probe pr(m, FA_K_ATTENTION, pairs * 4.0 * H * D, 0);
-      if ((rc = fa::launch_attention_varlen_items(ctx, a, items_d, (int32_t)n_items, s))) return rc;
+      if ((rc = fa::launch_attention_varlen_items(ctx, a, items, (int32_t)n_it, st))) return rc;
       pr.done();
     }
     {
       fa::GemmArgs g;
-      g.m = M; g.n = d; g.k = H * D; g.a = att; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = o; g.ldc = d;
-      g.ksplit = ks_o; g.c_split = M * d;
-      fa::Probe pr(m, FA_K_GEMM_O, 2.0 * M * d * H * D, 0);
-      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      g.m = rows; g.n = d; g.k = H * D; g.a = att + r0 * H * D; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = or_;
+      g.ldc = d; g.ksplit = ks_o; g.c_split = M * d;
+      fa::Probe pr(m, FA_K_GEMM_O, 2.0 * rows * d * H * D, 0);
+      if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
     }
     {
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
-      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_attn, L.g_pre_ffn, eps, s, o2_o))) return rc;
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)rows * d * 16.0);
+      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_attn, L.g_pre_ffn, eps, st, o2_o)))
+        return rc;
       pr.done();
     }
     {
       fa::GemmArgs g;
-      g.m = M; g.n = 2 * F; g.k = d; g.a = xn; g.lda = d; g.b = L.wgu; g.ldb = d; g.c = gu; g.ldc = F;
+      g.m = rows; g.n = 2 * F; g.k = d; g.a = xnr; g.lda = d; g.b = L.wgu; g.ldb = d; g.c = gu + r0 * F; g.ldc = F;
       g.epi = fa::Epi::GeGLU;
-      fa::Probe pr(m, FA_K_GEMM_GATEUP, 2.0 * M * 2 * F * d, 0);
-      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      fa::Probe pr(m, FA_K_GEMM_GATEUP, 2.0 * rows * 2 * F * d, 0);
+      if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
     }
     {
       fa::GemmArgs g;
-      g.m = M; g.n = d; g.k = F; g.a = gu; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = o; g.ldc = d;
+      g.m = rows; g.n = d; g.k = F; g.a = gu + r0 * F; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = or_; g.ldc = d;
       g.ksplit = ks_down; g.c_split = M * d;
-      fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * M * d * F, 0);
-      if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+      fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * rows * d * F, 0);
+      if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
     }
     // the last layer's "next norm" is the final RMSNorm (embed.go:237): xn = h
     const float* g_next = (l + 1 < NL) ? m->layers[l + 1].g_in : m->g_final;
     {
       // variant 2: the per-layer-input block reads x itself, so no norm here
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
-      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_post_ffn, v2 ? nullptr : g_next, eps, s, o2_down)))
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)rows * d * 16.0);
+      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_ffn, v2 ? nullptr : g_next, eps, st,
+                                         o2_dn)))
         return rc;
       pr.done();
     }
@@ -713,25 +799,50 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       // x = (x + RMSNorm(gelu(x . Wg^T) * ple_l . Wp^T; g)) * scalar (embed.go:359-371)
       {
         fa::GemmArgs g;
-        g.m = M; g.n = P; g.k = d; g.a = x; g.lda = d; g.b = L.wple_gate; g.ldb = d; g.c = gu; g.ldc = P;
-        g.epi = fa::Epi::Generic; g.act = FA_ACT_GELU; g.mul = ple + (int64_t)l * P; g.ldm = (int64_t)NL * P;
-        fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * M * P * d, 0);
-        if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+        g.m = rows; g.n = P; g.k = d; g.a = xr; g.lda = d; g.b = L.wple_gate; g.ldb = d; g.c = gu + r0 * P; g.ldc = P;
+        g.epi = fa::Epi::Generic; g.act = FA_ACT_GELU; g.mul = ple + r0 * NL * P + (int64_t)l * P;
+        g.ldm = (int64_t)NL * P;
+        fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * P * d, 0);
+        if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
         pr.done();
       }
       {
         fa::GemmArgs g;
-        g.m = M; g.n = d; g.k = P; g.a = gu; g.lda = P; g.b = L.wple_proj; g.ldb = P; g.c = o; g.ldc = d;
+        g.m = rows; g.n = d; g.k = P; g.a = gu + r0 * P; g.lda = P; g.b = L.wple_proj; g.ldb = P; g.c = or_; g.ldc = d;
         g.ksplit = ks_ple; g.c_split = M * d;
-        fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * M * d * P, 0);
-        if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
+        fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * d * P, 0);
+        if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
         pr.done();
       }
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)M * d * 16.0);
-      if ((rc = fa::launch_residual_norm(ctx, o, x, xn, M, d, L.g_ple_post, g_next, eps, s, o2_ple, L.scalar)))
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)rows * d * 16.0);
+      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_ple_post, g_next, eps, st, o2_pl, L.scalar)))
         return rc;
       pr.done();
     }
+    return FA_OK;
+  };
+  if (groups == 1) {
+    for (int l = 0; l < NL; l++)
+      if ((rc = run_layer(l, 0, M, items_d, n_items, s))) return rc;
+  } else {
+    // groups 1.. run on their own streams once the embeddings (and plan) are in
+    FA_HIP_CHECK(ctx, hipEventRecord(m->ev_fork, s));
+    for (int g = 1; g < groups; g++) FA_HIP_CHECK(ctx, hipStreamWaitEvent(m->mb_stream[g], m->ev_fork, 0));
+    rc = FA_OK;
+    for (int l = 0; l < NL && !rc; l++) {
+      int64_t item0 = 0;
+      for (int g = 0; g < groups && !rc; g++) {
+        const int64_t r0 = cu_h[gb[g]], rows = cu_h[gb[g + 1]] - r0;
+        rc = run_layer(l, r0, rows, items_d + 3 * item0, group_items[g], g ? m->mb_stream[g] : s);
+        item0 += group_items[g];
+      }
+    }
+    // joined also after an error: later calls reuse the workspace on s
+    for (int g = 1; g < groups; g++) {
+      FA_HIP_CHECK(ctx, hipEventRecord(m->ev_join[g], m->mb_stream[g]));
+      FA_HIP_CHECK(ctx, hipStreamWaitEvent(s, m->ev_join[g], 0));
+    }
+    if (rc) return rc;
   }
   {
     fa::Probe pr(m, FA_K_POOL_L2, 0, (double)M * d * 4.0 + (double)B * d * 4.0);

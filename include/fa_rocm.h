@@ -264,7 +264,10 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
 
 /* Same computation on device-resident data: d_ids [B x T] on the device,
  * lengths on the HOST (they set the launch shapes), d_out [B x dim] on the
- * device. Enqueues on fa_stream(ctx) and returns without waiting. */
+ * device. Enqueues on fa_stream(ctx) and returns without waiting. From
+ * 2 048 tokens on, the layers of three token-balanced groups of sequences
+ * run on the model's own extra streams, forked from and joined back into
+ * fa_stream(ctx), so the call stays ordered on that stream. */
 int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
                            int32_t dim, float* d_out);
 
@@ -286,6 +289,9 @@ enum {
   FA_K_PLE_NORM = 11,  /* EmbeddingGemma 2: per-layer input RMSNorm */
   FA_K_COUNT = 12
 };
+/* While enabled, every launch is bracketed by events and the forward runs
+ * on one stream (no micro-batches), so the durations are those of
+ * full-batch launches. */
 int fa_gemma_set_profiling(fa_model* m, int enabled);
 /* Accumulated launches, milliseconds, flops and bytes (algorithmic) for one
  * kind since the last reset; synchronises the stream. */
