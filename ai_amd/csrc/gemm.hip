@@ -418,6 +418,7 @@ using X64x128 = XTile<64, 128, 2, 2>;    // 4 waves of 32x64
 using X64x64 = XTile<64, 64, 2, 2>;      // 4 waves of 32x32
 using X256x128 = XTile<256, 128, 4, 2>;  // 8 waves of 64x64
 using X128x128w8 = XTile<128, 128, 4, 2>;  // 8 waves of 32x64
+using X128x256w8 = XTile<128, 256, 4, 2>;  // 8 waves of 32x128 (80 KB of LDS: two workgroups per CU)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -657,8 +658,9 @@ void dispatch_tile(TileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   }
 }
 
-enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, x128x128w8, kCount };
-const char* const kXTileNames[] = {"128x128", "128x64", "128x64v", "64x128", "64x64", "256x128", "128x128w8"};
+enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, x128x128w8, x128x256w8, kCount };
+const char* const kXTileNames[] = {"128x128", "128x64",    "128x64v",  "64x128",
+                                   "64x64",   "256x128",   "128x128w8", "128x256w8"};
 
 // FA_GEMM_XTILE=<name> forces a split-bf16 tile shape; FA_GEMM_MFMA=f32 runs
 // bf16 weights through the fp32 MFMA kernel instead (tuning, comparison).
@@ -690,8 +692,13 @@ bool use_f32_mfma() {
 // halves the last round (the encoder's o and down products at 5 517 rows:
 // 0.79 -> 0.76 and 1.06 -> 1.01 ms per forward). Below half a tile per CU,
 // 64x64 tiles (128x64 for GeGLU, which needs column-block pairs) spread the
-// work.
+// work. From 1.5 128x256 tiles per CU on, the 128x256 tile of eight 32x128
+// waves wins: it splits each A element for twice the columns (gate|up at
+// 5 517 x 2304 x 768: 75 vs 81 us; 32 768 rows: 6-7 % faster), while below
+// that its fewer tiles leave CUs idle (qkv at 1 840 rows: 31 vs 21 us).
 XTileId pick_xtile(int64_t m, int64_t n, int ksplit, Epi epi, int cus) {
+  const int64_t tiles256 = ((m + 127) / 128) * ((n + 255) / 256) * ksplit;
+  if (2 * tiles256 >= 3LL * cus) return XTileId::x128x256w8;
   const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128) * ksplit;
   if (2 * tiles128 < cus) return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
   if (tiles128 > 2 * cus && 4 * tiles128 <= 5 * 2 * cus) return XTileId::x64x128;
@@ -717,6 +724,7 @@ void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
     case XTileId::x64x64: dispatch_x3_epi<X64x64>(p, epi, s); break;
     case XTileId::x256x128: dispatch_x3_epi<X256x128>(p, epi, s); break;
     case XTileId::x128x128w8: dispatch_x3_epi<X128x128w8>(p, epi, s); break;
+    case XTileId::x128x256w8: dispatch_x3_epi<X128x256w8>(p, epi, s); break;
     default: dispatch_x3_epi<X128x128>(p, epi, s); break;
   }
 }
