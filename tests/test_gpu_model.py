@@ -56,8 +56,9 @@ def test_c1(models):
 def test_c2_subset(models):
     """C2 (32 x 256, ragged): the first 8 and the last 4 sequences through
     the oracle (each sequence's embedding does not depend on the others,
-    gemma_test.go:117-135). At 5 517 tokens the GPU runs the batch as two
-    micro-batches on two streams; these rows come from both."""
+    gemma_test.go:117-135). At 5 517 tokens the GPU runs the batch as three
+    micro-batches on three streams; these rows come from the first and the
+    last."""
     gm, om = models
     b = S.make_batch("C2")
     got = gm.embed_ids(b.ids, b.lengths)
@@ -77,6 +78,29 @@ def test_batch_and_padding_invariance(models):
         alone = gm.embed_ids(b.ids[i:i + 1, :L], b.lengths[i:i + 1])
         c = cos_rows(alone, full[i:i + 1])
         assert c.min() >= 0.9999
+
+
+@pytest.mark.parametrize("lengths", [[2000, 7, 300], [1500, 1500], [40] * 60 + [2048]])
+def test_microbatch_groups_match_single_sequences(models, lengths):
+    """From 2 048 tokens a batch runs as up to three token-balanced groups of
+    sequences on three streams; with one dominant sequence, two sequences
+    or many short ones every sequence's embedding still equals its
+    single-sequence run, and the shortest one the oracle's."""
+    gm, om = models
+    rng = np.random.default_rng(len(lengths))
+    T = max(lengths)
+    lens = np.array(lengths, np.int32)
+    ids = rng.integers(3, 262144, (len(lens), T)).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(T)[None, :] >= lens[:, None]] = 0
+    full = gm.embed_ids(ids, lens)
+    for i in sorted(set([0, len(lens) - 1, int(np.argmin(lens))])):
+        L = int(lens[i])
+        alone = gm.embed_ids(ids[i:i + 1, :L], lens[i:i + 1])
+        assert cos_rows(alone, full[i:i + 1]).min() >= 0.99999, (lengths, i)
+    i = int(np.argmin(lens))
+    L = int(lens[i])
+    compare(full[i:i + 1], om.embed(ids[i:i + 1, :L], lens[i:i + 1]), f"groups {lengths[:3]}.. [{i}]")
 
 
 def test_dim_truncation(models):
