@@ -692,13 +692,16 @@ bool use_f32_mfma() {
 // halves the last round (the encoder's o and down products at 5 517 rows:
 // 0.79 -> 0.76 and 1.06 -> 1.01 ms per forward). Below half a tile per CU,
 // 64x64 tiles (128x64 for GeGLU, which needs column-block pairs) spread the
-// work. From 1.5 128x256 tiles per CU on, the 128x256 tile of eight 32x128
-// waves wins: it splits each A element for twice the columns (gate|up at
-// 5 517 x 2304 x 768: 75 vs 81 us; 32 768 rows: 6-7 % faster), while below
-// that its fewer tiles leave CUs idle (qkv at 1 840 rows: 31 vs 21 us).
-XTileId pick_xtile(int64_t m, int64_t n, int ksplit, Epi epi, int cus) {
+// work. From 1.5 128x256 tiles per CU on, and with at least 24 K slabs per
+// tile, the 128x256 tile of eight 32x128 waves wins: it splits each A
+// element for twice the columns (gate|up at 5 517 x 2304 x 768: 75 vs 81 us;
+// 32 768 rows: 6-7 % faster), while below that its fewer tiles leave CUs
+// idle (qkv at 1 840 rows: 31 vs 21 us) and with 16 slabs its longer
+// prologue and epilogue lose (EmbeddingGemma 2's K = 512 products at 5 517
+// rows: 84 vs 79 us for gate|up).
+XTileId pick_xtile(int64_t m, int64_t n, int64_t k, int ksplit, Epi epi, int cus) {
   const int64_t tiles256 = ((m + 127) / 128) * ((n + 255) / 256) * ksplit;
-  if (2 * tiles256 >= 3LL * cus) return XTileId::x128x256w8;
+  if (2 * tiles256 >= 3LL * cus && k / (32LL * ksplit) >= 24) return XTileId::x128x256w8;
   const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128) * ksplit;
   if (2 * tiles128 < cus) return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
   if (tiles128 > 2 * cus && 4 * tiles128 <= 5 * 2 * cus) return XTileId::x64x128;
@@ -781,7 +784,7 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (fast && bf16 && !use_f32_mfma()) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     XTileId t = (XTileId)forced_xtile();
-    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, p.ksplit, g.epi, cus);
+    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.k, p.ksplit, g.epi, cus);
     dispatch_x3(t, p, g.epi, s);
   } else if (fast) {
     TileId t = (TileId)forced_tile();
