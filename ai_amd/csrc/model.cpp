@@ -667,10 +667,6 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   float* o = att + M * m->max_hd;
   float* gu = o + (int64_t)ksplit * M * d;
   float* ple = gu + M * std::max(F, P);
-  // per product: split only when K divides into whole 32-wide slabs
-  const int ks_down = F % (32 * ksplit) == 0 ? ksplit : 1, ks_ple = P % (32 * ksplit) == 0 ? ksplit : 1;
-  const float* o2_down = ks_down > 1 ? o + M * d : nullptr;
-  const float* o2_ple = ks_ple > 1 ? o + M * d : nullptr;
   float* pooled = ple + (v2 ? M * NL * P : 0);
   float* hbuf0 = pooled + (size_t)B * d;
   float* hbuf1 = hbuf0 + (size_t)B * maxw;
@@ -711,10 +707,21 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     const fa::Layer& L = m->layers[l];
     const int D = L.D, Hkv = L.Hkv;
     const bool sliding = L.sliding;
-    const int ks_o = (H * D) % (32 * ksplit) == 0 ? ksplit : 1;
+    // The N = hidden products (o, down, per-layer-input projection) split K
+    // in two when their 128x128 tiles, counted over the concurrent groups,
+    // give the CUs fewer than two each (C2: one stream 5 517 rows, or three
+    // groups of about 1 840: 4 % faster split); with more tiles the second
+    // partial's writes and reads cost more than the fill gains (C5's three
+    // groups of about 5 970 rows: 4.7 % faster unsplit).
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int64_t n_tiles = ((rows + 127) / 128) * ((d + 127) / 128) * groups;
+    const int ks = n_tiles < 2LL * cus ? ksplit : 1;
+    // per product: split only when K divides into whole 32-wide slabs
+    const int ks_o = (H * D) % (32 * ks) == 0 ? ks : 1, ks_down = F % (32 * ks) == 0 ? ks : 1,
+              ks_ple = P % (32 * ks) == 0 ? ks : 1;
     const float* o2_o = ks_o > 1 ? o + M * d + r0 * d : nullptr;
-    const float* o2_dn = o2_down ? o2_down + r0 * d : nullptr;
-    const float* o2_pl = o2_ple ? o2_ple + r0 * d : nullptr;
+    const float* o2_dn = ks_down > 1 ? o + M * d + r0 * d : nullptr;
+    const float* o2_pl = ks_ple > 1 ? o + M * d + r0 * d : nullptr;
     float* const xr = x + r0 * d;
     float* const xnr = xn + r0 * d;
     float* const qkvr = qkv + r0 * L.width;
