@@ -609,7 +609,8 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     int b = 0;
     int64_t cum = 0;
     for (int g = 1; g < want; g++) {
-      // first cut at or past g/want of the tokens, leaving a sequence for each later group
+      // cut before the sequence that would take the groups so far past g/want of the
+      // tokens, keeping at least one sequence in this group and in each later one
       while (b < B - (want - g) && (cum + lengths[b]) * want <= M * g) cum += lengths[b++];
       if (b == gb[g - 1]) cum += lengths[b++];
       gb[g] = b;
