@@ -15,6 +15,10 @@ Prints ONE JSON line (the driver's contract) with:
                    2.5 PFLOP/s dense bf16 MFMA peak, the unit the split-bf16
                    GEMM runs on (three bf16 products per fp32 multiply-add,
                    so its ceiling is a third of that peak)
+  throughput_roofline
+                   the timed throughput as a roofline fraction: the forward's
+                   algorithmic flops (all GEMMs + attention) per timed step /
+                   the timed step, against the bf16 and fp32 MFMA peaks
   cpu_baseline     the CPU oracle (a port of the reference's Go path, the Go
                    toolchain being absent) on a bounded sample of the same
                    workload, on this host's cores
@@ -220,6 +224,15 @@ def main():
     gemm_all = {"tflops": round(gemm_fl / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else 0,
                 "frac_fp32_mfma": round(gemm_fl / (gemm_ms * 1e-3) / FP32_MFMA_PEAK, 4) if gemm_ms else 0,
                 "ms_per_step": round(gemm_ms / a.steps, 3)}
+    # The timed throughput (sentences/s and tokens/s are one measurement) as
+    # a roofline fraction: the forward's algorithmic flops (every GEMM and
+    # the attention, as counted per launch in the event pass) per timed step
+    # over the timed step.
+    step_fl = sum(stats[n]["flops"] for n in N.KERNEL_KINDS) / a.steps
+    throughput_roofline = {"flops_per_step": step_fl,
+                           "tflops": round(step_fl / (ms_per_step * 1e-3) / 1e12, 2),
+                           "frac_bf16_mfma": round(step_fl / (ms_per_step * 1e-3) / BF16_MFMA_PEAK, 4),
+                           "frac_fp32_mfma": round(step_fl / (ms_per_step * 1e-3) / FP32_MFMA_PEAK, 4)}
 
     cpu = None
     if not a.no_cpu:
@@ -247,6 +260,7 @@ def main():
         "runs_ms_per_step": {"all": [round(r, 3) for r in runs], "min": round(min(runs), 3),
                              "median": round(sorted(runs)[1], 3)},
         "roofline": roofline,
+        "throughput_roofline": throughput_roofline,
         "gemm_all": gemm_all,
         "kernels": kernels,
         "profiled_ms_per_step": round(prof_ms, 3),
