@@ -63,6 +63,7 @@ struct VarlenParams {
   int32_t H, Hkv;
   int32_t window;
   float scale;
+  int64_t row0;  // packed row of qkv's and out's first row
 };
 
 // ---- the model path's kernel ------------------------------------------------
@@ -113,8 +114,8 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   const int q0 = p.items[3 * blockIdx.x + 1];
   const int h = p.items[3 * blockIdx.x + 2];
   const int hk = h / (p.H / p.Hkv);
-  const int start = p.cu[seq];
-  const int L = p.cu[seq + 1] - start;
+  const int L = p.cu[seq + 1] - p.cu[seq];
+  const int64_t start = p.cu[seq] - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
   const int dofs = half * HALF;
   const float* qbase = p.qkv + (int64_t)start * W + (int64_t)h * HD + dofs;
@@ -336,7 +337,7 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
     return set_error(ctx, FA_ERR_ARG, "attention: %d query heads not a multiple of %d kv heads", a.H, a.Hkv);
   if (n_items == 0) return FA_OK;
   VarlenParams p;
-  p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items;
+  p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items; p.row0 = a.row0;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
   if (a.D == 256)
     hipLaunchKernelGGL(attention_varlen_kernel<256>, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);

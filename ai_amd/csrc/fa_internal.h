@@ -180,6 +180,7 @@ struct AttnVarlenArgs {
   int32_t nseq, max_len, H, Hkv, D;
   int32_t window;
   float scale;
+  int64_t row0 = 0;  // packed row held by qkv's and out's first row (items' sequences start at or after it)
 };
 // d_items holds n_items triples (sequence, first query, head): one work item
 // per query block of attention_varlen_qblock() queries and head.

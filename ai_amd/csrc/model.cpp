@@ -725,7 +725,13 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     const float* o2_pl = ks_ple > 1 ? o + M * d + r0 * d : nullptr;
     float* const xr = x + r0 * d;
     float* const xnr = xn + r0 * d;
-    float* const qkvr = qkv + r0 * L.width;
+    // per-group regions of the buffers whose row width changes with the
+    // layer (EmbeddingGemma 2's head dims) or the product (gate|up vs the
+    // per-layer-input gate): groups on other streams may be at other
+    // layers, so each writes only inside [r0, r0 + rows) x the widest row
+    float* const qkvr = qkv + r0 * m->max_width;
+    float* const attr = att + r0 * m->max_hd;
+    float* const gur = gu + r0 * std::max(F, P);
     float* const or_ = o + r0 * d;
     int rc;
     {
@@ -744,7 +750,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     }
     {
       fa::AttnVarlenArgs a;
-      a.qkv = qkv; a.out = att; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
+      a.qkv = qkvr; a.out = attr; a.row0 = r0; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
       a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
       a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
       double pairs = 0;
@@ -765,7 +771,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     }
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = d; g.k = H * D; g.a = att + r0 * H * D; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = or_;
+      g.m = rows; g.n = d; g.k = H * D; g.a = attr; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = or_;
       g.ldc = d; g.ksplit = ks_o; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_O, 2.0 * rows * d * H * D, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -779,7 +785,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     }
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = 2 * F; g.k = d; g.a = xnr; g.lda = d; g.b = L.wgu; g.ldb = d; g.c = gu + r0 * F; g.ldc = F;
+      g.m = rows; g.n = 2 * F; g.k = d; g.a = xnr; g.lda = d; g.b = L.wgu; g.ldb = d; g.c = gur; g.ldc = F;
       g.epi = fa::Epi::GeGLU;
       fa::Probe pr(m, FA_K_GEMM_GATEUP, 2.0 * rows * 2 * F * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -787,7 +793,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     }
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = d; g.k = F; g.a = gu + r0 * F; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = or_; g.ldc = d;
+      g.m = rows; g.n = d; g.k = F; g.a = gur; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = or_; g.ldc = d;
       g.ksplit = ks_down; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * rows * d * F, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -807,7 +813,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       // x = (x + RMSNorm(gelu(x . Wg^T) * ple_l . Wp^T; g)) * scalar (embed.go:359-371)
       {
         fa::GemmArgs g;
-        g.m = rows; g.n = P; g.k = d; g.a = xr; g.lda = d; g.b = L.wple_gate; g.ldb = d; g.c = gu + r0 * P; g.ldc = P;
+        g.m = rows; g.n = P; g.k = d; g.a = xr; g.lda = d; g.b = L.wple_gate; g.ldb = d; g.c = gur; g.ldc = P;
         g.epi = fa::Epi::Generic; g.act = FA_ACT_GELU; g.mul = ple + r0 * NL * P + (int64_t)l * P;
         g.ldm = (int64_t)NL * P;
         fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * P * d, 0);
@@ -816,7 +822,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       }
       {
         fa::GemmArgs g;
-        g.m = rows; g.n = d; g.k = P; g.a = gu + r0 * P; g.lda = P; g.b = L.wple_proj; g.ldb = P; g.c = or_; g.ldc = d;
+        g.m = rows; g.n = d; g.k = P; g.a = gur; g.lda = P; g.b = L.wple_proj; g.ldb = P; g.c = or_; g.ldc = d;
         g.ksplit = ks_ple; g.c_split = M * d;
         fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * d * P, 0);
         if ((rc = fa::launch_gemm(ctx, g, st))) return rc;

@@ -101,6 +101,25 @@ def test_gpu_matches_oracle(eg2, B, T, lo):
     assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
 
 
+def test_gpu_microbatches(eg2):
+    """From 2 048 tokens the batch runs as three token-balanced groups of
+    sequences on three streams (per-layer inputs indexed by the group's
+    rows): each sequence equals its single-sequence run, the first and last
+    the oracle."""
+    shape, om, gm = eg2
+    ids, lengths = batch(77, 14, 220, 120, shape.vocab_size)
+    assert int(lengths.sum()) >= 2048
+    got = gm.embed_ids(ids, lengths)
+    for b in (0, 6, 13):
+        n = int(lengths[b])
+        one = gm.embed_ids(ids[b:b + 1, :n], lengths[b:b + 1])
+        assert cos_rows(one, got[b:b + 1])[0] >= 0.99999, b
+    for b in (0, 13):
+        n = int(lengths[b])
+        want = om.embed(ids[b:b + 1, :n], lengths[b:b + 1])
+        assert cos_rows(got[b:b + 1], want)[0] >= 0.9999, b
+
+
 def test_gpu_dim_and_batch_invariance(eg2):
     shape, om, gm = eg2
     ids, lengths = batch(5, 6, 120, 10, shape.vocab_size)
