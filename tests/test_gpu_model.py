@@ -101,6 +101,11 @@ def test_microbatch_groups_match_single_sequences(models, lengths):
     i = int(np.argmin(lens))
     L = int(lens[i])
     compare(full[i:i + 1], om.embed(ids[i:i + 1, :L], lens[i:i + 1]), f"groups {lengths[:3]}.. [{i}]")
+    # Matryoshka truncation on the micro-batched path (embed.go:421-427)
+    d256 = gm.embed_ids(ids, lens, dim=256).astype(np.float64)
+    want = full[:, :256].astype(np.float64)
+    want /= np.linalg.norm(want, axis=1, keepdims=True)
+    np.testing.assert_allclose(d256, want, atol=2e-6)
 
 
 def test_dim_truncation(models):
