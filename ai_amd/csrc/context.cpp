@@ -358,6 +358,7 @@ int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, cons
   if (topk < 1 || topk > 32 || topk > nd)
     return set_error(ctx, FA_ERR_ARG, "Similarities top-k: k=%d outside 1..min(32, %lld)", topk, (long long)nd);
   if (nq == 0) return FA_OK;
+  if (nq > 65535) return set_error(ctx, FA_ERR_ARG, "Similarities top-k: %lld queries > 65535", (long long)nq);
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   int rc;
   fa::DevBuf& sc = ctx->slot(S_C);
@@ -367,7 +368,9 @@ int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, cons
   g.a = queries; g.lda = d; g.b = docs; g.ldb = d; g.b_dtype = FA_DT_F32; g.b_layout = FA_B_NK;
   g.c = sc.as<float>(); g.ldc = nd;
   if ((rc = fa::launch_gemm(ctx, g, ctx->stream))) return rc;
-  return fa::launch_topk(ctx, sc.as<float>(), nq, nd, topk, idx, val, ctx->stream);
+  fa::DevBuf& cand = ctx->slot(S_TOPK);
+  if ((rc = cand.ensure(ctx, (size_t)fa::topk_scratch_bytes(nq, nd, topk)))) return rc;
+  return fa::launch_topk(ctx, sc.as<float>(), nq, nd, topk, idx, val, cand.ptr, ctx->stream);
 }
 
 int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
@@ -379,6 +382,7 @@ int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const fl
   if (topk < 1 || topk > 32 || topk > nd)
     return set_error(ctx, FA_ERR_ARG, "Similarities top-k: k=%d outside 1..min(32, %lld)", topk, (long long)nd);
   if (nq == 0) return FA_OK;
+  if (nq > 65535) return set_error(ctx, FA_ERR_ARG, "Similarities top-k: %lld queries > 65535", (long long)nq);
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void *dq, *dd;
   int rc;

@@ -49,29 +49,30 @@ struct DevBuf {
   }
 };
 
+// Scratch slots of fa_ctx (per-call device buffers of the entry points).
+namespace slots {
+enum : size_t {
+  S_A = 0, S_B, S_C, S_BIAS, S_ROWSCALE, S_MUL, S_RES, S_X, S_G, S_OUT, S_COS, S_SIN, S_Q, S_K, S_V, S_MASK,
+  S_CL_WORK, S_CL_X, S_CL_C, S_CL_OUT,  // cluster entry points
+  S_TOPK,                               // top-k candidates
+  S_COUNT
+};
+}  // namespace slots
+
 }  // namespace fa
 
 struct fa_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string last_error;
-  std::vector<fa::DevBuf> scratch;  // per-slot scratch for host-pointer entry points
+  // Per-slot scratch for the entry points. A fixed array: a reference to one
+  // slot stays valid while others are taken.
+  fa::DevBuf scratch[fa::slots::S_COUNT];
   int cu_count = 0;
-  fa::DevBuf& slot(size_t i) {
-    if (scratch.size() <= i) scratch.resize(i + 1);
-    return scratch[i];
-  }
+  fa::DevBuf& slot(size_t i) { return scratch[i]; }
 };
 
 namespace fa {
-
-// Scratch slots of fa_ctx (per-call device buffers of the entry points).
-namespace slots {
-enum : size_t {
-  S_A = 0, S_B, S_C, S_BIAS, S_ROWSCALE, S_MUL, S_RES, S_X, S_G, S_OUT, S_COS, S_SIN, S_Q, S_K, S_V, S_MASK,
-  S_CL_WORK, S_CL_X, S_CL_C, S_CL_OUT  // cluster entry points
-};
-}  // namespace slots
 
 // Copies host data into scratch slot `slot` (grown as needed) and returns
 // the device pointer via *out.
@@ -135,8 +136,12 @@ struct AttnGenericArgs {
 };
 int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s);
 
+// Per-row top-k of scores [nq x nd] (1 <= topk <= 32, nq <= 65535) into
+// idx/val [nq x topk]; scratch holds topk_scratch_bytes(nq, nd, topk) bytes
+// of per-chunk candidates.
+int topk_scratch_bytes(int64_t nq, int64_t nd, int32_t topk);
 int launch_topk(fa_ctx* ctx, const float* scores, int64_t nq, int64_t nd, int32_t topk, int32_t* idx, float* val,
-                hipStream_t s);
+                void* scratch, hipStream_t s);
 
 // ---- model-path kernels -------------------------------------------------------
 

@@ -140,7 +140,8 @@ int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, in
  * being unit length as cluster.Similarities requires, cluster.go:180-190) and
  * returns, per query, the topk largest scores in descending order with their
  * doc indices; equal scores are ordered by the lower index (the first-max
- * rule of (*Tensor).Argmax, tensor/reduce.go:269-297). 1 <= topk <= 32. */
+ * rule of (*Tensor).Argmax, tensor/reduce.go:269-297). 1 <= topk <= 32,
+ * nq <= 65535. NaN scores are never selected. */
 int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
                          int32_t topk, int32_t* idx, float* val);
 

@@ -6,6 +6,8 @@ are the reference's: |gpu - want| <= 1e-4 * (1 + |want|) for products
 (tensor/rope_test.go:83-102), 1e-4 for attention
 (tensor/attention_test.go:64-91). Max |delta| is printed for each case.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -231,3 +233,74 @@ def test_topk_ties_lower_index_first(ctx):
     N.check(ctx.h, N.lib().fa_similarities_topk(ctx.h, N.ptr(q), 1, N.ptr(docs), 300, 4, 5, N.ptr(idx), N.ptr(val)))
     assert idx[0, :4].tolist() == [3, 7, 100, 250]
     assert idx[0, 4] == 0  # first of the zero scores
+
+
+@pytest.mark.parametrize("nd", [32, 4097, 300_001])
+@pytest.mark.parametrize("k", [1, 8, 9, 16, 17, 32])
+def test_topk_exact_ties_across_chunks(ctx, nd, k):
+    """Scores from 21 exact levels (value/16 times a unit query), so equal
+    scores recur throughout the row: the top-k must be the first k of the
+    stable order (score descending, index ascending) whatever the split of
+    the row into chunks (reduce.go:286-289)."""
+    r = rng(nd + k)
+    nq, d = 3, 4
+    q = np.zeros((nq, d), np.float32)
+    q[:, 0] = 1.0
+    docs = np.zeros((nd, d), np.float32)
+    docs[:, 0] = r.integers(0, 21, nd) / 16.0
+    docs[:, 1] = 1.0  # orthogonal to the query
+    idx = np.empty((nq, k), np.int32)
+    val = np.empty((nq, k), np.float32)
+    N.check(ctx.h, N.lib().fa_similarities_topk(ctx.h, N.ptr(q), nq, N.ptr(docs), nd, d, k, N.ptr(idx), N.ptr(val)))
+    s = docs[:, 0]
+    want = np.lexsort((np.arange(nd), -s))[:k]
+    for i in range(nq):
+        assert idx[i].tolist() == want.tolist(), (nd, k, i)
+        assert np.array_equal(val[i], s[want])
+
+
+def test_topk_query_limit(ctx):
+    q = np.zeros((1, 4), np.float32)
+    docs = np.ones((8, 4), np.float32)
+    idx = np.empty((1, 1), np.int32)
+    rc = N.lib().fa_similarities_topk_dev(ctx.h, N.ptr(q), 65536, N.ptr(docs), 8, 4, 1, N.ptr(idx), N.ptr(idx))
+    assert rc != 0
+
+
+def test_similarities_topk_dev_fresh_context():
+    """The device-pointer entry point as the first call of a fresh context
+    (its scoring and candidate buffers are both taken on that call), twice,
+    against the oracle's top-10."""
+    c = N.Context(0)
+    L = N.lib()
+    r = rng(21)
+    nq, nd, d, k = 64, 20000, 768, 10
+    q = r.standard_normal((nq, d)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    docs = r.standard_normal((nd, d)).astype(np.float32)
+    docs /= np.linalg.norm(docs, axis=1, keepdims=True)
+    ptrs = [C.c_void_p() for _ in range(4)]
+    try:
+        for p, n in zip(ptrs, (q.nbytes, docs.nbytes, nq * k * 4, nq * k * 4)):
+            N.check(c.h, L.fa_device_alloc(c.h, n, C.byref(p)))
+        dq, dd, di, dv = ptrs
+        N.check(c.h, L.fa_memcpy_h2d(c.h, dq, q.ctypes.data, q.nbytes))
+        N.check(c.h, L.fa_memcpy_h2d(c.h, dd, docs.ctypes.data, docs.nbytes))
+        oi, ov = O.similarities_topk(q, docs, k)
+        for _ in range(2):
+            N.check(c.h, L.fa_similarities_topk_dev(c.h, dq, nq, dd, nd, d, k, di, dv))
+            idx = np.empty((nq, k), np.int32)
+            val = np.empty((nq, k), np.float32)
+            N.check(c.h, L.fa_memcpy_d2h(c.h, idx.ctypes.data, di, idx.nbytes))
+            N.check(c.h, L.fa_memcpy_d2h(c.h, val.ctypes.data, dv, val.nbytes))
+            c.sync()
+            s64 = q.astype(np.float64) @ docs.T.astype(np.float64)
+            for i in range(nq):
+                if not np.array_equal(idx[i], oi[i]):
+                    assert np.allclose(s64[i, idx[i]], s64[i, oi[i]], atol=1e-6), (i, idx[i], oi[i])
+            assert np.abs(val - ov).max() <= 1e-5
+    finally:
+        for p in ptrs:
+            if p.value:
+                L.fa_device_free(c.h, p)
+        c.close()
