@@ -2,6 +2,7 @@
 
   python -m ai_amd.bench_gemm                 # the encoder's product shapes
   python -m ai_amd.bench_gemm --shape 32768,768,768 --reps 5 --no-check
+  python -m ai_amd.bench_gemm --shape 128,2304,768 --shape 1,768,3072
 
 One JSON line per shape: mean launch time over back-to-back calls, fp32-
 equivalent TFLOP/s (2*M*N*K / time) and the max |error| against a float64
@@ -75,11 +76,12 @@ def run(shapes, reps: int, check: bool) -> list[dict]:
 
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--shape", help="M,N,K (default: the encoder's product shapes at C2 and M=32768)")
+    ap.add_argument("--shape", action="append",
+                    help="M,N,K, repeatable (default: the encoder's product shapes at C2 and M=32768)")
     ap.add_argument("--reps", type=int, default=30)
     ap.add_argument("--no-check", action="store_true", help="skip the float64 comparison")
     a = ap.parse_args()
-    shapes = [tuple(int(v) for v in a.shape.split(","))] if a.shape else SHAPES
+    shapes = [tuple(int(v) for v in sh.split(",")) for sh in a.shape] if a.shape else SHAPES
     run(shapes, a.reps, not a.no_check)
 
 

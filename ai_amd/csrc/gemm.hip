@@ -114,6 +114,21 @@ __device__ __forceinline__ int xcd_tile(const GemmParams& p) {
   return tile;
 }
 
+// The Generic epilogue of one element (the reference's order,
+// internal/blas/gemm.go:276-347); None returns v.
+template <Epi EPI>
+__device__ __forceinline__ float epi_value(const GemmParams& p, float v, int64_t row, int64_t col) {
+  if constexpr (EPI == Epi::Generic) {
+    if (p.bias) v = v + p.bias[col];
+    if (p.row_scale) v = v * p.row_scale[row];
+    if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
+    else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
+    if (p.mul) v = v * p.mul[row * p.ldm + col];
+    if (p.residual) v = v + p.residual[row * p.ldr + col];
+  }
+  return v;
+}
+
 // Writes a wave's accumulators (FM x FN blocks of 32x32 in the MFMA C
 // layout) through the epilogue. Shared by the fp32 and split-bf16 kernels,
 // whose 32x32 MFMAs have the same C layout.
@@ -151,18 +166,7 @@ __device__ __forceinline__ void store_c(const GemmParams& p, const f32x16 (&acc)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
-          if (row < M && col < N) {
-            float v = acc[i][j][r];
-            if constexpr (EPI == Epi::Generic) {
-              if (p.bias) v = v + p.bias[col];
-              if (p.row_scale) v = v * p.row_scale[row];
-              if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
-              else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
-              if (p.mul) v = v * p.mul[row * p.ldm + col];
-              if (p.residual) v = v + p.residual[row * p.ldr + col];
-            }
-            p.c[row * p.ldc + col] = v;
-          }
+          if (row < M && col < N) p.c[row * p.ldc + col] = epi_value<EPI>(p, acc[i][j][r], row, col);
         }
       }
     }
@@ -608,6 +612,162 @@ void launch_x3(GemmParams p, hipStream_t s) {
   hipLaunchKernelGGL((gemm_x3_kernel<TL, EPI>), grid, block, 0, s, p);
 }
 
+// ---------------------------------------------------------------------------
+// Split-bf16 kernel for few rows (a batch of short sentences, the pooled
+// head): the same products as gemm_x3_kernel, organised for latency instead
+// of operand reuse. A workgroup of NW waves computes one 32 x 64 tile of C
+// (two 32x32 column blocks); wave w takes the w-th of NW equal runs of the
+// tile's 32-wide K slabs and reads its operands from global memory straight
+// into MFMA operand registers (no operand is shared between waves, so no LDS
+// staging), splitting A into hi + mid + lo as it goes, with the next slab's
+// loads in flight during the current slab's MFMAs (a ring of four slabs in
+// flight measured slower). The NW partial tiles are
+// added through LDS in wave order (a fixed order: the result does not depend
+// on timing) and the workgroup's threads apply the epilogue. With K split
+// across grid.y (p.ksplit > 1) each part writes its partial product to
+// c + part * c_split without epilogue, as gemm_x3_kernel does.
+constexpr int kSmallNW = 8;
+
+template <int NW, Epi EPI>
+__global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) float red[NW][2][16][64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t M = p.m, N = p.n;
+  const float* __restrict__ A = p.a;
+  const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.b);
+  const int64_t m0 = (int64_t)(blockIdx.x / p.tiles_n) * 32;
+  const int64_t n0 = (int64_t)(blockIdx.x % p.tiles_n) * 64;
+  const int nk = p.nk / p.ksplit;  // slabs of this K part
+  const int s0 = (int)((int64_t)wave * nk / NW), s1 = (int)((int64_t)(wave + 1) * nk / NW);
+  const int64_t k_off = (int64_t)blockIdx.y * nk * 32 + (lane >> 5) * 8;
+
+  // lane l supplies row l%32 of A and column l%32 of each B block, k values
+  // 8*(l/32) .. +7 of each 16-wide step (the bijection of gemm_x3_kernel)
+  const float* arow = A + min(m0 + (lane & 31), M - 1) * p.lda + k_off;
+  const uint16_t* brow0 = B + min(n0 + (lane & 31), N - 1) * p.ldb + k_off;
+  const uint16_t* brow1 = B + min(n0 + 32 + (lane & 31), N - 1) * p.ldb + k_off;
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[j][r] = 0.f;
+
+  // one slab: two k-steps of 16; per step two float4 of A and one 16-byte
+  // vector of each B block
+  struct Regs {
+    f32x4 a[4];
+    u32x4 b[4];
+  };
+  auto load = [&](Regs& g, int kt) {
+    const int64_t o = (int64_t)kt * 32;
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+      g.a[2 * st] = *reinterpret_cast<const f32x4*>(arow + o + 16 * st);
+      g.a[2 * st + 1] = *reinterpret_cast<const f32x4*>(arow + o + 16 * st + 4);
+      g.b[2 * st] = *reinterpret_cast<const u32x4*>(brow0 + o + 16 * st);
+      g.b[2 * st + 1] = *reinterpret_cast<const u32x4*>(brow1 + o + 16 * st);
+    }
+  };
+  auto compute = [&](const Regs& g) {
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+      uint32_t h[8], m[8], l[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const Split3 sp = split3(g.a[2 * st + (e >> 2)][e & 3]);
+        h[e] = sp.h;
+        m[e] = sp.m;
+        l[e] = sp.l;
+      }
+      bf16x8 oa[3];
+      oa[0] = __builtin_bit_cast(bf16x8, (u32x4){pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]),
+                                                 pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7])});
+      oa[1] = __builtin_bit_cast(bf16x8, (u32x4){pack_hi16(m[0], m[1]), pack_hi16(m[2], m[3]),
+                                                 pack_hi16(m[4], m[5]), pack_hi16(m[6], m[7])});
+      oa[2] = __builtin_bit_cast(bf16x8, (u32x4){pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]),
+                                                 pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7])});
+      const bf16x8 b0 = __builtin_bit_cast(bf16x8, g.b[2 * st]);
+      const bf16x8 b1 = __builtin_bit_cast(bf16x8, g.b[2 * st + 1]);
+      // smallest terms first, as gemm_x3_kernel
+#pragma unroll
+      for (int t = 2; t >= 0; t--) {
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t], b0, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t], b1, acc[1], 0, 0, 0);
+      }
+    }
+  };
+  if (s0 < s1) {
+    Regs ra, rb;
+    load(ra, s0);
+    int kt = s0;
+    // the next slab's loads are issued before the current slab's MFMAs
+    for (; kt + 2 < s1; kt += 2) {
+      load(rb, kt + 1);
+      compute(ra);
+      load(ra, kt + 2);
+      compute(rb);
+    }
+    if (kt + 1 < s1) {
+      load(rb, kt + 1);
+      compute(ra);
+      compute(rb);
+    } else {
+      compute(ra);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) red[wave][j][r][lane] = acc[j][r];
+  __syncthreads();
+
+  // C element (j, r, l): row 8*(r/4) + 4*(l/32) + r%4, column 32*j + l%32
+  GemmParams q = p;
+  if (p.ksplit > 1) q.c = p.c + blockIdx.y * p.c_split;
+  if constexpr (EPI == Epi::GeGLU) {
+    if (p.ksplit == 1) {
+      // gate block 0 and up block 1 hold the same 32 features
+      const int64_t F = N / 2;
+      for (int e = tid; e < 16 * 64; e += NW * 64) {
+        const int r = e >> 6, l = e & 63;
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+          g += red[w][0][r][l];
+          u += red[w][1][r][l];
+        }
+        const int64_t row = m0 + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
+        const int64_t fcol = n0 / 2 + (l & 31);
+        if (row < M && fcol < F) p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
+      }
+      return;
+    }
+  }
+  for (int e = tid; e < 2 * 16 * 64; e += NW * 64) {
+    const int j = e >> 10, r = (e >> 6) & 15, l = e & 63;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) v += red[w][j][r][l];
+    const int64_t row = m0 + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
+    const int64_t col = n0 + 32 * j + (l & 31);
+    if (row < M && col < N)
+      q.c[row * q.ldc + col] = (EPI == Epi::Generic && p.ksplit == 1) ? epi_value<Epi::Generic>(q, v, row, col) : v;
+  }
+}
+
+template <Epi EPI>
+void launch_x3_small(GemmParams p, hipStream_t s) {
+  p.tiles_m = (int)((p.m + 31) / 32);
+  p.tiles_n = (int)((p.n + 63) / 64);
+  p.nk = (int)(p.k / 32);
+  if (p.ksplit < 1) p.ksplit = 1;
+  dim3 grid(p.tiles_m * p.tiles_n, p.ksplit), block(kSmallNW * 64);
+  hipLaunchKernelGGL((gemm_x3_small_kernel<kSmallNW, EPI>), grid, block, 0, s, p);
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 enum class TileId { k128x128 = 0, k64x64, k128x64v, k64x128, kCount };
@@ -658,9 +818,9 @@ void dispatch_tile(TileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   }
 }
 
-enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, x128x128w8, x128x256w8, kCount };
-const char* const kXTileNames[] = {"128x128", "128x64",    "128x64v",  "64x128",
-                                   "64x64",   "256x128",   "128x128w8", "128x256w8"};
+enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, x128x128w8, x128x256w8, small, kCount };
+const char* const kXTileNames[] = {"128x128", "128x64",    "128x64v",   "64x128", "64x64",
+                                   "256x128", "128x128w8", "128x256w8", "small"};
 
 // FA_GEMM_XTILE=<name> forces a split-bf16 tile shape; FA_GEMM_MFMA=f32 runs
 // bf16 weights through the fp32 MFMA kernel instead (tuning, comparison).
@@ -699,7 +859,15 @@ bool use_f32_mfma() {
 // idle (qkv at 1 840 rows: 31 vs 21 us) and with 16 slabs its longer
 // prologue and epilogue lose (EmbeddingGemma 2's K = 512 products at 5 517
 // rows: 84 vs 79 us for gate|up).
+//
+// Few rows: while its 32x64 tiles (K parts included) fit one per CU, the
+// small-M kernel (eight waves splitting each tile's K) wins on latency: at
+// 128 rows and K = 768, 8.4-8.8 vs 10.8-11.2 us per launch for N = 768,
+// 1280, 2304; one pooled row against K = 3072, 15.9 vs 33.7 us; 512 x 768
+// x 1152, 12.3 vs 15.2 us. With more tiles it loses (256 x 2304 x 768: 14.7
+// vs 11.2 us): every tile re-splits its A rows and re-reads its B columns.
 XTileId pick_xtile(int64_t m, int64_t n, int64_t k, int ksplit, Epi epi, int cus) {
+  if (((m + 31) / 32) * ((n + 63) / 64) * ksplit <= cus) return XTileId::small;
   const int64_t tiles256 = ((m + 127) / 128) * ((n + 255) / 256) * ksplit;
   if (2 * tiles256 >= 3LL * cus && k / (32LL * ksplit) >= 24) return XTileId::x128x256w8;
   const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128) * ksplit;
@@ -721,6 +889,13 @@ void dispatch_x3_epi(const GemmParams& p, Epi epi, hipStream_t s) {
 
 void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   switch (t) {
+    case XTileId::small:
+      switch (epi) {
+        case Epi::None: launch_x3_small<Epi::None>(p, s); break;
+        case Epi::Generic: launch_x3_small<Epi::Generic>(p, s); break;
+        case Epi::GeGLU: launch_x3_small<Epi::GeGLU>(p, s); break;
+      }
+      break;
     case XTileId::x128x64: dispatch_x3_epi<X128x64>(p, epi, s); break;
     case XTileId::x128x64v: dispatch_x3_epi<X128x64v>(p, epi, s); break;
     case XTileId::x64x128: dispatch_x3_epi<X64x128>(p, epi, s); break;

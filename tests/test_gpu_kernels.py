@@ -98,6 +98,25 @@ def test_matmul_fused_epilogue_vs_oracle(ctx, act):
         close(T.MatMulFused(a, b, f, ctx=ctx), O.gemm(a, b, **args), what=f"epilogue single {list(args)}")
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 3072, 768), (7, 257, 96), (33, 768, 3072), (128, 1280, 32), (200, 130, 1152)])
+def test_matmul_bf16_few_rows_fused_vs_oracle(ctx, m, n, k):
+    """bf16 [n x k] weights at few rows (the small-M split-bf16 kernel: eight
+    waves share each 32 x 64 tile's K, K = 32 leaving seven idle) with the
+    full epilogue, against the oracle's fused product."""
+    r = rng(m * 31 + n + k)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    wb = S.normal_bf16(17, f"few{m}x{n}x{k}", 0.05, (n, k))
+    wt = np.ascontiguousarray(S.bf16_to_f32(wb).T)
+    bias = r.uniform(-1, 1, n).astype(np.float32)
+    rs = r.uniform(0.5, 1.5, m).astype(np.float32)
+    mul = r.uniform(-1, 1, (m, n)).astype(np.float32)
+    res = r.uniform(-1, 1, (m, n)).astype(np.float32)
+    close(T.MatMul(a, wb, w_layout=N.FA_B_NK, ctx=ctx), O.gemm(a, wt), what=f"few rows {m}x{n}x{k}")
+    got = T.MatMulFused(a, wb, T.Fused(Bias=bias, RowScale=rs, Act=T.GELUAct, Mul=mul, Residual=res),
+                        w_layout=N.FA_B_NK, ctx=ctx)
+    close(got, O.gemm(a, wt, bias, rs, T.GELUAct, mul, res), what=f"few rows fused {m}x{n}x{k}")
+
+
 def test_matmul_padding_untouched(ctx):
     """A C with row gaps keeps the bytes between rows (gemm_test.go:50-55)."""
     r = rng(99)
