@@ -64,6 +64,12 @@ struct VarlenParams {
   int32_t window;
   float scale;
   int64_t row0;  // packed row of qkv's and out's first row
+  // kparts > 1: each item's key range is cut into kparts runs of whole
+  // tiles, one workgroup each; they write unnormalised partial outputs and
+  // (max, sum) pairs to part for attention_combine_kernel
+  int32_t kparts;
+  int64_t rows;  // rows of qkv and out (the partial buffers' row count)
+  float* part;
 };
 
 // ---- the model path's kernel ------------------------------------------------
@@ -110,9 +116,10 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   const int g = lane >> 4;
   const int lq = lane & 15;
 
-  const int seq = p.items[3 * blockIdx.x];
-  const int q0 = p.items[3 * blockIdx.x + 1];
-  const int h = p.items[3 * blockIdx.x + 2];
+  const int item = blockIdx.x / p.kparts, part = blockIdx.x % p.kparts;
+  const int seq = p.items[3 * item];
+  const int q0 = p.items[3 * item + 1];
+  const int h = p.items[3 * item + 2];
   const int hk = h / (p.H / p.Hkv);
   const int L = p.cu[seq + 1] - p.cu[seq];
   const int64_t start = p.cu[seq] - p.row0;  // the sequence's first row in qkv and out
@@ -145,6 +152,12 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   if (p.window > 0) {
     kbeg = max(0, q0 - p.window + 1);
     kend = min(L, qlast + p.window);
+  }
+  if (p.kparts > 1) {  // this part's run of tiles (possibly none)
+    const int per = ((kend - kbeg + KT - 1) / KT + p.kparts - 1) / p.kparts;
+    const int kb = kbeg + part * per * KT;
+    kend = min(kend, kb + per * KT);
+    kbeg = kb;
   }
 
   // wave w loads rows w, w+4, w+8, w+12 of K and of V, 1 KB (64 lanes x 16
@@ -250,6 +263,25 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   float l_tot = l_part + __shfl_xor(l_part, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
   const int OW = p.H * HD;
+  if (p.kparts > 1) {
+    // unnormalised O of this key run; lane lq < 16 of the first wave of the
+    // pair holds query lq's running max and sum
+    float* po = p.part + (int64_t)part * p.rows * OW;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int qr = qw0 + 4 * g + r;
+      if (qr < L) {
+        float* orow = po + (int64_t)(start + qr) * OW + (int64_t)h * HD + dofs;
+#pragma unroll
+        for (int db = 0; db < HALF / 16; db++) orow[db * 16 + lq] = oacc[db][r];
+      }
+    }
+    if (half == 0 && g == 0 && qvalid) {
+      float2* pml = reinterpret_cast<float2*>(p.part + (int64_t)p.kparts * p.rows * OW);
+      pml[((int64_t)part * p.rows + start + qi) * p.H + h] = make_float2(m_run, l_tot);
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int qr = qw0 + 4 * g + r;
@@ -259,6 +291,47 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
 #pragma unroll
       for (int db = 0; db < HALF / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
     }
+  }
+}
+
+// Sums the key runs of a split item: with M the largest run max, O =
+// (sum_p e^(m_p - M) O_p) / (sum_p e^(m_p - M) l_p), runs added in order.
+// One wave per (row, head), 16 bytes per lane per 256 dimensions.
+template <int HD>
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ part, int kparts,
+                                                                int64_t rows, int H, float* __restrict__ out) {
+  const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // row * H + head
+  if (id >= rows * H) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t OW = (int64_t)H * HD;
+  const int64_t row = id / H, h = id % H;
+  const float2* ml = reinterpret_cast<const float2*>(part + (int64_t)kparts * rows * OW);
+  float M = kNegBig;
+  for (int q = 0; q < kparts; q++) M = fmaxf(M, ml[q * rows * H + id].x);
+  float Lsum = 0.f;
+  f32x4 acc[HD / 256];
+#pragma unroll
+  for (int c = 0; c < HD / 256; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < kparts; q++) {
+    const float2 v = ml[q * rows * H + id];
+    const float w = exp_flush(v.x - M);
+    Lsum += w * v.y;
+    const float* src = part + (q * rows + row) * OW + h * HD + lane * 4;
+#pragma unroll
+    for (int c = 0; c < HD / 256; c++) {
+      const f32x4 o = *reinterpret_cast<const f32x4*>(src + c * 256);
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[c][e] += w * o[e];
+    }
+  }
+  const float inv = 1.f / Lsum;
+  float* dst = out + row * OW + h * HD + lane * 4;
+#pragma unroll
+  for (int c = 0; c < HD / 256; c++) {
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = acc[c][e] * inv;
+    *reinterpret_cast<f32x4*>(dst + c * 256) = o;
   }
 }
 
@@ -336,13 +409,25 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   if (a.Hkv <= 0 || a.H % a.Hkv != 0)
     return set_error(ctx, FA_ERR_ARG, "attention: %d query heads not a multiple of %d kv heads", a.H, a.Hkv);
   if (n_items == 0) return FA_OK;
+  if (a.kparts < 1 || a.kparts > kMaxKeyParts || (a.kparts > 1 && (!a.part || a.rows <= 0)))
+    return set_error(ctx, FA_ERR_ARG, "attention: %d key parts (1..%d, > 1 needs a partial buffer)", a.kparts,
+                     kMaxKeyParts);
   VarlenParams p;
   p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items; p.row0 = a.row0;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
+  p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
+  const dim3 grid((unsigned)((int64_t)n_items * a.kparts));
   if (a.D == 256)
-    hipLaunchKernelGGL(attention_varlen_kernel<256>, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
+    hipLaunchKernelGGL(attention_varlen_kernel<256>, grid, dim3(DL_NT), 0, s, p);
   else
-    hipLaunchKernelGGL(attention_varlen_kernel<512>, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
+    hipLaunchKernelGGL(attention_varlen_kernel<512>, grid, dim3(DL_NT), 0, s, p);
+  if (a.kparts > 1) {
+    const dim3 g2((unsigned)((a.rows * a.H + 3) / 4));
+    if (a.D == 256)
+      hipLaunchKernelGGL(attention_combine_kernel<256>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, a.H, a.out);
+    else
+      hipLaunchKernelGGL(attention_combine_kernel<512>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, a.H, a.out);
+  }
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

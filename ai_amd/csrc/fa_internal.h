@@ -186,7 +186,18 @@ struct AttnVarlenArgs {
   int32_t window;
   float scale;
   int64_t row0 = 0;  // packed row held by qkv's and out's first row (items' sequences start at or after it)
+  // kparts > 1 (at most kMaxKeyParts): every item's keys are cut into kparts
+  // runs, one workgroup each, summed by a second pass; part holds
+  // attention_part_floats(kparts, rows, H, D) floats and rows is the row
+  // count of qkv and out (every row a query)
+  int32_t kparts = 1;
+  int64_t rows = 0;
+  float* part = nullptr;
 };
+constexpr int kMaxKeyParts = 4;
+inline int64_t attention_part_floats(int kparts, int64_t rows, int H, int D) {
+  return (int64_t)kparts * rows * H * (D + 2);
+}
 // d_items holds n_items triples (sequence, first query, head): one work item
 // per query block of attention_varlen_qblock() queries and head.
 int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const int32_t* d_items, int32_t n_items,

@@ -39,6 +39,7 @@ namespace fa {
 namespace {
 
 constexpr int kMaxMicrobatches = 4;  // streams a forward may use (micro-batches)
+constexpr int64_t kAttnSplitRows = 1024;  // key-split attention only for batches up to this many tokens
 
 bool bf16_exact(float f, uint16_t* out) {
   uint32_t u;
@@ -659,7 +660,19 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
                         (v2 ? (int64_t)NL * P : 0);
   int maxw = std::max(d, std::max(full, v2 ? m->E : d));
   for (int o : m->dense_out) maxw = std::max(maxw, o);
-  const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw)) * 4 + 4096;
+  // Attention over few items (a short batch on one stream) cuts each
+  // item's keys into up to kMaxKeyParts runs of whole tiles, one workgroup
+  // each, so that more CUs share the key loop: C1's 12 items (128 tokens, 3
+  // heads) become 48 workgroups of two tiles.
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const int64_t n_items_all = n_items;
+  int kparts = 1;
+  if (groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
+    kparts = (int)std::min<int64_t>(fa::kMaxKeyParts, cus / std::max<int64_t>(n_items_all, 1));
+    kparts = std::max(1, std::min(kparts, (T + 31) / 32));  // at least two 16-key tiles per run
+  }
+  const int64_t part_floats = kparts > 1 ? fa::attention_part_floats(kparts, M, H, m->max_hd / H) : 0;
+  const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 4096;
   if ((rc = m->ws.ensure(ctx, ws_bytes))) return rc;
   float* x = m->ws.as<float>();
   float* xn = x + M * d;
@@ -671,6 +684,8 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   float* pooled = ple + (v2 ? M * NL * P : 0);
   float* hbuf0 = pooled + (size_t)B * d;
   float* hbuf1 = hbuf0 + (size_t)B * maxw;
+  float* attn_part = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(hbuf1 + (size_t)B * maxw) + 255) &
+                                              ~(uintptr_t)255);
   hipStream_t s = ctx->stream;
   // ---- row plan on device ----
   if ((rc = fa::launch_row_plan(ctx, cu_d, B, T, M, row_src_d, pos_d, s))) return rc;
@@ -714,7 +729,6 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     // groups of about 1 840: 4 % faster split); with more tiles the second
     // partial's writes and reads cost more than the fill gains (C5's three
     // groups of about 5 970 rows: 4.7 % faster unsplit).
-    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int64_t n_tiles = ((rows + 127) / 128) * ((d + 127) / 128) * groups;
     const int ks = n_tiles < 2LL * cus ? ksplit : 1;
     // per product: split only when K divides into whole 32-wide slabs
@@ -753,6 +767,9 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       a.qkv = qkvr; a.out = attr; a.row0 = r0; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
       a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
       a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
+      if (kparts > 1) {
+        a.kparts = kparts; a.rows = rows; a.part = attn_part;
+      }
       double pairs = 0;
       if (m->profiling) {
         for (int b = 0; b < B; b++) {
