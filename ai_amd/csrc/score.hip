@@ -5,13 +5,14 @@
 // are never selected.
 //
 // Two passes, one wavefront per workgroup. Pass 1: each (query, chunk of
-// the row) wave scans its chunk with four coalesced loads in flight per
-// lane, every lane keeping its best KK (value, index) pairs sorted in
-// registers (a candidate below the lane's k-th is dropped at once), then k
-// rounds of a wave-wide arg-best over the lanes' list heads (shuffles, no
-// barriers) write the chunk's top k. Pass 2: one wave per query merges the
-// chunks' candidates the same way. Every comparison uses the full order
-// (value, then index), so the result does not depend on the chunking.
+// up to 16 384 scores) wave scans its chunk with eight 16-byte loads in
+// flight per lane, keeping the chunk's best k so far as one sorted list spread over
+// lanes 0..k-1; a ballot against the list's k-th entry filters each step's
+// 64 scores, so after the first few hundred scores a step costs a load, a
+// compare and a ballot, and the rare survivors are inserted one at a time
+// with shuffles. Pass 2: one wave per query merges the chunks' candidates
+// the same way. Every comparison uses the full order (value, then index),
+// so the result does not depend on the chunking.
 #include <algorithm>
 #include <cstdint>
 
@@ -20,120 +21,128 @@
 namespace fa {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kMaxK = 32;
-constexpr int kChunk = 4096;    // scores per pass-1 wave
+constexpr int kChunk = 16384;   // scores per pass-1 wave
 constexpr int kMaxChunks = 64;  // per row
 
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);
 }
 
-// A lane's best k candidates, sorted, in the first k of KK registers; (tv,
-// ti) is the k-th (the admission threshold).
-template <int KK>
-struct LaneList {
-  float lv[KK];
-  int li[KK];
+// The wave's best k candidates so far as one sorted list spread over lanes
+// 0..k-1 (lane r holds the r-th best; lanes >= k hold nothing that
+// matters), with the k-th best (the admission threshold) in every lane.
+// A step offers one candidate per lane: a ballot finds the lanes whose
+// candidate beats the threshold (after the first few hundred scores, rarely
+// any), and each of those is inserted in lane order: its rank is the number
+// of list entries better than it, entries from that rank on move up one lane.
+struct WaveList {
+  float lv = -INFINITY;
+  int li = INT32_MAX;
   float tv = -INFINITY;
   int ti = INT32_MAX;
-  __device__ __forceinline__ LaneList() {
-#pragma unroll
-    for (int i = 0; i < KK; i++) {
-      lv[i] = -INFINITY;
-      li[i] = INT32_MAX;
-    }
-  }
-  __device__ __forceinline__ void insert(int k, float v, int j) {
-    if (!better(v, j, tv, ti)) return;  // also drops NaN
-    float cv = v;
-    int ci = j;
-    bool shifting = false;  // past the insertion point every entry moves down one
-#pragma unroll
-    for (int i = 0; i < KK; i++) {
-      if (i < k && (shifting || better(cv, ci, lv[i], li[i]))) {
-        shifting = true;
-        const float t = lv[i];
-        const int u = li[i];
-        lv[i] = cv;
-        li[i] = ci;
-        cv = t;
-        ci = u;
+
+  __device__ __forceinline__ void offer(int k, int lane, float v, int j) {
+    uint64_t mask = __ballot(better(v, j, tv, ti));  // NaN never passes
+    while (mask) {
+      const int src = __ffsll((unsigned long long)mask) - 1;
+      mask &= mask - 1;
+      const float cv = __shfl(v, src, 64);
+      const int ci = __shfl(j, src, 64);
+      if (!better(cv, ci, tv, ti)) continue;  // the threshold rose meanwhile
+      const uint64_t above = __ballot(lane < k && better(lv, li, cv, ci));
+      const int pos = __popcll((unsigned long long)above);
+      const float uv = __shfl_up(lv, 1, 64);
+      const int ui = __shfl_up(li, 1, 64);
+      if (lane > pos) {
+        lv = uv;
+        li = ui;
+      } else if (lane == pos) {
+        lv = cv;
+        li = ci;
       }
+      tv = __shfl(lv, k - 1, 64);
+      ti = __shfl(li, k - 1, 64);
     }
-#pragma unroll
-    for (int i = 0; i < KK; i++)
-      if (i == k - 1) {
-        tv = lv[i];
-        ti = li[i];
-      }
   }
 };
 
-// k rounds of a wave-wide arg-best over the lanes' list heads; lane 0
-// writes result r to out_v[r] (if out_v) and out_i[r]
-template <int KK>
-__device__ __forceinline__ void wave_select(LaneList<KK>& L, int k, int lane, float* out_v, int32_t* out_i) {
-  float (&lv)[KK] = L.lv;
-  int (&li)[KK] = L.li;
-  for (int r = 0; r < k; r++) {
-    float v = lv[0];
-    int i = li[0];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(v, o, 64);
-      const int oi = __shfl_xor(i, o, 64);
-      if (better(ov, oi, v, i)) {
-        v = ov;
-        i = oi;
-      }
-    }
-    if (lane == 0) {
-      if (out_v) out_v[r] = v;
-      out_i[r] = i;
-    }
-    // the owner (unique index; an exhausted list offers INT32_MAX) pops its head
-    if (li[0] == i && lv[0] == v) {
-#pragma unroll
-      for (int t = 0; t + 1 < KK; t++) {
-        lv[t] = lv[t + 1];
-        li[t] = li[t + 1];
-      }
-      lv[KK - 1] = -INFINITY;
-      li[KK - 1] = INT32_MAX;
-    }
-  }
-}
-
-template <int KK>
+// Pass 1: the top k of scores[q, c*chunk .. min(nd, (c+1)*chunk)) to
+// cv/ci[(q * nchunks + c) * k ..]. VEC = 4 (rows and chunks 16-byte
+// aligned): eight 16-byte loads per lane, 2 048 scores per round, the next
+// round loading while the current one is offered; VEC = 1: four 4-byte loads.
+template <int VEC>
 __global__ __launch_bounds__(64) void topk_chunk_kernel(const float* __restrict__ scores, int64_t nd, int k,
                                                         int chunk, float* __restrict__ cv, int32_t* __restrict__ ci) {
+  constexpr int U = VEC == 4 ? 8 : 4;  // loads in flight per lane
+  constexpr int ROUND = 64 * VEC * U;  // scores per round
   const int c = blockIdx.x, nchunks = gridDim.x;
   const int64_t q = blockIdx.y;
   const int lane = threadIdx.x;
   const float* row = scores + q * nd;
-  LaneList<KK> L;
+  WaveList W;
   const int64_t j0 = (int64_t)c * chunk, j1 = min(nd, j0 + chunk);
-  for (int64_t j = j0 + lane; j < j1; j += 256) {
-    float v[4];
+  if constexpr (VEC == 4) {
+    // the next round's loads are issued before the current round's offers
+    auto load = [&](f32x4 (&v)[U], int64_t base) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) v[u] = j + 64 * u < j1 ? row[j + 64 * u] : -INFINITY;
+      for (int u = 0; u < U; u++) {
+        const int64_t j = base + 4 * (lane + 64 * u);  // j1 is a multiple of 4
+        v[u] = j < j1 ? *reinterpret_cast<const f32x4*>(row + j) : f32x4{NAN, NAN, NAN, NAN};
+      }
+    };
+    auto offer_all = [&](const f32x4 (&v)[U], int64_t base) {
 #pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (j + 64 * u < j1) L.insert(k, v[u], (int)(j + 64 * u));
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) W.offer(k, lane, v[u][e], (int)(base + 4 * (lane + 64 * u) + e));
+    };
+    f32x4 va[U], vb[U];
+    load(va, j0);
+    for (int64_t base = j0; base < j1; base += 2 * ROUND) {
+      load(vb, base + ROUND);
+      offer_all(va, base);
+      if (base + ROUND >= j1) break;
+      load(va, base + 2 * ROUND);
+      offer_all(vb, base + ROUND);
+    }
+  } else {
+    for (int64_t base = j0; base < j1; base += ROUND) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int64_t j = base + lane + 64 * u;
+        v[u] = j < j1 ? row[j] : NAN;
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) W.offer(k, lane, v[u], (int)(base + lane + 64 * u));
+    }
   }
-  const int64_t o = (q * nchunks + c) * k;
-  wave_select<KK>(L, k, lane, cv + o, ci + o);
+  if (lane < k) {
+    const int64_t o = (q * nchunks + c) * k + lane;
+    cv[o] = W.lv;
+    ci[o] = W.li;
+  }
 }
 
-template <int KK>
+// Pass 2: one wave per query merges its chunks' ncand candidates.
 __global__ __launch_bounds__(64) void topk_merge_kernel(const float* __restrict__ cv, const int32_t* __restrict__ ci,
                                                         int ncand, int k, int32_t* __restrict__ idx,
                                                         float* __restrict__ val) {
   const int64_t q = blockIdx.x;
   const int lane = threadIdx.x;
-  LaneList<KK> L;
-  for (int t = lane; t < ncand; t += 64) L.insert(k, cv[q * ncand + t], ci[q * ncand + t]);
-  wave_select<KK>(L, k, lane, val ? val + q * k : nullptr, idx + q * k);
+  WaveList W;
+  for (int t0 = 0; t0 < ncand; t0 += 64) {
+    const int t = t0 + lane;
+    const bool ok = t < ncand;
+    W.offer(k, lane, ok ? cv[q * ncand + t] : NAN, ok ? ci[q * ncand + t] : INT32_MAX);
+  }
+  if (lane < k) {
+    if (val) val[q * k + lane] = W.lv;
+    idx[q * k + lane] = W.li;
+  }
 }
 
 }  // namespace
@@ -151,21 +160,17 @@ int launch_topk(fa_ctx* ctx, const float* scores, int64_t nq, int64_t nd, int32_
   if (nq == 0) return FA_OK;
   if (nq > 65535) return set_error(ctx, FA_ERR_ARG, "Similarities top-k: %lld queries > 65535", (long long)nq);
   const int64_t nchunks = std::min<int64_t>(kMaxChunks, (nd + kChunk - 1) / kChunk);
-  const int64_t chunk = (nd + nchunks - 1) / nchunks;
+  const bool vec = nd % 4 == 0 && (reinterpret_cast<uintptr_t>(scores) & 15) == 0;
+  const int64_t chunk = ((nd + nchunks - 1) / nchunks + 3) / 4 * 4;  // a multiple of 4
   float* cv = static_cast<float*>(scratch);
   int32_t* ci = reinterpret_cast<int32_t*>(cv + nq * nchunks * topk);
   const int ncand = (int)(nchunks * topk);
   dim3 g1((unsigned)nchunks, (unsigned)nq);
-  if (topk <= 8) {
-    hipLaunchKernelGGL(topk_chunk_kernel<8>, g1, dim3(64), 0, s, scores, nd, topk, (int)chunk, cv, ci);
-    hipLaunchKernelGGL(topk_merge_kernel<8>, dim3((unsigned)nq), dim3(64), 0, s, cv, ci, ncand, topk, idx, val);
-  } else if (topk <= 16) {
-    hipLaunchKernelGGL(topk_chunk_kernel<16>, g1, dim3(64), 0, s, scores, nd, topk, (int)chunk, cv, ci);
-    hipLaunchKernelGGL(topk_merge_kernel<16>, dim3((unsigned)nq), dim3(64), 0, s, cv, ci, ncand, topk, idx, val);
-  } else {
-    hipLaunchKernelGGL(topk_chunk_kernel<32>, g1, dim3(64), 0, s, scores, nd, topk, (int)chunk, cv, ci);
-    hipLaunchKernelGGL(topk_merge_kernel<32>, dim3((unsigned)nq), dim3(64), 0, s, cv, ci, ncand, topk, idx, val);
-  }
+  if (vec)
+    hipLaunchKernelGGL(topk_chunk_kernel<4>, g1, dim3(64), 0, s, scores, nd, topk, (int)chunk, cv, ci);
+  else
+    hipLaunchKernelGGL(topk_chunk_kernel<1>, g1, dim3(64), 0, s, scores, nd, topk, (int)chunk, cv, ci);
+  hipLaunchKernelGGL(topk_merge_kernel, dim3((unsigned)nq), dim3(64), 0, s, cv, ci, ncand, topk, idx, val);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

@@ -254,13 +254,14 @@ def test_topk_ties_lower_index_first(ctx):
     assert idx[0, 4] == 0  # first of the zero scores
 
 
-@pytest.mark.parametrize("nd", [32, 4097, 300_001])
+@pytest.mark.parametrize("nd", [32, 4097, 300_000, 300_001])
 @pytest.mark.parametrize("k", [1, 8, 9, 16, 17, 32])
 def test_topk_exact_ties_across_chunks(ctx, nd, k):
     """Scores from 21 exact levels (value/16 times a unit query), so equal
     scores recur throughout the row: the top-k must be the first k of the
     stable order (score descending, index ascending) whatever the split of
-    the row into chunks (reduce.go:286-289)."""
+    the row into chunks (reduce.go:286-289). nd % 4 == 0 takes the 16-byte
+    load path."""
     r = rng(nd + k)
     nq, d = 3, 4
     q = np.zeros((nq, d), np.float32)
