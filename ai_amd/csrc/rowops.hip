@@ -279,8 +279,18 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
   const int c = blockIdx.y * 64 + tx;
   const int r0 = cu[b], r1 = cu[b + 1];
   float s = 0.f;
-  if (c < d)
-    for (int r = r0 + ty; r < r1; r += 4) s += h[(int64_t)r * d + c];
+  if (c < d) {
+    // rows ty, ty + 4, ... added in order, eight loads in flight
+    int r = r0 + ty;
+    for (; r + 28 < r1; r += 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = h[(int64_t)(r + 4 * u) * d + c];
+#pragma unroll
+      for (int u = 0; u < 8; u++) s += v[u];
+    }
+    for (; r < r1; r += 4) s += h[(int64_t)r * d + c];
+  }
   part[ty][tx] = s;
   __syncthreads();
   if (ty == 0 && c < d) {

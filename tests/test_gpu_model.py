@@ -144,6 +144,20 @@ def test_c3_sliding_band(models):
     compare(got[:4], ref, "C3[0:4]")
 
 
+def test_key_split_attention_with_sliding_band(models):
+    """Two full 512-token sequences (1 024 tokens on one stream, 96
+    attention items): the attention cuts each item's keys into runs (the
+    key-split path) while the 20 sliding layers mask |i-j| >= 257. The
+    first sequence against the oracle, both against their rows in C3's
+    64-sequence batch (no key split)."""
+    gm, om = models
+    b = S.make_batch("C3")
+    two = gm.embed_ids(b.ids[:2], b.lengths[:2])
+    compare(two[:1], om.embed(b.ids[:1], b.lengths[:1]), "C3[0] key-split")
+    full = gm.embed_ids(b.ids, b.lengths)
+    assert cos_rows(two, full[:2]).min() >= 0.99999
+
+
 def test_c4_long_sequences(models):
     """C4 (8 x 2048, lengths 1024..2048): the GPU batch against the oracle for
     the shortest sequence (band active, far beyond one attention tile)."""
