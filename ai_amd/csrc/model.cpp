@@ -156,13 +156,27 @@ int64_t microbatch_min_rows() {
 // measured best on MI355X at 5 517, 11 550 and 32 768 tokens (C2: 6.41 ms
 // per forward on one stream, 5.49 with two groups, 5.43 with three, 5.92
 // with four) and within 3 % of best at 17 923.
-int microbatch_count() {
+// FA_MICROBATCH_GROUPS=<2..4> forces the group count (tuning); 0 when unset.
+int microbatch_count_forced() {
   static const int v = [] {
     const char* e = std::getenv("FA_MICROBATCH_GROUPS");
-    const int n = e ? std::atoi(e) : 3;
-    return std::max(2, std::min(n, kMaxMicrobatches));
+    if (!e) return 0;
+    return std::max(2, std::min(std::atoi(e), kMaxMicrobatches));
   }();
   return v;
+}
+
+// Group count by the batch, from sweeps of 2, 3 and 4 groups on MI355X:
+// long sequences (the mean key count per token, sum L^2 / sum L, at least
+// 1 024) make the forward attention-bound and gain from a fourth stream
+// (C4, 8 x 1 024..2 048: 16.29 -> 15.27 ms); from 16 384 tokens the
+// products are large enough on their own and two groups keep their tiles
+// full (C3, 64 x 512: 34.25 -> 33.59 ms; C5 equal); else three (C2: 5.46 ms
+// against 5.81 with two and 5.76 with four).
+int microbatch_count(int64_t tokens, double sum_l2) {
+  if (const int f = microbatch_count_forced()) return f;
+  if (sum_l2 >= 1024.0 * (double)tokens) return 4;
+  return tokens >= 16384 ? 2 : 3;
 }
 
 // Brackets one launch with events when profiling.
@@ -606,7 +620,9 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   int groups = 1;
   int gb[fa::kMaxMicrobatches + 1] = {0, B};
   if (M >= fa::microbatch_min_rows() && !m->profiling) {
-    const int want = std::min(fa::microbatch_count(), B);
+    double sum_l2 = 0;
+    for (int i = 0; i < B; i++) sum_l2 += (double)lengths[i] * lengths[i];
+    const int want = std::min(fa::microbatch_count(M, sum_l2), B);
     int b = 0;
     int64_t cum = 0;
     for (int g = 1; g < want; g++) {

@@ -266,7 +266,8 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
 /* Same computation on device-resident data: d_ids [B x T] on the device,
  * lengths on the HOST (they set the launch shapes), d_out [B x dim] on the
  * device. Enqueues on fa_stream(ctx) and returns without waiting. From
- * 2 048 tokens on, the layers of three token-balanced groups of sequences
+ * 2 048 tokens on, the layers of two to four token-balanced groups of
+ * sequences (four for long sequences, two from 16 384 tokens, else three)
  * run on the model's own extra streams, forked from and joined back into
  * fa_stream(ctx), so the call stays ordered on that stream. */
 int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,

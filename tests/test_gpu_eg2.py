@@ -102,8 +102,8 @@ def test_gpu_matches_oracle(eg2, B, T, lo):
 
 
 def test_gpu_microbatches(eg2):
-    """From 2 048 tokens the batch runs as three token-balanced groups of
-    sequences on three streams (per-layer inputs indexed by the group's
+    """From 2 048 tokens the batch runs as token-balanced groups of
+    sequences on their own streams (per-layer inputs indexed by the group's
     rows): each sequence equals its single-sequence run, the first and last
     the oracle."""
     shape, om, gm = eg2

@@ -82,8 +82,8 @@ def test_batch_and_padding_invariance(models):
 
 @pytest.mark.parametrize("lengths", [[2000, 7, 300], [1500, 1500], [40] * 60 + [2048]])
 def test_microbatch_groups_match_single_sequences(models, lengths):
-    """From 2 048 tokens a batch runs as up to three token-balanced groups of
-    sequences on three streams; with one dominant sequence, two sequences
+    """From 2 048 tokens a batch runs as two to four token-balanced groups
+    of sequences on their own streams; with one dominant sequence, two sequences
     or many short ones every sequence's embedding still equals its
     single-sequence run, and the shortest one the oracle's."""
     gm, om = models
