@@ -194,7 +194,7 @@ struct AttnVarlenArgs {
   int64_t rows = 0;
   float* part = nullptr;
 };
-constexpr int kMaxKeyParts = 4;
+constexpr int kMaxKeyParts = 8;
 inline int64_t attention_part_floats(int kparts, int64_t rows, int H, int D) {
   return (int64_t)kparts * rows * H * (D + 2);
 }

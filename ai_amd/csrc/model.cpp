@@ -156,6 +156,17 @@ int64_t microbatch_min_rows() {
 // measured best on MI355X at 5 517, 11 550 and 32 768 tokens (C2: 6.41 ms
 // per forward on one stream, 5.49 with two groups, 5.43 with three, 5.92
 // with four) and within 3 % of best at 17 923.
+// FA_ATTN_KEY_PARTS=<1..8> forces the key runs of the short-batch attention
+// (tuning); 0 when unset.
+int attention_key_parts_forced() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_ATTN_KEY_PARTS");
+    if (!e) return 0;
+    return std::max(1, std::min(std::atoi(e), kMaxKeyParts));
+  }();
+  return v;
+}
+
 // FA_MICROBATCH_GROUPS=<2..4> forces the group count (tuning); 0 when unset.
 int microbatch_count_forced() {
   static const int v = [] {
@@ -684,8 +695,9 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   const int64_t n_items_all = n_items;
   int kparts = 1;
   if (groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
-    kparts = (int)std::min<int64_t>(fa::kMaxKeyParts, cus / std::max<int64_t>(n_items_all, 1));
+    kparts = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_all, 1));
     kparts = std::max(1, std::min(kparts, (T + 31) / 32));  // at least two 16-key tiles per run
+    if (const int f = fa::attention_key_parts_forced()) kparts = f;
   }
   const int64_t part_floats = kparts > 1 ? fa::attention_part_floats(kparts, M, H, m->max_hd / H) : 0;
   const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 4096;
