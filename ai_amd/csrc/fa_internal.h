@@ -210,8 +210,10 @@ int attention_varlen_qblock();
 int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t nseq, int32_t d, float* pooled,
                 hipStream_t s);
 
-// out[b, :dim] = y[b, :dim] / sqrt(sum y^2 + 1e-12)
-int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int32_t dim, float* out, hipStream_t s);
+// out[b, :dim] = y[b, :dim] / sqrt(sum y^2 + 1e-12), y the sum of `parts`
+// partial products at y + p * pstride (added in part order)
+int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int32_t dim, float* out, hipStream_t s,
+                  int32_t parts = 1, int64_t pstride = 0);
 
 // Final RMSNorm with (1+g) of x rows into h.
 int launch_final_norm(fa_ctx* ctx, const float* x, int64_t rows, int32_t d, const float* g, float eps, float* h,

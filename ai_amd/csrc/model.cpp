@@ -922,10 +922,21 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     cur_w = m->E;
     nb = 1;
   }
+  // the last dense product splits K (its few rows give few tiles: 3072 -> 768
+  // for one pooled row is 12 of them) and the L2 norm adds the partials
+  int head_parts = 1;
   for (int i = 0; i < c.n_dense; i++) {
     fa::GemmArgs g;
     g.m = B; g.n = m->dense_out[i]; g.k = cur_w; g.a = cur; g.lda = cur_w; g.b = m->dense[i]; g.ldb = cur_w;
     g.c = bufs[(i + nb) & 1]; g.ldc = m->dense_out[i];
+    if (i + 1 == c.n_dense) {
+      for (int ks : {4, 2})
+        if (cur_w % (32 * ks) == 0 && (int64_t)ks * m->dense_out[i] <= maxw) {
+          head_parts = ks;
+          break;
+        }
+      g.ksplit = head_parts; g.c_split = (int64_t)B * m->dense_out[i];
+    }
     fa::Probe pr(m, FA_K_GEMM_HEAD, 2.0 * B * m->dense_out[i] * cur_w, 0);
     if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
     pr.done();
@@ -934,7 +945,9 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   }
   {
     fa::Probe pr(m, FA_K_POOL_L2, 0, (double)B * dim * 8.0);
-    if ((rc = fa::launch_l2norm(ctx, cur, B, cur_w, dim, d_out, s))) return rc;
+    if ((rc = fa::launch_l2norm(ctx, cur, B, cur_w, dim, d_out, s, head_parts,
+                                (int64_t)B * cur_w)))
+      return rc;
     pr.done();
   }
   return FA_OK;

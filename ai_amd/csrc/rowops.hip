@@ -301,17 +301,46 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
 }
 
 // out[b, :dim] = y[b, :dim] / sqrt(sum(y[b, :dim]^2) + 1e-12); one wave per row.
+// y = the sum of `parts` partial products y_p = y + p * pstride (K-split
+// head product), added in part order.
 __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ y, int nseq, int width, int dim,
-                                                     float* __restrict__ out) {
+                                                     int parts, int64_t pstride, float* __restrict__ out) {
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (b >= nseq) return;
   const float* r = y + (int64_t)b * width;
+  auto value = [&](int i) {
+    float v = r[i];
+    for (int p = 1; p < parts; p++) v += r[p * pstride + i];
+    return v;
+  };
+  constexpr int kHeld = 16;  // values per lane kept in registers (dim <= 1 024)
   float s = 0.f;
-  for (int i = lane; i < dim; i += kWave) s = fmaf(r[i], r[i], s);
+  if (dim <= kWave * kHeld) {
+    float v[kHeld];
+#pragma unroll
+    for (int t = 0; t < kHeld; t++) {
+      const int i = lane + kWave * t;
+      v[t] = i < dim ? value(i) : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < kHeld; t++) s = fmaf(v[t], v[t], s);
+    s = wave_sum(s);
+    const float nrm = sqrtf(s + 1e-12f);
+#pragma unroll
+    for (int t = 0; t < kHeld; t++) {
+      const int i = lane + kWave * t;
+      if (i < dim) out[(int64_t)b * dim + i] = v[t] / nrm;
+    }
+    return;
+  }
+  for (int i = lane; i < dim; i += kWave) {
+    const float v = value(i);
+    s = fmaf(v, v, s);
+  }
   s = wave_sum(s);
   const float nrm = sqrtf(s + 1e-12f);
-  for (int i = lane; i < dim; i += kWave) out[(int64_t)b * dim + i] = r[i] / nrm;
+  for (int i = lane; i < dim; i += kWave) out[(int64_t)b * dim + i] = value(i) / nrm;
 }
 
 __global__ __launch_bounds__(256) void row_plan_kernel(const int32_t* __restrict__ cu, int nseq, int T, int64_t rows,
@@ -432,9 +461,12 @@ int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t 
   return FA_OK;
 }
 
-int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int32_t dim, float* out, hipStream_t s) {
+int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int32_t dim, float* out, hipStream_t s,
+                  int32_t parts, int64_t pstride) {
   if (nseq == 0) return FA_OK;
-  hipLaunchKernelGGL(l2norm_kernel, dim3(blocks_for(nseq, 4)), dim3(256), 0, s, y, nseq, width, dim, out);
+  if (parts < 1) return set_error(ctx, FA_ERR_ARG, "l2norm: %d parts", parts);
+  hipLaunchKernelGGL(l2norm_kernel, dim3(blocks_for(nseq, 4)), dim3(256), 0, s, y, nseq, width, dim, parts, pstride,
+                     out);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
