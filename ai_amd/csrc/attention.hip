@@ -335,6 +335,287 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
   }
 }
 
+// ---- split-bf16 model-path kernel (head_dim 256) --------------------------------
+// attention_planes_kernel computes what attention_varlen_kernel<256> does on
+// the bf16 MFMA (v_mfma_f32_16x16x32_bf16, 16x the fp32 MFMA's rate) with
+// fp32 accuracy: every fp32 operand x is the exact sum of three bf16 terms
+// x0 + x1 + x2 (split3: 8 mantissa bits each), and a product a.b is the sum
+// of the six term products ai.bj with i + j <= 2 (the three dropped ones
+// are below 2^-24 relative), accumulated in fp32.
+//
+// Operands. q (fp32, normed and rotated in qkv) is split in registers once
+// per work item. Keys and values arrive split, written by
+// qknorm_rope_planes_kernel: keys [row][kv head][term][256]; values in quads
+// of four keys of one sequence (every sequence starts a quad, cu_quads),
+// [quad][kv head][dim][16]: per dimension the two 16-byte windows (V0|V1)
+// and (V0|V2) of the four keys' terms, in that order for dims with bit 3
+// clear and swapped otherwise (the 16 lanes reading one window per
+// instruction then cover all LDS banks).
+//
+// Formulation (lane l: g = l / 16, lq = l % 16). Work item and wave pairs as
+// in attention_varlen_kernel: waves 2b and 2b+1 own queries q0 + 16b .. +15
+// and the two 128-dim halves. Per tile of 16 keys:
+//   S^T[key, query] = K . Q^T over the wave's 128 dims: A = a key term from
+//   LDS (lane: key lq, dims 8g..8g+7 of a 32-dim chunk), B = a q term;
+//   4 chunks x 6 term pairs = 24 MFMAs; lane l ends with query lq's scores
+//   against keys 4g+r. The pair adds its partial scores through LDS in one
+//   fixed order, then the online softmax (lane-local + two shuffles).
+//   O^T[dim, query] += V^T . P^T: the 32 k-slots of one MFMA carry two term
+//   pairs of the 16 keys (slot 8g+j: key 4g+(j&3) of the first pair for
+//   j < 4, of the second for j >= 4), so A is one window read (lane: dim lq
+//   of the 16-dim block, quad g) and B the lane's own four probabilities'
+//   terms: (V0|V2)x(P2|P0), (V0|V1)x(P1|P1), (V0|V1)x(P0|P0) cover the six
+//   pairs in 3 MFMAs per 16 dims. Query lq sits in lane l of the O^T
+//   accumulator, so the softmax rescale (skipped while no row maximum of
+//   the wave moved) and the final 1/sum are lane-local.
+// MFMA time per tile and wave: 48 x 16 cycles, against 64 x 32 for the
+// fp32-MFMA kernel.
+//
+// Loads: buffer loads straight to LDS (a buffer resource per operand; the
+// per-lane offsets are fixed per work item and the tile offset is a scalar,
+// so no address arithmetic per tile; reads past the buffer return zeros).
+// One key buffer (three terms of 16 rows x 512 bytes, 16-byte chunks
+// XOR-swizzled by row) and one value buffer (four quads of 8 KB), 61 KB per
+// workgroup: two workgroups per CU. Per tile: barrier (the tile's keys
+// landed, every wave is done with the previous values), load the tile's
+// values, scores, exchange barrier (every wave is done with the keys, the
+// values landed), load the next tile's keys, softmax, P.V.
+constexpr int PL_VQ = 4096 + 64;  // uint16 per quad of values in LDS: 8 KB + 128 B
+
+struct PlanesParams {
+  const float* qkv;
+  const uint16_t* kp;
+  const uint16_t* vp;
+  float* out;
+  const int32_t* cu;
+  const int32_t* cu4;
+  const int32_t* items;
+  int32_t kp_bytes, vp_bytes;  // buffer extents (loads past them return zeros)
+  int32_t H, Hkv;
+  int32_t window;
+  float scale;
+  int64_t row0;  // packed row of qkv's and out's first row (kp and vp are indexed by absolute row and quad)
+};
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<const bf16x8*>(&v); }
+
+// raw buffer of `bytes` bytes (stride 0: offsets are byte offsets, range-checked)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+__global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
+  constexpr int HD = 256, HALF = 128;
+  __shared__ __attribute__((aligned(16))) uint16_t Kb[3 * KT * HD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vq[4 * PL_VQ];
+  __shared__ __attribute__((aligned(16))) float Sx[4][64 * 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS load addresses in scalars
+  const int qb = wave >> 1, half = wave & 1;
+  const int g = lane >> 4;
+  const int lq = lane & 15;
+
+  const int seq = p.items[3 * blockIdx.x];
+  const int q0 = p.items[3 * blockIdx.x + 1];
+  const int h = p.items[3 * blockIdx.x + 2];
+  const int hk = h / (p.H / p.Hkv);
+  const int start_abs = p.cu[seq];
+  const int L = p.cu[seq + 1] - start_abs;
+  const int64_t start = start_abs - p.row0;  // the sequence's first row in qkv and out
+  const int quad0 = p.cu4[seq];
+  const int W = (p.H + 2 * p.Hkv) * HD;
+  const int dofs = half * HALF;
+
+  const int qw0 = q0 + qb * QW;
+  const int qi = qw0 + lq;
+  const bool qvalid = qi < L;
+  // q terms: query lq, dims dofs + 32c + 8g .. +7
+  bf16x8 qt[3][HALF / 32];
+  {
+    const float* qr = p.qkv + (int64_t)(start + (qvalid ? qi : 0)) * W + (int64_t)h * HD + dofs + 8 * g;
+#pragma unroll
+    for (int c = 0; c < HALF / 32; c++) {
+      f32x4 x0 = *reinterpret_cast<const f32x4*>(qr + 32 * c);
+      f32x4 x1 = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
+      if (!qvalid) x0 = x1 = f32x4{0.f, 0.f, 0.f, 0.f};
+      uint32_t t0[8], t1[8], t2[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const Split3 sp = split3(e < 4 ? x0[e] : x1[e - 4]);
+        t0[e] = sp.h;
+        t1[e] = sp.m;
+        t2[e] = sp.l;
+      }
+      qt[0][c] = as_bf16x8(u32x4{pack_hi16(t0[0], t0[1]), pack_hi16(t0[2], t0[3]), pack_hi16(t0[4], t0[5]),
+                                 pack_hi16(t0[6], t0[7])});
+      qt[1][c] = as_bf16x8(u32x4{pack_hi16(t1[0], t1[1]), pack_hi16(t1[2], t1[3]), pack_hi16(t1[4], t1[5]),
+                                 pack_hi16(t1[6], t1[7])});
+      qt[2][c] = as_bf16x8(u32x4{pack_hi16(t2[0], t2[1]), pack_hi16(t2[2], t2[3]), pack_hi16(t2[4], t2[5]),
+                                 pack_hi16(t2[6], t2[7])});
+    }
+  }
+  f32x4 oacc[HALF / 16];  // O^T: dims dofs + 16db + 4g + r of query lq
+#pragma unroll
+  for (int db = 0; db < HALF / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig;
+  float l_part = 0.f;
+
+  const int qlast = min(q0 + QBLK, L) - 1;
+  int kbeg = 0, kend = L;
+  if (p.window > 0) {
+    // tiles start on a quad; keys below q0 - window + 1 fail every query's window test
+    kbeg = max(0, q0 - p.window + 1) & ~3;
+    kend = min(L, qlast + p.window);
+  }
+
+  const __amdgpu_buffer_rsrc_t krs = raw_rsrc(p.kp, p.kp_bytes), vrs = raw_rsrc(p.vp, p.vp_bytes);
+  // keys: 24 loads of 1 KB per tile (term, pair of rows), six per wave;
+  // byte offsets relative to the tile's first key row
+  int kvo[6];
+#pragma unroll
+  for (int j = 0; j < 6; j++) {
+    const int i = wave + 4 * j;
+    const int term = i >> 3, rp = i & 7;
+    const int r = 2 * rp + (lane >> 5);
+    const int chunk = (lane & 31) ^ (r & 15);  // the global chunk that lands at this position
+    kvo[j] = ((r * p.Hkv * 3 + term) * HD + chunk * 8) * 2;
+  }
+  const int krow_bytes = p.Hkv * 3 * HD * 2;
+  const int kbase = (start_abs * p.Hkv + hk) * 3 * HD * 2;
+  // values: 32 loads of 1 KB per tile (quad, eighth of the quad), eight per wave
+  int vvo[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int i = wave + 4 * j;
+    vvo[j] = ((i >> 3) * p.Hkv * 4096 + (i & 7) * 512 + lane * 8) * 2;
+  }
+  const int vquad_bytes = p.Hkv * 4096 * 2;
+  const int vbase = (quad0 * p.Hkv + hk) * 4096 * 2;
+
+  auto issue_k = [&](int k0) {
+    const int so = kbase + k0 * krow_bytes;
+#pragma unroll
+    for (int j = 0; j < 6; j++) {
+      const int i = wave + 4 * j;
+      const int term = i >> 3, rp = i & 7;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void*)&Kb[(term * KT + 2 * rp) * HD],
+                                               16, kvo[j], so, 0, 0);
+    }
+  };
+  auto issue_v = [&](int k0) {
+    const int so = vbase + (k0 >> 2) * vquad_bytes;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int i = wave + 4 * j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void*)&Vq[(i >> 3) * PL_VQ + (i & 7) * 512],
+                                               16, vvo[j], so, 0, 0);
+    }
+  };
+  issue_k(kbeg);
+
+  const int w0 = (lq & 8) ? 8 : 0;  // position of the (V0|V1) window of this lane's dims
+  for (int k0 = kbeg; k0 < kend; k0 += KT) {
+    // the tile's keys landed (own loads, then everyone's); every wave is done
+    // with the previous tile's values
+    dl_barrier<0x0070>();
+    issue_v(k0);
+
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < HALF / 32; c++) {
+      const int pos = ((dofs >> 3) + 4 * c + g) ^ lq;
+      const bf16x8 k0v = *reinterpret_cast<const bf16x8*>(&Kb[(0 * KT + lq) * HD + pos * 8]);
+      const bf16x8 k1v = *reinterpret_cast<const bf16x8*>(&Kb[(1 * KT + lq) * HD + pos * 8]);
+      const bf16x8 k2v = *reinterpret_cast<const bf16x8*>(&Kb[(2 * KT + lq) * HD + pos * 8]);
+      // smallest terms first
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2v, qt[0][c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1v, qt[1][c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0v, qt[2][c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1v, qt[0][c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0v, qt[1][c], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0v, qt[0][c], sacc, 0, 0, 0);
+    }
+    *reinterpret_cast<f32x4*>(&Sx[wave][lane * 4]) = sacc;
+    // partial scores written, every wave is done with the keys, the values landed
+    dl_barrier<0x0070>();
+    // the next tile's keys (past the last tile: a redundant load, so that no
+    // load is conditional)
+    issue_k(k0 + KT);
+    {
+      const f32x4 other = *reinterpret_cast<const f32x4*>(&Sx[wave ^ 1][lane * 4]);
+      const f32x4 lo = half == 0 ? sacc : other, hi = half == 0 ? other : sacc;
+#pragma unroll
+      for (int r = 0; r < 4; r++) sacc[r] = lo[r] + hi[r];
+    }
+
+    float tmax = kNegBig;
+    bool valid[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int j = k0 + g * 4 + r;
+      bool ok = qvalid && j < kend;
+      if (p.window > 0) ok = ok && (qi - j < p.window) && (j - qi < p.window);
+      valid[r] = ok;
+      const float t = sacc[r] * p.scale;
+      sacc[r] = t;
+      if (ok) tmax = fmaxf(tmax, t);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const bool moved = m_new != m_run;
+    const float alpha = exp_flush(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    uint32_t p0[4], p1[4], p2[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float pv = valid[r] ? exp_flush(sacc[r] - m_new) : 0.f;
+      psum += pv;
+      const Split3 sp = split3(pv);
+      p0[r] = sp.h;
+      p1[r] = sp.m;
+      p2[r] = sp.l;
+    }
+    l_part = l_part * alpha + psum;
+    if (__any(moved)) {
+#pragma unroll
+      for (int db = 0; db < HALF / 16; db++) oacc[db] *= alpha;
+    }
+    const uint32_t a0 = pack_hi16(p0[0], p0[1]), b0 = pack_hi16(p0[2], p0[3]);
+    const uint32_t a1 = pack_hi16(p1[0], p1[1]), b1 = pack_hi16(p1[2], p1[3]);
+    const uint32_t a2 = pack_hi16(p2[0], p2[1]), b2 = pack_hi16(p2[2], p2[3]);
+    const bf16x8 B1 = as_bf16x8(u32x4{a0, b0, a0, b0});  // P0 | P0
+    const bf16x8 B2 = as_bf16x8(u32x4{a1, b1, a1, b1});  // P1 | P1
+    const bf16x8 B3 = as_bf16x8(u32x4{a2, b2, a0, b0});  // P2 | P0
+#pragma unroll
+    for (int db = 0; db < HALF / 16; db++) {
+      const uint16_t* vr = &Vq[g * PL_VQ + (dofs + db * 16 + lq) * 16];
+      const bf16x8 A01 = *reinterpret_cast<const bf16x8*>(vr + w0);      // V0 | V1
+      const bf16x8 A02 = *reinterpret_cast<const bf16x8*>(vr + 8 - w0);  // V0 | V2
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A02, B3, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A01, B2, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A01, B1, oacc[db], 0, 0, 0);
+    }
+  }
+
+  __builtin_amdgcn_s_waitcnt(0x0070);  // no load to LDS outstanding at exit
+  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (qvalid) {
+    const float inv = 1.f / l_tot;
+    float* orow = p.out + (int64_t)(start + qi) * (p.H * HD) + (int64_t)h * HD + dofs + 4 * g;
+#pragma unroll
+    for (int db = 0; db < HALF / 16; db++) *reinterpret_cast<f32x4*>(orow + db * 16) = oacc[db] * inv;
+  }
+}
+
+
 // ---- generic attention (per-op drop-in) ------------------------------------------
 constexpr int GMAXD = 512;
 
@@ -431,6 +712,24 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
+
+int launch_attention_planes(fa_ctx* ctx, const AttnPlanesArgs& a, const int32_t* d_items, int32_t n_items,
+                            hipStream_t s) {
+  if (a.Hkv <= 0 || a.H % a.Hkv != 0)
+    return set_error(ctx, FA_ERR_ARG, "attention: %d query heads not a multiple of %d kv heads", a.H, a.Hkv);
+  if (n_items == 0) return FA_OK;
+  if (a.kp_bytes <= 0 || a.vp_bytes <= 0 || a.kp_bytes > INT32_MAX - (1 << 22) || a.vp_bytes > INT32_MAX - (1 << 22))
+    return set_error(ctx, FA_ERR_ARG, "attention: key/value planes of %lld / %lld bytes outside 1..2^31 - 4 MB",
+                     (long long)a.kp_bytes, (long long)a.vp_bytes);
+  PlanesParams p;
+  p.qkv = a.qkv; p.kp = a.kp; p.vp = a.vp; p.out = a.out; p.cu = a.cu_seqlens; p.cu4 = a.cu_quads;
+  p.kp_bytes = (int32_t)a.kp_bytes; p.vp_bytes = (int32_t)a.vp_bytes;
+  p.items = d_items; p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
+  hipLaunchKernelGGL(attention_planes_kernel, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
 
 int attention_varlen_qblock() { return QBLK; }
 

@@ -205,6 +205,41 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
 // Queries per workgroup of the varlen kernel (the item granularity).
 int attention_varlen_qblock();
 
+struct AttnPlanesArgs {
+  const float* qkv;
+  const uint16_t* kp;
+  const uint16_t* vp;
+  float* out;
+  const int32_t* cu_seqlens;
+  const int32_t* cu_quads;
+  int64_t kp_bytes, vp_bytes;
+  int32_t H, Hkv;
+  int32_t window;
+  float scale;
+  int64_t row0 = 0;  // packed row of qkv's and out's first row
+};
+int launch_attention_planes(fa_ctx* ctx, const AttnPlanesArgs& a, const int32_t* d_items, int32_t n_items,
+                            hipStream_t s);
+
+// head_dim 256, for the split-bf16 attention, one launch: q heads as
+// launch_qknorm_rope (in place, fp32); key heads normed, gained and
+// rotated, written as bf16 planes kp[row][kv head][term][256] (row = the
+// packed row of qkv, term 0..2: hi, mid, lo of the exact split) instead of
+// back into qkv; value heads (RMS-normed with unit gain when norm_v) in
+// quads of four tokens of one sequence: quad cu_quads[b] + t/4 holds tokens
+// t .. t+3 of sequence b as vp[quad][kv head][dim][16], per dim the windows
+// (V0|V1) and (V0|V2) of the four tokens' terms (4 bf16 per term), swapped
+// for dims with bit 3 set; zeros for tokens past the sequence. Writes quads
+// [q_lo, q_lo + quads); d_quad_seq[q] is quad q's sequence; qkv, d_pos and
+// kp start at packed row row0.
+int launch_qkv_planes(fa_ctx* ctx, float* qkv, int64_t rows, int64_t row0, int32_t H, int32_t Hkv, const float* gq,
+                      const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
+                      bool norm_v, const int32_t* d_cu_seqlens, const int32_t* d_cu_quads, const int32_t* d_quad_seq,
+                      int32_t q_lo, int32_t quads, uint16_t* kp, uint16_t* vp, hipStream_t s);
+
+// Zeroes bytes (a multiple of 16, 16-byte aligned) with a fill kernel.
+int launch_zero(fa_ctx* ctx, void* p, size_t bytes, hipStream_t s);
+
 // Masked mean pooling of the final normed hidden states over each
 // sequence's valid rows: pooled[b] = sum rows * (1/L_b).
 int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t nseq, int32_t d, float* pooled,

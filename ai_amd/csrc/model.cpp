@@ -85,6 +85,7 @@ struct fa_model {
   fa_gemma_config cfg{};
   int variant = 0;
   int max_width = 0, max_hd = 0;  // widest q|k|v row, widest attention output H*D
+  int hkv256 = 0;                 // most key/value heads of a head_dim-256 layer (split-bf16 attention)
   int P = 0, E = 0;               // variant 2: per-layer input width, embedding projection width
   uint16_t* wple_model = nullptr; // variant 2: [layers*P, d]
   float* g_ple_norm = nullptr;    // variant 2: [P]
@@ -156,6 +157,17 @@ int64_t microbatch_min_rows() {
 // measured best on MI355X at 5 517, 11 550 and 32 768 tokens (C2: 6.41 ms
 // per forward on one stream, 5.49 with two groups, 5.43 with three, 5.92
 // with four) and within 3 % of best at 17 923.
+// FA_ATTN_PLANES=0 / 1 forces the fp32-MFMA / split-bf16 attention for
+// the head_dim-256 layers (comparison); -1 when unset.
+int attention_planes_forced() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_ATTN_PLANES");
+    if (!e) return -1;
+    return std::atoi(e) != 0 ? 1 : 0;
+  }();
+  return v;
+}
+
 // FA_ATTN_KEY_PARTS=<1..8> forces the key runs of the short-batch attention
 // (tuning); 0 when unset.
 int attention_key_parts_forced() {
@@ -299,6 +311,7 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     dt = L.D;
     m->max_width = std::max(m->max_width, L.width);
     m->max_hd = std::max(m->max_hd, H * L.D);
+    if (L.D == 256) m->hkv256 = std::max(m->hkv256, L.Hkv);
   }
   if (rc) {
     delete m;
@@ -606,7 +619,13 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     n_items += (int64_t)((lengths[b] + qblk - 1) / qblk) * H;
   }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
-  const size_t plan_ints = (size_t)(B + 1) + 3 * (size_t)n_items;
+  double sum_l2 = 0;
+  for (int i = 0; i < B; i++) sum_l2 += (double)lengths[i] * lengths[i];
+  // each sequence's values in quads of four tokens (ceil(L/4)) for the
+  // split-bf16 attention: cu_quads [B+1] and each quad's sequence
+  int64_t n_quads = 0;
+  for (int b = 0; b < B; b++) n_quads += (lengths[b] + 3) / 4;
+  const size_t plan_ints = 2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_quads;
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
     m->plan_pending = false;
@@ -620,8 +639,15 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   }
   int32_t* cu_h = m->plan_host;
   int32_t* items_h = m->plan_host + (B + 1);
+  int32_t* cu4_h = items_h + 3 * n_items;
+  int32_t* qseq_h = cu4_h + (B + 1);
   cu_h[0] = 0;
-  for (int b = 0; b < B; b++) cu_h[b + 1] = cu_h[b] + lengths[b];
+  cu4_h[0] = 0;
+  for (int b = 0; b < B; b++) {
+    cu_h[b + 1] = cu_h[b] + lengths[b];
+    cu4_h[b + 1] = cu4_h[b] + (lengths[b] + 3) / 4;
+    for (int q = cu4_h[b]; q < cu4_h[b + 1]; q++) qseq_h[q] = b;
+  }
   // Micro-batches: with enough tokens the sequences are cut into groups of
   // about equal token count (contiguous rows) whose layers run on separate
   // streams, so that one group's kernels occupy the CUs the others leave
@@ -631,8 +657,6 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   int groups = 1;
   int gb[fa::kMaxMicrobatches + 1] = {0, B};
   if (M >= fa::microbatch_min_rows() && !m->profiling) {
-    double sum_l2 = 0;
-    for (int i = 0; i < B; i++) sum_l2 += (double)lengths[i] * lengths[i];
     const int want = std::min(fa::microbatch_count(M, sum_l2), B);
     int b = 0;
     int64_t cum = 0;
@@ -673,6 +697,8 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
   int32_t* cu_d = m->plan_dev.as<int32_t>();
   int32_t* items_d = cu_d + (B + 1);
+  int32_t* cu4_d = items_d + 3 * n_items;
+  int32_t* qseq_d = cu4_d + (B + 1);
   int32_t* row_src_d = cu_d + plan_ints;   // [M] b*T + t
   int32_t* pos_d = row_src_d + M;          // [M] t
   FA_HIP_CHECK(ctx, hipMemcpyAsync(cu_d, m->plan_host, plan_ints * 4, hipMemcpyHostToDevice, ctx->stream));
@@ -700,8 +726,23 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     if (const int f = fa::attention_key_parts_forced()) kparts = f;
   }
   const int64_t part_floats = kparts > 1 ? fa::attention_part_floats(kparts, M, H, m->max_hd / H) : 0;
-  const size_t ws_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 4096;
+  // Long sequences (a mean key count per token, sum L^2 / sum L, of at
+  // least 1 024; C4) make the forward attention-bound: there the head_dim-256
+  // layers take the split-bf16 attention, whose q/k/v pass writes keys and
+  // values as bf16 planes (key planes [M][hkv][3][256], value quads
+  // [quads + 4][hkv][256][16]; a tile's quads may run up to three past the
+  // last sequence's).
+  const int pforce = fa::attention_planes_forced();
+  const bool planes = !v2 && m->hkv256 > 0 && kparts == 1 &&
+                      (pforce == 1 || (pforce < 0 && sum_l2 >= 1024.0 * (double)M));
+  const size_t kp_elems = planes ? (size_t)M * m->hkv256 * 3 * 256 : 0;
+  const size_t vp_bytes = planes ? ((size_t)cu4_h[B] + 4) * m->hkv256 * 256 * 16 * 2 : 0;
+  const size_t f32_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 256;
+  const size_t kp_off = (f32_bytes + 255) & ~(size_t)255, vp_off = (kp_off + kp_elems * 2 + 255) & ~(size_t)255;
+  const size_t ws_bytes = vp_off + vp_bytes + 4096;
   if ((rc = m->ws.ensure(ctx, ws_bytes))) return rc;
+  uint16_t* kp = reinterpret_cast<uint16_t*>(m->ws.as<char>() + kp_off);
+  uint16_t* vp = reinterpret_cast<uint16_t*>(m->ws.as<char>() + vp_off);
   float* x = m->ws.as<float>();
   float* xn = x + M * d;
   float* qkv = xn + M * d;
@@ -717,6 +758,9 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   hipStream_t s = ctx->stream;
   // ---- row plan on device ----
   if ((rc = fa::launch_row_plan(ctx, cu_d, B, T, M, row_src_d, pos_d, s))) return rc;
+  // value-quad slots past each sequence's end stay zero (finite operands
+  // for the masked keys of a sequence's last quad)
+  if (planes && (rc = fa::launch_zero(ctx, vp, vp_bytes, s))) return rc;
   const float eps = c.rms_norm_eps;
   const float emb_scale = (float)std::sqrt((double)d);  // embed.go:176
   // model.go:100; variant 2 does not scale the scores (model.go:105-110)
@@ -747,7 +791,8 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   }
   // one layer over rows [r0, r0 + rows) (the sequences of one group, whose
   // attention items are items[0, n_it)) on stream st
-  auto run_layer = [&](int l, int64_t r0, int64_t rows, const int32_t* items, int64_t n_it, hipStream_t st) -> int {
+  auto run_layer = [&](int l, int b0, int b1, const int32_t* items, int64_t n_it, hipStream_t st) -> int {
+    const int64_t r0 = cu_h[b0], rows = cu_h[b1] - r0;
     const fa::Layer& L = m->layers[l];
     const int D = L.D, Hkv = L.Hkv;
     const bool sliding = L.sliding;
@@ -783,7 +828,16 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
     }
-    {
+    const bool pl = planes && D == 256;
+    if (pl) {
+      // read q, k, v (4 bytes per element); write q (4), k (6) and v (8) bytes
+      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * ((H + 2 * Hkv) * 4.0 + H * 4.0 + Hkv * 14.0) * D);
+      if ((rc = fa::launch_qkv_planes(ctx, qkvr, rows, r0, H, Hkv, L.g_q, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t,
+                                      v2, cu_d, cu4_d, qseq_d, cu4_h[b0], cu4_h[b1] - cu4_h[b0],
+                                      kp + r0 * Hkv * 3 * 256, vp, st)))
+        return rc;
+      pr.done();
+    } else {
       fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * (H + (v2 ? 2 : 1) * Hkv) * D * 8.0);
       if ((rc = fa::launch_qknorm_rope(ctx, qkvr, rows, H, Hkv, D, L.g_q, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t,
                                        st, v2)))
@@ -811,7 +865,15 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
         }
       }
       fa::Probe pr(m, FA_K_ATTENTION, pairs * 4.0 * H * D, 0);
-      if ((rc = fa::launch_attention_varlen_items(ctx, a, items, (int32_t)n_it, st))) return rc;
+      if (pl) {
+        fa::AttnPlanesArgs ap;
+        ap.qkv = qkvr; ap.kp = kp; ap.vp = vp; ap.out = attr; ap.row0 = r0; ap.cu_seqlens = cu_d; ap.cu_quads = cu4_d;
+        ap.kp_bytes = (int64_t)kp_elems * 2; ap.vp_bytes = (int64_t)vp_bytes;
+        ap.H = H; ap.Hkv = Hkv; ap.window = a.window; ap.scale = a.scale;
+        if ((rc = fa::launch_attention_planes(ctx, ap, items, (int32_t)n_it, st))) return rc;
+      } else {
+        if ((rc = fa::launch_attention_varlen_items(ctx, a, items, (int32_t)n_it, st))) return rc;
+      }
       pr.done();
     }
     {
@@ -882,7 +944,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   };
   if (groups == 1) {
     for (int l = 0; l < NL; l++)
-      if ((rc = run_layer(l, 0, M, items_d, n_items, s))) return rc;
+      if ((rc = run_layer(l, 0, B, items_d, n_items, s))) return rc;
   } else {
     // groups 1.. run on their own streams once the embeddings (and plan) are in
     FA_HIP_CHECK(ctx, hipEventRecord(m->ev_fork, s));
@@ -891,8 +953,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     for (int l = 0; l < NL && !rc; l++) {
       int64_t item0 = 0;
       for (int g = 0; g < groups && !rc; g++) {
-        const int64_t r0 = cu_h[gb[g]], rows = cu_h[gb[g + 1]] - r0;
-        rc = run_layer(l, r0, rows, items_d + 3 * item0, group_items[g], g ? m->mb_stream[g] : s);
+        rc = run_layer(l, gb[g], gb[g + 1], items_d + 3 * item0, group_items[g], g ? m->mb_stream[g] : s);
         item0 += group_items[g];
       }
     }
