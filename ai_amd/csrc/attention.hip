@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
 //
 // Operands. q (fp32, normed and rotated in qkv) is split in registers once
 // per work item. Keys and values arrive split, written by
-// qknorm_rope_planes_kernel: keys [row][kv head][term][256]; values in quads
+// qkv_planes_kernel: keys [row][kv head][term][256]; values in quads
 // of four keys of one sequence (every sequence starts a quad, cu_quads),
 // [quad][kv head][dim][16]: per dimension the two 16-byte windows (V0|V1)
 // and (V0|V2) of the four keys' terms, in that order for dims with bit 3
