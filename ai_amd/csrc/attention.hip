@@ -352,8 +352,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
 // clear and swapped otherwise (the 16 lanes reading one window per
 // instruction then cover all LDS banks).
 //
-// Formulation (lane l: g = l / 16, lq = l % 16). Work item and wave pairs as
-// in attention_varlen_kernel: waves 2b and 2b+1 own queries q0 + 16b .. +15
+// Formulation (lane l: g = l / 16, lq = l % 16). A work item is (sequence,
+// block of 64 queries, head), eight waves in four pairs; as in
+// attention_varlen_kernel, waves 2b and 2b+1 own queries q0 + 16b .. +15
 // and the two 128-dim halves. Per tile of 16 keys:
 //   S^T[key, query] = K . Q^T over the wave's 128 dims: A = a key term from
 //   LDS (lane: key lq, dims 8g..8g+7 of a 32-dim chunk), B = a q term;
@@ -375,12 +376,16 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
 // per-lane offsets are fixed per work item and the tile offset is a scalar,
 // so no address arithmetic per tile; reads past the buffer return zeros).
 // One key buffer (three terms of 16 rows x 512 bytes, 16-byte chunks
-// XOR-swizzled by row) and one value buffer (four quads of 8 KB), 61 KB per
-// workgroup: two workgroups per CU. Per tile: barrier (the tile's keys
+// XOR-swizzled by row) and one value buffer (four quads of 8 KB), 65 KB per
+// workgroup of eight waves, shared by 64 queries: the tiles' loads to LDS,
+// not the MFMAs, bound this kernel at 32 queries per tile. Per tile: barrier (the tile's keys
 // landed, every wave is done with the previous values), load the tile's
 // values, scores, exchange barrier (every wave is done with the keys, the
 // values landed), load the next tile's keys, softmax, P.V.
 constexpr int PL_VQ = 4096 + 64;  // uint16 per quad of values in LDS: 8 KB + 128 B
+constexpr int PL_W = 8;                 // waves per workgroup: four pairs
+constexpr int PL_NT = 64 * PL_W;
+constexpr int PL_QBLK = QW * PL_W / 2;  // queries per work item
 
 struct PlanesParams {
   const float* qkv;
@@ -407,11 +412,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, int
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-__global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
+__global__ __launch_bounds__(PL_NT) void attention_planes_kernel(PlanesParams p) {
   constexpr int HD = 256, HALF = 128;
   __shared__ __attribute__((aligned(16))) uint16_t Kb[3 * KT * HD];
   __shared__ __attribute__((aligned(16))) uint16_t Vq[4 * PL_VQ];
-  __shared__ __attribute__((aligned(16))) float Sx[4][64 * 4];
+  __shared__ __attribute__((aligned(16))) float Sx[PL_NT / 64][64 * 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
   float m_run = kNegBig;
   float l_part = 0.f;
 
-  const int qlast = min(q0 + QBLK, L) - 1;
+  const int qlast = min(q0 + PL_QBLK, L) - 1;
   int kbeg = 0, kend = L;
   if (p.window > 0) {
     // tiles start on a quad; keys below q0 - window + 1 fail every query's window test
@@ -474,12 +479,12 @@ __global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
   }
 
   const __amdgpu_buffer_rsrc_t krs = raw_rsrc(p.kp, p.kp_bytes), vrs = raw_rsrc(p.vp, p.vp_bytes);
-  // keys: 24 loads of 1 KB per tile (term, pair of rows), six per wave;
+  // keys: 24 loads of 1 KB per tile (term, pair of rows), three per wave;
   // byte offsets relative to the tile's first key row
-  int kvo[6];
+  int kvo[24 / PL_W];
 #pragma unroll
-  for (int j = 0; j < 6; j++) {
-    const int i = wave + 4 * j;
+  for (int j = 0; j < 24 / PL_W; j++) {
+    const int i = wave + PL_W * j;
     const int term = i >> 3, rp = i & 7;
     const int r = 2 * rp + (lane >> 5);
     const int chunk = (lane & 31) ^ (r & 15);  // the global chunk that lands at this position
@@ -487,11 +492,11 @@ __global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
   }
   const int krow_bytes = p.Hkv * 3 * HD * 2;
   const int kbase = (start_abs * p.Hkv + hk) * 3 * HD * 2;
-  // values: 32 loads of 1 KB per tile (quad, eighth of the quad), eight per wave
-  int vvo[8];
+  // values: 32 loads of 1 KB per tile (quad, eighth of the quad), four per wave
+  int vvo[32 / PL_W];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int i = wave + 4 * j;
+  for (int j = 0; j < 32 / PL_W; j++) {
+    const int i = wave + PL_W * j;
     vvo[j] = ((i >> 3) * p.Hkv * 4096 + (i & 7) * 512 + lane * 8) * 2;
   }
   const int vquad_bytes = p.Hkv * 4096 * 2;
@@ -500,8 +505,8 @@ __global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
   auto issue_k = [&](int k0) {
     const int so = kbase + k0 * krow_bytes;
 #pragma unroll
-    for (int j = 0; j < 6; j++) {
-      const int i = wave + 4 * j;
+    for (int j = 0; j < 24 / PL_W; j++) {
+      const int i = wave + PL_W * j;
       const int term = i >> 3, rp = i & 7;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void*)&Kb[(term * KT + 2 * rp) * HD],
                                                16, kvo[j], so, 0, 0);
@@ -510,8 +515,8 @@ __global__ __launch_bounds__(256) void attention_planes_kernel(PlanesParams p) {
   auto issue_v = [&](int k0) {
     const int so = vbase + (k0 >> 2) * vquad_bytes;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int i = wave + 4 * j;
+    for (int j = 0; j < 32 / PL_W; j++) {
+      const int i = wave + PL_W * j;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void*)&Vq[(i >> 3) * PL_VQ + (i & 7) * 512],
                                                16, vvo[j], so, 0, 0);
     }
@@ -725,13 +730,14 @@ int launch_attention_planes(fa_ctx* ctx, const AttnPlanesArgs& a, const int32_t*
   p.qkv = a.qkv; p.kp = a.kp; p.vp = a.vp; p.out = a.out; p.cu = a.cu_seqlens; p.cu4 = a.cu_quads;
   p.kp_bytes = (int32_t)a.kp_bytes; p.vp_bytes = (int32_t)a.vp_bytes;
   p.items = d_items; p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
-  hipLaunchKernelGGL(attention_planes_kernel, dim3((unsigned)n_items), dim3(DL_NT), 0, s, p);
+  hipLaunchKernelGGL(attention_planes_kernel, dim3((unsigned)n_items), dim3(PL_NT), 0, s, p);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
 
 
 int attention_varlen_qblock() { return QBLK; }
+int attention_planes_qblock() { return PL_QBLK; }
 
 int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s) {
   if (a.D > GMAXD) return set_error(ctx, FA_ERR_UNSUPPORTED, "Attention: head dimension %d > %d", a.D, GMAXD);

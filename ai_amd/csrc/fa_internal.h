@@ -204,6 +204,8 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
                                   hipStream_t s);
 // Queries per workgroup of the varlen kernel (the item granularity).
 int attention_varlen_qblock();
+// Queries per workgroup of the split-bf16 kernel (launch_attention_planes).
+int attention_planes_qblock();
 
 struct AttnPlanesArgs {
   const float* qkv;

@@ -670,9 +670,34 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     gb[want] = B;
     groups = want;
   }
+  // Attention over few items (a short batch on one stream) cuts each
+  // item's keys into up to kMaxKeyParts runs of whole tiles, one workgroup
+  // each, so that more CUs share the key loop: C1's 12 items (128 tokens, 3
+  // heads) become 48 workgroups of two tiles.
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const int64_t n_items_all = n_items;
+  int kparts = 1;
+  if (groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
+    kparts = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_all, 1));
+    kparts = std::max(1, std::min(kparts, (T + 31) / 32));  // at least two 16-key tiles per run
+    if (const int f = fa::attention_key_parts_forced()) kparts = f;
+  }
+  // With longer sequences (a mean key count per token, sum L^2 / sum L, of
+  // at least 320) the head_dim-256 layers take the split-bf16 attention,
+  // whose q/k/v pass writes keys and values as bf16 planes (key planes
+  // [M][hkv][3][256], value quads [quads + 4][hkv][256][16]; a tile's quads
+  // may run up to three past the last sequence's). Same-box A/B against the
+  // fp32-MFMA attention: C4 (about 1 440) 15.72 -> 14.10 ms, C3 (512) 33.6
+  // -> 31.9 ms, C2 (187) equal, C5 (85) 14.7 -> 15.0 ms: the pass costs a
+  // fixed amount per token while the attention's saving grows with the keys.
+  const int pforce = fa::attention_planes_forced();
+  const bool planes = !v2 && m->hkv256 > 0 && kparts == 1 &&
+                      (pforce == 1 || (pforce < 0 && sum_l2 >= 320.0 * (double)M));
   // Work items (sequence, query block, head) of each group, longest
   // sequences first: an item's work grows with its sequence's length, and
   // dispatching the long ones first shortens the tail.
+  // (64-query items for the split-bf16 attention)
+  const int qstep = planes ? fa::attention_planes_qblock() : qblk;
   std::vector<int>& order = m->seq_order;
   int64_t it = 0, group_items[fa::kMaxMicrobatches] = {};
   for (int gi = 0; gi < groups; gi++) {
@@ -682,7 +707,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
     const int64_t first = it;
     for (int b : order) {
-      for (int q0 = 0; q0 < lengths[b]; q0 += qblk) {
+      for (int q0 = 0; q0 < lengths[b]; q0 += qstep) {
         for (int h = 0; h < H; h++) {
           items_h[3 * it] = b;
           items_h[3 * it + 1] = q0;
@@ -713,28 +738,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
                         (v2 ? (int64_t)NL * P : 0);
   int maxw = std::max(d, std::max(full, v2 ? m->E : d));
   for (int o : m->dense_out) maxw = std::max(maxw, o);
-  // Attention over few items (a short batch on one stream) cuts each
-  // item's keys into up to kMaxKeyParts runs of whole tiles, one workgroup
-  // each, so that more CUs share the key loop: C1's 12 items (128 tokens, 3
-  // heads) become 48 workgroups of two tiles.
-  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  const int64_t n_items_all = n_items;
-  int kparts = 1;
-  if (groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
-    kparts = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_all, 1));
-    kparts = std::max(1, std::min(kparts, (T + 31) / 32));  // at least two 16-key tiles per run
-    if (const int f = fa::attention_key_parts_forced()) kparts = f;
-  }
   const int64_t part_floats = kparts > 1 ? fa::attention_part_floats(kparts, M, H, m->max_hd / H) : 0;
-  // Long sequences (a mean key count per token, sum L^2 / sum L, of at
-  // least 1 024; C4) make the forward attention-bound: there the head_dim-256
-  // layers take the split-bf16 attention, whose q/k/v pass writes keys and
-  // values as bf16 planes (key planes [M][hkv][3][256], value quads
-  // [quads + 4][hkv][256][16]; a tile's quads may run up to three past the
-  // last sequence's).
-  const int pforce = fa::attention_planes_forced();
-  const bool planes = !v2 && m->hkv256 > 0 && kparts == 1 &&
-                      (pforce == 1 || (pforce < 0 && sum_l2 >= 1024.0 * (double)M));
   const size_t kp_elems = planes ? (size_t)M * m->hkv256 * 3 * 256 : 0;
   const size_t vp_bytes = planes ? ((size_t)cu4_h[B] + 4) * m->hkv256 * 256 * 16 * 2 : 0;
   const size_t f32_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 256;
@@ -944,7 +948,7 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   };
   if (groups == 1) {
     for (int l = 0; l < NL; l++)
-      if ((rc = run_layer(l, 0, B, items_d, n_items, s))) return rc;
+      if ((rc = run_layer(l, 0, B, items_d, group_items[0], s))) return rc;
   } else {
     // groups 1.. run on their own streams once the embeddings (and plan) are in
     FA_HIP_CHECK(ctx, hipEventRecord(m->ev_fork, s));
