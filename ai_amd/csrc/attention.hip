@@ -378,7 +378,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
 // One key buffer (three terms of 16 rows x 512 bytes, 16-byte chunks
 // XOR-swizzled by row) and one value buffer (four quads of 8 KB), 65 KB per
 // workgroup of eight waves, shared by 64 queries: the tiles' loads to LDS,
-// not the MFMAs, bound this kernel at 32 queries per tile. Per tile: barrier (the tile's keys
+// not the MFMAs, bound this kernel at 32 queries per tile. Capped at 128
+// VGPRs (a 16-byte spill) for two workgroups per CU, four waves per SIMD:
+// C4 14.05 -> 13.19 ms, C3 32.3 -> 30.6 ms per forward against 142 VGPRs. Per tile: barrier (the tile's keys
 // landed, every wave is done with the previous values), load the tile's
 // values, scores, exchange barrier (every wave is done with the keys, the
 // values landed), load the next tile's keys, softmax, P.V.
@@ -412,7 +414,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, int
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-__global__ __launch_bounds__(PL_NT) void attention_planes_kernel(PlanesParams p) {
+__global__ __launch_bounds__(PL_NT, 4) void attention_planes_kernel(PlanesParams p) {
   constexpr int HD = 256, HALF = 128;
   __shared__ __attribute__((aligned(16))) uint16_t Kb[3 * KT * HD];
   __shared__ __attribute__((aligned(16))) uint16_t Vq[4 * PL_VQ];
