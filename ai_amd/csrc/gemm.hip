@@ -412,6 +412,12 @@ struct XTile {
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int FM = TM / 32, FN = TN / 32;
   static constexpr int S = BK / 16;   // MFMA k-steps per slab
+  // waves per SIMD the register allocation must allow: two eight-wave
+  // workgroups per CU need four (at most 128 VGPRs). The 128x256 tile
+  // compiled to 136-152 VGPRs ran one workgroup per CU; capped (a 28-32 byte
+  // spill) the C2 gate|up launch takes 65.9 instead of 71.7 us, 32 768 rows
+  // 376.7 instead of 393.4 us.
+  static constexpr int MINW = (WM * WN == 8 && BN == 256) ? 4 : 1;
   static_assert(TM % 32 == 0 && TN % 32 == 0, "tile shape");
 };
 
@@ -440,7 +446,7 @@ __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <class TL, Epi EPI>
-__global__ __launch_bounds__(TL::NT) void gemm_x3_kernel(GemmParams p) {
+__global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p) {
   constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, NT = TL::NT;
   constexpr int FM = TL::FM, FN = TL::FN;
   static_assert(TL::S == 2 && BK == 32, "two MFMA k-steps per 32-wide slab");
