@@ -88,6 +88,8 @@ _SIGS = {
     "fa_gemma_finalize": (C.c_int, [vp]),
     "fa_gemma_embed_ids": (C.c_int, [vp, vp, vp, i32, i32, i32, vp]),
     "fa_gemma_embed_ids_dev": (C.c_int, [vp, vp, vp, i32, i32, i32, vp]),
+    "fa_gemma_encode_ids": (C.c_int, [vp, vp, vp, i32, i32, i32, vp]),
+    "fa_gemma_encode_ids_dev": (C.c_int, [vp, vp, vp, i32, i32, i32, vp]),
     "fa_gemma_set_profiling": (C.c_int, [vp, C.c_int]),
     "fa_gemma_kernel_stats": (C.c_int, [vp, C.c_int, P_i64, C.POINTER(f64), C.POINTER(f64), C.POINTER(f64)]),
     "fa_gemma_reset_stats": (C.c_int, [vp]),

@@ -243,6 +243,22 @@ int collect_stats(fa_model* m) {
   return FA_OK;
 }
 
+// Host-side check of a host batch: lengths in 1..T and every valid id inside
+// the vocabulary (an out-of-range id would read outside the table).
+int check_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, int B, int T) {
+  const int V = m->cfg.vocab_size;
+  for (int b = 0; b < B; b++) {
+    if (lengths[b] < 1 || lengths[b] > T)
+      return set_error(m->ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
+    for (int t = 0; t < lengths[b]; t++) {
+      const int32_t id = ids[(size_t)b * T + t];
+      if (id < 0 || id >= V)
+        return set_error(m->ctx, FA_ERR_ARG, "gemma: token id %d at [%d,%d] outside 0..%d", id, b, t, V - 1);
+    }
+  }
+  return FA_OK;
+}
+
 int parse_layer(const std::string& s, int nl, int* l, std::string* rest) {
   if (s.rfind("layers.", 0) != 0) return -1;
   size_t dot = s.find('.', 7);
@@ -593,19 +609,33 @@ int fa_gemma_finalize(fa_model* m) {
   return FA_OK;
 }
 
-int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
-                           int32_t dim, float* d_out) {
+}  // extern "C"
+
+namespace fa {
+namespace {
+
+// The forward pass over device-resident ids. With hidden == nullptr: every
+// layer, pooling, the head and L2 into d_out [B x dim]. With hidden != nullptr
+// (encode): the packed rows [M x d] of the final hidden states (n_layers < 0)
+// or of the residual stream after the first n_layers layers into hidden;
+// d_out and dim are unused.
+int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T, int32_t dim,
+            float* d_out, int n_layers, float* hidden) {
   if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
   fa_ctx* ctx = m->ctx;
   const fa_gemma_config& c = m->cfg;
   if (!m->finalized) return set_error(ctx, FA_ERR_STATE, "gemma: embed before every weight was set (finalize)");
   if (B < 0 || T < 0) return set_error(ctx, FA_ERR_ARG, "gemma: negative batch shape [%d x %d]", B, T);
   if (B == 0) return FA_OK;
-  if (!d_ids || !lengths || !d_out) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
+  if (!d_ids || !lengths || !(hidden ? hidden : d_out)) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
   if (T > c.max_tokens) return set_error(ctx, FA_ERR_ARG, "gemma: T=%d exceeds max_tokens %d", T, c.max_tokens);
   const bool v2 = m->variant == 2;
   const int d = c.hidden_size, H = c.num_attention_heads, F = c.intermediate_size, NL = c.num_hidden_layers,
             P = m->P;
+  if (hidden && n_layers > NL)
+    return set_error(ctx, FA_ERR_ARG, "gemma: encode after %d layers, the model has %d", n_layers, NL);
+  const bool final_states = !hidden || n_layers < 0;
+  const int n_run = final_states ? NL : n_layers;
   const int full = c.n_dense > 0 ? m->dense_out.back() : (v2 ? m->E : d);
   if (dim <= 0) dim = full;
   if (dim > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
@@ -947,14 +977,14 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
     return FA_OK;
   };
   if (groups == 1) {
-    for (int l = 0; l < NL; l++)
+    for (int l = 0; l < n_run; l++)
       if ((rc = run_layer(l, 0, B, items_d, group_items[0], s))) return rc;
   } else {
     // groups 1.. run on their own streams once the embeddings (and plan) are in
     FA_HIP_CHECK(ctx, hipEventRecord(m->ev_fork, s));
     for (int g = 1; g < groups; g++) FA_HIP_CHECK(ctx, hipStreamWaitEvent(m->mb_stream[g], m->ev_fork, 0));
     rc = FA_OK;
-    for (int l = 0; l < NL && !rc; l++) {
+    for (int l = 0; l < n_run && !rc; l++) {
       int64_t item0 = 0;
       for (int g = 0; g < groups && !rc; g++) {
         rc = run_layer(l, gb[g], gb[g + 1], items_d + 3 * item0, group_items[g], g ? m->mb_stream[g] : s);
@@ -967,6 +997,12 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
       FA_HIP_CHECK(ctx, hipStreamWaitEvent(s, m->ev_join[g], 0));
     }
     if (rc) return rc;
+  }
+  if (hidden) {
+    // after the last layer xn holds the final RMSNorm of x (embed.go:237)
+    const float* src = final_states ? xn : x;
+    FA_HIP_CHECK(ctx, hipMemcpyAsync(hidden, src, (size_t)M * d * 4, hipMemcpyDeviceToDevice, s));
+    return FA_OK;
   }
   {
     fa::Probe pr(m, FA_K_POOL_L2, 0, (double)M * d * 4.0 + (double)B * d * 4.0);
@@ -1018,6 +1054,44 @@ int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* len
   return FA_OK;
 }
 
+}  // namespace
+}  // namespace fa
+
+extern "C" {
+
+int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
+                           int32_t dim, float* d_out) {
+  return fa::forward(m, d_ids, lengths, B, T, dim, d_out, 0, nullptr);
+}
+
+int fa_gemma_encode_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
+                            int32_t n_layers, float* d_hidden) {
+  return fa::forward(m, d_ids, lengths, B, T, 0, nullptr, n_layers < 0 ? -1 : n_layers, d_hidden);
+}
+
+int fa_gemma_encode_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, int32_t B, int32_t T,
+                        int32_t n_layers, float* hidden) {
+  if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
+  fa_ctx* ctx = m->ctx;
+  if (B < 0 || T < 0) return set_error(ctx, FA_ERR_ARG, "gemma: negative batch shape [%d x %d]", B, T);
+  if (B == 0) return FA_OK;
+  if (!ids || !lengths || !hidden) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
+  int rc;
+  if ((rc = fa::check_ids(m, ids, lengths, B, T))) return rc;
+  int64_t M = 0;
+  for (int b = 0; b < B; b++) M += lengths[b];
+  const int d = m->cfg.hidden_size;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
+  if ((rc = m->out_dev.ensure(ctx, (size_t)M * d * 4))) return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, ids, (size_t)B * T * 4, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = fa_gemma_encode_ids_dev(m, m->ids_dev.as<int32_t>(), lengths, B, T, n_layers, m->out_dev.as<float>())))
+    return rc;
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(hidden, m->out_dev.ptr, (size_t)M * d * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
 int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, int32_t B, int32_t T, int32_t dim,
                        float* out) {
   if (!m) return set_error(nullptr, FA_ERR_ARG, "gemma: NULL model");
@@ -1028,19 +1102,10 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
   const fa_gemma_config& c = m->cfg;
   const int full = c.n_dense > 0 ? m->dense_out.back() : (m->variant == 2 ? m->E : c.hidden_size);
   const int dd = dim <= 0 ? full : dim;
-  // validate ids on the host: an out-of-range id would read outside the table
-  for (int b = 0; b < B; b++) {
-    if (lengths[b] < 1 || lengths[b] > T)
-      return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
-    for (int t = 0; t < lengths[b]; t++) {
-      int32_t id = ids[(size_t)b * T + t];
-      if (id < 0 || id >= c.vocab_size)
-        return set_error(ctx, FA_ERR_ARG, "gemma: token id %d at [%d,%d] outside 0..%d", id, b, t, c.vocab_size - 1);
-    }
-  }
+  int rc;
+  if ((rc = fa::check_ids(m, ids, lengths, B, T))) return rc;
   if (dd > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
-  int rc;
   if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
   if ((rc = m->out_dev.ensure(ctx, (size_t)B * dd * 4))) return rc;
   FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, ids, (size_t)B * T * 4, hipMemcpyHostToDevice, ctx->stream));

@@ -129,6 +129,20 @@ class Model:
                                                out.ctypes.data))
         return out
 
+    def encode_ids(self, ids: np.ndarray, lengths: np.ndarray, n_layers: int = -1) -> np.ndarray:
+        """Hidden states [sum(lengths), hidden] of the valid tokens, packed in
+        batch order: the final ones (n_layers < 0, as (*Model).encode returns
+        them, embed.go:160-240) or the residual stream after n_layers layers."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        lengths = np.ascontiguousarray(lengths, dtype=np.int32)
+        if ids.ndim != 2 or lengths.shape != (ids.shape[0],):
+            raise GemmaError(f"gemma: ids {list(ids.shape)} and lengths {list(lengths.shape)} do not match")
+        B, T = ids.shape
+        out = np.empty((int(lengths.astype(np.int64).sum()), int(self.shape.hidden_size)), np.float32)
+        self._check(N.lib().fa_gemma_encode_ids(self.h, ids.ctypes.data, lengths.ctypes.data, B, T, n_layers,
+                                                out.ctypes.data))
+        return out
+
     def embed_ids_dev(self, d_ids: int, lengths: np.ndarray, B: int, T: int, d_out: int, dim: int = 0) -> None:
         """Enqueue the forward pass on device-resident ids/outputs (no sync)."""
         lengths = np.ascontiguousarray(lengths, dtype=np.int32)

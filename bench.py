@@ -4,11 +4,19 @@
 One step = one forward pass (token ids -> 768-d L2-normalised embeddings) of
 the BASELINE.json workload named by --config (default C2: batch 32 x seq 256,
 lengths uniform in [64, 256], Zipf ids), with random-init bf16-resident
-weights of the EmbeddingGemma-300M architecture. Inputs are resident in HBM
-before the timed region; outputs stay there.
+weights of the EmbeddingGemma-300M architecture.
 
 Prints ONE JSON line (the driver's contract) with:
-  value            sentences/s over the timed steps (whole job, 1 GPU)
+  value            sentences/s over the timed steps (whole job, 1 GPU), each
+                   step timed as the metric defines t_batch: token ids on the
+                   host -> embeddings on the host (fa_gemma_embed_ids: the ids'
+                   host-to-device copy, the forward, the embeddings'
+                   device-to-host copy and a stream synchronisation per step),
+                   as the reference's benchEmbed times Embed host to host
+                   (cmd/bench/main.go:350-354)
+  device_resident  the same forward with ids already in HBM and the
+                   embeddings left there, steps enqueued back to back
+                   (fa_gemma_embed_ids_dev): the device-side throughput
   roofline         the dominant kernel (the gate|up GEMM with the GeGLU
                    epilogue) timed with HIP events on the library's stream:
                    algorithmic flops (2*M*N*K) / mean launch duration vs the
@@ -80,10 +88,42 @@ def calibrate_copy() -> None:
     print(json.dumps({"calibration": "device copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 3}))
 
 
+def host_cpu() -> dict:
+    """This host's CPU model, the logical CPUs this process may run on and the
+    physical cores among them (hyperthreads counted once, as the reference's
+    topology_linux.go:12-28 counts them)."""
+    model, cores = "unknown", set()
+    allowed = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    try:
+        cpu, phys = None, None
+        info = {}
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                cpu = int(v)
+            elif k == "model name":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id" and cpu is not None:
+                info[cpu] = (phys, v)
+        cores = {info[c] for c in allowed if c in info}
+    except OSError:
+        pass
+    return {"cpu_model": model, "logical_cpus": len(allowed),
+            "physical_cores": len(cores) if cores else len(allowed)}
+
+
 def cpu_baseline(batch, budget_s: float, model: str = "eg300m") -> dict:
     """The oracle on consecutive groups of 4 sequences of the workload (each
     padded to its own longest, as the reference's embedBatch pads), until the
-    budget is spent. Test infrastructure used as the checker-side baseline."""
+    budget is spent. Test infrastructure used as the checker-side baseline.
+    OpenMP threads stay at the environment's OMP_NUM_THREADS; they are bound
+    close to the launching core (OMP_PROC_BIND=close, set before the oracle
+    library starts its runtime)."""
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_PLACES", "cores")
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     from ai_amd import synth as S
@@ -116,10 +156,12 @@ def cpu_baseline(batch, budget_s: float, model: str = "eg300m") -> dict:
         i += group
     om.close()
     threads = O.lib().orc_num_threads()
+    hc = host_cpu()
     return {"value": round(done / elapsed, 3), "unit": "sentences/s", "cores": threads, "kind": "port",
             "sample": f"{done} sequences of {batch.name} in groups of {group}, each padded to its group's max "
                       f"length ({tokens} valid tokens, {elapsed:.1f} s, {O.isa()}, OMP threads {threads})",
-            "tokens_per_s": round(tokens / elapsed, 1)}
+            "tokens_per_s": round(tokens / elapsed, 1), "threads": threads, "isa": O.isa(),
+            "omp_proc_bind": os.environ.get("OMP_PROC_BIND"), "omp_places": os.environ.get("OMP_PLACES"), **hc}
 
 
 def main():
@@ -151,14 +193,29 @@ def main():
     def step():
         model.embed_ids_dev(d_ids.value, batch.lengths, B, T, d_out.value)
 
+    # host to host: ids [B, T] and lengths on the host, embeddings back on the
+    # host, one synchronisation per step (inside fa_gemma_embed_ids)
+    h_out = np.empty((B, model.Dim()), np.float32)
+    ids_c = np.ascontiguousarray(batch.ids, np.int32)
+    lens_c = np.ascontiguousarray(batch.lengths, np.int32)
+
+    def host_step():
+        N.check(ctx.h, N.lib().fa_gemma_embed_ids(model.h, ids_c.ctypes.data, lens_c.ctypes.data, B, T, 0,
+                                                  h_out.ctypes.data))
+
+    def timed(fn, steps):
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        ctx.sync()
+        return time.perf_counter() - t0
+
     for _ in range(a.warmup):
+        host_step()
         step()
     ctx.sync()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    ctx.sync()
-    elapsed = time.perf_counter() - t0
+    elapsed = timed(host_step, a.steps)
     ms_per_step = elapsed / a.steps * 1e3
     sent_s = B * a.steps / elapsed
     tok_s = batch.tokens * a.steps / elapsed
@@ -166,14 +223,11 @@ def main():
     # Two more timed regions of the same K steps: min / median over three runs
     # (the reference's protocol, cmd/bench/main.go:46-66); the headline value
     # stays the first region above.
-    runs = [ms_per_step]
-    for _ in range(2):
-        ctx.sync()
-        t2 = time.perf_counter()
-        for _ in range(a.steps):
-            step()
-        ctx.sync()
-        runs.append((time.perf_counter() - t2) / a.steps * 1e3)
+    runs = [ms_per_step] + [timed(host_step, a.steps) / a.steps * 1e3 for _ in range(2)]
+    # the device-resident forward (ids in HBM, embeddings left there, no
+    # per-step synchronisation)
+    dev_runs = [timed(step, a.steps) / a.steps * 1e3 for _ in range(3)]
+    dev_med = sorted(dev_runs)[1]
 
     # Second pass over the same steps with every launch bracketed by HIP events.
     model.set_profiling(True)
@@ -259,6 +313,11 @@ def main():
         "tokens_per_s": round(tok_s, 1),
         "runs_ms_per_step": {"all": [round(r, 3) for r in runs], "min": round(min(runs), 3),
                              "median": round(sorted(runs)[1], 3)},
+        "timing": "host ids -> host embeddings per step (fa_gemma_embed_ids, synchronised every step)",
+        "device_resident": {"sentences_per_s": round(B / (dev_med * 1e-3), 1),
+                            "tokens_per_s": round(batch.tokens / (dev_med * 1e-3), 1),
+                            "ms_per_step": {"all": [round(r, 3) for r in dev_runs], "median": round(dev_med, 3)},
+                            "note": "ids resident in HBM, embeddings left in HBM, steps enqueued back to back"},
         "roofline": roofline,
         "throughput_roofline": throughput_roofline,
         "gemm_all": gemm_all,

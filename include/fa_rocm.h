@@ -273,6 +273,21 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
 int fa_gemma_embed_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
                            int32_t dim, float* d_out);
 
+/* The encoder's hidden states of a batch, as (*Model).encode returns them
+ * before pooling (models/gemma/embed.go:160-240): with n_layers < 0, the
+ * final hidden states h = RMSNorm(x; 1+w_final); with 0 <= n_layers <=
+ * num_hidden_layers, the residual stream x after the first n_layers layers
+ * (0: the scaled embedding gather, embed.go:175-176), for layer-by-layer
+ * inspection. hidden receives the valid rows only, packed
+ * in batch order: [sum(lengths) x hidden_size], sequence b's token t at row
+ * lengths[0] + ... + lengths[b-1] + t. Arguments and errors as
+ * fa_gemma_embed_ids. Host pointers; returns when hidden is filled. */
+int fa_gemma_encode_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, int32_t B, int32_t T,
+                        int32_t n_layers, float* hidden);
+/* Device-pointer variant (lengths on the host; enqueue only). */
+int fa_gemma_encode_ids_dev(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B, int32_t T,
+                            int32_t n_layers, float* d_hidden);
+
 /* Per-kernel timing with HIP events on the model's stream, for roofline
  * reporting: when enabled, each kernel launch of the forward pass is
  * bracketed by events and its duration accumulated under its kind. */

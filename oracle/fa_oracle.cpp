@@ -627,23 +627,27 @@ ORC_API int orc_model_finalize(void* p) {
   return 0;
 }
 
-// Model.encode for Variant 0 (embed.go:160-240) followed by pool
-// (embed.go:381-404), applyHead and l2normalize (embed.go:408-429,472-475).
-// ids is [B*T] right-padded with 0 (embed.go:122-138); out is [B, dim].
-ORC_API int orc_model_embed(void* p, const int32_t* ids, const int32_t* lengths, int B, int T, int dim, float* out) {
-  OrcModel* m = (OrcModel*)p;
+// Model.encode for Variant 0 (embed.go:160-240): h [B*T, d] = the final
+// hidden states. ids is [B*T] right-padded with 0 (embed.go:122-138). For
+// inspection, snapshot i (0 <= i < n_snap) copies the residual stream x after
+// the first snap[i] layers (0 <= snap[i] <= layers; 0 is the scaled
+// embedding gather) into snaps + i*B*T*d, or h itself when snap[i] < 0.
+static int orc_encode(OrcModel* m, const int32_t* ids, const int32_t* lengths, int B, int T, const int* snap,
+                      int n_snap, float* snaps, std::vector<float>& h) {
   if (!m->finalized) return -5;
   const OrcConfig& c = m->cfg;
   const int H = c.heads, Hkv = c.kv_heads, D = c.head_dim, d = c.hidden, F = c.ffn;
   const i64 M = (i64)B * T;
   const float eps = c.eps;
   const float scale = (float)(1.0 / std::sqrt(c.qpas));  // model.go:100
-  int full = d;
-  if (c.n_dense > 0) full = m->dense_out[c.n_dense - 1];
-  if (dim <= 0) dim = full;
-  if (dim > full) return -6;
   for (i64 i = 0; i < M; i++)
     if (ids[i] < 0 || ids[i] >= c.vocab) return -7;
+  for (int i = 0; i < n_snap; i++)
+    if (snap[i] > c.layers) return -8;
+  auto take = [&](int layers_done, const std::vector<float>& src) {
+    for (int i = 0; i < n_snap; i++)
+      if (snap[i] == layers_done) std::memcpy(snaps + (size_t)i * M * d, src.data(), sizeof(float) * M * d);
+  };
 
   std::vector<int32_t> positions(T);
   for (int t = 0; t < T; t++) positions[t] = t;
@@ -679,6 +683,7 @@ ORC_API int orc_model_embed(void* p, const int32_t* ids, const int32_t* lengths,
           mask_sl[((size_t)b * T + i) * T + j] = padm[(size_t)b * T + j] + winm[(size_t)i * T + j];
   }
   std::vector<float> cs, sn, tmp;
+  take(0, x);
 
   for (int l = 0; l < c.layers; l++) {
     const OrcLayer& L = m->layers[l];
@@ -743,9 +748,37 @@ ORC_API int orc_model_embed(void* p, const int32_t* ids, const int32_t* lengths,
     orc_rmsnorm(o0.data(), L.postFFNNorm.data(), eps, M, d, o.data());
 #pragma omp parallel for schedule(static)
     for (i64 i = 0; i < M * d; i++) x[i] = x[i] + o[i];
+    take(l + 1, x);
   }
-  std::vector<float> h((size_t)M * d);
+  h.resize((size_t)M * d);
   orc_rmsnorm(x.data(), m->norm.data(), eps, M, d, h.data());
+  for (int i = 0; i < n_snap; i++)
+    if (snap[i] < 0) std::memcpy(snaps + (size_t)i * M * d, h.data(), sizeof(float) * M * d);
+  return 0;
+}
+
+// The encoder's states for inspection (orc_encode's snapshots); snaps is
+// [n_snap, B*T, d].
+ORC_API int orc_model_encode(void* p, const int32_t* ids, const int32_t* lengths, int B, int T, const int* snap,
+                             int n_snap, float* snaps) {
+  std::vector<float> h;
+  return orc_encode((OrcModel*)p, ids, lengths, B, T, snap, n_snap, snaps, h);
+}
+
+// Model.encode (orc_encode) followed by pool (embed.go:381-404), applyHead
+// and l2normalize (embed.go:408-429,472-475). out is [B, dim].
+ORC_API int orc_model_embed(void* p, const int32_t* ids, const int32_t* lengths, int B, int T, int dim, float* out) {
+  OrcModel* m = (OrcModel*)p;
+  if (!m->finalized) return -5;
+  const OrcConfig& c = m->cfg;
+  const int d = c.hidden;
+  int full = d;
+  if (c.n_dense > 0) full = m->dense_out[c.n_dense - 1];
+  if (dim <= 0) dim = full;
+  if (dim > full) return -6;
+  std::vector<float> h;
+  const int rc = orc_encode(m, ids, lengths, B, T, nullptr, 0, nullptr, h);
+  if (rc) return rc;
 
   // pool: masked mean (embed.go:381-404)
   std::vector<float> pooled((size_t)B * d, 0.f);

@@ -35,6 +35,7 @@ _SIGS = {
     "orc_model_set": (C.c_int, [vp, C.c_char_p, vp, i64]),
     "orc_model_finalize": (C.c_int, [vp]),
     "orc_model_embed": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "orc_model_encode": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp, C.c_int, vp]),
     "orc_num_threads": (C.c_int, []),
     "orc_model2_create": (vp, [C.c_int] * 8 + [f64, f64, f32, vp, vp, vp, C.c_int, vp]),
     "orc_model2_destroy": (None, [vp]),
@@ -286,6 +287,20 @@ class OracleModel:
         if rc != 0:
             raise ValueError(f"oracle embed: {rc}")
         return out
+
+    def encode(self, ids, lengths, layers=(-1,)):
+        """Hidden states after each count of layers in `layers` (-1: the final,
+        normed ones), packed to the valid rows: [len(layers), sum(lengths), hidden]."""
+        ids = np.ascontiguousarray(ids, np.int32); lengths = np.ascontiguousarray(lengths, np.int32)
+        B, T = ids.shape
+        snap = np.ascontiguousarray(layers, np.int32)
+        d = self.shape.hidden_size
+        out = np.empty((snap.size, B, T, d), np.float32)
+        rc = lib().orc_model_encode(self.h, P(ids), P(lengths), B, T, P(snap), snap.size, P(out))
+        if rc != 0:
+            raise ValueError(f"oracle encode: {rc}")
+        valid = np.arange(T)[None, :] < lengths[:, None]
+        return out[:, valid]
 
     def close(self):
         if self.h:

@@ -1,7 +1,21 @@
 """End-to-end parity of the GPU encoder (libfa_rocm.so) with the CPU oracle.
 
-Bar: cosine >= 0.9999 per sentence, top-1
-nearest-neighbour indices identical; max |delta| printed.
+Bars. BASELINE.json's north_star asks for cosine >= 0.9999 per sentence,
+kernel outputs within 1e-4 relative error and identical nearest-neighbour
+indices. The measured agreement is far tighter (max |delta| about 2e-7 on
+the unit-length embeddings), so the assertions here are:
+
+* embeddings: cosine >= 0.999999 and max |delta| <= 1e-5 per batch, every row
+  of C1, C2, C4 and C5 (and a spread of C3's) against the oracle;
+* hidden states after every layer (fa_gemma_encode_ids against the oracle's
+  snapshots of embed.go:160-240): per token row ||delta|| / ||ref|| <= 1e-5,
+  which pins the gather, q/k norm + RoPE, both attention kernels, the K-split
+  products and the residual norms layer by layer;
+* top-1 neighbours among the batch and C5's top-10 lists identical wherever
+  the scores' float64 gaps exceed what the measured embedding difference can
+  move a score by.
+
+max |delta| and the worst relative error are printed for every comparison.
 """
 import numpy as np
 import pytest
@@ -11,6 +25,10 @@ from ai_amd import gemma as G
 from ai_amd import synth as S
 
 pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.999999
+MAXD = 1e-5
+STATE_REL = 1e-5
 
 
 @pytest.fixture(scope="module")
@@ -39,12 +57,54 @@ def compare(gpu, ref, what):
     np.fill_diagonal(nn_g, -np.inf)
     np.fill_diagonal(nn_r, -np.inf)
     top1_g, top1_r = nn_g.argmax(1), nn_r.argmax(1)
-    print(f"{what}: cosine min={c.min():.8f} mean={c.mean():.8f} max|d|={d:.3g} top1 equal={np.array_equal(top1_g, top1_r)}",
-          flush=True)
-    assert c.min() >= 0.9999
+    print(f"{what}: {gpu.shape[0]} rows, cosine min={c.min():.9f} max|d|={d:.3g} "
+          f"top1 equal={np.array_equal(top1_g, top1_r)}", flush=True)
+    assert c.min() >= COS_MIN, what
+    assert d <= MAXD, what
     if gpu.shape[0] > 2:
-        assert np.array_equal(top1_g, top1_r)
+        assert np.array_equal(top1_g, top1_r), what
     return c
+
+
+def oracle_embed(om, ids, lengths, group=8, dim=0):
+    """The oracle's embeddings of every row, run in groups of similar length
+    (each padded to its own longest: padding invariance, gemma_test.go:117-135)."""
+    order = np.argsort(-lengths, kind="stable")
+    out = None
+    for g0 in range(0, len(order), group):
+        sel = order[g0:g0 + group]
+        Tm = int(lengths[sel].max())
+        e = om.embed(ids[sel, :Tm], lengths[sel], dim=dim)
+        if out is None:
+            out = np.empty((len(lengths), e.shape[1]), np.float32)
+        out[sel] = e
+    return out
+
+
+def packed_rows(lengths, sel):
+    """Row indices of sequences `sel` in the packed [sum(lengths), d] layout."""
+    off = np.concatenate([[0], np.cumsum(lengths.astype(np.int64))])
+    return np.concatenate([np.arange(off[b], off[b + 1]) for b in sel])
+
+
+def compare_states(gm, om, ids, lengths, sel, what, layers=None):
+    """Hidden states of the rows `sel` of a GPU batch (run whole, so the
+    micro-batches and the batch's attention path are the ones exercised)
+    against the oracle's after each layer count in `layers` (-1: final)."""
+    nl = gm.shape.num_hidden_layers
+    layers = list(range(nl + 1)) + [-1] if layers is None else layers
+    sel = np.asarray(sel)
+    Tm = int(lengths[sel].max())
+    ref = om.encode(ids[sel, :Tm], lengths[sel], layers=layers)
+    rows = packed_rows(lengths, sel)
+    worst = 0.0
+    for i, n in enumerate(layers):
+        got = gm.encode_ids(ids, lengths, n_layers=n)[rows].astype(np.float64)
+        want = ref[i].astype(np.float64)
+        rel = (np.linalg.norm(got - want, axis=1) / np.linalg.norm(want, axis=1)).max()
+        worst = max(worst, rel)
+        assert rel <= STATE_REL, (what, n, rel, np.abs(got - want).max())
+    print(f"{what}: hidden states after {len(layers)} layer counts, worst row rel err {worst:.3g}", flush=True)
 
 
 def test_c1(models):
@@ -53,19 +113,56 @@ def test_c1(models):
     compare(gm.embed_ids(b.ids, b.lengths), om.embed(b.ids, b.lengths), "C1")
 
 
-def test_c2_subset(models):
-    """C2 (32 x 256, ragged): the first 8 and the last 4 sequences through
-    the oracle (each sequence's embedding does not depend on the others,
-    gemma_test.go:117-135). At 5 517 tokens the GPU runs the batch as three
-    micro-batches on three streams; these rows come from the first and the
-    last."""
+def test_c1_layer_states(models):
+    gm, om = models
+    b = S.make_batch("C1")
+    compare_states(gm, om, b.ids, b.lengths, [0], "C1 states")
+
+
+def test_c2_all_rows(models):
+    """C2 (32 x 256, ragged): every sequence through the oracle. At 5 517
+    tokens the GPU runs the batch as three micro-batches on three streams."""
     gm, om = models
     b = S.make_batch("C2")
-    got = gm.embed_ids(b.ids, b.lengths)
-    for sub in (slice(0, 8), slice(28, 32)):
-        Tm = int(b.lengths[sub].max())
-        ref = om.embed(b.ids[sub, :Tm], b.lengths[sub])
-        compare(got[sub], ref, f"C2[{sub.start}:{sub.stop}]")
+    compare(gm.embed_ids(b.ids, b.lengths), oracle_embed(om, b.ids, b.lengths), "C2 all")
+
+
+def test_c2_layer_states(models):
+    """Hidden states after every layer at C2, for sequences of the first,
+    middle and last micro-batch groups."""
+    gm, om = models
+    b = S.make_batch("C2")
+    compare_states(gm, om, b.ids, b.lengths, [0, 1, 2, 15, 16, 30, 31], "C2 states")
+
+
+def test_pool_head_l2_from_hidden_states(models):
+    """Pooling, the Dense head and L2 (embed.go:381-429,472-475) on the GPU's
+    own final hidden states, restated in float64: pins pool_kernel, the head
+    products (K-split last product) and l2norm_kernel apart from the encoder."""
+    gm, _ = models
+    b = S.make_batch("C2")
+    h = gm.encode_ids(b.ids, b.lengths).astype(np.float64)
+    emb = gm.embed_ids(b.ids, b.lengths)
+    off = np.concatenate([[0], np.cumsum(b.lengths.astype(np.int64))])
+    y = np.stack([h[off[i]:off[i + 1]].mean(0) for i in range(b.B)])
+    for i, o in enumerate(gm.shape.dense_out):
+        w = S.bf16_to_f32(S.make_weight(f"dense.{i}.linear.weight", (o, y.shape[1]), "m")).astype(np.float64)
+        y = y @ w.T
+    y /= np.linalg.norm(y, axis=1, keepdims=True)
+    d = np.abs(emb - y).max()
+    print(f"pool+head+L2 from GPU hidden states: max|d|={d:.3g}", flush=True)
+    assert d <= 2e-6
+
+
+def test_encode_arguments(models):
+    gm, _ = models
+    b = S.make_batch("C1")
+    with pytest.raises(G.GemmaError):
+        gm.encode_ids(b.ids, b.lengths, n_layers=gm.shape.num_hidden_layers + 1)
+    x0 = gm.encode_ids(b.ids, b.lengths, n_layers=0)
+    e = S.bf16_to_f32(S.make_weight("embed_tokens.weight", (262144, 768), "m"))
+    want = e[b.ids[0, :b.lengths[0]]] * np.float32(np.sqrt(768.0))
+    assert np.array_equal(x0, want)
 
 
 def test_batch_and_padding_invariance(models):
@@ -76,16 +173,16 @@ def test_batch_and_padding_invariance(models):
     for i in (0, 5, 17):
         L = int(b.lengths[i])
         alone = gm.embed_ids(b.ids[i:i + 1, :L], b.lengths[i:i + 1])
-        c = cos_rows(alone, full[i:i + 1])
-        assert c.min() >= 0.9999
+        assert cos_rows(alone, full[i:i + 1]).min() >= COS_MIN
+        assert np.abs(alone - full[i:i + 1]).max() <= MAXD
 
 
 @pytest.mark.parametrize("lengths", [[2000, 7, 300], [1500, 1500], [40] * 60 + [2048]])
 def test_microbatch_groups_match_single_sequences(models, lengths):
     """From 2 048 tokens a batch runs as two to four token-balanced groups
-    of sequences on their own streams; with one dominant sequence, two sequences
-    or many short ones every sequence's embedding still equals its
-    single-sequence run, and the shortest one the oracle's."""
+    of sequences on their own streams; with one dominant sequence, two
+    sequences or many short ones, the longest and the shortest sequence
+    against the oracle and the others against their single-sequence runs."""
     gm, om = models
     rng = np.random.default_rng(len(lengths))
     T = max(lengths)
@@ -94,13 +191,13 @@ def test_microbatch_groups_match_single_sequences(models, lengths):
     ids[:, 0] = 2
     ids[np.arange(T)[None, :] >= lens[:, None]] = 0
     full = gm.embed_ids(ids, lens)
-    for i in sorted(set([0, len(lens) - 1, int(np.argmin(lens))])):
+    for i in sorted(set([0, len(lens) - 1])):
         L = int(lens[i])
         alone = gm.embed_ids(ids[i:i + 1, :L], lens[i:i + 1])
-        assert cos_rows(alone, full[i:i + 1]).min() >= 0.99999, (lengths, i)
-    i = int(np.argmin(lens))
-    L = int(lens[i])
-    compare(full[i:i + 1], om.embed(ids[i:i + 1, :L], lens[i:i + 1]), f"groups {lengths[:3]}.. [{i}]")
+        assert cos_rows(alone, full[i:i + 1]).min() >= COS_MIN, (lengths, i)
+    for i in sorted(set([int(np.argmin(lens)), int(np.argmax(lens))])):
+        L = int(lens[i])
+        compare(full[i:i + 1], om.embed(ids[i:i + 1, :L], lens[i:i + 1]), f"groups {lengths[:3]}.. [{i}] L={L}")
     # Matryoshka truncation on the micro-batched path (embed.go:421-427)
     d256 = gm.embed_ids(ids, lens, dim=256).astype(np.float64)
     want = full[:, :256].astype(np.float64)
@@ -116,7 +213,7 @@ def test_dim_truncation(models):
     r = om.embed(b.ids, b.lengths, dim=256)
     assert g.shape == (1, 256)
     assert abs(np.linalg.norm(g) - 1) < 1e-5
-    assert cos_rows(g, r).min() >= 0.9999
+    compare(g, r, "C1 dim 256")
     with pytest.raises(G.GemmaError):
         gm.embed_ids(b.ids, b.lengths, dim=769)
 
@@ -130,90 +227,157 @@ def test_bad_inputs(models):
         gm.embed_ids(np.full((1, 4), 262144, np.int32), np.array([4], np.int32))  # id out of range
     with pytest.raises(G.GemmaError):
         gm.embed_ids(ids, np.array([0], np.int32))
+    with pytest.raises(G.GemmaError):
+        gm.encode_ids(np.full((1, 4), -1, np.int32), np.array([4], np.int32))
 
 
 def test_c3_sliding_band(models):
     """C3 (64 x 512, all full length): T = 512 > 257, so the 20 sliding layers
     mask |i-j| >= 257 (embed.go:169-172,183-186) and differ from the global
-    ones. All 64 on the GPU, the first 4 through the oracle."""
+    ones. All 64 on the GPU (two micro-batches, split-bf16 attention), every
+    fourth through the oracle, and one sequence of each group layer by layer."""
     gm, om = models
     b = S.make_batch("C3")
     got = gm.embed_ids(b.ids, b.lengths)
     assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
-    ref = om.embed(b.ids[:4], b.lengths[:4])
-    compare(got[:4], ref, "C3[0:4]")
+    sel = np.arange(0, 64, 4)
+    compare(got[sel], oracle_embed(om, b.ids[sel], b.lengths[sel]), "C3 every 4th")
+    compare_states(gm, om, b.ids, b.lengths, [1, 62], "C3 states", layers=[1, 5, 6, 12, 24, -1])
 
 
 def test_key_split_attention_with_sliding_band(models):
     """Two full 512-token sequences (1 024 tokens on one stream, 96
     attention items): the attention cuts each item's keys into runs (the
-    key-split path) while the 20 sliding layers mask |i-j| >= 257. The
-    first sequence against the oracle, both against their rows in C3's
-    64-sequence batch (no key split)."""
+    key-split path) while the 20 sliding layers mask |i-j| >= 257. Both
+    against the oracle, layer by layer for the first."""
     gm, om = models
     b = S.make_batch("C3")
     two = gm.embed_ids(b.ids[:2], b.lengths[:2])
-    compare(two[:1], om.embed(b.ids[:1], b.lengths[:1]), "C3[0] key-split")
-    full = gm.embed_ids(b.ids, b.lengths)
-    assert cos_rows(two, full[:2]).min() >= 0.99999
+    compare(two, om.embed(b.ids[:2], b.lengths[:2]), "C3[0:2] key-split")
+    compare_states(gm, om, b.ids[:2], b.lengths[:2], [0], "C3[0:2] key-split states", layers=[1, 6, 24, -1])
 
 
 def test_c4_long_sequences(models):
-    """C4 (8 x 2048, lengths 1024..2048): the GPU batch against the oracle for
-    the shortest sequence (band active, far beyond one attention tile)."""
+    """C4 (8 x 2048, lengths 1024..2048; four micro-batches, split-bf16
+    attention with the 257 band on sliding layers and every key on global
+    ones): all eight sequences against the oracle, and the longest layer by
+    layer."""
     gm, om = models
     b = S.make_batch("C4")
     got = gm.embed_ids(b.ids, b.lengths)
-    i = int(np.argmin(b.lengths))
-    L = int(b.lengths[i])
-    ref = om.embed(b.ids[i:i + 1, :L], b.lengths[i:i + 1])
-    compare(got[i:i + 1], ref, f"C4[{i}] L={L}")
-    # the other sequences: unit norm and batch invariance against a single-sequence run
+    compare(got, oracle_embed(om, b.ids, b.lengths, group=1), f"C4 all (L {b.lengths.min()}..{b.lengths.max()})")
     j = int(np.argmax(b.lengths))
-    alone = gm.embed_ids(b.ids[j:j + 1, :int(b.lengths[j])], b.lengths[j:j + 1])
-    assert cos_rows(alone, got[j:j + 1]).min() >= 0.9999
+    compare_states(gm, om, b.ids, b.lengths, [j], f"C4[{j}] L={int(b.lengths[j])} states",
+                   layers=[1, 2, 5, 6, 12, 18, 24, -1])
 
 
-def _topk_agree(q, docs, gi, oi, k, what):
-    """Top-k index lists agree wherever the float64 scores leave no near-tie
-    (gap > 1e-5 among the k+1 best); elsewhere the GPU's list must still be a
-    valid top-k within that tolerance. Ties order by lower index
+def test_c4_with_full_context_sequence(models):
+    """C4 with its longest sequence replaced by a full 2 048-token one (the
+    maximum context): the batch still takes four micro-batches and the
+    split-bf16 attention; the 2 048-token sequence against the oracle."""
+    gm, om = models
+    b = S.make_batch("C4")
+    ids, lens = b.ids.copy(), b.lengths.copy()
+    j = int(np.argmax(lens))
+    rng = np.random.default_rng(2048)
+    ids[j] = rng.integers(3, 262144, 2048)
+    ids[j, 0] = 2
+    lens[j] = 2048
+    got = gm.embed_ids(ids, lens)
+    compare(got[j:j + 1], om.embed(ids[j:j + 1], lens[j:j + 1]), f"C4 + full 2048 [{j}]")
+
+
+def _shape_variant(**kw):
+    return S.ModelShape(**kw)
+
+
+def test_window_bound_at_sequence_length_masks_agree(ctx):
+    """Appendix C-1 of the build's survey: when the window bound is at least
+    T the sliding layers apply no band, so at T = 512 a sliding_window whose
+    bidirectional bound (512/2+1 = 257 by default) is raised to 1 025, or the
+    unidirectional bound 512 (config.go:331-339: no mask when T <= w,
+    embed.go:169-172), both give the unbanded model; with the local RoPE base
+    set to the global one, local and global layers then compute the same
+    thing, so the model equals its all-global twin (pattern 1). The default
+    model's 257 band must differ. Rows of C3 on the GPU, two against the
+    oracle per variant."""
+    b = S.make_batch("C3")
+    sel = np.arange(0, 64, 8)
+    ids, lens = b.ids[sel], b.lengths[sel]
+    variants = {
+        "wide": dict(sliding_window=2048),
+        "unidirectional": dict(use_bidirectional=0),
+        "wide_same_base": dict(sliding_window=2048, rope_local_base_freq=1e6),
+        "all_global_same_base": dict(sliding_window_pattern=1, rope_local_base_freq=1e6),
+        "default": dict(),
+    }
+    out = {}
+    for name, kw in variants.items():
+        shape = _shape_variant(**kw)
+        gm = G.Model(shape, ctx)
+        gm.load_synthetic()
+        out[name] = gm.embed_ids(ids, lens)
+        gm.close()
+        if name in ("wide", "unidirectional", "wide_same_base"):
+            om = O.OracleModel(shape)
+            om.load_synthetic()
+            compare(out[name][:2], om.embed(ids[:2], lens[:2]), f"masks: {name} vs oracle")
+            om.close()
+    d_bound = np.abs(out["wide"] - out["unidirectional"]).max()
+    d_glob = np.abs(out["wide_same_base"] - out["all_global_same_base"]).max()
+    d_band = np.abs(out["wide"] - out["default"]).max()
+    print(f"masks agree: wide vs unidirectional max|d|={d_bound:.3g}, sliding vs global (same base) "
+          f"max|d|={d_glob:.3g}, band 257 vs none max|d|={d_band:.3g}", flush=True)
+    assert d_bound <= 1e-6
+    assert d_glob <= 1e-6
+    assert d_band > 1e-3
+
+
+def _topk_checked(s64, gi, oi, bound, what):
+    """Identity of top-k lists wherever the float64 scores s64's k+1 best are
+    separated by more than 2*bound per row (bound: how far either side's
+    score may be from s64); rows below that are reported and must still hold
+    valid top-k members within the bound. Ties order by lower index
     (reduce.go:286-289)."""
-    s = q.astype(np.float64) @ docs.astype(np.float64).T
-    srt = -np.sort(-s, axis=1)[:, :k + 1]
+    k = gi.shape[1]
+    srt = -np.sort(-s64, axis=1)[:, :k + 1]
     gaps = np.diff(-srt, axis=1).min(1)
-    clear = gaps > 1e-5
-    assert np.array_equal(gi[clear], oi[clear]), what
-    kth = srt[:, k - 1]
-    got_scores = np.take_along_axis(s, gi.astype(np.int64), 1)
-    assert (got_scores.min(1) >= kth - 1e-5).all(), what
-    print(f"{what}: {int(clear.sum())}/{len(clear)} rows without near-ties, all identical", flush=True)
-    return clear
+    bound = np.broadcast_to(np.asarray(bound, np.float64).reshape(-1), gaps.shape)
+    clear = gaps > 2 * bound
+    bad = np.nonzero(clear & (gi != oi).any(1))[0]
+    assert bad.size == 0, (what, bad[:10])
+    got_scores = np.take_along_axis(s64, gi.astype(np.int64), 1)
+    assert (got_scores.min(1) >= srt[:, k - 1] - 2 * bound).all(), what
+    unclear = np.nonzero(~clear)[0]
+    same_unclear = int((gi[unclear] == oi[unclear]).all(1).sum())
+    print(f"{what}: top-{k} identical on all {int(clear.sum())} rows whose gaps exceed the bound; "
+          f"{unclear.size} near-tie rows (of which {same_unclear} identical): {unclear.tolist()[:20]}", flush=True)
 
 
 def test_c5_scoring_top10(models, ctx):
-    """C5 (256 x 128 ragged) + scoring against 100 000 unit docs: embeddings
-    vs the oracle on 8 queries; GPU top-10 (fa_similarities_topk) vs the
-    oracle's top-10 on the same queries, and end to end from the oracle's own
-    embeddings of those 8."""
+    """C5 (256 x 128 ragged) + scoring against 100 000 unit docs: every
+    embedding against the oracle; GPU top-10 (fa_similarities_topk) against
+    the oracle's top-10 on the same queries (score error of either side
+    <= 1e-6), and end to end against the oracle's top-10 of its own
+    embeddings (a score moves by at most ||q_gpu - q_oracle|| for unit docs)."""
     from ai_amd import _native as N
     gm, om = models
     b = S.make_batch("C5")
     q = gm.embed_ids(b.ids, b.lengths)
-    sub = slice(0, 8)
-    Tm = int(b.lengths[sub].max())
-    ref = om.embed(b.ids[sub, :Tm], b.lengths[sub])
-    compare(q[sub], ref, "C5[0:8]")
+    ref = oracle_embed(om, b.ids, b.lengths, group=16)
+    compare(q, ref, "C5 all")
     docs = b.corpus
     k = 10
     idx = np.empty((q.shape[0], k), np.int32)
     val = np.empty((q.shape[0], k), np.float32)
     N.check(ctx.h, N.lib().fa_similarities_topk(ctx.h, N.ptr(q), q.shape[0], N.ptr(docs), docs.shape[0], 768, k,
                                                 N.ptr(idx), N.ptr(val)))
-    nq = 64
-    oi, ov = O.similarities_topk(q[:nq], docs, k)
-    clear = _topk_agree(q[:nq], docs, idx[:nq], oi, k, "C5 scoring, same queries")
-    assert clear.mean() >= 0.9
-    assert np.allclose(val[:nq], ov, atol=1e-5)
+    d64 = docs.astype(np.float64)
+    s_same = q.astype(np.float64) @ d64.T
+    oi, ov = O.similarities_topk(q, docs, k)
+    _topk_checked(s_same, idx, oi, 1e-6, "C5 scoring, same queries")
+    assert np.abs(val - np.take_along_axis(s_same, idx.astype(np.int64), 1)).max() <= 1e-6
+    s_ref = ref.astype(np.float64) @ d64.T
     oi2, _ = O.similarities_topk(ref, docs, k)
-    _topk_agree(ref, docs, idx[sub], oi2, k, "C5 scoring, oracle embeddings end to end")
+    dq = np.linalg.norm(q.astype(np.float64) - ref, axis=1)[:, None]
+    _topk_checked(s_ref, idx, oi2, dq + 1e-6, "C5 scoring end to end (GPU vs oracle embeddings)")

@@ -292,9 +292,11 @@ def test_similarities_topk_bruteforce():
 
 # ---- the encoder -----------------------------------------------------------------------------
 
-def f64_encoder(shape, weights, ids, lengths, dim=0):
+def f64_encoder(shape, weights, ids, lengths, dim=0, states=None):
     """Independent float64 restatement of models/gemma/embed.go:160-240,381-475
-    over unpadded sequences (one at a time), with unfolded weights."""
+    over unpadded sequences (one at a time), with unfolded weights. With a
+    list `states`, appends per sequence the residual stream after 0, 1, ...
+    layers followed by the final normed hidden states."""
     d, H, Hkv, D = shape.hidden_size, shape.num_attention_heads, shape.num_key_value_heads, shape.head_dim
     w = {k: v.astype(np.float64) for k, v in weights.items()}
     wb = shape.sliding_window // 2 + 1 if shape.use_bidirectional else shape.sliding_window
@@ -307,6 +309,7 @@ def f64_encoder(shape, weights, ids, lengths, dim=0):
             return v / np.sqrt((v ** 2).mean(-1, keepdims=True) + shape.rms_norm_eps) * (1 + g)
 
         pos = np.arange(L)
+        seq_states = [x.copy()]
         for l in range(shape.num_hidden_layers):
             p = f"layers.{l}."
             sliding = (l + 1) % shape.sliding_window_pattern != 0
@@ -345,7 +348,10 @@ def f64_encoder(shape, weights, ids, lengths, dim=0):
             up = h @ w[p + "mlp.up_proj.weight"].T
             gu = 0.5 * gt * (1 + np.tanh(0.7978845608028654 * (gt + 0.044715 * gt ** 3))) * up
             x = x + rms(gu @ w[p + "mlp.down_proj.weight"].T, w[p + "post_feedforward_layernorm.weight"])
+            seq_states.append(x.copy())
         hfin = rms(x, w["norm.weight"])
+        if states is not None:
+            states.append(seq_states + [hfin])
         y = hfin.mean(0)
         for i in range(len(shape.dense_out)):
             y = w[f"dense.{i}.linear.weight"] @ y
@@ -435,3 +441,33 @@ def test_oracle_padding_and_batch_invariance(tiny):
     wide = np.zeros((ids.shape[0], 37), np.int32)
     wide[:, :20] = ids
     assert cos_rows(om.embed(wide, lengths).astype(np.float64), full.astype(np.float64)).min() >= 0.9999
+
+
+def test_oracle_encode_states_vs_float64(tiny):
+    """orc_model_encode's snapshots (the residual stream after each layer and
+    the final hidden states) against the float64 restatement's, layer by
+    layer; snapshot 0 is the gather times float32(sqrt(d)) exactly, and pooling
+    the final states reproduces orc_model_embed."""
+    shape, ws, ids, lengths = tiny
+    om = oracle_model(shape, ws)
+    nl = shape.num_hidden_layers
+    st = []
+    f64_encoder(shape, ws, ids, lengths, states=st)
+    snaps = om.encode(ids, lengths, layers=list(range(nl + 1)) + [-1])
+    rows = np.concatenate([np.arange(int(L)) + b * ids.shape[1] for b, L in enumerate(lengths)])
+    want0 = ws["embed_tokens.weight"][ids.reshape(-1)[rows]] * np.float32(math.sqrt(shape.hidden_size))
+    assert np.array_equal(snaps[0], want0.astype(np.float32))
+    for i in range(nl + 2):
+        ref = np.concatenate([s[i] for s in st])
+        err = np.abs(snaps[i] - ref).max() / np.abs(ref).max()
+        assert err < 2e-5, (i, err)
+    # pool + head + L2 of the final states in float64 against orc_model_embed
+    h = snaps[-1].astype(np.float64)
+    off = np.concatenate([[0], np.cumsum(lengths)])
+    y = np.stack([h[off[b]:off[b + 1]].mean(0) for b in range(len(lengths))])
+    for i in range(len(shape.dense_out)):
+        y = y @ ws[f"dense.{i}.linear.weight"].astype(np.float64).T
+    y /= np.linalg.norm(y, axis=1, keepdims=True)
+    assert np.abs(om.embed(ids, lengths) - y).max() < 1e-6
+    with pytest.raises(ValueError):
+        om.encode(ids, lengths, layers=[nl + 1])
