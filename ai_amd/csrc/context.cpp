@@ -361,6 +361,16 @@ int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, cons
   if (nq > 65535) return set_error(ctx, FA_ERR_ARG, "Similarities top-k: %lld queries > 65535", (long long)nq);
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   int rc;
+  // Batches of queries: the fused kernels (no score matrix; blocks of 256
+  // queries share each pass over the docs). Few queries: the fp32-MFMA
+  // product and the two-pass top-k, which read the docs once without
+  // computing a 256-query block.
+  if (nq >= 128 && fa::score_fused_ok(queries, d, docs, d, d, topk)) {
+    const int nwg = fa::score_workgroups(nd, ctx->cu_count);
+    fa::DevBuf& ws = ctx->slot(S_TOPK);
+    if ((rc = ws.ensure(ctx, fa::score_scratch_bytes(d, nwg)))) return rc;
+    return fa::launch_score_topk(ctx, queries, nq, d, docs, nd, d, d, topk, idx, val, ws.ptr, nwg, ctx->stream);
+  }
   fa::DevBuf& sc = ctx->slot(S_C);
   if ((rc = sc.ensure(ctx, (size_t)(nq * nd) * 4))) return rc;
   fa::GemmArgs g;

@@ -140,6 +140,17 @@ int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t 
 // idx/val [nq x topk]; scratch holds topk_scratch_bytes(nq, nd, topk) bytes
 // of per-chunk candidates.
 int topk_scratch_bytes(int64_t nq, int64_t nd, int32_t topk);
+
+// Fused similarities + top-k (score.hip): no score matrix. Needs
+// score_fused_ok(); scratch holds score_scratch_bytes(d, nwg) bytes with
+// nwg = score_workgroups(nd, cus) workgroups per query block; the exact top
+// k (1 <= topk <= 16) by float32-rounded dot product into idx/val [nq x topk].
+int score_workgroups(int64_t nd, int cus);
+size_t score_scratch_bytes(int d, int nwg);
+bool score_fused_ok(const float* q, int64_t ldq, const float* docs, int64_t ldd, int d, int topk);
+int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, const float* docs, int64_t nd,
+                      int64_t ldd, int d, int topk, int32_t* idx, float* val, void* scratch, int nwg,
+                      hipStream_t s);
 int launch_topk(fa_ctx* ctx, const float* scores, int64_t nq, int64_t nd, int32_t topk, int32_t* idx, float* val,
                 void* scratch, hipStream_t s);
 

@@ -17,11 +17,13 @@
 #include <cstdint>
 
 #include "fa_internal.h"
+#include "device_math.h"
 
 namespace fa {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxK = 32;
 constexpr int kChunk = 16384;   // scores per pass-1 wave
@@ -140,12 +142,465 @@ __global__ __launch_bounds__(64) void topk_merge_kernel(const float* __restrict_
     W.offer(k, lane, ok ? cv[q * ncand + t] : NAN, ok ? ci[q * ncand + t] : INT32_MAX);
   }
   if (lane < k) {
-    if (val) val[q * k + lane] = W.lv;
-    idx[q * k + lane] = W.li;
+    if (val) val[q * k + lane] = W.li == INT32_MAX ? NAN : W.lv;
+    idx[q * k + lane] = W.li == INT32_MAX ? -1 : W.li;
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused scoring: similarities and top-k without a score matrix.
+//
+// Per block of up to 256 queries, four launches:
+//  1. score_qsplit_kernel: each query row split into hi + mid bf16 planes
+//     (hi = the row with its low 16 bits cleared, mid the same of the
+//     remainder) and its float64 norm.
+//  2. score_stage1_kernel: one workgroup per range of 32-doc blocks; tiles of
+//     256 queries x 128 docs on v_mfma_f32_32x32x16_bf16 with the docs split
+//     into hi + mid as they are staged in LDS and three products per pair
+//     (hi.hi + hi.mid + mid.hi, fp32 accumulate): an approximate score s'
+//     within eps(d) * |q| * |doc| of the exact dot product. Each lane keeps,
+//     for its two queries, the best four (s', index) of the docs it owns (the
+//     MFMA C layout gives a lane 16 docs of every 32-doc block); any doc a
+//     lane drops is no better than its list's fourth entry, which the lane
+//     reports as its discard bound. Doc norms are taken during the split.
+//  3. score_merge_kernel: one wave per query merges the 16 candidates of every
+//     workgroup to the best 16 by s', rescoring them exactly (float64 dot
+//     products rounded to float32) and ordering them by (value desc, index
+//     asc). The result is exact when the k-th rescored value exceeds every
+//     discard bound (lanes' and the merge's own 16th) plus eps * |q| *
+//     max|doc|: then no dropped doc can reach the top k. Otherwise the query
+//     is flagged.
+//  4. score_fallback_kernel: flagged queries (near-ties of more than a few
+//     docs around the k-th score, e.g. duplicated rows) are scanned exactly
+//     over every doc; the others return at once.
+// The output is the exact top k by float32-rounded dot product, larger first,
+// equal values by lower index (tensor/reduce.go:269-297); NaN scores rank
+// below every number.
+constexpr int kSQB = 256;    // queries per block
+constexpr int kSDB = 128;    // docs per tile
+constexpr int kSKL = 4;      // entries per lane list
+constexpr int kSCand = 16;   // candidates per (query, workgroup): 2 doc waves x 2 lane halves x kSKL
+constexpr int kSMerge = 16;  // candidates rescored per query
+constexpr int kSMaxK = 16;
+constexpr int kSMaxWG = 256;
+
+typedef __bf16 sbf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t su32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int s_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// 1. One wave per query row of the block: hi/mid planes [kSQB x d] (zero rows
+// past nq) and |q| in float64 rounded up to float32.
+__global__ __launch_bounds__(64) void score_qsplit_kernel(const float* __restrict__ q, int64_t ldq, int nq, int d,
+                                                          uint16_t* __restrict__ qh, uint16_t* __restrict__ qm,
+                                                          float* __restrict__ qnorm) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  double ss = 0;
+  for (int t = lane; t < d; t += 64) {
+    const float x = r < nq ? q[(int64_t)r * ldq + t] : 0.f;
+    const Split3 sp = split3(x);
+    qh[(int64_t)r * d + t] = (uint16_t)(sp.h >> 16);
+    qm[(int64_t)r * d + t] = (uint16_t)(sp.m >> 16);
+    ss += (double)x * x;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if (lane == 0) qnorm[r] = (float)(sqrt(ss) * (1.0 + 1e-6));
+}
+
+struct Stage1Params {
+  const uint16_t* qh;
+  const uint16_t* qm;
+  const float* docs;
+  int64_t ldd, nd;
+  int d, nq, nwg;
+  int64_t nblocks;  // 32-doc blocks
+  float* cv;
+  int32_t* ci;
+  float* bound;
+  float* wgnorm;
+};
+
+// 2. Workgroup w: docs [32*b0, min(32*b1, nd)) with b = w*nblocks/nwg. Eight
+// waves: wave (wq, wd) owns queries 64*wq .. +63 (two 32-column blocks) and
+// docs 64*wd .. +63 of each 128-doc tile (two 32-row blocks). K advances in
+// 32-wide slabs over (tile, slab) items: item i in LDS buffer i&1, item i+1
+// split from registers during item i's MFMAs, item i+2 loading.
+__global__ __launch_bounds__(512) void score_stage1_kernel(Stage1Params p) {
+  __shared__ __attribute__((aligned(16))) uint16_t Dp[2][2][kSDB * 32];
+  __shared__ __attribute__((aligned(16))) uint16_t Qp[2][2][kSQB * 32];
+  __shared__ float red[8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wq = wave >> 1, wd = wave & 1;
+  const int w = blockIdx.x;
+  const int64_t b0 = (int64_t)w * p.nblocks / p.nwg, b1 = (int64_t)(w + 1) * p.nblocks / p.nwg;
+  const int64_t dbeg = b0 * 32, dend = min(b1 * 32, p.nd);
+  const int ntile = (int)((b1 - b0 + 3) / 4);
+  const int nk = p.d / 32;
+  const int d = p.d;
+
+  // staging: doc row tid/4, chunk tid%4 (8 floats); query rows (tid + 512 i)/4
+  const int srow = tid >> 2, sc = tid & 3;
+  struct Regs {
+    f32x4 a[2];
+    su32x4 b[4];
+  };
+  auto load = [&](Regs& g, int item) {
+    const int t = item / nk, kt = item - t * nk;
+    const int64_t row = min(dbeg + (int64_t)t * kSDB + srow, p.nd - 1);
+    const float* src = p.docs + row * p.ldd + kt * 32 + sc * 8;
+    g.a[0] = *reinterpret_cast<const f32x4*>(src);
+    g.a[1] = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int idx = tid + 512 * (i & 1), qr = idx >> 2, c = idx & 3;
+      const uint16_t* pl = (i < 2) ? p.qh : p.qm;
+      g.b[i] = *reinterpret_cast<const su32x4*>(pl + (int64_t)qr * d + kt * 32 + c * 8);
+    }
+  };
+  float ss = 0.f, mx = 0.f;
+  auto split_store = [&](const Regs& g, int buf, int item) {
+    const int t = item / nk, kt = item - t * nk;
+    uint32_t h[8], m[8];
+    if (kt == 0) ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = g.a[e >> 2][e & 3];
+      const Split3 sp = split3(x);
+      h[e] = sp.h;
+      m[e] = sp.m;
+      ss = fmaf(x, x, ss);
+    }
+    const int o = srow * 32 + ((sc ^ s_swz(srow)) << 3);
+    *reinterpret_cast<uint4*>(&Dp[buf][0][o]) =
+        make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
+    *reinterpret_cast<uint4*>(&Dp[buf][1][o]) =
+        make_uint4(pack_hi16(m[0], m[1]), pack_hi16(m[2], m[3]), pack_hi16(m[4], m[5]), pack_hi16(m[6], m[7]));
+    if (kt == nk - 1) {  // the row's sum of squares is complete: four threads hold its parts
+      float tot = ss + __shfl_xor(ss, 1, 64);
+      tot += __shfl_xor(tot, 2, 64);
+      if (dbeg + (int64_t)t * kSDB + srow < dend) mx = fmaxf(mx, tot);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int idx = tid + 512 * (i & 1), qr = idx >> 2, c = idx & 3;
+      *reinterpret_cast<su32x4*>(&Qp[buf][i >> 1][qr * 32 + ((c ^ s_swz(qr)) << 3)]) = g.b[i];
+    }
+  };
+  const int sw = s_swz(lane & 31), hh = lane >> 5;
+  auto read_ops = [&](int buf, int s, sbf16x8 (&oa)[2][2], sbf16x8 (&ob)[2][2]) {
+    const int co = ((2 * s + hh) ^ sw) << 3;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        oa[t][i] = *reinterpret_cast<const sbf16x8*>(&Dp[buf][t][(wd * 64 + i * 32 + (lane & 31)) * 32 + co]);
+        ob[t][i] = *reinterpret_cast<const sbf16x8*>(&Qp[buf][t][(wq * 64 + i * 32 + (lane & 31)) * 32 + co]);
+      }
+  };
+  f32x16 acc[2][2];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  };
+  zero_acc();
+  // doc blocks of this wave inside the range in the item's tile (0, 1 or 2)
+  auto nvalid = [&](int item) {
+    const int t = item / nk;
+    const int64_t blk0 = dbeg + (int64_t)t * kSDB + wd * 64;
+    return (int)min<int64_t>(2, max<int64_t>(0, (dend - blk0 + 31) / 32));
+  };
+  auto mfma_step = [&](const sbf16x8 (&oa)[2][2], const sbf16x8 (&ob)[2][2], int nv) {
+    // mid.hi, hi.mid, then hi.hi (smallest first)
+    if (nv == 2) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[1][i], ob[0][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][i], ob[1][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][i], ob[0][j], acc[i][j], 0, 0, 0);
+        }
+    } else if (nv == 1) {
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[1][0], ob[0][j], acc[0][j], 0, 0, 0);
+        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][0], ob[1][j], acc[0][j], 0, 0, 0);
+        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][0], ob[0][j], acc[0][j], 0, 0, 0);
+      }
+    }
+  };
+  // lane lists: query column j of this wave, best kSKL (value desc, index asc)
+  float lv[2][kSKL];
+  int li[2][kSKL];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int e = 0; e < kSKL; e++) {
+      lv[j][e] = -INFINITY;
+      li[j][e] = INT32_MAX;
+    }
+  // C element (i, j, r) of lane l: doc row 8*(r/4) + 4*(l/32) + r%4 of block i,
+  // query column l%32 of block j
+  auto epilogue = [&](int item) {
+    const int t = item / nk;
+    const int64_t tile0 = dbeg + (int64_t)t * kSDB + wd * 64 + 4 * hh;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int64_t doc = tile0 + i * 32 + 8 * (r >> 2) + (r & 3);
+        const bool ok = doc < dend;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          float cv = ok ? acc[i][j][r] : NAN;
+          int ci = (int)doc;
+#pragma unroll
+          for (int e = 0; e < kSKL; e++) {
+            const bool b = better(cv, ci, lv[j][e], li[j][e]);
+            const float tv = lv[j][e];
+            const int ti = li[j][e];
+            lv[j][e] = b ? cv : tv;
+            li[j][e] = b ? ci : ti;
+            cv = b ? tv : cv;
+            ci = b ? ti : ci;
+          }
+        }
+      }
+    zero_acc();
+  };
+  // items i0 .. i1-1 of one tile (i1 - i0 = nk slabs)
+  auto body = [&](int item, int last, int nv, const Regs& use, Regs& fill) {
+    const int buf = item & 1;
+    load(fill, min(item + 2, last));
+    sbf16x8 a0[2][2], b0[2][2], a1[2][2], b1[2][2];
+    read_ops(buf, 0, a0, b0);
+    read_ops(buf, 1, a1, b1);
+    mfma_step(a0, b0, nv);
+    split_store(use, buf ^ 1, item + 1);
+    mfma_step(a1, b1, nv);
+    __syncthreads();
+  };
+  for (int t = 0; t < ntile; t++) {
+    const int i0 = t * nk, last = i0 + nk - 1;
+    const int nv = nvalid(i0);
+    {
+      Regs rA, rB;
+      load(rA, i0);
+      split_store(rA, i0 & 1, i0);
+      load(rA, min(i0 + 1, last));
+      __syncthreads();
+      int item = i0;
+      for (; item + 2 <= last; item += 2) {
+        body(item, last, nv, rA, rB);
+        body(item + 1, last, nv, rB, rA);
+      }
+      if (item + 1 <= last) {
+        body(item, last, nv, rA, rB);
+        item++;
+      }
+      sbf16x8 a0[2][2], b0[2][2], a1[2][2], b1[2][2];
+      read_ops(item & 1, 0, a0, b0);
+      read_ops(item & 1, 1, a1, b1);
+      mfma_step(a0, b0, nv);
+      mfma_step(a1, b1, nv);
+    }
+    epilogue(i0);
+    __syncthreads();  // the next tile's first slab overwrites the buffers read above
+  }
+  // candidates and discard bounds of this workgroup
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int qr = wq * 64 + j * 32 + (lane & 31);
+    if (qr < p.nq) {
+      const int64_t base = ((int64_t)qr * p.nwg + w) * kSCand + wd * 8 + hh * kSKL;
+#pragma unroll
+      for (int e = 0; e < kSKL; e++) {
+        p.cv[base + e] = lv[j][e];
+        p.ci[base + e] = li[j][e];
+      }
+      p.bound[((int64_t)qr * p.nwg + w) * 4 + wd * 2 + hh] = lv[j][kSKL - 1];
+    }
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    float m = red[0];
+    for (int i = 1; i < 8; i++) m = fmaxf(m, red[i]);
+    p.wgnorm[w] = m;
+  }
+}
+
+// float64 dot product of two float32 rows of length d (d % 4 == 0, 16-byte
+// aligned), rounded to float32.
+__device__ __forceinline__ float exact_dot(const float* __restrict__ a, const float* __restrict__ b, int d) {
+  double s = 0;
+  for (int t = 0; t < d; t += 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(a + t), y = *reinterpret_cast<const f32x4*>(b + t);
+    s = fma((double)x[0], (double)y[0], s);
+    s = fma((double)x[1], (double)y[1], s);
+    s = fma((double)x[2], (double)y[2], s);
+    s = fma((double)x[3], (double)y[3], s);
+  }
+  return (float)s;
+}
+
+struct MergeParams {
+  const float* cv;
+  const int32_t* ci;
+  const float* bound;
+  const float* wgnorm;
+  const float* qnorm;
+  const float* q;
+  int64_t ldq;
+  const float* docs;
+  int64_t ldd;
+  int nwg, d, k;
+  float eps;  // score error bound of stage 1 per |q| |doc|
+  int32_t* idx;
+  float* val;
+  int32_t* flag;
+};
+
+// 3. One wave per query.
+__global__ __launch_bounds__(64) void score_merge_kernel(MergeParams p) {
+  const int64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int ncand = p.nwg * kSCand;
+  WaveList W;
+  for (int t0 = 0; t0 < ncand; t0 += 64) {
+    const int t = t0 + lane;
+    const bool ok = t < ncand;
+    W.offer(kSMerge, lane, ok ? p.cv[q * ncand + t] : NAN, ok ? p.ci[q * ncand + t] : INT32_MAX);
+  }
+  float xb = -INFINITY, dn2 = 0.f;
+  for (int t = lane; t < p.nwg * 4; t += 64) xb = fmaxf(xb, p.bound[q * p.nwg * 4 + t]);
+  for (int t = lane; t < p.nwg; t += 64) dn2 = fmaxf(dn2, p.wgnorm[t]);
+  xb = wave_max(xb);
+  dn2 = wave_max(dn2);
+  xb = fmaxf(xb, __shfl(W.lv, kSMerge - 1, 64));  // the merge's own discards
+  // exact rescoring of the kSMerge candidates, then the top k of those
+  const bool have = lane < kSMerge && W.li != INT32_MAX;
+  const float e = have ? exact_dot(p.q + q * p.ldq, p.docs + (int64_t)W.li * p.ldd, p.d) : NAN;
+  WaveList X;
+  X.offer(p.k, lane, e, have ? W.li : INT32_MAX);
+  const float ek = __shfl(X.lv, p.k - 1, 64);
+  const float margin = p.eps * p.qnorm[q] * sqrtf(dn2) * (1.f + 1e-4f);
+  const bool exact = ek > xb + margin;  // false for NaN: flagged
+  if (exact && lane < p.k) {
+    p.idx[q * p.k + lane] = X.li;
+    if (p.val) p.val[q * p.k + lane] = X.lv;
+  }
+  if (lane == 0) p.flag[q] = exact ? 0 : 1;
+}
+
+// 4. Flagged queries: every doc's exact score, four waves' lists merged.
+__global__ __launch_bounds__(256) void score_fallback_kernel(const float* __restrict__ qs, int64_t ldq,
+                                                             const float* __restrict__ docs, int64_t ldd, int64_t nd,
+                                                             int d, int k, const int32_t* __restrict__ flag,
+                                                             int32_t* __restrict__ idx, float* __restrict__ val) {
+  const int64_t q = blockIdx.x;
+  if (flag[q] == 0) return;
+  __shared__ float sv[4][kSMaxK];
+  __shared__ int si[4][kSMaxK];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  WaveList W;
+  for (int64_t base = 0; base < nd; base += 256) {
+    const int64_t j = base + tid;
+    const bool ok = j < nd;
+    W.offer(k, lane, ok ? exact_dot(qs + q * ldq, docs + j * ldd, d) : NAN, ok ? (int)j : INT32_MAX);
+  }
+  if (lane < k) {
+    sv[wave][lane] = W.lv;
+    si[wave][lane] = W.li;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    for (int w2 = 1; w2 < 4; w2++) W.offer(k, lane, lane < k ? sv[w2][lane] : NAN, lane < k ? si[w2][lane] : INT32_MAX);
+    if (lane < k) {
+      idx[q * k + lane] = W.li == INT32_MAX ? -1 : W.li;
+      if (val) val[q * k + lane] = W.li == INT32_MAX ? NAN : W.lv;
+    }
+  }
+}
+
+struct ScoreScratch {
+  uint16_t *qh, *qm;
+  float *qnorm, *cv, *bound, *wgnorm;
+  int32_t *ci, *flag;
+};
+
+size_t score_layout(int d, int nwg, char* base, ScoreScratch* s) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* ptr = base ? base + off : nullptr;
+    off += (bytes + 255) & ~(size_t)255;
+    return ptr;
+  };
+  ScoreScratch t;
+  t.qh = (uint16_t*)take((size_t)kSQB * d * 2);
+  t.qm = (uint16_t*)take((size_t)kSQB * d * 2);
+  t.qnorm = (float*)take(kSQB * 4);
+  t.cv = (float*)take((size_t)kSQB * nwg * kSCand * 4);
+  t.ci = (int32_t*)take((size_t)kSQB * nwg * kSCand * 4);
+  t.bound = (float*)take((size_t)kSQB * nwg * 4 * 4);
+  t.wgnorm = (float*)take((size_t)nwg * 4);
+  t.flag = (int32_t*)take(kSQB * 4);
+  if (s) *s = t;
+  return off;
+}
+
 }  // namespace
+
+int score_workgroups(int64_t nd, int cus) {
+  const int64_t nb = (nd + 31) / 32;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({nb, (int64_t)kSMaxWG, (int64_t)std::max(cus, 1)}));
+}
+
+size_t score_scratch_bytes(int d, int nwg) { return score_layout(d, nwg, nullptr, nullptr); }
+
+bool score_fused_ok(const float* q, int64_t ldq, const float* docs, int64_t ldd, int d, int topk) {
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  return d > 0 && d % 32 == 0 && topk >= 1 && topk <= kSMaxK && al(q) && al(docs) && ldq % 4 == 0 && ldd % 4 == 0;
+}
+
+int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, const float* docs, int64_t nd,
+                      int64_t ldd, int d, int topk, int32_t* idx, float* val, void* scratch, int nwg,
+                      hipStream_t s) {
+  if (!score_fused_ok(q, ldq, docs, ldd, d, topk))
+    return set_error(ctx, FA_ERR_ARG, "Similarities: fused scoring needs d %% 32 == 0, 1 <= k <= %d and 16-byte "
+                     "aligned rows", kSMaxK);
+  ScoreScratch sc;
+  score_layout(d, nwg, static_cast<char*>(scratch), &sc);
+  // stage-1 error per |q| |doc|: the dropped split terms (3 * 2^-14 + 2 * 2^-21
+  // + 2^-28) and fp32 accumulation over 3d products (3d * 2^-24, times 1.02 for
+  // the kept terms' magnitude), plus the rounding of a rescored value
+  const float eps = (float)(3.0 * std::ldexp(1.0, -14) + 2.0 * std::ldexp(1.0, -21) + std::ldexp(1.0, -28) +
+                            1.02 * 3.0 * d * std::ldexp(1.0, -24) + std::ldexp(1.0, -22));
+  for (int64_t q0 = 0; q0 < nq; q0 += kSQB) {
+    const int nb = (int)std::min<int64_t>(kSQB, nq - q0);
+    const float* qb = q + q0 * ldq;
+    hipLaunchKernelGGL(score_qsplit_kernel, dim3(kSQB), dim3(64), 0, s, qb, ldq, nb, d, sc.qh, sc.qm, sc.qnorm);
+    Stage1Params p1;
+    p1.qh = sc.qh; p1.qm = sc.qm; p1.docs = docs; p1.ldd = ldd; p1.nd = nd; p1.d = d; p1.nq = nb; p1.nwg = nwg;
+    p1.nblocks = (nd + 31) / 32; p1.cv = sc.cv; p1.ci = sc.ci; p1.bound = sc.bound; p1.wgnorm = sc.wgnorm;
+    hipLaunchKernelGGL(score_stage1_kernel, dim3(nwg), dim3(512), 0, s, p1);
+    MergeParams pm;
+    pm.cv = sc.cv; pm.ci = sc.ci; pm.bound = sc.bound; pm.wgnorm = sc.wgnorm; pm.qnorm = sc.qnorm; pm.q = qb;
+    pm.ldq = ldq; pm.docs = docs; pm.ldd = ldd; pm.nwg = nwg; pm.d = d; pm.k = topk; pm.eps = eps;
+    pm.idx = idx + q0 * topk; pm.val = val ? val + q0 * topk : nullptr; pm.flag = sc.flag;
+    hipLaunchKernelGGL(score_merge_kernel, dim3(nb), dim3(64), 0, s, pm);
+    hipLaunchKernelGGL(score_fallback_kernel, dim3(nb), dim3(256), 0, s, qb, ldq, docs, ldd, nd, d, topk, sc.flag,
+                       idx + q0 * topk, val ? val + q0 * topk : nullptr);
+  }
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
 
 int topk_scratch_bytes(int64_t nq, int64_t nd, int32_t topk) {
   const int64_t nchunks = std::min<int64_t>(kMaxChunks, (nd + kChunk - 1) / kChunk);

@@ -434,7 +434,11 @@ ORC_API int orc_attention(const float* q, const float* k, const float* v, int B,
 
 // ---------------------------------------------------------------------------
 // Similarities + top-k (cluster/cluster.go:185-190; ties -> lower index as
-// tensor/reduce.go:286-289's first-max rule).
+// tensor/reduce.go:286-289's first-max rule). NaN scores rank below every
+// number (a NaN never compares greater in the reference's Argmax loop; the
+// loop only returns a NaN when it is the row's first element, an artifact
+// this build does not follow); slots past a row's non-NaN scores hold index
+// -1 and value NaN.
 // ---------------------------------------------------------------------------
 ORC_API int orc_similarities_topk(const float* Q, i64 nq, const float* Dm, i64 nd, int d, int topk, int32_t* idx,
                                   float* val) {
@@ -454,11 +458,14 @@ ORC_API int orc_similarities_topk(const float* Q, i64 nq, const float* Dm, i64 n
       }
       for (i64 j = 0; j < nd; j++) order[j] = (int32_t)j;
       std::partial_sort(order.begin(), order.begin() + topk, order.end(), [&](int32_t a, int32_t b) {
-        if (sc[a] != sc[b]) return sc[a] > sc[b];
+        const bool na = std::isnan(sc[a]), nb = std::isnan(sc[b]);
+        if (na != nb) return nb;
+        if (!na && sc[a] != sc[b]) return sc[a] > sc[b];
         return a < b;
       });
       for (int t = 0; t < topk; t++) {
-        idx[qi * topk + t] = order[t];
+        const bool nan = std::isnan(sc[order[t]]);
+        idx[qi * topk + t] = nan ? -1 : order[t];
         if (val) val[qi * topk + t] = sc[order[t]];
       }
     }

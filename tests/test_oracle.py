@@ -290,6 +290,26 @@ def test_similarities_topk_bruteforce():
     assert idx[0, :4].tolist() == [5, 10, 20, 30]
 
 
+def test_similarities_topk_nan_rule():
+    """NaN scores rank below every number (never selected while a number
+    remains), whatever their position, the first included; slots past a
+    row's non-NaN scores hold index -1. A mistake such as NaN-first order or
+    the reference Argmax's "first element wins when it is NaN" fails here."""
+    r = np.random.default_rng(6)
+    q = r.standard_normal((2, 8)).astype(np.float32)
+    docs = r.standard_normal((12, 8)).astype(np.float32)
+    docs[[0, 4, 9]] = np.nan
+    idx, val = O.similarities_topk(q, docs, 12)
+    s = q.astype(np.float64) @ docs.T.astype(np.float64)
+    for i in range(2):
+        ok = [j for j in np.lexsort((np.arange(12), -np.nan_to_num(s[i], nan=-np.inf))) if not np.isnan(s[i, j])]
+        assert idx[i, :9].tolist() == ok
+        assert idx[i, 9:].tolist() == [-1, -1, -1]
+        assert np.isnan(val[i, 9:]).all()
+    idx1, _ = O.similarities_topk(q, docs, 1)
+    assert idx1[:, 0].tolist() == [int(np.nanargmax(s[i])) for i in range(2)]
+
+
 # ---- the encoder -----------------------------------------------------------------------------
 
 def f64_encoder(shape, weights, ids, lengths, dim=0, states=None):
