@@ -467,34 +467,171 @@ struct MergeParams {
   int32_t* flag;
 };
 
-// 3. One wave per query.
-__global__ __launch_bounds__(64) void score_merge_kernel(MergeParams p) {
+// Sorting networks over (value, index) pairs in the full order (value desc,
+// index asc). NaN candidates enter as (-inf, INT32_MAX), below every pair
+// that stands for a doc.
+__device__ __forceinline__ void cas_desc(float& va, int& ia, float& vb, int& ib) {
+  // after the call (va, ia) is the better of the two
+  const bool sw = better(vb, ib, va, ia);
+  const float tv = va;
+  const int ti = ia;
+  va = sw ? vb : va;
+  ia = sw ? ib : ia;
+  vb = sw ? tv : vb;
+  ib = sw ? ti : ib;
+}
+
+// Bitonic sort of N register pairs, best first.
+template <int N>
+__device__ __forceinline__ void sort_list(float (&v)[N], int (&ix)[N]) {
+#pragma unroll
+  for (int k = 2; k <= N; k *= 2)
+#pragma unroll
+    for (int j = k / 2; j > 0; j /= 2)
+#pragma unroll
+      for (int i = 0; i < N; i++) {
+        const int l = i ^ j;
+        if (l > i) {
+          if ((i & k) == 0) cas_desc(v[i], ix[i], v[l], ix[l]);
+          else cas_desc(v[l], ix[l], v[i], ix[i]);
+        }
+      }
+}
+
+// Two sorted lists (best first) -> the best N of their union, sorted: the
+// pairwise better of A[i] and B[N-1-i] is a bitonic sequence holding those
+// N, then half-cleaners sort it.
+template <int N>
+__device__ __forceinline__ void merge_lists(float (&v)[N], int (&ix)[N], const float (&bv)[N], const int (&bi)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; i++)
+    if (better(bv[N - 1 - i], bi[N - 1 - i], v[i], ix[i])) {
+      v[i] = bv[N - 1 - i];
+      ix[i] = bi[N - 1 - i];
+    }
+#pragma unroll
+  for (int j = N / 2; j > 0; j /= 2)
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      const int l = i ^ j;
+      if (l > i) cas_desc(v[i], ix[i], v[l], ix[l]);
+    }
+}
+
+// 3. Four waves per query: each thread loads and sorts kSMerge candidates,
+// the lanes of a wave merge their lists pairwise (lane ^ 1, ^ 2, ... ^ 32)
+// until every lane holds the wave's best kSMerge, wave 0 merges the four
+// waves' lists, rescores them exactly and checks the bound.
+__global__ __launch_bounds__(256) void score_merge_kernel(MergeParams p) {
+  __shared__ float sv[4][kSMerge];
+  __shared__ int si[4][kSMerge];
+  __shared__ float sx[4], sd[4];
   const int64_t q = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int ncand = p.nwg * kSCand;
-  WaveList W;
-  for (int t0 = 0; t0 < ncand; t0 += 64) {
-    const int t = t0 + lane;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ncand = p.nwg * kSCand;  // at most kSMaxWG * kSCand = kSMerge per thread
+  static_assert(kSMaxWG * kSCand == 256 * kSMerge, "one list of kSMerge candidates per thread");
+  float v[kSMerge];
+  int ix[kSMerge];
+#pragma unroll
+  for (int u = 0; u < kSMerge; u++) {
+    const int t = tid + 256 * u;
     const bool ok = t < ncand;
-    W.offer(kSMerge, lane, ok ? p.cv[q * ncand + t] : NAN, ok ? p.ci[q * ncand + t] : INT32_MAX);
+    const float c = ok ? p.cv[q * ncand + t] : NAN;
+    const bool nan = !(c == c);
+    v[u] = nan ? -INFINITY : c;
+    ix[u] = (ok && !nan) ? p.ci[q * ncand + t] : INT32_MAX;
   }
   float xb = -INFINITY, dn2 = 0.f;
-  for (int t = lane; t < p.nwg * 4; t += 64) xb = fmaxf(xb, p.bound[q * p.nwg * 4 + t]);
-  for (int t = lane; t < p.nwg; t += 64) dn2 = fmaxf(dn2, p.wgnorm[t]);
+  for (int t = tid; t < p.nwg * 4; t += 256) xb = fmaxf(xb, p.bound[q * p.nwg * 4 + t]);
+  for (int t = tid; t < p.nwg; t += 256) dn2 = fmaxf(dn2, p.wgnorm[t]);
+  sort_list(v, ix);
+#pragma unroll
+  for (int m = 1; m < 64; m *= 2) {
+    float bv[kSMerge];
+    int bi[kSMerge];
+#pragma unroll
+    for (int u = 0; u < kSMerge; u++) {
+      bv[u] = __shfl_xor(v[u], m, 64);
+      bi[u] = __shfl_xor(ix[u], m, 64);
+    }
+    merge_lists(v, ix, bv, bi);
+  }
   xb = wave_max(xb);
   dn2 = wave_max(dn2);
-  xb = fmaxf(xb, __shfl(W.lv, kSMerge - 1, 64));  // the merge's own discards
-  // exact rescoring of the kSMerge candidates, then the top k of those
-  const bool have = lane < kSMerge && W.li != INT32_MAX;
-  const float e = have ? exact_dot(p.q + q * p.ldq, p.docs + (int64_t)W.li * p.ldd, p.d) : NAN;
-  WaveList X;
-  X.offer(p.k, lane, e, have ? W.li : INT32_MAX);
-  const float ek = __shfl(X.lv, p.k - 1, 64);
+  if (lane == 0) {
+#pragma unroll
+    for (int u = 0; u < kSMerge; u++) {
+      sv[wave][u] = v[u];
+      si[wave][u] = ix[u];
+    }
+    sx[wave] = xb;
+    sd[wave] = dn2;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w2 = 1; w2 < 4; w2++) {
+    float bv[kSMerge];
+    int bi[kSMerge];
+#pragma unroll
+    for (int u = 0; u < kSMerge; u++) {
+      bv[u] = sv[w2][u];
+      bi[u] = si[w2][u];
+    }
+    merge_lists(v, ix, bv, bi);
+    xb = fmaxf(xb, sx[w2]);
+    dn2 = fmaxf(dn2, sd[w2]);
+  }
+  xb = fmaxf(xb, v[kSMerge - 1]);  // the merge's own discards
+  // exact rescoring: float64 dot products of the query with the kSMerge
+  // candidates, the wave's lanes taking four columns each per 256, rounded to
+  // float32; lane u keeps candidate u's value
+  double part[kSMerge];
+#pragma unroll
+  for (int u = 0; u < kSMerge; u++) part[u] = 0.0;
+  const float* qrow = p.q + q * p.ldq;
+  for (int t = 4 * lane; t < p.d; t += 256) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(qrow + t);
+#pragma unroll
+    for (int u = 0; u < kSMerge; u++) {
+      if (ix[u] == INT32_MAX) continue;
+      const f32x4 y = *reinterpret_cast<const f32x4*>(p.docs + (int64_t)ix[u] * p.ldd + t);
+      part[u] = fma((double)x[0], (double)y[0], part[u]);
+      part[u] = fma((double)x[1], (double)y[1], part[u]);
+      part[u] = fma((double)x[2], (double)y[2], part[u]);
+      part[u] = fma((double)x[3], (double)y[3], part[u]);
+    }
+  }
+  float e = -INFINITY;
+  int me = INT32_MAX;
+#pragma unroll
+  for (int u = 0; u < kSMerge; u++) {
+    double t = part[u];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    if (lane == u && ix[u] != INT32_MAX) {
+      e = (float)t;
+      me = ix[u];
+    }
+  }
+  // rank of this lane's exact value among the kSMerge
+  int rank = 0;
+#pragma unroll
+  for (int u = 0; u < kSMerge; u++) {
+    const float eu = __shfl(e, u, 64);
+    const int iu = __shfl(me, u, 64);
+    rank += better(eu, iu, e, me) ? 1 : 0;
+  }
+  // the k-th best exact value: the lane of rank k-1
+  const uint64_t at = __ballot(lane < kSMerge && rank == p.k - 1);
+  const int src = at ? __ffsll((unsigned long long)at) - 1 : 0;
+  const float ek = __shfl(e, src, 64);
+  const int ik = __shfl(me, src, 64);
   const float margin = p.eps * p.qnorm[q] * sqrtf(dn2) * (1.f + 1e-4f);
-  const bool exact = ek > xb + margin;  // false for NaN: flagged
-  if (exact && lane < p.k) {
-    p.idx[q * p.k + lane] = X.li;
-    if (p.val) p.val[q * p.k + lane] = X.lv;
+  // no lane of rank k-1: fewer than k candidates stand for docs
+  const bool exact = at != 0 && ik != INT32_MAX && ek > xb + margin;  // false for NaN: flagged
+  if (exact && lane < kSMerge && rank < p.k) {
+    p.idx[q * p.k + rank] = me;
+    if (p.val) p.val[q * p.k + rank] = e;
   }
   if (lane == 0) p.flag[q] = exact ? 0 : 1;
 }
@@ -594,7 +731,7 @@ int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, cons
     pm.cv = sc.cv; pm.ci = sc.ci; pm.bound = sc.bound; pm.wgnorm = sc.wgnorm; pm.qnorm = sc.qnorm; pm.q = qb;
     pm.ldq = ldq; pm.docs = docs; pm.ldd = ldd; pm.nwg = nwg; pm.d = d; pm.k = topk; pm.eps = eps;
     pm.idx = idx + q0 * topk; pm.val = val ? val + q0 * topk : nullptr; pm.flag = sc.flag;
-    hipLaunchKernelGGL(score_merge_kernel, dim3(nb), dim3(64), 0, s, pm);
+    hipLaunchKernelGGL(score_merge_kernel, dim3(nb), dim3(256), 0, s, pm);
     hipLaunchKernelGGL(score_fallback_kernel, dim3(nb), dim3(256), 0, s, qb, ldq, docs, ldd, nd, d, topk, sc.flag,
                        idx + q0 * topk, val ? val + q0 * topk : nullptr);
   }

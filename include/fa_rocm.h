@@ -141,13 +141,20 @@ int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, in
  * returns, per query, the topk largest scores in descending order with their
  * doc indices; equal scores are ordered by the lower index (the first-max
  * rule of (*Tensor).Argmax, tensor/reduce.go:269-297). 1 <= topk <= 32,
- * nq <= 65535. NaN scores are never selected. */
+ * nq <= 65535. NaN scores rank below every number (the reference's Argmax
+ * returns a NaN only when it is a row's first element; this build never
+ * selects one); slots past a row's non-NaN scores get index -1 and value NaN.
+ * From 128 queries with d % 32 == 0, topk <= 16 and 16-byte aligned rows the
+ * scores are the exact dot products rounded to float32 and no score matrix is
+ * formed (blocks of 256 queries); otherwise an fp32-MFMA product is followed
+ * by a two-pass top-k. */
 int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
                          int32_t topk, int32_t* idx, float* val);
 
 /* Device-pointer variant of fa_similarities_topk (enqueue only). */
 int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
                              int32_t topk, int32_t* idx, float* val);
+
 
 /* ---- cluster (cluster/cluster.go) ------------------------------------ */
 
