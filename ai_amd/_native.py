@@ -76,6 +76,7 @@ _SIGS = {
                                i64, i64, f32, vp]),
     "fa_similarities_topk": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
     "fa_similarities_topk_dev": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
+    "fa_similarities_topk_dev_noalloc": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
     "fa_cluster_normalize": (C.c_int, [vp, vp, i64, i32, vp]),
     "fa_cluster_normalize_dev": (C.c_int, [vp, vp, i64, i32, vp]),
     "fa_cluster_nearest": (C.c_int, [vp, vp, i64, vp, i64, i32, vp, vp]),

@@ -106,6 +106,13 @@ int fa_create(int device, fa_ctx** out) {
   }
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->cu_count = prop.multiProcessorCount;
+  const int rc = fa::noalloc_scratch_init(c);
+  if (rc) {
+    std::string msg = c->last_error;
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return set_error(nullptr, rc, "%s", msg.c_str());
+  }
   *out = c;
   return FA_OK;
 }

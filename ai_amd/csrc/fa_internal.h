@@ -146,6 +146,9 @@ int topk_scratch_bytes(int64_t nq, int64_t nd, int32_t topk);
 // nwg = score_workgroups(nd, cus) workgroups per query block; the exact top
 // k (1 <= topk <= 16) by float32-rounded dot product into idx/val [nq x topk].
 int score_workgroups(int64_t nd, int cus);
+// Records the device address of the no-alloc entry point's fixed scratch
+// array for ctx's device (current); once per device.
+int noalloc_scratch_init(fa_ctx* ctx);
 size_t score_scratch_bytes(int d, int nwg);
 bool score_fused_ok(const float* q, int64_t ldq, const float* docs, int64_t ldd, int d, int topk);
 int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, const float* docs, int64_t nd,

@@ -15,6 +15,7 @@
 // so the result does not depend on the chunking.
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 #include "fa_internal.h"
 #include "device_math.h"
@@ -739,6 +740,36 @@ int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, cons
   return FA_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of fa_similarities_topk_dev_noalloc: the fused path's query planes,
+// norms, candidates, discard bounds, doc norms and flags for one block of 256
+// queries, in a fixed array of each device (held until the process ends). Its
+// device address comes from hipGetSymbolAddress once per device, at context
+// creation on that device; host code never passes the array's name itself.
+// Calls on one device share the array: calls that overlap on one GPU race.
+// No kernel relies on its previous contents (every value read in a call is
+// written earlier in the same call).
+constexpr size_t kNoAllocScratchBytes = (size_t)12 << 20;
+__device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int noalloc_scratch_init(fa_ctx* ctx) {
+  const int dev = ctx->device;
+  if (dev < 0 || dev >= kMaxDevices) return set_error(ctx, FA_ERR_UNSUPPORTED, "device %d outside 0..%d", dev,
+                                                      kMaxDevices - 1);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return FA_OK;
+  void* ptr = nullptr;
+  FA_HIP_CHECK(ctx, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));  // the device is current (fa_create)
+  g_scratch_ptr[dev] = ptr;
+  return FA_OK;
+}
+
 int topk_scratch_bytes(int64_t nq, int64_t nd, int32_t topk) {
   const int64_t nchunks = std::min<int64_t>(kMaxChunks, (nd + kChunk - 1) / kChunk);
   return (int)(nq * nchunks * topk * 8);
@@ -768,3 +799,31 @@ int launch_topk(fa_ctx* ctx, const float* scores, int64_t nq, int64_t nd, int32_
 }
 
 }  // namespace fa
+
+extern "C" int fa_similarities_topk_dev_noalloc(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs,
+                                                int64_t nd, int32_t d, int32_t topk, int32_t* idx, float* val) {
+  using fa::set_error;
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "Similarities: ctx is NULL");
+  if (nq < 0 || nd <= 0 || d <= 0)
+    return set_error(ctx, FA_ERR_ARG, "Similarities: shapes [%lld x %d] and [%lld x %d]", (long long)nq, d,
+                     (long long)nd, d);
+  if (topk < 1 || topk > fa::kSMaxK || topk > nd)
+    return set_error(ctx, FA_ERR_ARG, "Similarities (no-alloc): k=%d outside 1..min(%d, %lld)", topk, fa::kSMaxK,
+                     (long long)nd);
+  if (nq == 0) return FA_OK;
+  if (!queries || !docs || !idx) return set_error(ctx, FA_ERR_ARG, "Similarities: NULL buffer");
+  if (d > 2048) return set_error(ctx, FA_ERR_ARG, "Similarities (no-alloc): d=%d exceeds the fixed scratch's 2048", d);
+  if (!fa::score_fused_ok(queries, d, docs, d, d, topk))
+    return set_error(ctx, FA_ERR_ARG, "Similarities (no-alloc): needs d %% 32 == 0 and 16-byte aligned rows, got d=%d",
+                     d);
+  const int nwg = fa::score_workgroups(nd, ctx->cu_count);
+  const size_t need = fa::score_scratch_bytes(d, nwg);
+  if (need > fa::kNoAllocScratchBytes)
+    return set_error(ctx, FA_ERR_ARG, "Similarities (no-alloc): d=%d needs %zu bytes of scratch, the fixed array has %zu "
+                     "(d <= 2048 fits)", d, need, fa::kNoAllocScratchBytes);
+  void* ptr = ctx->device >= 0 && ctx->device < fa::kMaxDevices ? fa::g_scratch_ptr[ctx->device] : nullptr;
+  if (!ptr) return set_error(ctx, FA_ERR_STATE, "Similarities (no-alloc): scratch address of device %d unknown",
+                             ctx->device);
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  return fa::launch_score_topk(ctx, queries, nq, d, docs, nd, d, d, topk, idx, val, ptr, nwg, ctx->stream);
+}

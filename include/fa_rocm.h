@@ -155,6 +155,16 @@ int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const fl
 int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
                              int32_t topk, int32_t* idx, float* val);
 
+/* fa_similarities_topk_dev without any allocation: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops). Always the exact fused path (any
+ * nq), with its scratch in a fixed 12 MiB array per device instead of the
+ * context's buffers: d % 32 == 0 and d <= 2048, 1 <= topk <= 16, 16-byte
+ * aligned rows, else FA_ERR_ARG. Device pointers; enqueues on
+ * fa_stream(ctx). Calls on one GPU share the array: calls that overlap on one
+ * GPU (other contexts, other streams) race. */
+int fa_similarities_topk_dev_noalloc(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd,
+                                     int32_t d, int32_t topk, int32_t* idx, float* val);
 
 /* ---- cluster (cluster/cluster.go) ------------------------------------ */
 

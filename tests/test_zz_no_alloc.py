@@ -1,0 +1,83 @@
+"""fa_similarities_topk_dev_noalloc (fixed per-device scratch, no allocation)
+against fa_similarities_topk_dev, through the C ABI: two calls in a row, the
+second with fewer queries and docs, must give identical indices and values
+(the same kernels on the same inputs); sizes beyond the fixed scratch are
+refused."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from ai_amd import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def unit(a):
+    return (a / np.linalg.norm(a, axis=1, keepdims=True)).astype(np.float32)
+
+
+def dev(ctx, a):
+    p = C.c_void_p()
+    N.check(ctx.h, N.lib().fa_device_alloc(ctx.h, max(a.nbytes, 4), C.byref(p)))
+    N.check(ctx.h, N.lib().fa_memcpy_h2d(ctx.h, p, a.ctypes.data, a.nbytes))
+    return p
+
+
+def run(ctx, fn, dq, nq, dd, nd, d, k):
+    L = N.lib()
+    di, dv = C.c_void_p(), C.c_void_p()
+    N.check(ctx.h, L.fa_device_alloc(ctx.h, nq * k * 4, C.byref(di)))
+    N.check(ctx.h, L.fa_device_alloc(ctx.h, nq * k * 4, C.byref(dv)))
+    N.check(ctx.h, fn(ctx.h, dq, nq, dd, nd, d, k, di, dv))
+    ctx.sync()
+    idx = np.empty((nq, k), np.int32)
+    val = np.empty((nq, k), np.float32)
+    N.check(ctx.h, L.fa_memcpy_d2h(ctx.h, idx.ctypes.data, di, idx.nbytes))
+    N.check(ctx.h, L.fa_memcpy_d2h(ctx.h, val.ctypes.data, dv, val.nbytes))
+    L.fa_device_free(ctx.h, di)
+    L.fa_device_free(ctx.h, dv)
+    return idx, val
+
+
+@pytest.fixture(scope="module")
+def nctx():
+    c = N.Context(0)
+    yield c
+    c.close()
+
+
+def test_noalloc_matches_dev_entry_point(nctx):
+    L = N.lib()
+    r = np.random.default_rng(77)
+    q = unit(r.standard_normal((300, 768)))
+    docs = unit(r.standard_normal((20000, 768)))
+    docs[1000:1040] = docs[7]  # ties that take the exact fallback for the query below
+    q[5] = docs[7]
+    dq, dd = dev(nctx, q), dev(nctx, docs)
+    for nq, nd, k in ((300, 20000, 16), (130, 5000, 10)):
+        a_i, a_v = run(nctx, L.fa_similarities_topk_dev_noalloc, dq, nq, dd, nd, 768, k)
+        b_i, b_v = run(nctx, L.fa_similarities_topk_dev, dq, nq, dd, nd, 768, k)
+        assert np.array_equal(a_i, b_i), (nq, nd, k)
+        assert np.array_equal(a_v, b_v), (nq, nd, k)
+        s = q[:nq].astype(np.float64) @ docs[:nd].astype(np.float64).T
+        top = np.argsort(-s, axis=1, kind="stable")[:, 0]
+        assert (a_i[:, 0] == top).mean() > 0.99
+        print(f"no-alloc == dev entry point at nq={nq} nd={nd} k={k}", flush=True)
+    assert a_i[5].tolist() == [7] + list(range(1000, 1009))
+    L.fa_device_free(nctx.h, dq)
+    L.fa_device_free(nctx.h, dd)
+
+
+def test_noalloc_refuses_what_the_scratch_cannot_hold(nctx):
+    L = N.lib()
+    q = np.zeros((4, 4096), np.float32)
+    dq = dev(nctx, q)
+    out = C.c_void_p()
+    N.check(nctx.h, L.fa_device_alloc(nctx.h, 4 * 4 * 17, C.byref(out)))
+    assert L.fa_similarities_topk_dev_noalloc(nctx.h, dq, 4, dq, 4, 4096, 1, out, out) == N.FA_ERR_ARG
+    assert b"2048" in L.fa_last_error(nctx.h)
+    assert L.fa_similarities_topk_dev_noalloc(nctx.h, dq, 4, dq, 4, 64, 17, out, out) == N.FA_ERR_ARG
+    assert L.fa_similarities_topk_dev_noalloc(nctx.h, dq, 4, dq, 4, 48, 1, out, out) == N.FA_ERR_ARG
+    L.fa_device_free(nctx.h, dq)
+    L.fa_device_free(nctx.h, out)
