@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "fa_internal.h"
 #include "device_math.h"
@@ -315,25 +316,19 @@ __global__ __launch_bounds__(512) void score_stage1_kernel(Stage1Params p) {
     const int64_t blk0 = dbeg + (int64_t)t * kSDB + wd * 64;
     return (int)min<int64_t>(2, max<int64_t>(0, (dend - blk0 + 31) / 32));
   };
-  auto mfma_step = [&](const sbf16x8 (&oa)[2][2], const sbf16x8 (&ob)[2][2], int nv) {
+  // NV: doc blocks of this wave inside the range (a tile's constant, so the
+  // slab loop below is compiled once per value and has no branch)
+  auto mfma_step = [&](const sbf16x8 (&oa)[2][2], const sbf16x8 (&ob)[2][2], auto nvc) {
+    constexpr int NV = decltype(nvc)::value;
     // mid.hi, hi.mid, then hi.hi (smallest first)
-    if (nv == 2) {
 #pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[1][i], ob[0][j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][i], ob[1][j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][i], ob[0][j], acc[i][j], 0, 0, 0);
-        }
-    } else if (nv == 1) {
+    for (int i = 0; i < NV; i++)
 #pragma unroll
       for (int j = 0; j < 2; j++) {
-        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[1][0], ob[0][j], acc[0][j], 0, 0, 0);
-        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][0], ob[1][j], acc[0][j], 0, 0, 0);
-        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][0], ob[0][j], acc[0][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[1][i], ob[0][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][i], ob[1][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[0][i], ob[0][j], acc[i][j], 0, 0, 0);
       }
-    }
   };
   // lane lists: query column j of this wave, best kSKL (value desc, index asc)
   float lv[2][kSKL];
@@ -374,42 +369,46 @@ __global__ __launch_bounds__(512) void score_stage1_kernel(Stage1Params p) {
       }
     zero_acc();
   };
-  // items i0 .. i1-1 of one tile (i1 - i0 = nk slabs)
-  auto body = [&](int item, int last, int nv, const Regs& use, Regs& fill) {
+  // items i0 .. last of one tile (nk slabs)
+  auto body = [&](int item, int last, auto nvc, const Regs& use, Regs& fill) {
     const int buf = item & 1;
     load(fill, min(item + 2, last));
     sbf16x8 a0[2][2], b0[2][2], a1[2][2], b1[2][2];
     read_ops(buf, 0, a0, b0);
     read_ops(buf, 1, a1, b1);
-    mfma_step(a0, b0, nv);
+    mfma_step(a0, b0, nvc);
     split_store(use, buf ^ 1, item + 1);
-    mfma_step(a1, b1, nv);
+    mfma_step(a1, b1, nvc);
     __syncthreads();
   };
-  for (int t = 0; t < ntile; t++) {
-    const int i0 = t * nk, last = i0 + nk - 1;
-    const int nv = nvalid(i0);
-    {
-      Regs rA, rB;
-      load(rA, i0);
-      split_store(rA, i0 & 1, i0);
-      load(rA, min(i0 + 1, last));
-      __syncthreads();
-      int item = i0;
-      for (; item + 2 <= last; item += 2) {
-        body(item, last, nv, rA, rB);
-        body(item + 1, last, nv, rB, rA);
-      }
-      if (item + 1 <= last) {
-        body(item, last, nv, rA, rB);
-        item++;
-      }
-      sbf16x8 a0[2][2], b0[2][2], a1[2][2], b1[2][2];
-      read_ops(item & 1, 0, a0, b0);
-      read_ops(item & 1, 1, a1, b1);
-      mfma_step(a0, b0, nv);
-      mfma_step(a1, b1, nv);
+  auto tile = [&](int i0, auto nvc) {
+    const int last = i0 + nk - 1;
+    Regs rA, rB;
+    load(rA, i0);
+    split_store(rA, i0 & 1, i0);
+    load(rA, min(i0 + 1, last));
+    __syncthreads();
+    int item = i0;
+    for (; item + 2 <= last; item += 2) {
+      body(item, last, nvc, rA, rB);
+      body(item + 1, last, nvc, rB, rA);
     }
+    if (item + 1 <= last) {
+      body(item, last, nvc, rA, rB);
+      item++;
+    }
+    sbf16x8 a0[2][2], b0[2][2], a1[2][2], b1[2][2];
+    read_ops(item & 1, 0, a0, b0);
+    read_ops(item & 1, 1, a1, b1);
+    mfma_step(a0, b0, nvc);
+    mfma_step(a1, b1, nvc);
+  };
+  for (int t = 0; t < ntile; t++) {
+    const int i0 = t * nk;
+    const int nv = nvalid(i0);
+    // a wave with no doc block in range computes one (the epilogue ignores it)
+    if (nv == 2) tile(i0, std::integral_constant<int, 2>{});
+    else tile(i0, std::integral_constant<int, 1>{});
     epilogue(i0);
     __syncthreads();  // the next tile's first slab overwrites the buffers read above
   }
@@ -594,8 +593,10 @@ __global__ __launch_bounds__(256) void score_merge_kernel(MergeParams p) {
     const f32x4 x = *reinterpret_cast<const f32x4*>(qrow + t);
 #pragma unroll
     for (int u = 0; u < kSMerge; u++) {
-      if (ix[u] == INT32_MAX) continue;
-      const f32x4 y = *reinterpret_cast<const f32x4*>(p.docs + (int64_t)ix[u] * p.ldd + t);
+      // an empty slot reads doc 0 and is ignored below: no branch, so the
+      // loads of all slots are in flight together
+      const int64_t row = ix[u] == INT32_MAX ? 0 : ix[u];
+      const f32x4 y = *reinterpret_cast<const f32x4*>(p.docs + row * p.ldd + t);
       part[u] = fma((double)x[0], (double)y[0], part[u]);
       part[u] = fma((double)x[1], (double)y[1], part[u]);
       part[u] = fma((double)x[2], (double)y[2], part[u]);
