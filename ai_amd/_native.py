@@ -19,7 +19,7 @@ SYNTH_HEADER = os.path.join(ROOT, "include", "fa_synth.h")
 
 FA_OK, FA_ERR_ARG, FA_ERR_HIP, FA_ERR_OOM, FA_ERR_STATE, FA_ERR_UNSUPPORTED = range(6)
 FA_DT_F32, FA_DT_BF16 = 0, 1
-FA_ACT_NONE, FA_ACT_RELU, FA_ACT_GELU = 0, 1, 2
+FA_ACT_NONE, FA_ACT_RELU, FA_ACT_GELU, FA_ACT_TANH = 0, 1, 2, 3
 FA_B_KN, FA_B_NK = 0, 1
 KERNEL_KINDS = ["gemm_qkv", "gemm_o", "gemm_gateup", "gemm_down", "gemm_head", "attention", "qknorm_rope",
                 "residual_norm", "gather", "pool_l2", "gemm_ple", "ple_norm"]
@@ -51,7 +51,8 @@ class GemmaConfig(C.Structure):
                 ("rope_local_base_freq", f64), ("rope_theta", f64), ("query_pre_attn_scalar", f64),
                 ("rms_norm_eps", f32), ("max_tokens", i32), ("n_dense", i32), ("dense_out", i32 * 4),
                 ("variant", i32), ("hidden_size_per_layer_input", i32), ("embedding_dim", i32),
-                ("layer_head_dim", i32 * 64), ("layer_kv_heads", i32 * 64), ("layer_sliding", i32 * 64)]
+                ("layer_head_dim", i32 * 64), ("layer_kv_heads", i32 * 64), ("layer_sliding", i32 * 64),
+                ("dense_act", i32 * 4)]
 
 
 _SIGS = {

@@ -74,13 +74,80 @@ def run(shapes, reps: int, check: bool) -> list[dict]:
     return out
 
 
+def dropin(reps: int) -> None:
+    """tensor.MatMulFused as the Go drop-in calls it for the GeGLU gate
+    (models/gemma/embed.go:227): x [5517 x 768] . W [768 x 1152] with RowScale,
+    GELU and Mul, W float32 in the reference's [k x n] layout (and bf16, and
+    [n x k]). Host entry point (fa_matmul_fused: copies in and out included,
+    as the cgo shim calls it) and device-pointer entry point
+    (fa_matmul_fused_dev, operands resident)."""
+    ctx = N.Context(0)
+    L = N.lib()
+    m, k, n = 5517, 768, 1152
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w32 = S.normal_f32(5, "dropin", 0.02, (k, n))
+    rs = rng.uniform(0.5, 1.5, m).astype(np.float32)
+    mul = rng.standard_normal((m, n)).astype(np.float32)
+    c = np.empty((m, n), np.float32)
+    for wname, dt, layout, w in (("f32", N.FA_DT_F32, N.FA_B_KN, w32),
+                                 ("f32", N.FA_DT_F32, N.FA_B_NK, np.ascontiguousarray(w32.T)),
+                                 ("bf16", N.FA_DT_BF16, N.FA_B_KN, S.f32_to_bf16(w32)),
+                                 ("bf16", N.FA_DT_BF16, N.FA_B_NK, np.ascontiguousarray(S.f32_to_bf16(w32).T))):
+        ldb = w.shape[1]
+        e = N.Epilogue()
+        e.act = N.FA_ACT_GELU
+        e.row_scale = rs.ctypes.data
+        e.mul = mul.ctypes.data
+        e.ldm = n
+
+        def host():
+            N.check(ctx.h, L.fa_matmul_fused(ctx.h, m, n, k, a.ctypes.data, k, w.ctypes.data, ldb, dt, layout,
+                                             C.byref(e), c.ctypes.data, n))
+        ptrs = {}
+        for key, arr in (("a", a), ("w", w), ("rs", rs), ("mul", mul), ("c", c)):
+            p = C.c_void_p()
+            N.check(ctx.h, L.fa_device_alloc(ctx.h, arr.nbytes, C.byref(p)))
+            N.check(ctx.h, L.fa_memcpy_h2d(ctx.h, p, arr.ctypes.data, arr.nbytes))
+            ptrs[key] = p
+        ed = N.Epilogue()
+        ed.act = N.FA_ACT_GELU
+        ed.row_scale = ptrs["rs"].value
+        ed.mul = ptrs["mul"].value
+        ed.ldm = n
+
+        def dev():
+            N.check(ctx.h, L.fa_matmul_fused_dev(ctx.h, m, n, k, ptrs["a"], k, ptrs["w"], ldb, dt, layout,
+                                                 C.byref(ed), ptrs["c"], n))
+        out = dict(op="MatMulFused gate", M=m, K=k, N=n, w=wname, layout="KN" if layout == N.FA_B_KN else "NK")
+        for label, fn in (("host_us", host), ("dev_us", dev)):
+            for _ in range(3):
+                fn()
+            ctx.sync()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            ctx.sync()
+            out[label] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+        out["dev_tflops_fp32_equiv"] = round(2 * m * n * k / (out["dev_us"] * 1e-6) / 1e12, 1)
+        print(json.dumps(out), flush=True)
+        for p in ptrs.values():
+            L.fa_device_free(ctx.h, p)
+    ctx.close()
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--shape", action="append",
                     help="M,N,K, repeatable (default: the encoder's product shapes at C2 and M=32768)")
     ap.add_argument("--reps", type=int, default=30)
     ap.add_argument("--no-check", action="store_true", help="skip the float64 comparison")
+    ap.add_argument("--dropin", action="store_true",
+                    help="time the MatMulFused drop-in at the gate shape with float32/bf16 weights in both layouts")
     a = ap.parse_args()
+    if a.dropin:
+        dropin(a.reps)
+        return
     shapes = [tuple(int(v) for v in sh.split(",")) for sh in a.shape] if a.shape else SHAPES
     run(shapes, a.reps, not a.no_check)
 

@@ -168,6 +168,37 @@ int fa_memcpy_d2h(fa_ctx* ctx, void* dst, const void* src, size_t bytes) {
   return FA_OK;
 }
 
+namespace fa {
+namespace {
+
+// The split-bf16 products need B as bf16 [n x k] rows, A's rows 16-byte
+// aligned and k a whole number of 32-wide slabs. Other B operands (fp32,
+// tensor.MatMul's [k x n] weights, matmul.go:42-72) are rewritten into that
+// form in scratch first: fp32 as three planes hi + mid + lo (exact, the
+// six-term product), bf16 [k x n] transposed. Shapes the fast kernels cannot
+// take keep the fp32-MFMA kernel with its checked loader.
+int prepare_b(fa_ctx* ctx, GemmArgs& g) {
+  const bool a_ok = (reinterpret_cast<uintptr_t>(g.a) & 15) == 0 && g.lda % 4 == 0;
+  if (!(g.k > 0 && g.k % 32 == 0 && a_ok)) return FA_OK;
+  if (g.b_dtype == FA_DT_BF16 && g.b_layout == FA_B_NK) return FA_OK;  // already the fast form (when aligned)
+  const int terms = g.b_dtype == FA_DT_F32 ? 3 : 1;
+  DevBuf& pb = ctx->slot(slots::S_BPLANES);
+  int rc;
+  if ((rc = pb.ensure(ctx, (size_t)terms * g.n * g.k * 2))) return rc;
+  if ((rc = launch_split_b(ctx, g.b, g.b_dtype, g.ldb, g.b_layout, g.n, g.k, pb.as<uint16_t>(), ctx->stream)))
+    return rc;
+  g.b = pb.ptr;
+  g.b_dtype = FA_DT_BF16;
+  g.b_layout = FA_B_NK;
+  g.ldb = g.k;
+  g.b_terms = terms;
+  g.b_plane = g.n * g.k;
+  return FA_OK;
+}
+
+}  // namespace
+}  // namespace fa
+
 int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
                     int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc) {
   if (!ctx) return set_error(ctx, FA_ERR_ARG, "MatMulFused: ctx is NULL");
@@ -184,7 +215,7 @@ int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a
   if (ldb < brow && bcnt > 0)
     return set_error(ctx, FA_ERR_ARG, "MatMulFused: ldb %lld too small", (long long)ldb);
   if (ldc < n && m > 0) return set_error(ctx, FA_ERR_ARG, "MatMulFused: ldc %lld < n %lld", (long long)ldc, (long long)n);
-  if (e && e->act != FA_ACT_NONE && e->act != FA_ACT_RELU && e->act != FA_ACT_GELU)
+  if (e && (e->act < FA_ACT_NONE || e->act > FA_ACT_TANH))
     return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown activation %d", e->act);
   if (e && e->mul && e->ldm < n) return set_error(ctx, FA_ERR_ARG, "MatMulFused: Mul leading dimension < n");
   if (e && e->residual && e->ldr < n)
@@ -219,6 +250,7 @@ int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a
     // rows of C with gaps: keep the caller's bytes between rows
     FA_HIP_CHECK(ctx, hipMemcpyAsync(dc, c, cbytes, hipMemcpyHostToDevice, ctx->stream));
   }
+  if ((rc = fa::prepare_b(ctx, g))) return rc;
   if ((rc = fa::launch_gemm(ctx, g, ctx->stream))) return rc;
   FA_HIP_CHECK(ctx, hipMemcpyAsync(c, dc, cbytes, hipMemcpyDeviceToHost, ctx->stream));
   FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
@@ -236,7 +268,7 @@ int fa_matmul_fused_dev(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const floa
   const int64_t brow = b_layout == FA_B_KN ? n : k, bcnt = b_layout == FA_B_KN ? k : n;
   if ((lda < k && m > 0) || (ldb < brow && bcnt > 0) || (ldc < n && m > 0))
     return set_error(ctx, FA_ERR_ARG, "MatMulFused: leading dimension too small");
-  if (e && e->act != FA_ACT_NONE && e->act != FA_ACT_RELU && e->act != FA_ACT_GELU)
+  if (e && (e->act < FA_ACT_NONE || e->act > FA_ACT_TANH))
     return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown activation %d", e->act);
   if (m == 0 || n == 0) return FA_OK;
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
@@ -249,6 +281,8 @@ int fa_matmul_fused_dev(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const floa
     g.bias = e->bias; g.row_scale = e->row_scale; g.act = e->act;
     g.mul = e->mul; g.ldm = e->ldm; g.residual = e->residual; g.ldr = e->ldr;
   }
+  int rc;
+  if ((rc = fa::prepare_b(ctx, g))) return rc;
   return fa::launch_gemm(ctx, g, ctx->stream);
 }
 

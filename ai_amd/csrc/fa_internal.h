@@ -55,6 +55,7 @@ enum : size_t {
   S_A = 0, S_B, S_C, S_BIAS, S_ROWSCALE, S_MUL, S_RES, S_X, S_G, S_OUT, S_COS, S_SIN, S_Q, S_K, S_V, S_MASK,
   S_CL_WORK, S_CL_X, S_CL_C, S_CL_OUT,  // cluster entry points
   S_TOPK,                               // top-k candidates
+  S_BPLANES,                            // B operand as bf16 [n x k] planes (matmul drop-in)
   S_COUNT
 };
 }  // namespace slots
@@ -110,7 +111,17 @@ struct GemmArgs {
   // c + s * c_split, and the consumer adds the parts in order s = 0, 1, ...
   int ksplit = 1;
   int64_t c_split = 0;
+  // b_terms = 3: B (bf16, [n x k]) is three planes hi, mid, lo of fp32
+  // values, b_plane elements apart (fp32 weights that are not bf16-exact)
+  int b_terms = 1;
+  int64_t b_plane = 0;
 };
+
+// B [k x n] (FA_B_KN) or [n x k] (FA_B_NK), leading dimension ldb -> bf16
+// planes [n][k] at planes (k % 8 == 0): fp32 B as three planes hi, mid, lo
+// (GemmArgs.b_terms = 3), bf16 B transposed as one plane.
+int launch_split_b(fa_ctx* ctx, const void* b, int b_dtype, int64_t ldb, int layout, int64_t n, int64_t k,
+                   uint16_t* planes, hipStream_t s);
 
 // Launches C = epi(A . B) on stream. For Epi::GeGLU, B is the interleaved
 // gate/up weight [2F x K] (32-row groups alternating gate, up) and C is
@@ -166,7 +177,9 @@ int launch_row_plan(fa_ctx* ctx, const int32_t* cu_seqlens, int32_t nseq, int32_
 
 // Embedding gather of packed tokens: x[r] = E[ids_packed[r]] * scale and
 // xn[r] = x[r] * rms_inv(x[r]) * g (the first layer's input norm).
-int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_src, const uint16_t* E,
+// E: bf16 [vocab x d], or with plane > 0 three planes hi, mid, lo plane
+// elements apart (a float32 table that is not bf16-exact), summed exactly.
+int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_src, const uint16_t* E, int64_t plane,
                         int64_t vocab, int64_t rows, int32_t d, float scale, const float* g_next, float eps, float* x,
                         float* xn, hipStream_t s);
 

@@ -98,6 +98,9 @@ struct GemmParams {
   // writes its partial product to c + s * c_split (epilogue None)
   int ksplit;
   int64_t c_split;
+  // split-bf16 kernel with BT = 3: B is three bf16 planes (hi, mid, lo of
+  // fp32 weights) b_plane elements apart
+  int64_t b_plane;
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -123,6 +126,7 @@ __device__ __forceinline__ float epi_value(const GemmParams& p, float v, int64_t
     if (p.row_scale) v = v * p.row_scale[row];
     if (p.act == FA_ACT_RELU) v = fmaxf(v, 0.f);
     else if (p.act == FA_ACT_GELU) v = gelu_tanh_ref(v);
+    else if (p.act == FA_ACT_TANH) v = tanh_ref(v);
     if (p.mul) v = v * p.mul[row * p.ldm + col];
     if (p.residual) v = v + p.residual[row * p.ldr + col];
   }
@@ -445,13 +449,19 @@ __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3
 // placed in scratch memory by the compiler).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <class TL, Epi EPI>
+// BT = 3 (fp32 weights that are not bf16-exact, and fp32 B operands): B
+// arrives as three bf16 planes hi + mid + lo (split like A), and each operand
+// pair takes the six term products with i + j <= 2; the three dropped ones
+// are below 2^-21 of |a| |w| (truncation splits: |mid| < 2^-7 |x|, |lo| <
+// 2^-14 |x|).
+template <class TL, Epi EPI, int BT = 1>
 __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p) {
   constexpr int BM = TL::BM, BN = TL::BN, BK = TL::BK, NT = TL::NT;
   constexpr int FM = TL::FM, FN = TL::FN;
   static_assert(TL::S == 2 && BK == 32, "two MFMA k-steps per 32-wide slab");
+  static_assert(BT == 1 || BT == 3, "one or three B planes");
   __shared__ __attribute__((aligned(16))) uint16_t As[2][3][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BT][BN * BK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -488,7 +498,7 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
     gb[i] = B + min(n0 + row, N - 1) * p.ldb + k_off + c * 8;
     lb[i] = row * BK + ((c ^ lds_swz(row)) << 3);
   }
-  auto load_global = [&](f32x4 (&ra)[2 * NA], u32x4 (&rb)[NB], int kt) {
+  auto load_global = [&](f32x4 (&ra)[2 * NA], u32x4 (&rb)[BT * NB], int kt) {
 #pragma unroll
     for (int i = 0; i < NA; i++) {
       const int64_t off = ga[i] + (int64_t)kt * BK;
@@ -496,11 +506,14 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
       ra[2 * i + 1] = *reinterpret_cast<const f32x4*>(A + off + 4);
     }
 #pragma unroll
-    for (int i = 0; i < NB; i++) rb[i] = *reinterpret_cast<const u32x4*>(gb[i] + (int64_t)kt * BK);
+    for (int t = 0; t < BT; t++)
+#pragma unroll
+      for (int i = 0; i < NB; i++)
+        rb[t * NB + i] = *reinterpret_cast<const u32x4*>(gb[i] + t * p.b_plane + (int64_t)kt * BK);
   };
 
   // hi + mid + lo = a exactly (split3, device_math.h), two bf16 per dword.
-  auto split_store = [&](const f32x4 (&ra)[2 * NA], const u32x4 (&rb)[NB], int buf) {
+  auto split_store = [&](const f32x4 (&ra)[2 * NA], const u32x4 (&rb)[BT * NB], int buf) {
 #pragma unroll
     for (int i = 0; i < NA; i++) {
       uint32_t h[8], m[8], l[8];
@@ -519,7 +532,9 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
           make_uint4(pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7]));
     }
 #pragma unroll
-    for (int i = 0; i < NB; i++) *reinterpret_cast<u32x4*>(&Bs[buf][lb[i]]) = rb[i];
+    for (int t = 0; t < BT; t++)
+#pragma unroll
+      for (int i = 0; i < NB; i++) *reinterpret_cast<u32x4*>(&Bs[buf][t][lb[i]]) = rb[t * NB + i];
   };
 
   // Operand reads: lane half h takes chunk 2s+h of its row; every row read by
@@ -528,7 +543,7 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
   const int brow = wn * TL::TN + (lane & 31);
   const int sw = lds_swz(lane & 31);
   const int h = lane >> 5;
-  auto read_ops = [&](int buf, int s, bf16x8 (&oa)[3][FM], bf16x8 (&ob)[FN]) {
+  auto read_ops = [&](int buf, int s, bf16x8 (&oa)[3][FM], bf16x8 (&ob)[BT][FN]) {
     const int co = ((2 * s + h) ^ sw) << 3;
 #pragma unroll
     for (int t = 0; t < 3; t++)
@@ -536,8 +551,10 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
       for (int i = 0; i < FM; i++)
         oa[t][i] = *reinterpret_cast<const bf16x8*>(&As[buf][t][(arow + 32 * i) * BK + co]);
 #pragma unroll
-    for (int j = 0; j < FN; j++)
-      ob[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(brow + 32 * j) * BK + co]);
+    for (int t = 0; t < BT; t++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        ob[t][j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][t][(brow + 32 * j) * BK + co]);
   };
 
   f32x16 acc[FM][FN];
@@ -548,26 +565,31 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  auto mfma_step = [&](const bf16x8 (&oa)[3][FM], const bf16x8 (&ob)[FN]) {
-    // smallest terms first
+  auto mfma_step = [&](const bf16x8 (&oa)[3][FM], const bf16x8 (&ob)[BT][FN]) {
+    // smallest terms first: (t, u) pairs by decreasing t + u, u <= t + u <= 2
 #pragma unroll
-    for (int t = 2; t >= 0; t--)
+    for (int sum = 2; sum >= 0; sum--)
 #pragma unroll
-      for (int i = 0; i < FM; i++)
+      for (int u = 0; u < BT; u++) {
+        const int t = sum - u;
+        if (t < 0 || (BT == 1 && u > 0)) continue;
 #pragma unroll
-        for (int j = 0; j < FN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t][i], ob[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t][i], ob[u][j], acc[i][j], 0, 0, 0);
+      }
   };
 
   // Slab kt is in LDS buffer kt&1; `use` holds the global values of slab
   // kt+1 and `fill` receives slab kt+2 (clamped to the last slab: a
   // redundant load keeps the body free of branches, so the split's VALU work
   // and the LDS traffic interleave with the MFMAs).
-  auto body = [&](int kt, const f32x4 (&ra_use)[2 * NA], const u32x4 (&rb_use)[NB], f32x4 (&ra_fill)[2 * NA],
-                  u32x4 (&rb_fill)[NB]) {
+  auto body = [&](int kt, const f32x4 (&ra_use)[2 * NA], const u32x4 (&rb_use)[BT * NB], f32x4 (&ra_fill)[2 * NA],
+                  u32x4 (&rb_fill)[BT * NB]) {
     const int buf = kt & 1;
     load_global(ra_fill, rb_fill, min(kt + 2, nk - 1));
-    bf16x8 a0[3][FM], b0[FN], a1[3][FM], b1[FN];
+    bf16x8 a0[3][FM], b0[BT][FN], a1[3][FM], b1[BT][FN];
     read_ops(buf, 0, a0, b0);
     read_ops(buf, 1, a1, b1);
     mfma_step(a0, b0);
@@ -577,7 +599,7 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
   };
 
   f32x4 raA[2 * NA], raB[2 * NA];
-  u32x4 rbA[NB], rbB[NB];
+  u32x4 rbA[BT * NB], rbB[BT * NB];
   load_global(raA, rbA, 0);
   split_store(raA, rbA, 0);
   load_global(raA, rbA, min(1, nk - 1));
@@ -593,7 +615,7 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
   }
   {
     const int buf = kt & 1;
-    bf16x8 a0[3][FM], b0[FN], a1[3][FM], b1[FN];
+    bf16x8 a0[3][FM], b0[BT][FN], a1[3][FM], b1[BT][FN];
     read_ops(buf, 0, a0, b0);
     read_ops(buf, 1, a1, b1);
     mfma_step(a0, b0);
@@ -608,14 +630,14 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
   }
 }
 
-template <class TL, Epi EPI>
+template <class TL, Epi EPI, int BT = 1>
 void launch_x3(GemmParams p, hipStream_t s) {
   p.tiles_m = (int)((p.m + TL::BM - 1) / TL::BM);
   p.tiles_n = (int)((p.n + TL::BN - 1) / TL::BN);
   p.nk = (int)(p.k / TL::BK);
   if (p.ksplit < 1) p.ksplit = 1;
   dim3 grid(p.tiles_m * p.tiles_n, p.ksplit), block(TL::NT);
-  hipLaunchKernelGGL((gemm_x3_kernel<TL, EPI>), grid, block, 0, s, p);
+  hipLaunchKernelGGL((gemm_x3_kernel<TL, EPI, BT>), grid, block, 0, s, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -913,6 +935,70 @@ void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   }
 }
 
+// B as three bf16 planes (BT = 3): 128x128 tiles of eight 32x64 waves (96 KB
+// of LDS: one workgroup per CU) once they give every CU half a tile, else
+// 64x64 tiles (128x64 for GeGLU) of four waves.
+void dispatch_x3_bt3(const GemmParams& p, Epi epi, int cus, hipStream_t s) {
+  const int64_t tiles128 = ((p.m + 127) / 128) * ((p.n + 127) / 128) * std::max(p.ksplit, 1);
+  const bool big = 2 * tiles128 >= cus;
+  switch (epi) {
+    case Epi::None:
+      if (big) launch_x3<X128x128w8, Epi::None, 3>(p, s); else launch_x3<X64x64, Epi::None, 3>(p, s);
+      break;
+    case Epi::Generic:
+      if (big) launch_x3<X128x128w8, Epi::Generic, 3>(p, s); else launch_x3<X64x64, Epi::Generic, 3>(p, s);
+      break;
+    case Epi::GeGLU:
+      if (big) launch_x3<X128x128w8, Epi::GeGLU, 3>(p, s); else launch_x3<X128x64v, Epi::GeGLU, 3>(p, s);
+      break;
+  }
+}
+
+// fp32 B [k x n] (FA_B_KN, rows of n) or [n x k] (FA_B_NK) -> three bf16
+// planes [3][n][k] (hi, mid, lo: split3). One thread per (column, 8 k
+// values); consecutive threads take consecutive columns of one 8-row band
+// (KN: coalesced reads of each k row) or consecutive chunks of one column
+// (NK: contiguous reads and writes).
+// A bf16 source (bf16 != 0) is transposed only: one plane, its values as they are.
+__global__ __launch_bounds__(256) void split_b_kernel(const void* __restrict__ bsrc, int64_t ldb, int kn, int bf16,
+                                                      int64_t n, int64_t k, uint16_t* __restrict__ planes) {
+  const float* b = static_cast<const float*>(bsrc);
+  const uint16_t* b16 = static_cast<const uint16_t*>(bsrc);
+  const int64_t kc_n = k / 8;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= n * kc_n) return;
+  int64_t col, kc;
+  if (kn) {
+    kc = gid / n;
+    col = gid - kc * n;
+  } else {
+    col = gid / kc_n;
+    kc = gid - col * kc_n;
+  }
+  uint32_t h[8], m[8], l[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int64_t at = kn ? (kc * 8 + e) * ldb + col : col * ldb + kc * 8 + e;
+    const float x = bf16 ? __uint_as_float((uint32_t)b16[at] << 16) : b[at];
+    const Split3 sp = split3(x);
+    h[e] = sp.h;
+    m[e] = sp.m;
+    l[e] = sp.l;
+  }
+  const int64_t o = col * k + kc * 8, plane = n * k;
+  if (bf16) {
+    *reinterpret_cast<uint4*>(planes + o) =
+        make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
+    return;
+  }
+  *reinterpret_cast<uint4*>(planes + o) =
+      make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
+  *reinterpret_cast<uint4*>(planes + plane + o) =
+      make_uint4(pack_hi16(m[0], m[1]), pack_hi16(m[2], m[3]), pack_hi16(m[4], m[5]), pack_hi16(m[6], m[7]));
+  *reinterpret_cast<uint4*>(planes + 2 * plane + o) =
+      make_uint4(pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7]));
+}
+
 bool x3_has_geglu(XTileId t) {
   switch (t) {
     case XTileId::x128x64: return X128x64::FN % 2 == 0;
@@ -931,6 +1017,17 @@ int gemm_ksplit() {
   return v;
 }
 
+int launch_split_b(fa_ctx* ctx, const void* b, int b_dtype, int64_t ldb, int layout, int64_t n, int64_t k,
+                   uint16_t* planes, hipStream_t s) {
+  if (n <= 0 || k <= 0) return FA_OK;
+  if (k % 8 != 0) return set_error(ctx, FA_ERR_ARG, "MatMul: split of B needs k %% 8 == 0, got %lld", (long long)k);
+  const int64_t threads = n * (k / 8);
+  hipLaunchKernelGGL(split_b_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, b, ldb,
+                     layout == FA_B_KN ? 1 : 0, b_dtype == FA_DT_BF16 ? 1 : 0, n, k, planes);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
 int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.m < 0 || g.n < 0 || g.k < 0)
     return set_error(ctx, FA_ERR_ARG, "MatMul: negative size m=%lld n=%lld k=%lld", (long long)g.m,
@@ -945,6 +1042,8 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   p.bias = g.bias; p.row_scale = g.row_scale; p.mul = g.mul; p.ldm = g.ldm;
   p.residual = g.residual; p.ldr = g.ldr; p.act = g.act;
   p.ksplit = 1;
+  p.b_plane = g.b_plane;
+  if (g.b_terms != 1 && g.b_terms != 3) return set_error(ctx, FA_ERR_ARG, "MatMul: %d B planes", g.b_terms);
   if (((g.m + 63) / 64) * ((g.n + 63) / 64) > INT32_MAX / 4) return set_error(ctx, FA_ERR_ARG, "MatMul: too many tiles");
   const bool bf16 = g.b_dtype == FA_DT_BF16;
   const bool nk = g.b_layout == FA_B_NK;
@@ -962,7 +1061,12 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   const bool fast = nk && g.k > 0 && g.k % 32 == 0 && aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 &&
                     (bf16 ? g.ldb % 8 == 0 : g.ldb % 4 == 0);
   if (p.ksplit > 1 && !fast) return set_error(ctx, FA_ERR_ARG, "MatMul: K split needs 16-byte aligned rows");
-  if (fast && bf16 && !use_f32_mfma()) {
+  if (g.b_terms == 3) {
+    if (!(fast && bf16))
+      return set_error(ctx, FA_ERR_ARG, "MatMul: three B planes need bf16 [n x k] planes, k %% 32 == 0 and 16-byte "
+                       "aligned rows");
+    dispatch_x3_bt3(p, g.epi, ctx->cu_count > 0 ? ctx->cu_count : 256, s);
+  } else if (fast && bf16 && !use_f32_mfma()) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     XTileId t = (XTileId)forced_xtile();
     if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.k, p.ksplit, g.epi, cus);

@@ -49,19 +49,31 @@ bool bf16_exact(float f, uint16_t* out) {
   return true;
 }
 
+// A weight matrix [rows, cols] in HBM: bf16 values as stored in the
+// checkpoint (terms = 1), or, once any of its float32 values is not
+// bf16-exact, three bf16 planes hi, mid, lo of the float32 values (terms = 3,
+// rows*cols elements apart; hi + mid + lo is the value exactly), which the
+// products take through the six-term split kernel.
+struct Mat {
+  uint16_t* p = nullptr;
+  int64_t rows = 0, cols = 0;
+  int terms = 1;
+  int64_t plane() const { return rows * cols; }
+};
+
 struct Layer {
   int D = 0, Hkv = 0, width = 0;  // head dim, key/value heads, q|k|v width (H+2Hkv)*D
   bool sliding = true;
   const float *cos_t = nullptr, *sin_t = nullptr;  // RoPE tables of this layer's base and D
-  uint16_t* wqkv = nullptr;   // [(H+2Hkv)*D, d]
-  uint16_t* wo = nullptr;     // [d, H*D]
-  uint16_t* wgu = nullptr;    // [2F, d], 32-row groups gate/up alternating
-  uint16_t* wdown = nullptr;  // [d, F]
+  Mat wqkv;   // [(H+2Hkv)*D, d]
+  Mat wo;     // [d, H*D]
+  Mat wgu;    // [2F, d], 32-row groups gate/up alternating
+  Mat wdown;  // [d, F]
   float *g_in = nullptr, *g_post_attn = nullptr, *g_pre_ffn = nullptr, *g_post_ffn = nullptr;
   float *g_q = nullptr, *g_k = nullptr;
   // variant 2: per-layer-input block and layer scalar
-  uint16_t* wple_gate = nullptr;  // [P, d]
-  uint16_t* wple_proj = nullptr;  // [d, P]
+  Mat wple_gate;  // [P, d]
+  Mat wple_proj;  // [d, P]
   float* g_ple_post = nullptr;
   float scalar = 1.f;
 };
@@ -87,15 +99,15 @@ struct fa_model {
   int max_width = 0, max_hd = 0;  // widest q|k|v row, widest attention output H*D
   int hkv256 = 0;                 // most key/value heads of a head_dim-256 layer (split-bf16 attention)
   int P = 0, E = 0;               // variant 2: per-layer input width, embedding projection width
-  uint16_t* wple_model = nullptr; // variant 2: [layers*P, d]
+  fa::Mat wple_model;             // variant 2: [layers*P, d]
   float* g_ple_norm = nullptr;    // variant 2: [P]
-  uint16_t* wemb_proj = nullptr;  // variant 2: [E, d]
+  fa::Mat wemb_proj;              // variant 2: [E, d]
   std::vector<void*> allocations;
-  uint16_t* embed = nullptr;
+  fa::Mat embed;
   std::vector<fa::Layer> layers;
   float* g_final = nullptr;
-  std::vector<uint16_t*> dense;
-  std::vector<int> dense_in, dense_out;
+  std::vector<fa::Mat> dense;
+  std::vector<int> dense_in, dense_out, dense_act;  // dense_act: FA_ACT_NONE or FA_ACT_TANH
   float *cos_local = nullptr, *sin_local = nullptr, *cos_global = nullptr, *sin_global = nullptr;
   int d_local = 0, d_global = 0;  // head dims of the sliding and the full layers
   std::set<std::string> seen;
@@ -128,6 +140,25 @@ int alloc_dev(fa_model* m, size_t bytes, void** out) {
   if (e != hipSuccess) return set_error(m->ctx, FA_ERR_OOM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
   m->allocations.push_back(*out);
   return FA_OK;
+}
+
+// Frees one of the model's allocations (a matrix promoted to three planes).
+void free_dev(fa_model* m, void* ptr) {
+  for (auto& a : m->allocations)
+    if (a == ptr) {
+      (void)hipFree(a);
+      a = m->allocations.back();
+      m->allocations.pop_back();
+      return;
+    }
+}
+
+// B operand of a product over w's rows [row0, ...): one bf16 plane or three.
+void set_b(GemmArgs& g, const Mat& w, int64_t row0 = 0) {
+  g.b = w.p + row0 * w.cols;
+  g.ldb = w.cols;
+  g.b_terms = w.terms;
+  g.b_plane = w.plane();
 }
 
 hipEvent_t take_event(fa_model* m) {
@@ -341,12 +372,19 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     rc = fa::alloc_dev(m, bytes, &p);
     return rc ? nullptr : p;
   };
-  m->embed = (uint16_t*)A((size_t)c.vocab_size * d * 2);
+  auto M_ = [&](int64_t rows, int64_t cols) {
+    fa::Mat w;
+    w.rows = rows;
+    w.cols = cols;
+    w.p = (uint16_t*)A((size_t)rows * cols * 2);
+    return w;
+  };
+  m->embed = M_(c.vocab_size, d);
   for (auto& L : m->layers) {
-    L.wqkv = (uint16_t*)A((size_t)L.width * d * 2);
-    L.wo = (uint16_t*)A((size_t)d * H * L.D * 2);
-    L.wgu = (uint16_t*)A((size_t)2 * F * d * 2);
-    L.wdown = (uint16_t*)A((size_t)d * F * 2);
+    L.wqkv = M_(L.width, d);
+    L.wo = M_(d, (int64_t)H * L.D);
+    L.wgu = M_(2LL * F, d);
+    L.wdown = M_(d, F);
     L.g_in = (float*)A(d * 4);
     L.g_post_attn = (float*)A(d * 4);
     L.g_pre_ffn = (float*)A(d * 4);
@@ -354,23 +392,26 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     L.g_q = (float*)A(L.D * 4);
     L.g_k = (float*)A(L.D * 4);
     if (v2) {
-      L.wple_gate = (uint16_t*)A((size_t)m->P * d * 2);
-      L.wple_proj = (uint16_t*)A((size_t)d * m->P * 2);
+      L.wple_gate = M_(m->P, d);
+      L.wple_proj = M_(d, m->P);
       L.g_ple_post = (float*)A(d * 4);
     }
   }
   m->g_final = (float*)A(d * 4);
   if (v2) {
-    m->wple_model = (uint16_t*)A((size_t)NL * m->P * d * 2);
+    m->wple_model = M_((int64_t)NL * m->P, d);
     m->g_ple_norm = (float*)A(m->P * 4);
-    m->wemb_proj = (uint16_t*)A((size_t)m->E * d * 2);
+    m->wemb_proj = M_(m->E, d);
   }
   int in = v2 ? m->E : d;
   for (int i = 0; i < c.n_dense; i++) {
     if (c.dense_out[i] <= 0) rc = set_error(ctx, FA_ERR_ARG, "gemma: dense_out[%d] = %d", i, c.dense_out[i]);
+    if (c.dense_act[i] != FA_ACT_NONE && c.dense_act[i] != FA_ACT_TANH)
+      rc = set_error(ctx, FA_ERR_ARG, "gemma: dense_act[%d] = %d (identity or tanh)", i, c.dense_act[i]);
     m->dense_in.push_back(in);
     m->dense_out.push_back(c.dense_out[i]);
-    m->dense.push_back((uint16_t*)A((size_t)in * c.dense_out[i] * 2));
+    m->dense_act.push_back(c.dense_act[i]);
+    m->dense.push_back(M_(c.dense_out[i], in));
     in = c.dense_out[i];
   }
   if (m->d_local) {
@@ -452,29 +493,72 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
     for (int i = 0; i < ndim; i++) r += (i ? "," : "") + std::to_string(shape[i]);
     return r + "]";
   };
-  // matrix [rows, cols] -> bf16 rows at dst (row stride cols); source row r
-  // goes to destination row dst_row(r), copied in runs of consecutive rows
-  auto put_matrix = [&](uint16_t* dst, int64_t rows, int64_t cols, auto&& dst_row) -> int {
+  // matrix [rows, cols] -> rows of dst (row stride cols); source row r goes to
+  // destination row dst_row(r), copied in runs of consecutive rows. bf16 data
+  // and bf16-exact float32 data keep one bf16 plane; float32 data with any
+  // other value turns dst into three planes (hi, mid, lo: the same split as
+  // the kernels' split3), the rows written before kept as hi with zero mid
+  // and lo.
+  auto put_matrix = [&](fa::Mat& dst, int64_t rows, int64_t cols, auto&& dst_row) -> int {
+    const size_t n = (size_t)rows * cols;
     std::vector<uint16_t> tmp;
     const uint16_t* src16 = (const uint16_t*)data;
+    bool exact = true;
     if (dtype == FA_DT_F32) {
-      tmp.resize((size_t)rows * cols);
+      tmp.resize(n);
       const float* src = (const float*)data;
-      for (int64_t r = 0; r < rows; r++)
-        for (int64_t k = 0; k < cols; k++)
-          if (!fa::bf16_exact(src[r * cols + k], &tmp[(size_t)r * cols + k]))
-            return set_error(ctx, FA_ERR_UNSUPPORTED,
-                             "gemma: weight %s is not exactly representable in bf16 (row %lld col %lld); this build "
-                             "keeps matrices bf16-resident",
-                             name, (long long)r, (long long)k);
+      for (size_t i = 0; i < n && exact; i++) exact = fa::bf16_exact(src[i], &tmp[i]);
+      if (!exact) {
+        tmp.resize(3 * n);
+        for (size_t i = 0; i < n; i++) {
+          uint32_t u;
+          std::memcpy(&u, &src[i], 4);
+          const uint32_t hi = u & 0xFFFF0000u;
+          float fh, r1;
+          std::memcpy(&fh, &hi, 4);
+          r1 = src[i] - fh;  // exact in float32
+          uint32_t u1;
+          std::memcpy(&u1, &r1, 4);
+          const uint32_t mid = u1 & 0xFFFF0000u;
+          float fm, r2;
+          std::memcpy(&fm, &mid, 4);
+          r2 = r1 - fm;  // at most 8 significant bits: exact in bf16
+          uint32_t u2;
+          std::memcpy(&u2, &r2, 4);
+          tmp[i] = (uint16_t)(hi >> 16);
+          tmp[n + i] = (uint16_t)(mid >> 16);
+          tmp[2 * n + i] = (uint16_t)(u2 >> 16);
+        }
+      }
       src16 = tmp.data();
     }
-    for (int64_t r0 = 0; r0 < rows;) {
-      int64_t r1 = r0 + 1;
-      while (r1 < rows && dst_row(r1) == dst_row(r1 - 1) + 1) r1++;
-      FA_HIP_CHECK(ctx, hipMemcpy(dst + (size_t)dst_row(r0) * cols, src16 + (size_t)r0 * cols,
-                                  (size_t)(r1 - r0) * cols * 2, hipMemcpyHostToDevice));
-      r0 = r1;
+    if (!exact && dst.terms == 1) {
+      // promote to three planes: the rows set so far become hi, mid = lo = 0
+      void* np = nullptr;
+      int rc2 = fa::alloc_dev(m, (size_t)3 * dst.plane() * 2, &np);
+      if (rc2) return rc2;
+      FA_HIP_CHECK(ctx, hipMemcpy(np, dst.p, (size_t)dst.plane() * 2, hipMemcpyDeviceToDevice));
+      FA_HIP_CHECK(ctx, hipMemset((uint16_t*)np + dst.plane(), 0, (size_t)2 * dst.plane() * 2));
+      fa::free_dev(m, dst.p);
+      dst.p = (uint16_t*)np;
+      dst.terms = 3;
+    }
+    const int src_terms = exact ? 1 : 3;
+    std::vector<uint16_t> zeros;
+    for (int t = 0; t < dst.terms; t++) {
+      const uint16_t* from = src16 + (t < src_terms ? (size_t)t * n : 0);
+      if (t >= src_terms) {  // rows of an exact matrix in a three-plane one: zero mid and lo
+        if (zeros.empty()) zeros.assign(n, 0);
+        from = zeros.data();
+      }
+      uint16_t* plane = dst.p + (size_t)t * dst.plane();
+      for (int64_t r0 = 0; r0 < rows;) {
+        int64_t r1 = r0 + 1;
+        while (r1 < rows && dst_row(r1) == dst_row(r1 - 1) + 1) r1++;
+        FA_HIP_CHECK(ctx, hipMemcpy(plane + (size_t)dst_row(r0) * cols, from + (size_t)r0 * cols,
+                                    (size_t)(r1 - r0) * cols * 2, hipMemcpyHostToDevice));
+        r0 = r1;
+      }
     }
     return FA_OK;
   };
@@ -537,10 +621,10 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
       rc = put_matrix(L.wqkv, H * D, d, identity);
     } else if (rest == "self_attn.k_proj.weight") {
       if (!shape_is({Hkv * D, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
-      rc = put_matrix(L.wqkv + (size_t)H * D * d, Hkv * D, d, identity);
+      rc = put_matrix(L.wqkv, Hkv * D, d, [o = (int64_t)H * D](int64_t r) { return o + r; });
     } else if (rest == "self_attn.v_proj.weight") {
       if (!shape_is({Hkv * D, d})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
-      rc = put_matrix(L.wqkv + (size_t)(H + Hkv) * D * d, Hkv * D, d, identity);
+      rc = put_matrix(L.wqkv, Hkv * D, d, [o = (int64_t)(H + Hkv) * D](int64_t r) { return o + r; });
     } else if (rest == "self_attn.o_proj.weight") {
       if (!shape_is({d, H * D})) return set_error(ctx, FA_ERR_ARG, "gemma: %s shape %s", name, shape_str().c_str());
       rc = put_matrix(L.wo, d, H * D, identity);
@@ -803,8 +887,8 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   const int wbound = v2 ? c.sliding_window + 1 : c.use_bidirectional ? c.sliding_window / 2 + 1 : c.sliding_window;
   {
     fa::Probe pr(m, FA_K_GATHER, 0, (double)M * (2.0 * d + 8.0 * d + 4));
-    if ((rc = fa::launch_embed_gather(ctx, d_ids, row_src_d, m->embed, c.vocab_size, M, d, emb_scale,
-                                      m->layers[0].g_in, eps, x, xn, s)))
+    if ((rc = fa::launch_embed_gather(ctx, d_ids, row_src_d, m->embed.p, m->embed.terms == 3 ? m->embed.plane() : 0,
+                                      c.vocab_size, M, d, emb_scale, m->layers[0].g_in, eps, x, xn, s)))
       return rc;
     pr.done();
   }
@@ -812,7 +896,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     // per-layer inputs: RMSNorm(x0 . W_ple^T * hidden^-1/2) per layer (embed.go:274-279)
     {
       fa::GemmArgs g;
-      g.m = M; g.n = (int64_t)NL * P; g.k = d; g.a = x; g.lda = d; g.b = m->wple_model; g.ldb = d; g.c = ple;
+      g.m = M; g.n = (int64_t)NL * P; g.k = d; g.a = x; g.lda = d; fa::set_b(g, m->wple_model); g.c = ple;
       g.ldc = (int64_t)NL * P;
       fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * M * NL * P * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
@@ -857,7 +941,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     int rc;
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = L.width; g.k = d; g.a = xnr; g.lda = d; g.b = L.wqkv; g.ldb = d; g.c = qkvr; g.ldc = L.width;
+      g.m = rows; g.n = L.width; g.k = d; g.a = xnr; g.lda = d; fa::set_b(g, L.wqkv); g.c = qkvr; g.ldc = L.width;
       fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * rows * L.width * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
@@ -912,7 +996,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = d; g.k = H * D; g.a = attr; g.lda = H * D; g.b = L.wo; g.ldb = H * D; g.c = or_;
+      g.m = rows; g.n = d; g.k = H * D; g.a = attr; g.lda = H * D; fa::set_b(g, L.wo); g.c = or_;
       g.ldc = d; g.ksplit = ks_o; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_O, 2.0 * rows * d * H * D, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -926,7 +1010,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = 2 * F; g.k = d; g.a = xnr; g.lda = d; g.b = L.wgu; g.ldb = d; g.c = gur; g.ldc = F;
+      g.m = rows; g.n = 2 * F; g.k = d; g.a = xnr; g.lda = d; fa::set_b(g, L.wgu); g.c = gur; g.ldc = F;
       g.epi = fa::Epi::GeGLU;
       fa::Probe pr(m, FA_K_GEMM_GATEUP, 2.0 * rows * 2 * F * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -934,7 +1018,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::GemmArgs g;
-      g.m = rows; g.n = d; g.k = F; g.a = gur; g.lda = F; g.b = L.wdown; g.ldb = F; g.c = or_; g.ldc = d;
+      g.m = rows; g.n = d; g.k = F; g.a = gur; g.lda = F; fa::set_b(g, L.wdown); g.c = or_; g.ldc = d;
       g.ksplit = ks_down; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * rows * d * F, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -954,7 +1038,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       // x = (x + RMSNorm(gelu(x . Wg^T) * ple_l . Wp^T; g)) * scalar (embed.go:359-371)
       {
         fa::GemmArgs g;
-        g.m = rows; g.n = P; g.k = d; g.a = xr; g.lda = d; g.b = L.wple_gate; g.ldb = d; g.c = gur; g.ldc = P;
+        g.m = rows; g.n = P; g.k = d; g.a = xr; g.lda = d; fa::set_b(g, L.wple_gate); g.c = gur; g.ldc = P;
         g.epi = fa::Epi::Generic; g.act = FA_ACT_GELU; g.mul = ple + r0 * NL * P + (int64_t)l * P;
         g.ldm = (int64_t)NL * P;
         fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * P * d, 0);
@@ -963,7 +1047,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       }
       {
         fa::GemmArgs g;
-        g.m = rows; g.n = d; g.k = P; g.a = gur; g.lda = P; g.b = L.wple_proj; g.ldb = P; g.c = or_; g.ldc = d;
+        g.m = rows; g.n = d; g.k = P; g.a = gur; g.lda = P; fa::set_b(g, L.wple_proj); g.c = or_; g.ldc = d;
         g.ksplit = ks_ple; g.c_split = M * d;
         fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * d * P, 0);
         if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -1015,7 +1099,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   int nb = 0;
   if (v2) {  // the embedding projection, applied to the pooled vector (embed.go:408-414)
     fa::GemmArgs g;
-    g.m = B; g.n = m->E; g.k = d; g.a = pooled; g.lda = d; g.b = m->wemb_proj; g.ldb = d; g.c = bufs[0]; g.ldc = m->E;
+    g.m = B; g.n = m->E; g.k = d; g.a = pooled; g.lda = d; fa::set_b(g, m->wemb_proj); g.c = bufs[0]; g.ldc = m->E;
     fa::Probe pr(m, FA_K_GEMM_HEAD, 2.0 * B * m->E * d, 0);
     if ((rc = fa::launch_gemm(ctx, g, s))) return rc;
     pr.done();
@@ -1024,13 +1108,18 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     nb = 1;
   }
   // the last dense product splits K (its few rows give few tiles: 3072 -> 768
-  // for one pooled row is 12 of them) and the L2 norm adds the partials
+  // for one pooled row is 12 of them) and the L2 norm adds the partials,
+  // unless a Tanh follows it (model.go:296-301, embed.go:415-418: applied in
+  // the product's epilogue, so on the whole sum)
   int head_parts = 1;
   for (int i = 0; i < c.n_dense; i++) {
     fa::GemmArgs g;
-    g.m = B; g.n = m->dense_out[i]; g.k = cur_w; g.a = cur; g.lda = cur_w; g.b = m->dense[i]; g.ldb = cur_w;
+    g.m = B; g.n = m->dense_out[i]; g.k = cur_w; g.a = cur; g.lda = cur_w; fa::set_b(g, m->dense[i]);
     g.c = bufs[(i + nb) & 1]; g.ldc = m->dense_out[i];
-    if (i + 1 == c.n_dense) {
+    if (m->dense_act[i] == FA_ACT_TANH) {
+      g.epi = fa::Epi::Generic;
+      g.act = FA_ACT_TANH;
+    } else if (i + 1 == c.n_dense) {
       for (int ks : {4, 2})
         if (cur_w % (32 * ks) == 0 && (int64_t)ks * m->dense_out[i] <= maxw) {
           head_parts = ks;

@@ -106,8 +106,8 @@ __device__ __forceinline__ float sumsq(const f32x4 (&v)[NC]) {
 template <int NC>
 __global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* __restrict__ ids,
                                                            const int32_t* __restrict__ row_src,
-                                                           const uint16_t* __restrict__ E, int64_t vocab,
-                                                           int64_t rows, float scale,
+                                                           const uint16_t* __restrict__ E, int64_t plane,
+                                                           int64_t vocab, int64_t rows, float scale,
                                                            const float* __restrict__ g, float eps,
                                                            float* __restrict__ x, float* __restrict__ xn) {
   constexpr int d = NC * 256;
@@ -122,10 +122,24 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* __rest
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     uint2 h = *reinterpret_cast<const uint2*>(e + c * 256 + lane * 4);
-    v[c].x = __uint_as_float(h.x << 16) * scale;
-    v[c].y = __uint_as_float(h.x & 0xFFFF0000u) * scale;
-    v[c].z = __uint_as_float(h.y << 16) * scale;
-    v[c].w = __uint_as_float(h.y & 0xFFFF0000u) * scale;
+    v[c].x = __uint_as_float(h.x << 16);
+    v[c].y = __uint_as_float(h.x & 0xFFFF0000u);
+    v[c].z = __uint_as_float(h.y << 16);
+    v[c].w = __uint_as_float(h.y & 0xFFFF0000u);
+    if (plane) {  // + mid + lo: the float32 value exactly
+#pragma unroll
+      for (int t = 1; t < 3; t++) {
+        h = *reinterpret_cast<const uint2*>(e + t * plane + c * 256 + lane * 4);
+        v[c].x += __uint_as_float(h.x << 16);
+        v[c].y += __uint_as_float(h.x & 0xFFFF0000u);
+        v[c].z += __uint_as_float(h.y << 16);
+        v[c].w += __uint_as_float(h.y & 0xFFFF0000u);
+      }
+    }
+    v[c].x *= scale;
+    v[c].y *= scale;
+    v[c].z *= scale;
+    v[c].w *= scale;
   }
   const float inv = rms_inv(sumsq<NC>(v), d, eps);
 #pragma unroll
@@ -548,16 +562,16 @@ int launch_rope(fa_ctx* ctx, const float* x, const float* cos_t, const float* si
   return FA_OK;
 }
 
-int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_src, const uint16_t* E,
+int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_src, const uint16_t* E, int64_t plane,
                         int64_t vocab, int64_t rows, int32_t d, float scale, const float* g_next, float eps, float* x,
                         float* xn, hipStream_t s) {
   if (rows == 0) return FA_OK;
   dim3 grid(blocks_for(rows, 4)), block(256);
   switch (d) {
-    case 256: hipLaunchKernelGGL(embed_gather_kernel<1>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
-    case 512: hipLaunchKernelGGL(embed_gather_kernel<2>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
-    case 768: hipLaunchKernelGGL(embed_gather_kernel<3>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
-    case 1024: hipLaunchKernelGGL(embed_gather_kernel<4>, grid, block, 0, s, d_ids, d_row_src, E, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 256: hipLaunchKernelGGL(embed_gather_kernel<1>, grid, block, 0, s, d_ids, d_row_src, E, plane, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 512: hipLaunchKernelGGL(embed_gather_kernel<2>, grid, block, 0, s, d_ids, d_row_src, E, plane, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 768: hipLaunchKernelGGL(embed_gather_kernel<3>, grid, block, 0, s, d_ids, d_row_src, E, plane, vocab, rows, scale, g_next, eps, x, xn); break;
+    case 1024: hipLaunchKernelGGL(embed_gather_kernel<4>, grid, block, 0, s, d_ids, d_row_src, E, plane, vocab, rows, scale, g_next, eps, x, xn); break;
     default: return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden size %d not in {256,512,768,1024}", d);
   }
   FA_CHECK_LAUNCH(ctx);

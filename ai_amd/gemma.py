@@ -36,6 +36,7 @@ def _config_struct(shape) -> N.GemmaConfig:
     c.n_dense = len(shape.dense_out)
     for i, o in enumerate(shape.dense_out):
         c.dense_out[i] = int(o)
+        c.dense_act[i] = int(shape.dense_act[i]) if i < len(shape.dense_act) else N.FA_ACT_NONE
     return c
 
 

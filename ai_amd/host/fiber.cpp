@@ -356,7 +356,10 @@ Model::Model(const Config& cfg) : cfg_(cfg) {
   c.max_tokens = cfg.MaxTokens;
   if (cfg.Dense.size() > 4) throw Error("gemma: at most 4 Dense layers");
   c.n_dense = (int32_t)cfg.Dense.size();
-  for (size_t i = 0; i < cfg.Dense.size(); i++) c.dense_out[i] = cfg.Dense[i];
+  for (size_t i = 0; i < cfg.Dense.size(); i++) {
+    c.dense_out[i] = cfg.Dense[i];
+    c.dense_act[i] = i < cfg.DenseAct.size() ? cfg.DenseAct[i] : FA_ACT_NONE;
+  }
   if (cfg.Variant == 2) {
     if (cfg.NumHiddenLayers > FA_GEMMA_MAX_LAYERS)
       throw Error("gemma: " + std::to_string(cfg.NumHiddenLayers) + " layers; this build runs at most " +
@@ -628,6 +631,7 @@ Config LoadConfig(const std::string& dir) {
     c.MaxTokens = (maxpos == 0 || maxpos > 2048) ? 2048 : (int)maxpos;  // model.go:100-104
   }
   c.Dense.clear();
+  c.DenseAct.clear();
   return c;
 }
 
@@ -638,10 +642,10 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
     if (o.MaxTokens > 0) cfg.MaxTokens = std::min(o.MaxTokens, cfg.Variant == 2 ? 8192 : 2048);
     if (o.BatchTokens <= 0) throw Error("gemma: BatchTokens must be positive");
     // sentence-transformers head (model.go:236-310): mean pooling, Dense
-    // layers without bias or activation, Normalize
+    // layers without bias, identity or Tanh, Normalize
     struct DenseMod {
       std::string path;
-      int in, out;
+      int in, out, act;
     };
     std::vector<DenseMod> dense;
     stage = "modules.json";
@@ -663,9 +667,11 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
           const json::Value dc = read_json(mdir + "/config.json", "Dense config");
           if (dc.get_bool("bias")) throw Error("gemma: Dense layers with bias are not supported");
           const std::string act = dc.get_string("activation_function");
-          if (!(act.empty() || act == "torch.nn.modules.linear.Identity"))
+          int a = FA_ACT_NONE;
+          if (act == "torch.nn.modules.activation.Tanh") a = FA_ACT_TANH;
+          else if (!(act.empty() || act == "torch.nn.modules.linear.Identity"))
             throw Error("gemma: Dense activation \"" + act + "\" not supported");
-          dense.push_back({mdir, (int)dc.get_int("in_features"), (int)dc.get_int("out_features")});
+          dense.push_back({mdir, (int)dc.get_int("in_features"), (int)dc.get_int("out_features"), a});
         }
       }
     }
@@ -675,6 +681,7 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
       if (d.in != width)
         throw Error("gemma: Dense in_features " + std::to_string(d.in) + " after width " + std::to_string(width));
       cfg.Dense.push_back(d.out);
+      cfg.DenseAct.push_back(d.act);
       width = d.out;
     }
     // every file is read and checked before the GPU is touched

@@ -137,6 +137,7 @@ struct Config {
   float RMSNormEps = 1e-6f;
   int MaxTokens = 2048;
   std::vector<int> Dense = {3072, 768};
+  std::vector<int> DenseAct;  // per Dense layer: FA_ACT_NONE (identity) or FA_ACT_TANH; empty: all identity
   // EmbeddingGemma 2 only (zero / empty for Variant 0)
   int Variant = 0;
   int HiddenSizePerLayerInput = 0, EmbeddingDim = 0;
@@ -184,8 +185,9 @@ class Model {
  public:
   // Reads a model directory in the Hugging Face / sentence-transformers
   // layout: config.json, tokenizer.json, *.safetensors (+ index), and the
-  // modules.json Pooling (mean), Dense (no bias, identity) and Normalize
-  // modules with config_sentence_transformers.json prompts (model.go:76-330).
+  // modules.json Pooling (mean), Dense (no bias; identity or Tanh) and
+  // Normalize modules with config_sentence_transformers.json prompts
+  // (model.go:76-330).
   // EmbeddingGemma 2 directories add the per-layer-input weights, the layer
   // scalars and the embedding projection (model.go:163-205).
   static std::unique_ptr<Model> Load(const std::string& dir, const LoadOpts& o = {});

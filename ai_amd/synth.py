@@ -95,6 +95,7 @@ class ModelShape:
     rms_norm_eps: float = 1e-6
     max_tokens: int = 2048
     dense_out: list = field(default_factory=lambda: [3072, 768])
+    dense_act: list = field(default_factory=list)  # per Dense layer: 0 identity, 3 Tanh; empty: identity
 
 
 def weight_specs(s: ModelShape):

@@ -44,8 +44,12 @@ enum { FA_DT_F32 = 0, FA_DT_BF16 = 1 };
 
 /* Activation of a fused product: tensor.NoAct/ReLUAct/GELUAct
  * (tensor/matmul_fused.go:25-32). GELU is the tanh approximation
- * (internal/kernel/math.go:117-143). */
-enum { FA_ACT_NONE = 0, FA_ACT_RELU = 1, FA_ACT_GELU = 2 };
+ * (internal/kernel/math.go:117-143). FA_ACT_TANH is (*Tensor).Tanh
+ * (tensor/ops_unary.go:114, internal/kernel/generic.go:313-359) applied to
+ * the product, which tensor.Fused does not offer: the gemma head's Dense
+ * layers with a Tanh activation (models/gemma/model.go:296-301,
+ * embed.go:415-418). */
+enum { FA_ACT_NONE = 0, FA_ACT_RELU = 1, FA_ACT_GELU = 2, FA_ACT_TANH = 3 };
 
 /* Layout of a product's right operand B (logical shape [k x n]):
  * FA_B_KN: row-major [k x n] with leading dimension ldb (the reference's
@@ -245,6 +249,9 @@ typedef struct fa_gemma_config {
   int32_t layer_head_dim[FA_GEMMA_MAX_LAYERS];  /* per layer; 0 = head_dim */
   int32_t layer_kv_heads[FA_GEMMA_MAX_LAYERS];  /* per layer; 0 = num_key_value_heads */
   int32_t layer_sliding[FA_GEMMA_MAX_LAYERS];   /* variant 2: 1 sliding window, 0 full attention */
+  /* Activation after each head Dense layer: FA_ACT_NONE (identity) or
+   * FA_ACT_TANH ("torch.nn.modules.activation.Tanh", model.go:296-301). */
+  int32_t dense_act[4];
 } fa_gemma_config;
 
 /* Create an empty model on ctx (no weights yet). Replaces the allocation
@@ -259,10 +266,12 @@ void fa_gemma_destroy(fa_model* m);
  * "layers.<i>.self_attn.{q,k,v,o}_proj.weight", "layers.<i>.self_attn.
  * {q,k}_norm.weight", "layers.<i>.mlp.{gate,up,down}_proj.weight", and the
  * head's "dense.<i>.linear.weight" (model.go:277-304). Shapes are the
- * checkpoint's ([out, in] for matrices). Matrices are kept bf16-resident:
- * FA_DT_BF16 data is stored as is; FA_DT_F32 data must be exactly
- * representable in bf16 (else FA_ERR_UNSUPPORTED). Norm vectors are kept
- * in float32 with Gemma's 1+w applied (model.go:131-140). */
+ * checkpoint's ([out, in] for matrices). FA_DT_BF16 matrices, and FA_DT_F32
+ * ones whose values are all bf16-exact, are kept as bf16; any other FA_DT_F32
+ * matrix (a float32 or float16 checkpoint, safetensors/convert.go:23-55) is
+ * kept exactly as three bf16 planes hi + mid + lo and its products run the
+ * six-term split kernel. Norm vectors are kept in float32 with Gemma's 1+w
+ * applied (model.go:131-140). */
 int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t* shape, int32_t ndim,
                         const void* data);
 

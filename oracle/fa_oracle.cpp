@@ -483,6 +483,7 @@ struct OrcConfig {
   float eps;
   int n_dense;
   int dense_out[4];
+  int dense_tanh[4];  // Dense layer followed by Tanh (model.go:296-301)
 };
 
 struct OrcLayer {
@@ -525,7 +526,10 @@ ORC_API void* orc_model_create(int hidden, int layers, int heads, int kv_heads, 
   c.ffn = ffn; c.vocab = vocab; c.sliding_window = sliding_window; c.bidirectional = bidirectional;
   c.pattern = pattern > 0 ? pattern : 6; c.rope_local = rope_local; c.rope_theta = rope_theta; c.qpas = qpas;
   c.eps = eps; c.n_dense = n_dense;
-  for (int i = 0; i < n_dense; i++) c.dense_out[i] = dense_out[i];
+  for (int i = 0; i < n_dense; i++) {
+    c.dense_out[i] = dense_out[i];
+    c.dense_tanh[i] = 0;
+  }
   m->layers.resize(layers);
   m->dense.resize(n_dense);
   m->dense_in.resize(n_dense);
@@ -540,6 +544,15 @@ ORC_API void* orc_model_create(int hidden, int layers, int heads, int kv_heads, 
 }
 
 ORC_API void orc_model_destroy(void* p) { delete (OrcModel*)p; }
+
+// Dense layer i of the head followed by Tanh (torch.nn.modules.activation.Tanh,
+// model.go:296-301; applied after the product, embed.go:415-418).
+ORC_API int orc_model_set_dense_tanh(void* p, int i, int on) {
+  OrcModel* m = (OrcModel*)p;
+  if (i < 0 || i >= m->cfg.n_dense) return -3;
+  m->cfg.dense_tanh[i] = on != 0;
+  return 0;
+}
 
 // transpose [out, in] -> [in, out] (model.go:121-127)
 static std::vector<float> transpose_w(const float* w, int out, int in) {
@@ -807,6 +820,8 @@ ORC_API int orc_model_embed(void* p, const int32_t* ids, const int32_t* lengths,
     int no = m->dense_out[i];
     y2.assign((size_t)B * no, 0.f);
     orc_gemm(B, no, cur, y.data(), cur, m->dense[i].data(), no, y2.data(), no, nullptr, nullptr, 0, nullptr, 0, nullptr, 0);
+    if (c.dense_tanh[i])  // (*Tensor).Tanh: kernel.Tanh, the rational of generic.go:313-359
+      for (auto& v : y2) v = orc_tanhf(v);
     y.swap(y2);
     cur = no;
   }

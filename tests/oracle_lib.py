@@ -36,6 +36,7 @@ _SIGS = {
     "orc_model_finalize": (C.c_int, [vp]),
     "orc_model_embed": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
     "orc_model_encode": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp, C.c_int, vp]),
+    "orc_model_set_dense_tanh": (C.c_int, [vp, C.c_int, C.c_int]),
     "orc_num_threads": (C.c_int, []),
     "orc_model2_create": (vp, [C.c_int] * 8 + [f64, f64, f32, vp, vp, vp, C.c_int, vp]),
     "orc_model2_destroy": (None, [vp]),
@@ -257,6 +258,9 @@ class OracleModel:
                                         s.rms_norm_eps, len(s.dense_out), C.cast(do, vp))
         assert self.h
         self.shape = shape
+        for i, act in enumerate(getattr(s, "dense_act", [])):
+            if act == 3:
+                assert lib().orc_model_set_dense_tanh(self.h, i, 1) == 0
 
     def set(self, name, data):
         a = f32c(data)

@@ -375,6 +375,8 @@ def f64_encoder(shape, weights, ids, lengths, dim=0, states=None):
         y = hfin.mean(0)
         for i in range(len(shape.dense_out)):
             y = w[f"dense.{i}.linear.weight"] @ y
+            if i < len(shape.dense_act) and shape.dense_act[i] == 3:  # Tanh Dense (model.go:296-301)
+                y = np.tanh(y)
         if dim:
             y = y[:dim]
         outs.append(y / math.sqrt((y ** 2).sum() + 1e-12))
@@ -491,3 +493,17 @@ def test_oracle_encode_states_vs_float64(tiny):
     assert np.abs(om.embed(ids, lengths) - y).max() < 1e-6
     with pytest.raises(ValueError):
         om.encode(ids, lengths, layers=[nl + 1])
+
+
+def test_oracle_tanh_dense_head(tiny):
+    """A Dense layer with a Tanh activation (model.go:296-301, applied after
+    the product, embed.go:415-418) against the float64 restatement; dropping
+    the Tanh must move the result."""
+    shape, ws, ids, lengths = tiny
+    sh = tiny_shape(dense_act=[3, 0])
+    om = oracle_model(sh, ws)
+    got = om.embed(ids, lengths)
+    want = f64_encoder(sh, ws, ids, lengths)
+    assert np.abs(got - want).max() <= 1e-4
+    plain = f64_encoder(shape, ws, ids, lengths)
+    assert np.abs(plain - want).max() > 1e-3
