@@ -125,6 +125,10 @@ struct fa_model {
   hipEvent_t ev_fork = nullptr, ev_join[fa::kMaxMicrobatches] = {};
   std::vector<int> seq_order;
   fa::DevBuf ids_dev, out_dev;
+  // pinned staging of the host entry points' ids and results (asynchronous
+  // copies; the entry points synchronise before returning)
+  void* io_host = nullptr;
+  size_t io_host_bytes = 0;
   // profiling
   bool profiling = false;
   std::vector<hipEvent_t> event_pool;
@@ -271,6 +275,19 @@ int collect_stats(fa_model* m) {
     m->event_pool.push_back(p.b);
   }
   m->pending.clear();
+  return FA_OK;
+}
+
+// The pinned staging buffer of the host entry points, grown to at least bytes.
+int io_staging(fa_model* m, size_t bytes, char** out) {
+  if (bytes > m->io_host_bytes) {
+    if (m->io_host) (void)hipHostFree(m->io_host);
+    m->io_host = nullptr;
+    m->io_host_bytes = 0;
+    FA_HIP_CHECK(m->ctx, hipHostMalloc(&m->io_host, bytes, hipHostMallocDefault));
+    m->io_host_bytes = bytes;
+  }
+  *out = static_cast<char*>(m->io_host);
   return FA_OK;
 }
 
@@ -457,6 +474,7 @@ void fa_gemma_destroy(fa_model* m) {
   m->ids_dev.release();
   m->out_dev.release();
   if (m->plan_host) (void)hipHostFree(m->plan_host);
+  if (m->io_host) (void)hipHostFree(m->io_host);
   if (m->plan_done) (void)hipEventDestroy(m->plan_done);
   if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
   for (int i = 0; i < fa::kMaxMicrobatches; i++) {
@@ -1173,11 +1191,16 @@ int fa_gemma_encode_ids(fa_model* m, const int32_t* ids, const int32_t* lengths,
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
   if ((rc = m->out_dev.ensure(ctx, (size_t)M * d * 4))) return rc;
-  FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, ids, (size_t)B * T * 4, hipMemcpyHostToDevice, ctx->stream));
+  char* io;
+  const size_t ib = (size_t)B * T * 4, ob = (size_t)M * d * 4;
+  if ((rc = fa::io_staging(m, ib + ob, &io))) return rc;
+  std::memcpy(io, ids, ib);
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, io, ib, hipMemcpyHostToDevice, ctx->stream));
   if ((rc = fa_gemma_encode_ids_dev(m, m->ids_dev.as<int32_t>(), lengths, B, T, n_layers, m->out_dev.as<float>())))
     return rc;
-  FA_HIP_CHECK(ctx, hipMemcpyAsync(hidden, m->out_dev.ptr, (size_t)M * d * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(io + ib, m->out_dev.ptr, ob, hipMemcpyDeviceToHost, ctx->stream));
   FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  std::memcpy(hidden, io + ib, ob);
   return FA_OK;
 }
 
@@ -1197,10 +1220,15 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
   if ((rc = m->out_dev.ensure(ctx, (size_t)B * dd * 4))) return rc;
-  FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, ids, (size_t)B * T * 4, hipMemcpyHostToDevice, ctx->stream));
+  char* io;
+  const size_t ib = (size_t)B * T * 4, ob = (size_t)B * dd * 4;
+  if ((rc = fa::io_staging(m, ib + ob, &io))) return rc;
+  std::memcpy(io, ids, ib);
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(m->ids_dev.ptr, io, ib, hipMemcpyHostToDevice, ctx->stream));
   if ((rc = fa_gemma_embed_ids_dev(m, m->ids_dev.as<int32_t>(), lengths, B, T, dd, m->out_dev.as<float>()))) return rc;
-  FA_HIP_CHECK(ctx, hipMemcpyAsync(out, m->out_dev.ptr, (size_t)B * dd * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FA_HIP_CHECK(ctx, hipMemcpyAsync(io + ib, m->out_dev.ptr, ob, hipMemcpyDeviceToHost, ctx->stream));
   FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  std::memcpy(out, io + ib, ob);
   return FA_OK;
 }
 
