@@ -75,7 +75,6 @@ struct Tile {
 using T128x128 = Tile<128, 128, 32, 2, 2>;  // 4 waves of 64x64
 using T64x64 = Tile<64, 64, 32, 2, 2>;      // 4 waves of 32x32
 using T128x64v = Tile<128, 64, 32, 4, 1>;   // 4 waves of 32x64 (column-block pairs for GeGLU)
-using T64x128 = Tile<64, 128, 32, 2, 2>;    // 4 waves of 32x64
 
 struct GemmParams {
   int64_t m, n, k;
@@ -425,12 +424,9 @@ struct XTile {
   static_assert(TM % 32 == 0 && TN % 32 == 0, "tile shape");
 };
 
-using X128x128 = XTile<128, 128, 2, 2>;  // 4 waves of 64x64
-using X128x64 = XTile<128, 64, 2, 2>;    // 4 waves of 64x32
 using X128x64v = XTile<128, 64, 4, 1>;   // 4 waves of 32x64 (column-block pairs for GeGLU)
 using X64x128 = XTile<64, 128, 2, 2>;    // 4 waves of 32x64
 using X64x64 = XTile<64, 64, 2, 2>;      // 4 waves of 32x32
-using X256x128 = XTile<256, 128, 4, 2>;  // 8 waves of 64x64
 using X128x128w8 = XTile<128, 128, 4, 2>;  // 8 waves of 32x64
 using X128x256w8 = XTile<128, 256, 4, 2>;  // 8 waves of 32x128 (80 KB of LDS: two workgroups per CU)
 
@@ -798,8 +794,8 @@ void launch_x3_small(GemmParams p, hipStream_t s) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
-enum class TileId { k128x128 = 0, k64x64, k128x64v, k64x128, kCount };
-const char* const kTileNames[] = {"128x128", "64x64", "128x64v", "64x128"};
+enum class TileId { k128x128 = 0, k64x64, k128x64v, kCount };
+const char* const kTileNames[] = {"128x128", "64x64", "128x64v"};
 
 // FA_GEMM_TILE=<name> forces a tile shape on the fast path (tuning).
 int forced_tile() {
@@ -841,14 +837,12 @@ void dispatch_tile(TileId t, const GemmParams& p, Epi epi, hipStream_t s) {
   switch (t) {
     case TileId::k64x64: dispatch_fast<T64x64, BBF16>(p, epi, s); break;
     case TileId::k128x64v: dispatch_fast<T128x64v, BBF16>(p, epi, s); break;
-    case TileId::k64x128: dispatch_fast<T64x128, BBF16>(p, epi, s); break;
     default: dispatch_fast<T128x128, BBF16>(p, epi, s); break;
   }
 }
 
-enum class XTileId { x128x128 = 0, x128x64, x128x64v, x64x128, x64x64, x256x128, x128x128w8, x128x256w8, small, kCount };
-const char* const kXTileNames[] = {"128x128", "128x64",    "128x64v",   "64x128", "64x64",
-                                   "256x128", "128x128w8", "128x256w8", "small"};
+enum class XTileId { x128x64v = 0, x64x128, x64x64, x128x128w8, x128x256w8, small, kCount };
+const char* const kXTileNames[] = {"128x64v", "64x128", "64x64", "128x128w8", "128x256w8", "small"};
 
 // FA_GEMM_XTILE=<name> forces a split-bf16 tile shape; FA_GEMM_MFMA=f32 runs
 // bf16 weights through the fp32 MFMA kernel instead (tuning, comparison).
@@ -924,14 +918,11 @@ void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
         case Epi::GeGLU: launch_x3_small<Epi::GeGLU>(p, s); break;
       }
       break;
-    case XTileId::x128x64: dispatch_x3_epi<X128x64>(p, epi, s); break;
     case XTileId::x128x64v: dispatch_x3_epi<X128x64v>(p, epi, s); break;
     case XTileId::x64x128: dispatch_x3_epi<X64x128>(p, epi, s); break;
     case XTileId::x64x64: dispatch_x3_epi<X64x64>(p, epi, s); break;
-    case XTileId::x256x128: dispatch_x3_epi<X256x128>(p, epi, s); break;
-    case XTileId::x128x128w8: dispatch_x3_epi<X128x128w8>(p, epi, s); break;
     case XTileId::x128x256w8: dispatch_x3_epi<X128x256w8>(p, epi, s); break;
-    default: dispatch_x3_epi<X128x128>(p, epi, s); break;
+    default: dispatch_x3_epi<X128x128w8>(p, epi, s); break;
   }
 }
 
@@ -999,13 +990,7 @@ __global__ __launch_bounds__(256) void split_b_kernel(const void* __restrict__ b
       make_uint4(pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7]));
 }
 
-bool x3_has_geglu(XTileId t) {
-  switch (t) {
-    case XTileId::x128x64: return X128x64::FN % 2 == 0;
-    case XTileId::x64x64: return X64x64::FN % 2 == 0;
-    default: return true;
-  }
-}
+bool x3_has_geglu(XTileId t) { return t != XTileId::x64x64; }
 
 }  // namespace
 

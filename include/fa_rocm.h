@@ -20,6 +20,23 @@
  * one context must be serialised by the caller (the reference's Embed is not
  * documented as goroutine-safe either, models/gemma/embed.go:15). Distinct
  * contexts may be used from distinct threads.
+ *
+ * HIP graphs: fa_similarities_topk_dev_noalloc is the entry point meant for
+ * capture. The others are not capture-safe: they may grow device buffers on
+ * a call, and fa_gemma_embed_ids_dev uploads its per-call plan from a pinned
+ * host buffer that the next call rewrites and records events of the model.
+ *
+ * Tuning switches (environment, read once per process; unset = the measured
+ * defaults; for A/B measurements only, results stay within the parity bars):
+ *   FA_GEMM_XTILE=128x64v|64x128|64x64|128x128w8|128x256w8|small
+ *                               force a split-bf16 product tile
+ *   FA_GEMM_TILE=128x128|64x64|128x64v   force an fp32-MFMA product tile
+ *   FA_GEMM_MFMA=f32            bf16 weights through the fp32-MFMA kernel
+ *   FA_GEMM_KSPLIT=1            no K split of the encoder's N = hidden products
+ *   FA_MICROBATCH=0|<rows>      micro-batches off / from this many tokens (2048)
+ *   FA_MICROBATCH_GROUPS=2..4   force the micro-batch count
+ *   FA_ATTN_PLANES=0|1          force the fp32-MFMA / split-bf16 attention
+ *   FA_ATTN_KEY_PARTS=1..8      force the key runs of the short-batch attention
  */
 #ifndef FA_ROCM_H
 #define FA_ROCM_H
