@@ -167,12 +167,19 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
   int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  f32x4 ov[NC], xv[NC];
+  f32x4 ov[NC], xv[NC], gp[NC], gn[NC];
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     const int col = c * 256 + lane * 4;
     ov[c] = *reinterpret_cast<const f32x4*>(o + row * d + col);
     xv[c] = *reinterpret_cast<const f32x4*>(x + row * d + col);
+  }
+  // the gains load with the rows, not after the reductions
+#pragma unroll
+  for (int c = 0; c < NC; c++) gp[c] = *reinterpret_cast<const f32x4*>(g_post + c * 256 + lane * 4);
+  if (g_next) {
+#pragma unroll
+    for (int c = 0; c < NC; c++) gn[c] = *reinterpret_cast<const f32x4*>(g_next + c * 256 + lane * 4);
   }
   if (o2) {
 #pragma unroll
@@ -185,7 +192,7 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     const int col = c * 256 + lane * 4;
-    f32x4 gg = *reinterpret_cast<const f32x4*>(g_post + col);
+    const f32x4 gg = gp[c];
     xv[c].x = xv[c].x + ov[c].x * inv * gg.x;
     xv[c].y = xv[c].y + ov[c].y * inv * gg.y;
     xv[c].z = xv[c].z + ov[c].z * inv * gg.z;
@@ -200,7 +207,7 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     const int col = c * 256 + lane * 4;
-    f32x4 gg = *reinterpret_cast<const f32x4*>(g_next + col);
+    const f32x4 gg = gn[c];
     f32x4 r;
     r.x = xv[c].x * inv2 * gg.x; r.y = xv[c].y * inv2 * gg.y; r.z = xv[c].z * inv2 * gg.z; r.w = xv[c].w * inv2 * gg.w;
     *reinterpret_cast<f32x4*>(xn + row * d + col) = r;
@@ -229,11 +236,26 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   if (row >= rows || head >= H + Hkv + (norm_v ? Hkv : 0)) return;
   const int width = (H + 2 * Hkv) * D;
   float* p = qkv + row * width + (int64_t)head * D;
-  f32x4 v[NQ];
+  // every load is issued before the reduction: the head's values, its gains
+  // and the token's RoPE table row (one dependent step through pos)
+  f32x4 v[NQ], gg[NQ];
+  const float* g = head < H ? gq : gk;
+  const bool rot = head < H + Hkv;
 #pragma unroll
   for (int c = 0; c < NQ; c++) v[c] = *reinterpret_cast<const f32x4*>(p + c * 256 + lane * 4);
+  if (rot) {
+#pragma unroll
+    for (int c = 0; c < NQ; c++) gg[c] = *reinterpret_cast<const f32x4*>(g + c * 256 + lane * 4);
+  }
+  const int t = pos[row];
+  const int i0 = D == 256 ? (lane & 31) * 4 : lane * 4;
+  f32x4 cv = {0.f, 0.f, 0.f, 0.f}, svv = {0.f, 0.f, 0.f, 0.f};
+  if (rot) {
+    cv = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
+    svv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
+  }
   const float inv = rms_inv(sumsq<NQ>(v), D, eps);
-  if (head >= H + Hkv) {  // value head: unit gain, no rotation
+  if (!rot) {  // value head: unit gain, no rotation
 #pragma unroll
     for (int c = 0; c < NQ; c++) {
       f32x4 r;
@@ -242,21 +264,16 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
     }
     return;
   }
-  const float* g = head < H ? gq : gk;
 #pragma unroll
   for (int c = 0; c < NQ; c++) {
-    const f32x4 gg = *reinterpret_cast<const f32x4*>(g + c * 256 + lane * 4);
-    v[c].x = v[c].x * inv * gg.x; v[c].y = v[c].y * inv * gg.y;
-    v[c].z = v[c].z * inv * gg.z; v[c].w = v[c].w * inv * gg.w;
+    v[c].x = v[c].x * inv * gg[c].x; v[c].y = v[c].y * inv * gg[c].y;
+    v[c].z = v[c].z * inv * gg[c].z; v[c].w = v[c].w * inv * gg[c].w;
   }
-  const int t = pos[row];
+  const f32x4 c = cv, sv = svv;
   if constexpr (D == 256) {
     f32x4 w;
     w.x = __shfl_xor(v[0].x, 32, 64); w.y = __shfl_xor(v[0].y, 32, 64);
     w.z = __shfl_xor(v[0].z, 32, 64); w.w = __shfl_xor(v[0].w, 32, 64);
-    const int i0 = (lane & 31) * 4;
-    const f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
-    const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
     f32x4 r;
     if (lane < 32) {  // y_i = x_i c - x_{i+h} s
       r.x = v[0].x * c.x - w.x * sv.x; r.y = v[0].y * c.y - w.y * sv.y;
@@ -267,9 +284,6 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
     }
     *reinterpret_cast<f32x4*>(p + lane * 4) = r;
   } else {
-    const int i0 = lane * 4;
-    const f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
-    const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
     const f32x4 x0 = v[0], x1 = v[1];
     f32x4 r0, r1;
     r0.x = x0.x * c.x - x1.x * sv.x; r0.y = x0.y * c.y - x1.y * sv.y;
