@@ -299,12 +299,16 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
 // One wave per (row, head), 16 bytes per lane per 256 dimensions.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ part, int kparts,
-                                                                int64_t rows, int H, float* __restrict__ out) {
-  const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // row * H + head
-  if (id >= rows * H) return;
+                                                                int64_t rows, int64_t row_off, int64_t n, int H,
+                                                                float* __restrict__ out) {
+  // rows: the partial buffers' row count; this launch sums rows row_off ..
+  // row_off + n - 1 of them into out's rows 0 .. n - 1
+  const int64_t lid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // local row * H + head
+  if (lid >= n * H) return;
   const int lane = threadIdx.x & 63;
   const int64_t OW = (int64_t)H * HD;
-  const int64_t row = id / H, h = id % H;
+  const int64_t lrow = lid / H, h = lid % H;
+  const int64_t row = row_off + lrow, id = row * H + h;
   const float2* ml = reinterpret_cast<const float2*>(part + (int64_t)kparts * rows * OW);
   float M = kNegBig;
   for (int q = 0; q < kparts; q++) M = fmaxf(M, ml[q * rows * H + id].x);
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
     }
   }
   const float inv = 1.f / Lsum;
-  float* dst = out + row * OW + h * HD + lane * 4;
+  float* dst = out + lrow * OW + h * HD + lane * 4;
 #pragma unroll
   for (int c = 0; c < HD / 256; c++) {
     f32x4 o;
@@ -335,293 +339,374 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
   }
 }
 
-// ---- split-bf16 model-path kernel (head_dim 256) --------------------------------
-// attention_planes_kernel computes what attention_varlen_kernel<256> does on
-// the bf16 MFMA (v_mfma_f32_16x16x32_bf16, 16x the fp32 MFMA's rate) with
-// fp32 accuracy: every fp32 operand x is the exact sum of three bf16 terms
-// x0 + x1 + x2 (split3: 8 mantissa bits each), and a product a.b is the sum
-// of the six term products ai.bj with i + j <= 2 (the three dropped ones
-// are below 2^-24 relative), accumulated in fp32.
-//
-// Operands. q (fp32, normed and rotated in qkv) is split in registers once
-// per work item. Keys and values arrive split, written by
-// qkv_planes_kernel: keys [row][kv head][term][256]; values in quads
-// of four keys of one sequence (every sequence starts a quad, cu_quads),
-// [quad][kv head][dim][16]: per dimension the two 16-byte windows (V0|V1)
-// and (V0|V2) of the four keys' terms, in that order for dims with bit 3
-// clear and swapped otherwise (the 16 lanes reading one window per
-// instruction then cover all LDS banks).
-//
-// Formulation (lane l: g = l / 16, lq = l % 16). A work item is (sequence,
-// block of 64 queries, head), eight waves in four pairs; as in
-// attention_varlen_kernel, waves 2b and 2b+1 own queries q0 + 16b .. +15
-// and the two 128-dim halves. Per tile of 16 keys:
-//   S^T[key, query] = K . Q^T over the wave's 128 dims: A = a key term from
-//   LDS (lane: key lq, dims 8g..8g+7 of a 32-dim chunk), B = a q term;
-//   4 chunks x 6 term pairs = 24 MFMAs; lane l ends with query lq's scores
-//   against keys 4g+r. The pair adds its partial scores through LDS in one
-//   fixed order, then the online softmax (lane-local + two shuffles).
-//   O^T[dim, query] += V^T . P^T: the 32 k-slots of one MFMA carry two term
-//   pairs of the 16 keys (slot 8g+j: key 4g+(j&3) of the first pair for
-//   j < 4, of the second for j >= 4), so A is one window read (lane: dim lq
-//   of the 16-dim block, quad g) and B the lane's own four probabilities'
-//   terms: (V0|V2)x(P2|P0), (V0|V1)x(P1|P1), (V0|V1)x(P0|P0) cover the six
-//   pairs in 3 MFMAs per 16 dims. Query lq sits in lane l of the O^T
-//   accumulator, so the softmax rescale (skipped while no row maximum of
-//   the wave moved) and the final 1/sum are lane-local.
-// MFMA time per tile and wave: 48 x 16 cycles, against 64 x 32 for the
-// fp32-MFMA kernel.
-//
-// Loads: buffer loads straight to LDS (a buffer resource per operand; the
-// per-lane offsets are fixed per work item and the tile offset is a scalar,
-// so no address arithmetic per tile; reads past the buffer return zeros).
-// One key buffer (three terms of 16 rows x 512 bytes, 16-byte chunks
-// XOR-swizzled by row) and one value buffer (four quads of 8 KB), 65 KB per
-// workgroup of eight waves, shared by 64 queries: the tiles' loads to LDS,
-// not the MFMAs, bound this kernel at 32 queries per tile. Capped at 128
-// VGPRs (a 16-byte spill) for two workgroups per CU, four waves per SIMD:
-// C4 14.05 -> 13.19 ms, C3 32.3 -> 30.6 ms per forward against 142 VGPRs. Per tile: barrier (the tile's keys
-// landed, every wave is done with the previous values), load the tile's
-// values, scores, exchange barrier (every wave is done with the keys, the
-// values landed), load the next tile's keys, softmax, P.V.
-constexpr int PL_VQ = 4096 + 64;  // uint16 per quad of values in LDS: 8 KB + 128 B
-constexpr int PL_W = 8;                 // waves per workgroup: four pairs
-constexpr int PL_NT = 64 * PL_W;
-constexpr int PL_QBLK = QW * PL_W / 2;  // queries per work item
-
-struct PlanesParams {
-  const float* qkv;
-  const uint16_t* kp;
-  const uint16_t* vp;
-  float* out;
-  const int32_t* cu;
-  const int32_t* cu4;
-  const int32_t* items;
-  int32_t kp_bytes, vp_bytes;  // buffer extents (loads past them return zeros)
-  int32_t H, Hkv;
-  int32_t window;
-  float scale;
-  int64_t row0;  // packed row of qkv's and out's first row (kp and vp are indexed by absolute row and quad)
-};
-
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<const bf16x8*>(&v); }
 
-// raw buffer of `bytes` bytes (stride 0: offsets are byte offsets, range-checked)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, int32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+// ---- split-bf16 model-path kernel over key/value tile images (head_dim 256) -----
+// attention_tiles_kernel computes attention_varlen_kernel<256>'s result on
+// the bf16 MFMA (v_mfma_f32_16x16x32_bf16) with fp32 accuracy: every fp32
+// operand is the exact sum of three bf16 terms (split3) and a product a.b
+// the sum of the six term products ai.bj with i + j <= 2 (the three dropped
+// ones are below 2^-24 relative), accumulated in fp32.
+//
+// Rows. The query rows of kv head hk are the pairs (token t, query head
+// hk*G + g) of the G = H/Hkv heads that share it, numbered r = t*G + g. A
+// work item is (sequence, 128 consecutive rows, hk[, run of key tiles]); its
+// eight waves own 16 rows each, so one key/value tile in LDS serves every
+// query head of the group (and a short sequence fills an item's rows G
+// times sooner than with one head per item).
+//
+// Operands. Keys and values arrive as LDS images written once per layer by
+// kv_tiles_kernel: per (tile of 32 keys of one sequence, kv head) a key
+// image [term][key][256] whose 16-byte chunk c of key k sits at c ^ k, and
+// a value image [term][dim][32 slots] whose slot 8g + 4h + r holds key 16h +
+// 4g + r (chunk g of dim d at position g ^ ((d >> 1) & 3)); 48 KB each,
+// copied to LDS unchanged by direct global->LDS loads (1 KB per wave
+// instruction). Two key buffers and one value buffer: 144 KB, one
+// workgroup per CU, two waves per SIMD.
+//
+// Formulation (lane l: lq = l % 16, g = l / 16). The q terms stay in
+// registers: lane l holds row lq's dims 32c + 8g .. +7 (c = 0..7), three
+// terms, 96 VGPRs.
+//   S^T[key, row] = K . Q^T per block of 16 keys: A = a key term (lane l:
+//   key lq, dims 32c + 8g ..), B = a q term; 8 chunks x 6 term pairs per
+//   block. Lane l ends with row lq's scores against keys 4g + r and 16 + 4g
+//   + r: the row's softmax is lane-local plus two exchanges (xor 16, 32).
+//   O^T[dim, row] += V^T . P^T, one 32-key step per block of 16 dims x 6
+//   pairs: the lane's own eight probabilities are B (slot 8g + e: key 4g + e
+//   for e < 4, 16 + 4g + e - 4 after), A one 16-byte value-image read per
+//   term (dim 16db + lq, slots 8g ..). Row lq's O sits in the lanes with
+//   that lq (dims 16db + 4g + r), so the rescale and the final 1/sum are
+//   lane-local.
+// Lazy maximum: a row's exponent offset m moves only when a tile's maximum
+// exceeds it by more than 8 (O and the sum are then scaled by e^(m_old -
+// m_new)), so weights stay below e^8 and O is rarely touched outside the
+// MFMAs. A weight is 0 when its exponent t - m is below -87 (the reference
+// flushes against the row's final maximum; the two differ only in weights
+// below e^-87 of the row's largest).
+//
+// Per tile: barrier (the tile's keys landed; every wave is done with the
+// previous values and keys), load the tile's values and the next tile's keys
+// (past the last tile: the last again, so no load is conditional), scores,
+// softmax, barrier (the values landed), P.V.
+constexpr int TL_KEYS = 32;              // keys per tile
+constexpr int TL_W = 8;                  // waves per workgroup
+constexpr int TL_ROWS = 16 * TL_W;       // query rows per work item
+constexpr int TL_IMG = 3 * 32 * 256;     // bf16 per key or value image
+constexpr float TL_TAU = 8.f;            // lazy-maximum slack
+
+struct TilesParams {
+  const float* qkv;
+  const uint16_t* img;   // [tile][Hkv][key image | value image]
+  float* out;
+  const int32_t* cu;     // cu_seqlens
+  const int32_t* cut;    // first tile of each sequence
+  const int32_t* items;  // triples (sequence, first row, kv head)
+  int32_t H, Hkv;
+  int32_t window;
+  float scale;
+  int64_t row0;  // packed row of qkv's and out's first row
+  // kparts > 1: each item's tiles are cut into kparts runs, one workgroup
+  // each, written unnormalised with (max, sum) per row and head to part
+  // [kparts][rows][H * 256] (rows: packed rows of the whole batch, indexed
+  // by absolute row) for attention_combine_kernel
+  int32_t kparts;
+  int64_t rows;
+  float* part;
+  // q's RMSNorm gain (1 + g) and RoPE tables [positions][128], applied as q is loaded
+  const float* gq;
+  const float *cs, *sn;
+  float eps;
+};
+
+__device__ __forceinline__ void split_pack8(const f32x4& x0, const f32x4& x1, bf16x8& t0, bf16x8& t1, bf16x8& t2) {
+  uint32_t h[8], m[8], l[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const Split3 sp = split3(e < 4 ? x0[e] : x1[e - 4]);
+    h[e] = sp.h;
+    m[e] = sp.m;
+    l[e] = sp.l;
+  }
+  t0 = as_bf16x8(u32x4{pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7])});
+  t1 = as_bf16x8(u32x4{pack_hi16(m[0], m[1]), pack_hi16(m[2], m[3]), pack_hi16(m[4], m[5]), pack_hi16(m[6], m[7])});
+  t2 = as_bf16x8(u32x4{pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7])});
 }
 
-__global__ __launch_bounds__(PL_NT, 4) void attention_planes_kernel(PlanesParams p) {
-  constexpr int HD = 256, HALF = 128;
-  __shared__ __attribute__((aligned(16))) uint16_t Kb[3 * KT * HD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vq[4 * PL_VQ];
-  __shared__ __attribute__((aligned(16))) float Sx[PL_NT / 64][64 * 4];
+__global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesParams p) {
+  constexpr int HD = 256;
+  constexpr int TERM = TL_IMG / 3;  // bf16 per term of an image
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[TL_IMG];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs0[TL_IMG];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs1[TL_IMG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS load addresses in scalars
-  const int qb = wave >> 1, half = wave & 1;
-  const int g = lane >> 4;
-  const int lq = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 15, g = lane >> 4;
 
-  const int seq = p.items[3 * blockIdx.x];
-  const int q0 = p.items[3 * blockIdx.x + 1];
-  const int h = p.items[3 * blockIdx.x + 2];
-  const int hk = h / (p.H / p.Hkv);
-  const int start_abs = p.cu[seq];
-  const int L = p.cu[seq + 1] - start_abs;
-  const int64_t start = start_abs - p.row0;  // the sequence's first row in qkv and out
-  const int quad0 = p.cu4[seq];
+  const int item = blockIdx.x / p.kparts, part = blockIdx.x % p.kparts;
+  const int seq = p.items[3 * item];
+  const int rb = p.items[3 * item + 1];
+  const int hk = p.items[3 * item + 2];
+  const int G = p.H / p.Hkv;
+  const int L = p.cu[seq + 1] - p.cu[seq];
+  const int64_t start = p.cu[seq] - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
-  const int dofs = half * HALF;
+  const int nrows = G * L;
+  const int row = rb + 16 * wave + lq;
+  const bool qvalid = row < nrows;
+  const int tok = (qvalid ? row : rb) / G;
+  const int head = hk * G + (qvalid ? row : rb) % G;
 
-  const int qw0 = q0 + qb * QW;
-  const int qi = qw0 + lq;
-  const bool qvalid = qi < L;
-  // q terms: query lq, dims dofs + 32c + 8g .. +7
-  bf16x8 qt[3][HALF / 32];
+  bf16x8 qt[3][HD / 32];
   {
-    const float* qr = p.qkv + (int64_t)(start + (qvalid ? qi : 0)) * W + (int64_t)h * HD + dofs + 8 * g;
+    // q normed (RMSNorm, gain) and rotated (RoPE at the token's position)
+    // as it is loaded: the row's dims are spread over the four lanes with
+    // this lq (sum of squares: two exchanges), and dims i and i + 128 sit in
+    // the same lane (chunks c and c + 4)
+    const float* qr = p.qkv + (start + tok) * W + (int64_t)head * HD + 8 * g;
+    f32x4 x[HD / 32][2];
+    float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < HALF / 32; c++) {
-      f32x4 x0 = *reinterpret_cast<const f32x4*>(qr + 32 * c);
-      f32x4 x1 = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
-      if (!qvalid) x0 = x1 = f32x4{0.f, 0.f, 0.f, 0.f};
-      uint32_t t0[8], t1[8], t2[8];
+    for (int c = 0; c < HD / 32; c++) {
+      x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
+      x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
+    }
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const Split3 sp = split3(e < 4 ? x0[e] : x1[e - 4]);
-        t0[e] = sp.h;
-        t1[e] = sp.m;
-        t2[e] = sp.l;
+    for (int c = 0; c < HD / 32; c++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) ss = fmaf(x[c][e >> 2][e & 3], x[c][e >> 2][e & 3], ss);
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float inv = rms_inv(ss, HD, p.eps);
+    const float* gr = p.gq + 8 * g;
+    const float* cr = p.cs + (int64_t)tok * (HD / 2) + 8 * g;
+    const float* sr = p.sn + (int64_t)tok * (HD / 2) + 8 * g;
+#pragma unroll
+    for (int c = 0; c < HD / 64; c++) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const f32x4 ga = *reinterpret_cast<const f32x4*>(gr + 32 * c + 4 * h);
+        const f32x4 gb = *reinterpret_cast<const f32x4*>(gr + 32 * (c + HD / 64) + 4 * h);
+        const f32x4 co = *reinterpret_cast<const f32x4*>(cr + 32 * c + 4 * h);
+        const f32x4 si = *reinterpret_cast<const f32x4*>(sr + 32 * c + 4 * h);
+        f32x4& lo = x[c][h];
+        f32x4& hi = x[c + HD / 64][h];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float a = lo[e] * inv * ga[e], b = hi[e] * inv * gb[e];
+          lo[e] = a * co[e] - b * si[e];  // y_i = x_i c - x_{i+h} s
+          hi[e] = a * si[e] + b * co[e];  // y_{i+h} = x_i s + x_{i+h} c
+        }
       }
-      qt[0][c] = as_bf16x8(u32x4{pack_hi16(t0[0], t0[1]), pack_hi16(t0[2], t0[3]), pack_hi16(t0[4], t0[5]),
-                                 pack_hi16(t0[6], t0[7])});
-      qt[1][c] = as_bf16x8(u32x4{pack_hi16(t1[0], t1[1]), pack_hi16(t1[2], t1[3]), pack_hi16(t1[4], t1[5]),
-                                 pack_hi16(t1[6], t1[7])});
-      qt[2][c] = as_bf16x8(u32x4{pack_hi16(t2[0], t2[1]), pack_hi16(t2[2], t2[3]), pack_hi16(t2[4], t2[5]),
-                                 pack_hi16(t2[6], t2[7])});
+    }
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) {
+      if (!qvalid) x[c][0] = x[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      split_pack8(x[c][0], x[c][1], qt[0][c], qt[1][c], qt[2][c]);
     }
   }
-  f32x4 oacc[HALF / 16];  // O^T: dims dofs + 16db + 4g + r of query lq
-#pragma unroll
-  for (int db = 0; db < HALF / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegBig;
-  float l_part = 0.f;
 
-  const int qlast = min(q0 + PL_QBLK, L) - 1;
+  // the item's key tiles: the union of its rows' windows
+  const int tok_lo = rb / G, tok_hi = (min(rb + TL_ROWS, nrows) - 1) / G;
   int kbeg = 0, kend = L;
   if (p.window > 0) {
-    // tiles start on a quad; keys below q0 - window + 1 fail every query's window test
-    kbeg = max(0, q0 - p.window + 1) & ~3;
-    kend = min(L, qlast + p.window);
+    kbeg = max(0, tok_lo - p.window + 1);
+    kend = min(L, tok_hi + p.window);
+  }
+  int tb = kbeg / TL_KEYS, te = (kend + TL_KEYS - 1) / TL_KEYS;
+  if (p.kparts > 1) {  // this part's run of tiles (possibly none)
+    const int per = (te - tb + p.kparts - 1) / p.kparts;
+    const int nb = tb + part * per;
+    te = min(te, nb + per);
+    tb = nb;
   }
 
-  const __amdgpu_buffer_rsrc_t krs = raw_rsrc(p.kp, p.kp_bytes), vrs = raw_rsrc(p.vp, p.vp_bytes);
-  // keys: 24 loads of 1 KB per tile (term, pair of rows), three per wave;
-  // byte offsets relative to the tile's first key row
-  int kvo[24 / PL_W];
+  const uint16_t* img0 = p.img + ((int64_t)p.cut[seq] * p.Hkv + hk) * (2 * TL_IMG);
+  const int64_t tstride = (int64_t)p.Hkv * 2 * TL_IMG;
+  // 48 loads of 1 KB per image, six per wave
+  auto issue = [&](const uint16_t* src, uint16_t* dst) {
 #pragma unroll
-  for (int j = 0; j < 24 / PL_W; j++) {
-    const int i = wave + PL_W * j;
-    const int term = i >> 3, rp = i & 7;
-    const int r = 2 * rp + (lane >> 5);
-    const int chunk = (lane & 31) ^ (r & 15);  // the global chunk that lands at this position
-    kvo[j] = ((r * p.Hkv * 3 + term) * HD + chunk * 8) * 2;
-  }
-  const int krow_bytes = p.Hkv * 3 * HD * 2;
-  const int kbase = (start_abs * p.Hkv + hk) * 3 * HD * 2;
-  // values: 32 loads of 1 KB per tile (quad, eighth of the quad), four per wave
-  int vvo[32 / PL_W];
-#pragma unroll
-  for (int j = 0; j < 32 / PL_W; j++) {
-    const int i = wave + PL_W * j;
-    vvo[j] = ((i >> 3) * p.Hkv * 4096 + (i & 7) * 512 + lane * 8) * 2;
-  }
-  const int vquad_bytes = p.Hkv * 4096 * 2;
-  const int vbase = (quad0 * p.Hkv + hk) * 4096 * 2;
-
-  auto issue_k = [&](int k0) {
-    const int so = kbase + k0 * krow_bytes;
-#pragma unroll
-    for (int j = 0; j < 24 / PL_W; j++) {
-      const int i = wave + PL_W * j;
-      const int term = i >> 3, rp = i & 7;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void*)&Kb[(term * KT + 2 * rp) * HD],
-                                               16, kvo[j], so, 0, 0);
+    for (int j = 0; j < 48 / TL_W; j++) {
+      const int c = wave + TL_W * j;
+      __builtin_amdgcn_global_load_lds(src + c * 512 + lane * 8, (__attribute__((address_space(3))) void*)&dst[c * 512],
+                                       16, 0, 0);
     }
   };
-  auto issue_v = [&](int k0) {
-    const int so = vbase + (k0 >> 2) * vquad_bytes;
+
+  f32x4 oacc[HD / 16];  // O^T: dims 16db + 4g + r of row lq
 #pragma unroll
-    for (int j = 0; j < 32 / PL_W; j++) {
-      const int i = wave + PL_W * j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void*)&Vq[(i >> 3) * PL_VQ + (i & 7) * 512],
-                                               16, vvo[j], so, 0, 0);
+  for (int db = 0; db < HD / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig;
+  float l_part = 0.f;
+  const int vsw = (lq >> 1) & 3;
+  // the row's valid keys: klo <= j < khi (none for a row past the item)
+  int klo = 0, khi = qvalid ? L : 0;
+  if (p.window > 0 && qvalid) {
+    klo = max(0, tok - p.window + 1);
+    khi = min(L, tok + p.window);
+  }
+
+  auto qk = [&](const uint16_t* Kc, f32x4 (&sacc)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int key = 16 * kb + lq;
+      const uint16_t* kr = Kc + key * HD;
+#pragma unroll
+      for (int c = 0; c < HD / 32; c++) {
+        const int pos = ((4 * c + g) ^ key) * 8;
+        const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kr + pos);
+        const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kr + TERM + pos);
+        const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(kr + 2 * TERM + pos);
+        // smallest terms first
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qt[0][c], sacc[kb], 0, 0, 0);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[2][c], sacc[kb], 0, 0, 0);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qt[1][c], sacc[kb], 0, 0, 0);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qt[0][c], sacc[kb], 0, 0, 0);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[1][c], sacc[kb], 0, 0, 0);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[0][c], sacc[kb], 0, 0, 0);
+      }
     }
   };
-  issue_k(kbeg);
-
-  const int w0 = (lq & 8) ? 8 : 0;  // position of the (V0|V1) window of this lane's dims
-  for (int k0 = kbeg; k0 < kend; k0 += KT) {
-    // the tile's keys landed (own loads, then everyone's); every wave is done
-    // with the previous tile's values
-    dl_barrier<0x0070>();
-    issue_v(k0);
-
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+  // O^T += V^T . P^T for one tile (terms b0, b1, b2 of the probabilities)
+  auto pv = [&](const uint16_t* Vc, const bf16x8& b0, const bf16x8& b1, const bf16x8& b2) {
+    const int vpos = (g ^ vsw) * 8;
 #pragma unroll
-    for (int c = 0; c < HALF / 32; c++) {
-      const int pos = ((dofs >> 3) + 4 * c + g) ^ lq;
-      const bf16x8 k0v = *reinterpret_cast<const bf16x8*>(&Kb[(0 * KT + lq) * HD + pos * 8]);
-      const bf16x8 k1v = *reinterpret_cast<const bf16x8*>(&Kb[(1 * KT + lq) * HD + pos * 8]);
-      const bf16x8 k2v = *reinterpret_cast<const bf16x8*>(&Kb[(2 * KT + lq) * HD + pos * 8]);
-      // smallest terms first
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2v, qt[0][c], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1v, qt[1][c], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0v, qt[2][c], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1v, qt[0][c], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0v, qt[1][c], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0v, qt[0][c], sacc, 0, 0, 0);
+    for (int db = 0; db < HD / 16; db++) {
+      const uint16_t* vr = Vc + (16 * db + lq) * 32 + vpos;
+      const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(vr);
+      const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(vr + TERM);
+      const bf16x8 v2 = *reinterpret_cast<const bf16x8*>(vr + 2 * TERM);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v2, b0, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, b2, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, b1, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, b0, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, b1, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, b0, oacc[db], 0, 0, 0);
     }
-    *reinterpret_cast<f32x4*>(&Sx[wave][lane * 4]) = sacc;
-    // partial scores written, every wave is done with the keys, the values landed
-    dl_barrier<0x0070>();
-    // the next tile's keys (past the last tile: a redundant load, so that no
-    // load is conditional)
-    issue_k(k0 + KT);
-    {
-      const f32x4 other = *reinterpret_cast<const f32x4*>(&Sx[wave ^ 1][lane * 4]);
-      const f32x4 lo = half == 0 ? sacc : other, hi = half == 0 ? other : sacc;
+  };
+  // softmax of tile tt's scores against the lazy offset: the new offset and
+  // the scale alpha for what O and the sum held, this tile's probability
+  // terms and their sum
+  auto softmax = [&](int tt, const f32x4 (&sacc)[2], float& alpha, bool& moved, bf16x8& b0, bf16x8& b1,
+                     bf16x8& b2) {
+    float t[8];
+    float tmax = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; r++) sacc[r] = lo[r] + hi[r];
-    }
-
-    float tmax = kNegBig;
-    bool valid[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int j = k0 + g * 4 + r;
-      bool ok = qvalid && j < kend;
-      if (p.window > 0) ok = ok && (qi - j < p.window) && (j - qi < p.window);
-      valid[r] = ok;
-      const float t = sacc[r] * p.scale;
-      sacc[r] = t;
-      if (ok) tmax = fmaxf(tmax, t);
+    for (int e = 0; e < 8; e++) {
+      const int j = tt * TL_KEYS + 16 * (e >> 2) + 4 * g + (e & 3);
+      const bool ok = (unsigned)(j - klo) < (unsigned)(khi - klo);
+      t[e] = ok ? sacc[e >> 2][e & 3] * p.scale : -INFINITY;
+      tmax = fmaxf(tmax, t[e]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const bool moved = m_new != m_run;
-    const float alpha = exp_flush(m_run - m_new);
-    m_run = m_new;
+    const bool need = tmax > m_run + TL_TAU;
+    moved = __any(need);
+    const float mn = need ? tmax : m_run;
+    alpha = exp_flush(m_run - mn);  // 1 where the offset stays, 0 for the first valid tile
+    m_run = mn;
+    uint32_t ph[8], pm[8], pl[8];
     float psum = 0.f;
-    uint32_t p0[4], p1[4], p2[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float pv = valid[r] ? exp_flush(sacc[r] - m_new) : 0.f;
-      psum += pv;
-      const Split3 sp = split3(pv);
-      p0[r] = sp.h;
-      p1[r] = sp.m;
-      p2[r] = sp.l;
+    for (int e = 0; e < 8; e++) {
+      const float pv_ = exp_flush(t[e] - mn);  // masked keys: -inf, flushed to 0
+      psum += pv_;
+      const Split3 sp = split3(pv_);
+      ph[e] = sp.h;
+      pm[e] = sp.m;
+      pl[e] = sp.l;
     }
     l_part = l_part * alpha + psum;
-    if (__any(moved)) {
+    b0 = as_bf16x8(u32x4{pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]), pack_hi16(ph[4], ph[5]),
+                         pack_hi16(ph[6], ph[7])});
+    b1 = as_bf16x8(u32x4{pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]), pack_hi16(pm[4], pm[5]),
+                         pack_hi16(pm[6], pm[7])});
+    b2 = as_bf16x8(u32x4{pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]), pack_hi16(pl[4], pl[5]),
+                         pack_hi16(pl[6], pl[7])});
+  };
+
+  // Software pipeline, iteration tt: [barrier: K(tt), V(tt-1) landed; every
+  // wave done with iteration tt-1] load V(tt); S(tt) = K(tt).Q^T; [barrier:
+  // every wave done with the keys] load K(tt+1) (the last again past the
+  // end); P.V of tile tt-1 and the softmax of tile tt in one block (the
+  // softmax's VALU work beside the MFMAs), then O's rescale, which must see
+  // tile tt-1's terms. Then P.V of the last tile. One key buffer and two
+  // value buffers (144 KB).
+  bf16x8 pb0, pb1, pb2;  // tile tt-1's probability terms
+  // Tile tb + i's values go to Vs0 for even i, Vs1 for odd i: every LDS
+  // access names its buffer statically (the compiler then keeps the other
+  // buffer's loads in flight across the reads).
+  // barrier, this tile's value loads into Vn, scores, barrier, the next
+  // tile's key loads
+  auto front = [&](int tt, uint16_t* Vn, f32x4 (&sacc)[2]) {
+    dl_barrier<0x0F70>();  // vmcnt(0): K(tt), V(tt-1) landed (own loads, then everyone's)
+    issue(img0 + tt * tstride + TL_IMG, Vn);
+    qk(Ks, sacc);
+    dl_barrier<0xC07F>();  // every wave's key reads done (no wait for the loads)
+    issue(img0 + min(tt + 1, te - 1) * tstride, Ks);
+  };
+  auto iter = [&](int tt, uint16_t* Vn, const uint16_t* Vp) {
+    f32x4 sacc[2];
+    front(tt, Vn, sacc);
+    pv(Vp, pb0, pb1, pb2);
+    float alpha;
+    bool moved;
+    softmax(tt, sacc, alpha, moved, pb0, pb1, pb2);
+    if (moved) {
 #pragma unroll
-      for (int db = 0; db < HALF / 16; db++) oacc[db] *= alpha;
+      for (int db = 0; db < HD / 16; db++) oacc[db] *= alpha;
     }
-    const uint32_t a0 = pack_hi16(p0[0], p0[1]), b0 = pack_hi16(p0[2], p0[3]);
-    const uint32_t a1 = pack_hi16(p1[0], p1[1]), b1 = pack_hi16(p1[2], p1[3]);
-    const uint32_t a2 = pack_hi16(p2[0], p2[1]), b2 = pack_hi16(p2[2], p2[3]);
-    const bf16x8 B1 = as_bf16x8(u32x4{a0, b0, a0, b0});  // P0 | P0
-    const bf16x8 B2 = as_bf16x8(u32x4{a1, b1, a1, b1});  // P1 | P1
-    const bf16x8 B3 = as_bf16x8(u32x4{a2, b2, a0, b0});  // P2 | P0
-#pragma unroll
-    for (int db = 0; db < HALF / 16; db++) {
-      const uint16_t* vr = &Vq[g * PL_VQ + (dofs + db * 16 + lq) * 16];
-      const bf16x8 A01 = *reinterpret_cast<const bf16x8*>(vr + w0);      // V0 | V1
-      const bf16x8 A02 = *reinterpret_cast<const bf16x8*>(vr + 8 - w0);  // V0 | V2
-      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A02, B3, oacc[db], 0, 0, 0);
-      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A01, B2, oacc[db], 0, 0, 0);
-      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A01, B1, oacc[db], 0, 0, 0);
+  };
+  if (tb < te) {
+    issue(img0 + tb * tstride, Ks);
+    {
+      f32x4 sacc[2];
+      front(tb, Vs0, sacc);
+      float alpha;
+      bool moved;
+      softmax(tb, sacc, alpha, moved, pb0, pb1, pb2);  // O is still zero
+    }
+    int tt = tb + 1;
+    for (; tt + 1 < te; tt += 2) {
+      iter(tt, Vs1, Vs0);
+      __builtin_amdgcn_sched_barrier(0);  // no code motion between the two halves (register pressure)
+      iter(tt + 1, Vs0, Vs1);
+    }
+    if (tt < te) {
+      iter(tt, Vs1, Vs0);
+      dl_barrier<0x0F70>();  // V(te-1) landed everywhere
+      pv(Vs1, pb0, pb1, pb2);
+    } else {
+      dl_barrier<0x0F70>();
+      pv(Vs0, pb0, pb1, pb2);
     }
   }
 
-  __builtin_amdgcn_s_waitcnt(0x0070);  // no load to LDS outstanding at exit
   float l_tot = l_part + __shfl_xor(l_part, 16, 64);
   l_tot += __shfl_xor(l_tot, 32, 64);
-  if (qvalid) {
-    const float inv = 1.f / l_tot;
-    float* orow = p.out + (int64_t)(start + qi) * (p.H * HD) + (int64_t)h * HD + dofs + 4 * g;
+  if (!qvalid) return;
+  const int OW = p.H * HD;
+  if (p.kparts > 1) {
+    const int64_t arow = p.cu[seq] + tok;  // absolute packed row
+    float* orow = p.part + ((int64_t)part * p.rows + arow) * OW + (int64_t)head * HD + 4 * g;
 #pragma unroll
-    for (int db = 0; db < HALF / 16; db++) *reinterpret_cast<f32x4*>(orow + db * 16) = oacc[db] * inv;
+    for (int db = 0; db < HD / 16; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db];
+    if (g == 0) {
+      float2* pml = reinterpret_cast<float2*>(p.part + (int64_t)p.kparts * p.rows * OW);
+      pml[((int64_t)part * p.rows + arow) * p.H + head] = make_float2(m_run, l_tot);
+    }
+    return;
   }
+  const float inv = 1.f / l_tot;
+  float* orow = p.out + (start + tok) * OW + (int64_t)head * HD + 4 * g;
+#pragma unroll
+  for (int db = 0; db < HD / 16; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db] * inv;
 }
-
 
 // ---- generic attention (per-op drop-in) ------------------------------------------
 constexpr int GMAXD = 512;
@@ -712,34 +797,40 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   if (a.kparts > 1) {
     const dim3 g2((unsigned)((a.rows * a.H + 3) / 4));
     if (a.D == 256)
-      hipLaunchKernelGGL(attention_combine_kernel<256>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, a.H, a.out);
+      hipLaunchKernelGGL(attention_combine_kernel<256>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, (int64_t)0,
+                         a.rows, a.H, a.out);
     else
-      hipLaunchKernelGGL(attention_combine_kernel<512>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, a.H, a.out);
+      hipLaunchKernelGGL(attention_combine_kernel<512>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, (int64_t)0,
+                         a.rows, a.H, a.out);
   }
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
 
-int launch_attention_planes(fa_ctx* ctx, const AttnPlanesArgs& a, const int32_t* d_items, int32_t n_items,
-                            hipStream_t s) {
+int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d_items, int32_t n_items,
+                           hipStream_t s) {
   if (a.Hkv <= 0 || a.H % a.Hkv != 0)
     return set_error(ctx, FA_ERR_ARG, "attention: %d query heads not a multiple of %d kv heads", a.H, a.Hkv);
   if (n_items == 0) return FA_OK;
-  if (a.kp_bytes <= 0 || a.vp_bytes <= 0 || a.kp_bytes > INT32_MAX - (1 << 22) || a.vp_bytes > INT32_MAX - (1 << 22))
-    return set_error(ctx, FA_ERR_ARG, "attention: key/value planes of %lld / %lld bytes outside 1..2^31 - 4 MB",
-                     (long long)a.kp_bytes, (long long)a.vp_bytes);
-  PlanesParams p;
-  p.qkv = a.qkv; p.kp = a.kp; p.vp = a.vp; p.out = a.out; p.cu = a.cu_seqlens; p.cu4 = a.cu_quads;
-  p.kp_bytes = (int32_t)a.kp_bytes; p.vp_bytes = (int32_t)a.vp_bytes;
-  p.items = d_items; p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
-  hipLaunchKernelGGL(attention_planes_kernel, dim3((unsigned)n_items), dim3(PL_NT), 0, s, p);
+  if (a.kparts < 1 || a.kparts > kMaxKeyParts || (a.kparts > 1 && (!a.part || a.rows <= 0 || a.nrows <= 0)))
+    return set_error(ctx, FA_ERR_ARG, "attention: %d key parts (1..%d, > 1 needs a partial buffer)", a.kparts,
+                     kMaxKeyParts);
+  TilesParams p;
+  p.qkv = a.qkv; p.img = a.img; p.out = a.out; p.cu = a.cu_seqlens; p.cut = a.cu_tiles; p.items = d_items;
+  p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
+  p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
+  p.gq = a.gq; p.cs = a.cos_t; p.sn = a.sin_t; p.eps = a.eps;
+  hipLaunchKernelGGL(attention_tiles_kernel, dim3((unsigned)((int64_t)n_items * a.kparts)), dim3(64 * TL_W), 0, s, p);
+  if (a.kparts > 1)
+    hipLaunchKernelGGL(attention_combine_kernel<256>, dim3((unsigned)((a.nrows * a.H + 3) / 4)), dim3(256), 0, s,
+                       a.part, a.kparts, a.rows, a.row0, a.nrows, a.H, a.out);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
 
-
 int attention_varlen_qblock() { return QBLK; }
-int attention_planes_qblock() { return PL_QBLK; }
+int attention_tiles_rows() { return TL_ROWS; }
+int attention_tiles_keys() { return TL_KEYS; }
 
 int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s) {
   if (a.D > GMAXD) return set_error(ctx, FA_ERR_UNSUPPORTED, "Attention: head dimension %d > %d", a.D, GMAXD);

@@ -231,40 +231,47 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
                                   hipStream_t s);
 // Queries per workgroup of the varlen kernel (the item granularity).
 int attention_varlen_qblock();
-// Queries per workgroup of the split-bf16 kernel (launch_attention_planes).
-int attention_planes_qblock();
+// head_dim 256, split-bf16 attention over key/value tile images: writes,
+// for tiles [t_lo, t_lo + tiles), the key image (keys normed, gained,
+// rotated) and value image of each (tile, kv head) into img
+// [tile][Hkv][2][3*32*256] bf16. Tile tt of sequence b (d_cu_tiles[b] <= tt
+// < d_cu_tiles[b+1], every sequence starting a tile) holds its tokens 32 (tt
+// - d_cu_tiles[b]) .. +31; d_tile_seq[tt] = b. qkv and d_pos start at packed
+// row row0.
+int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
+                    const int32_t* d_pos, const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
+                    const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
+                    hipStream_t s);
 
-struct AttnPlanesArgs {
-  const float* qkv;
-  const uint16_t* kp;
-  const uint16_t* vp;
+struct AttnTilesArgs {
+  const float* qkv;       // raw q read here (rows of the launch start at packed row row0)
+  const uint16_t* img;    // launch_kv_tiles's images
   float* out;
   const int32_t* cu_seqlens;
-  const int32_t* cu_quads;
-  int64_t kp_bytes, vp_bytes;
+  const int32_t* cu_tiles;
   int32_t H, Hkv;
   int32_t window;
   float scale;
-  int64_t row0 = 0;  // packed row of qkv's and out's first row
+  int64_t row0 = 0;
+  // kparts > 1: part holds attention_part_floats(kparts, rows, H, 256)
+  // floats indexed by absolute packed row (rows: the batch's row count);
+  // the launch's own rows are [row0, row0 + nrows)
+  int32_t kparts = 1;
+  int64_t rows = 0, nrows = 0;
+  float* part = nullptr;
+  // q's RMSNorm gain (1 + g), eps and RoPE tables [positions][128]: q is
+  // normed and rotated as the kernel loads it
+  const float* gq = nullptr;
+  float eps = 0.f;
+  const float *cos_t = nullptr, *sin_t = nullptr;
 };
-int launch_attention_planes(fa_ctx* ctx, const AttnPlanesArgs& a, const int32_t* d_items, int32_t n_items,
-                            hipStream_t s);
-
-// head_dim 256, for the split-bf16 attention, one launch: q heads as
-// launch_qknorm_rope (in place, fp32); key heads normed, gained and
-// rotated, written as bf16 planes kp[row][kv head][term][256] (row = the
-// packed row of qkv, term 0..2: hi, mid, lo of the exact split) instead of
-// back into qkv; value heads (RMS-normed with unit gain when norm_v) in
-// quads of four tokens of one sequence: quad cu_quads[b] + t/4 holds tokens
-// t .. t+3 of sequence b as vp[quad][kv head][dim][16], per dim the windows
-// (V0|V1) and (V0|V2) of the four tokens' terms (4 bf16 per term), swapped
-// for dims with bit 3 set; zeros for tokens past the sequence. Writes quads
-// [q_lo, q_lo + quads); d_quad_seq[q] is quad q's sequence; qkv, d_pos and
-// kp start at packed row row0.
-int launch_qkv_planes(fa_ctx* ctx, float* qkv, int64_t rows, int64_t row0, int32_t H, int32_t Hkv, const float* gq,
-                      const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
-                      bool norm_v, const int32_t* d_cu_seqlens, const int32_t* d_cu_quads, const int32_t* d_quad_seq,
-                      int32_t q_lo, int32_t quads, uint16_t* kp, uint16_t* vp, hipStream_t s);
+// d_items holds n_items triples (sequence, first row, kv head): one item per
+// attention_tiles_rows() rows (token, query head of the kv head's group),
+// row r = token * (H / Hkv) + head - kv head * (H / Hkv).
+int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d_items, int32_t n_items,
+                           hipStream_t s);
+int attention_tiles_rows();
+int attention_tiles_keys();
 
 // Zeroes bytes (a multiple of 16, 16-byte aligned) with a fill kernel.
 int launch_zero(fa_ctx* ctx, void* p, size_t bytes, hipStream_t s);

@@ -97,7 +97,6 @@ struct fa_model {
   fa_gemma_config cfg{};
   int variant = 0;
   int max_width = 0, max_hd = 0;  // widest q|k|v row, widest attention output H*D
-  int hkv256 = 0;                 // most key/value heads of a head_dim-256 layer (split-bf16 attention)
   int P = 0, E = 0;               // variant 2: per-layer input width, embedding projection width
   fa::Mat wple_model;             // variant 2: [layers*P, d]
   float* g_ple_norm = nullptr;    // variant 2: [P]
@@ -192,17 +191,6 @@ int64_t microbatch_min_rows() {
 // measured best on MI355X at 5 517, 11 550 and 32 768 tokens (C2: 6.41 ms
 // per forward on one stream, 5.49 with two groups, 5.43 with three, 5.92
 // with four) and within 3 % of best at 17 923.
-// FA_ATTN_PLANES=0 / 1 forces the fp32-MFMA / split-bf16 attention for
-// the head_dim-256 layers (comparison); -1 when unset.
-int attention_planes_forced() {
-  static const int v = [] {
-    const char* e = std::getenv("FA_ATTN_PLANES");
-    if (!e) return -1;
-    return std::atoi(e) != 0 ? 1 : 0;
-  }();
-  return v;
-}
-
 // FA_ATTN_KEY_PARTS=<1..8> forces the key runs of the short-batch attention
 // (tuning); 0 when unset.
 int attention_key_parts_forced() {
@@ -375,7 +363,6 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
     dt = L.D;
     m->max_width = std::max(m->max_width, L.width);
     m->max_hd = std::max(m->max_hd, H * L.D);
-    if (L.D == 256) m->hkv256 = std::max(m->hkv256, L.Hkv);
   }
   if (rc) {
     delete m;
@@ -742,22 +729,33 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   if (dim <= 0) dim = full;
   if (dim > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
   // ---- plan (host): cu_seqlens and attention work items ----
-  const int qblk = fa::attention_varlen_qblock();
-  int64_t M = 0, n_items = 0;
+  // Models whose layers all have head_dim 256 (EmbeddingGemma) take the
+  // split-bf16 tile attention: items of attention_tiles_rows() (token, query
+  // head) rows per kv head, keys and values as per-tile images (every
+  // sequence starts a tile of attention_tiles_keys() tokens: cu_tiles [B+1]
+  // and each tile's sequence). Others take the fp32-MFMA attention, items of
+  // attention_varlen_qblock() queries per head.
+  int64_t M_all = 0;
+  for (int b = 0; b < B; b++) M_all += std::max(0, lengths[b]);
+  const bool tiles = !v2 && m->max_hd == H * 256 && M_all > fa::kAttnSplitRows;
+  const int tkeys = fa::attention_tiles_keys();
+  const int G = H / c.num_key_value_heads;
+  const int istep = tiles ? fa::attention_tiles_rows() : fa::attention_varlen_qblock();
+  const int iheads = tiles ? c.num_key_value_heads : H;  // items per row block
+  int64_t M = 0, n_items = 0, n_tiles = 0;
   for (int b = 0; b < B; b++) {
     if (lengths[b] < 1 || lengths[b] > T)
       return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
     M += lengths[b];
-    n_items += (int64_t)((lengths[b] + qblk - 1) / qblk) * H;
+    const int64_t rows_b = tiles ? (int64_t)G * lengths[b] : lengths[b];
+    n_items += (rows_b + istep - 1) / istep * iheads;
+    n_tiles += (lengths[b] + tkeys - 1) / tkeys;
   }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   double sum_l2 = 0;
   for (int i = 0; i < B; i++) sum_l2 += (double)lengths[i] * lengths[i];
-  // each sequence's values in quads of four tokens (ceil(L/4)) for the
-  // split-bf16 attention: cu_quads [B+1] and each quad's sequence
-  int64_t n_quads = 0;
-  for (int b = 0; b < B; b++) n_quads += (lengths[b] + 3) / 4;
-  const size_t plan_ints = 2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_quads;
+  if (!tiles) n_tiles = 0;
+  const size_t plan_ints = 2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles;
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
     m->plan_pending = false;
@@ -771,14 +769,14 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   }
   int32_t* cu_h = m->plan_host;
   int32_t* items_h = m->plan_host + (B + 1);
-  int32_t* cu4_h = items_h + 3 * n_items;
-  int32_t* qseq_h = cu4_h + (B + 1);
+  int32_t* cut_h = items_h + 3 * n_items;
+  int32_t* tseq_h = cut_h + (B + 1);
   cu_h[0] = 0;
-  cu4_h[0] = 0;
+  cut_h[0] = 0;
   for (int b = 0; b < B; b++) {
     cu_h[b + 1] = cu_h[b] + lengths[b];
-    cu4_h[b + 1] = cu4_h[b] + (lengths[b] + 3) / 4;
-    for (int q = cu4_h[b]; q < cu4_h[b + 1]; q++) qseq_h[q] = b;
+    cut_h[b + 1] = cut_h[b] + (tiles ? (lengths[b] + tkeys - 1) / tkeys : 0);
+    for (int q = cut_h[b]; q < cut_h[b + 1]; q++) tseq_h[q] = b;
   }
   // Micro-batches: with enough tokens the sequences are cut into groups of
   // about equal token count (contiguous rows) whose layers run on separate
@@ -803,33 +801,32 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     groups = want;
   }
   // Attention over few items (a short batch on one stream) cuts each
-  // item's keys into up to kMaxKeyParts runs of whole tiles, one workgroup
-  // each, so that more CUs share the key loop: C1's 12 items (128 tokens, 3
-  // heads) become 48 workgroups of two tiles.
+  // item's keys into up to four runs of whole tiles, one workgroup each, so
+  // that more CUs share the key loop: C1's 12 fp32 items (128 tokens, 3
+  // heads) become 48 workgroups of two 16-key tiles, its 3 tile items 12
+  // workgroups of one 32-key tile.
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   const int64_t n_items_all = n_items;
   int kparts = 1;
-  if (groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
+  if (!tiles && groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
     kparts = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_all, 1));
     kparts = std::max(1, std::min(kparts, (T + 31) / 32));  // at least two 16-key tiles per run
     if (const int f = fa::attention_key_parts_forced()) kparts = f;
   }
-  // With longer sequences (a mean key count per token, sum L^2 / sum L, of
-  // at least 320) the head_dim-256 layers take the split-bf16 attention,
-  // whose q/k/v pass writes keys and values as bf16 planes (key planes
-  // [M][hkv][3][256], value quads [quads + 4][hkv][256][16]; a tile's quads
-  // may run up to three past the last sequence's). Same-box A/B against the
-  // fp32-MFMA attention: C4 (about 1 440) 15.72 -> 14.10 ms, C3 (512) 33.6
-  // -> 31.9 ms, C2 (187) equal, C5 (85) 14.7 -> 15.0 ms: the pass costs a
-  // fixed amount per token while the attention's saving grows with the keys.
-  const int pforce = fa::attention_planes_forced();
-  const bool planes = !v2 && m->hkv256 > 0 && kparts == 1 &&
-                      (pforce == 1 || (pforce < 0 && sum_l2 >= 320.0 * (double)M));
-  // Work items (sequence, query block, head) of each group, longest
-  // sequences first: an item's work grows with its sequence's length, and
-  // dispatching the long ones first shortens the tail.
-  // (64-query items for the split-bf16 attention)
-  const int qstep = planes ? fa::attention_planes_qblock() : qblk;
+  if (tiles) {
+    // fewer tile items than CUs (one or two long sequences): each item's key
+    // tiles are cut into runs of at least four, one workgroup each
+    const int max_tiles = (T + tkeys - 1) / tkeys;
+    if (n_items_all < cus) {
+      kparts = (int)std::min<int64_t>(fa::kMaxKeyParts, cus / std::max<int64_t>(n_items_all, 1));
+      kparts = std::max(1, std::min(kparts, max_tiles / 4));
+    }
+    if (const int f = fa::attention_key_parts_forced()) kparts = std::min(f, max_tiles);
+  }
+  // Work items of each group, longest sequences first: an item's work grows
+  // with its sequence's length, and dispatching the long ones first
+  // shortens the tail. Tile items (sequence, first row, kv head); fp32
+  // items (sequence, first query, head).
   std::vector<int>& order = m->seq_order;
   int64_t it = 0, group_items[fa::kMaxMicrobatches] = {};
   for (int gi = 0; gi < groups; gi++) {
@@ -839,8 +836,9 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
     const int64_t first = it;
     for (int b : order) {
-      for (int q0 = 0; q0 < lengths[b]; q0 += qstep) {
-        for (int h = 0; h < H; h++) {
+      const int rows_b = tiles ? G * lengths[b] : lengths[b];
+      for (int q0 = 0; q0 < rows_b; q0 += istep) {
+        for (int h = 0; h < iheads; h++) {
           items_h[3 * it] = b;
           items_h[3 * it + 1] = q0;
           items_h[3 * it + 2] = h;
@@ -854,8 +852,8 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
   int32_t* cu_d = m->plan_dev.as<int32_t>();
   int32_t* items_d = cu_d + (B + 1);
-  int32_t* cu4_d = items_d + 3 * n_items;
-  int32_t* qseq_d = cu4_d + (B + 1);
+  int32_t* cut_d = items_d + 3 * n_items;
+  int32_t* tseq_d = cut_d + (B + 1);
   int32_t* row_src_d = cu_d + plan_ints;   // [M] b*T + t
   int32_t* pos_d = row_src_d + M;          // [M] t
   FA_HIP_CHECK(ctx, hipMemcpyAsync(cu_d, m->plan_host, plan_ints * 4, hipMemcpyHostToDevice, ctx->stream));
@@ -871,14 +869,13 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   int maxw = std::max(d, std::max(full, v2 ? m->E : d));
   for (int o : m->dense_out) maxw = std::max(maxw, o);
   const int64_t part_floats = kparts > 1 ? fa::attention_part_floats(kparts, M, H, m->max_hd / H) : 0;
-  const size_t kp_elems = planes ? (size_t)M * m->hkv256 * 3 * 256 : 0;
-  const size_t vp_bytes = planes ? ((size_t)cu4_h[B] + 4) * m->hkv256 * 256 * 16 * 2 : 0;
+  // key/value tile images: [tile][Hkv][key | value][3 * 32 * 256] bf16
+  const size_t img_bytes = (size_t)n_tiles * c.num_key_value_heads * 2 * (3 * 32 * 256) * 2;
   const size_t f32_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 256;
-  const size_t kp_off = (f32_bytes + 255) & ~(size_t)255, vp_off = (kp_off + kp_elems * 2 + 255) & ~(size_t)255;
-  const size_t ws_bytes = vp_off + vp_bytes + 4096;
+  const size_t img_off = (f32_bytes + 255) & ~(size_t)255;
+  const size_t ws_bytes = img_off + img_bytes + 4096;
   if ((rc = m->ws.ensure(ctx, ws_bytes))) return rc;
-  uint16_t* kp = reinterpret_cast<uint16_t*>(m->ws.as<char>() + kp_off);
-  uint16_t* vp = reinterpret_cast<uint16_t*>(m->ws.as<char>() + vp_off);
+  uint16_t* img = reinterpret_cast<uint16_t*>(m->ws.as<char>() + img_off);
   float* x = m->ws.as<float>();
   float* xn = x + M * d;
   float* qkv = xn + M * d;
@@ -894,9 +891,6 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   hipStream_t s = ctx->stream;
   // ---- row plan on device ----
   if ((rc = fa::launch_row_plan(ctx, cu_d, B, T, M, row_src_d, pos_d, s))) return rc;
-  // value-quad slots past each sequence's end stay zero (finite operands
-  // for the masked keys of a sequence's last quad)
-  if (planes && (rc = fa::launch_zero(ctx, vp, vp_bytes, s))) return rc;
   const float eps = c.rms_norm_eps;
   const float emb_scale = (float)std::sqrt((double)d);  // embed.go:176
   // model.go:100; variant 2 does not scale the scores (model.go:105-110)
@@ -964,13 +958,14 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
     }
-    const bool pl = planes && D == 256;
-    if (pl) {
-      // read q, k, v (4 bytes per element); write q (4), k (6) and v (8) bytes
-      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * ((H + 2 * Hkv) * 4.0 + H * 4.0 + Hkv * 14.0) * D);
-      if ((rc = fa::launch_qkv_planes(ctx, qkvr, rows, r0, H, Hkv, L.g_q, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t,
-                                      v2, cu_d, cu4_d, qseq_d, cu4_h[b0], cu4_h[b1] - cu4_h[b0],
-                                      kp + r0 * Hkv * 3 * 256, vp, st)))
+    if (tiles) {
+      // read k and v (4 bytes per element); write their images (6 bytes per
+      // element each, tiles padded to 32 tokens); q is normed and rotated
+      // by the attention as it loads it
+      const int64_t ntl = cut_h[b1] - cut_h[b0];
+      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * 2 * Hkv * 4.0 * D + (double)ntl * Hkv * 2 * 3 * 32 * 256 * 2);
+      if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t, cu_d, cut_d, tseq_d,
+                                    cut_h[b0], (int32_t)ntl, img, st)))
         return rc;
       pr.done();
     } else {
@@ -1001,12 +996,15 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
         }
       }
       fa::Probe pr(m, FA_K_ATTENTION, pairs * 4.0 * H * D, 0);
-      if (pl) {
-        fa::AttnPlanesArgs ap;
-        ap.qkv = qkvr; ap.kp = kp; ap.vp = vp; ap.out = attr; ap.row0 = r0; ap.cu_seqlens = cu_d; ap.cu_quads = cu4_d;
-        ap.kp_bytes = (int64_t)kp_elems * 2; ap.vp_bytes = (int64_t)vp_bytes;
-        ap.H = H; ap.Hkv = Hkv; ap.window = a.window; ap.scale = a.scale;
-        if ((rc = fa::launch_attention_planes(ctx, ap, items, (int32_t)n_it, st))) return rc;
+      if (tiles) {
+        fa::AttnTilesArgs at;
+        at.qkv = qkvr; at.img = img; at.out = attr; at.row0 = r0; at.cu_seqlens = cu_d; at.cu_tiles = cut_d;
+        at.H = H; at.Hkv = Hkv; at.window = a.window; at.scale = a.scale;
+        at.gq = L.g_q; at.eps = eps; at.cos_t = L.cos_t; at.sin_t = L.sin_t;
+        if (kparts > 1) {
+          at.kparts = kparts; at.rows = M; at.nrows = rows; at.part = attn_part;
+        }
+        if ((rc = fa::launch_attention_tiles(ctx, at, items, (int32_t)n_it, st))) return rc;
       } else {
         if ((rc = fa::launch_attention_varlen_items(ctx, a, items, (int32_t)n_it, st))) return rc;
       }

@@ -328,145 +328,149 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
   }
 }
 
-// out[b, :dim] = y[b, :dim] / sqrt(sum(y[b, :dim]^2) + 1e-12); one wave per row.
-// head_dim 256 for the split-bf16 attention: the q heads as
-// qknorm_rope_kernel<256> (fp32, in place); the key heads normed, gained and
-// rotated the same way and written as the three bf16 terms of the exact
-// split (split3), kp[row][kv head][term][256], 8 bytes per lane and term,
-// not back into qkv. Value heads: value_quad.
-__device__ __forceinline__ void qk_planes_head(float* __restrict__ qkv, int64_t row, int head, int lane, int H,
-                                               int Hkv, const float* __restrict__ gq, const float* __restrict__ gk,
-                                               float eps, const int32_t* __restrict__ pos,
-                                               const float* __restrict__ cs, const float* __restrict__ sn,
-                                               uint16_t* __restrict__ kp) {
-  constexpr int D = 256, half = D / 2;
-  const int width = (H + 2 * Hkv) * D;
-  float* p = qkv + row * width + (int64_t)head * D;
-  f32x4 v[1];
-  v[0] = *reinterpret_cast<const f32x4*>(p + lane * 4);
-  const float inv = rms_inv(sumsq<1>(v), D, eps);
-  const float* g = head < H ? gq : gk;
-  {
-    const f32x4 gg = *reinterpret_cast<const f32x4*>(g + lane * 4);
-    v[0].x = v[0].x * inv * gg.x; v[0].y = v[0].y * inv * gg.y;
-    v[0].z = v[0].z * inv * gg.z; v[0].w = v[0].w * inv * gg.w;
-  }
-  const int t = pos[row];
-  f32x4 w;
-  w.x = __shfl_xor(v[0].x, 32, 64); w.y = __shfl_xor(v[0].y, 32, 64);
-  w.z = __shfl_xor(v[0].z, 32, 64); w.w = __shfl_xor(v[0].w, 32, 64);
-  const int i0 = (lane & 31) * 4;
-  const f32x4 c = *reinterpret_cast<const f32x4*>(cs + (int64_t)t * half + i0);
-  const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + (int64_t)t * half + i0);
-  f32x4 r;
-  if (lane < 32) {  // y_i = x_i c - x_{i+h} s
-    r.x = v[0].x * c.x - w.x * sv.x; r.y = v[0].y * c.y - w.y * sv.y;
-    r.z = v[0].z * c.z - w.z * sv.z; r.w = v[0].w * c.w - w.w * sv.w;
-  } else {  // y_{i+h} = x_i s + x_{i+h} c
-    r.x = w.x * sv.x + v[0].x * c.x; r.y = w.y * sv.y + v[0].y * c.y;
-    r.z = w.z * sv.z + v[0].z * c.z; r.w = w.w * sv.w + v[0].w * c.w;
-  }
-  if (head < H) {
-    *reinterpret_cast<f32x4*>(p + lane * 4) = r;
-    return;
-  }
-  uint32_t t0[4], t1[4], t2[4];
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const Split3 sp = split3(r[e]);
-    t0[e] = sp.h;
-    t1[e] = sp.m;
-    t2[e] = sp.l;
-  }
-  uint16_t* o = kp + (row * Hkv + (head - H)) * 3 * D + lane * 4;
-  *reinterpret_cast<uint2*>(o) = make_uint2(pack_hi16(t0[0], t0[1]), pack_hi16(t0[2], t0[3]));
-  *reinterpret_cast<uint2*>(o + D) = make_uint2(pack_hi16(t1[0], t1[1]), pack_hi16(t1[2], t1[3]));
-  *reinterpret_cast<uint2*>(o + 2 * D) = make_uint2(pack_hi16(t2[0], t2[1]), pack_hi16(t2[2], t2[3]));
-}
-
-// Value heads of head_dim-256 layers for the split-bf16 attention, one wave
-// per (quad, kv head): quad q holds tokens t = 4(q - cu4[b]) .. +3 of sequence b = quad_seq[q]
-// (cu4[b] <= q < cu4[b+1]; packed rows cu[b] + t, rows of qkv counted from row0). The
-// values are RMS-normed with unit gain when norm_v and written as
-// vp[q][kv head][dim][16]: per dim the 16-byte windows (V0|V1) and (V0|V2)
-// of the four tokens' exact split terms, swapped for dims with bit 3 set;
-// zeros for tokens past the sequence. 128 contiguous bytes per lane.
-__device__ __forceinline__ void value_quad(const float* __restrict__ qkv, int64_t row0, int q, int hv, int lane,
-                                           int H, int Hkv, float eps, int norm_v, const int32_t* __restrict__ cu,
-                                           const int32_t* __restrict__ cu4, const int32_t* __restrict__ quad_seq,
-                                           uint16_t* __restrict__ vp) {
-  constexpr int D = 256;
-  const int lo = quad_seq[q];  // cu4[lo] <= q < cu4[lo + 1]
-  const int t = 4 * (q - cu4[lo]);
-  const int n = min(4, cu[lo + 1] - cu[lo] - t);
-  const int width = (H + 2 * Hkv) * D;
-  const float* p = qkv + (int64_t)(cu[lo] + t - row0) * width + (int64_t)(H + Hkv + hv) * D + lane * 4;
-  f32x4 vv[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    f32x4 x[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-    if (i < n) {
-      x[0] = *reinterpret_cast<const f32x4*>(p + (int64_t)i * width);
-      if (norm_v) {
-        const float inv = rms_inv(sumsq<1>(x), D, eps);
-        x[0].x *= inv; x[0].y *= inv; x[0].z *= inv; x[0].w *= inv;
-      }
-    }
-    vv[i] = x[0];
-  }
-  uint16_t* o = vp + ((int64_t)q * Hkv + hv) * (D * 16) + lane * 64;
-  const bool swap = (lane >> 1) & 1;  // bit 3 of the dims lane*4 .. lane*4+3
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    uint32_t th[4], tm[4], tl[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const Split3 sp = split3(vv[i][e]);
-      th[i] = sp.h;
-      tm[i] = sp.m;
-      tl[i] = sp.l;
-    }
-    const uint32_t v0a = pack_hi16(th[0], th[1]), v0b = pack_hi16(th[2], th[3]);
-    const uint4 w01 = make_uint4(v0a, v0b, pack_hi16(tm[0], tm[1]), pack_hi16(tm[2], tm[3]));
-    const uint4 w02 = make_uint4(v0a, v0b, pack_hi16(tl[0], tl[1]), pack_hi16(tl[2], tl[3]));
-    *reinterpret_cast<uint4*>(o + e * 16) = swap ? w02 : w01;
-    *reinterpret_cast<uint4*>(o + e * 16 + 8) = swap ? w01 : w02;
-  }
-}
-
-// One launch for a layer's q, k and v heads (head_dim 256, split-bf16
-// attention): the first blocks take (four quads, value head) of the value
-// quads [q_lo, q_lo + quads) (value_quad; first, as their loads depend on
-// the plan's), the rest (row, four heads) of the q and key heads
-// (qk_planes_head).
-struct QkvPlanesParams {
-  float* qkv;
-  int64_t rows, row0;
-  int H, Hkv, ny;
-  const float *gq, *gk;
+// Key and value images of head_dim-256 layers for attention_tiles_kernel,
+// one block per (tile of 32 tokens of one sequence, kv head): tile tt of
+// sequence b (cut[b] <= tt < cut[b+1]) holds tokens 32 (tt - cut[b]) .. +31.
+// Image pair [tt][kv head][key image | value image], 3 * 32 * 256 bf16 each:
+//   key image [term][key][256]: the normed, gained and rotated key's exact
+//   split terms, the 16-byte chunk c (dims 8c .. 8c+7) of key k at
+//   position c ^ k (the 16 keys of one operand read hit distinct banks);
+//   value image [term][dim][32 slots]: slot 8g + 4h + r holds key 16h + 4g +
+//   r (the order in which the attention's probabilities meet the values),
+//   the 16-byte chunk g of dim d at position g ^ ((d >> 1) & 3).
+// Tokens past the sequence are zeros.
+struct KvTilesParams {
+  const float* qkv;
+  int64_t row0;
+  int H, Hkv;
+  const float* gk;
   float eps;
   const int32_t* pos;
   const float *cs, *sn;
-  int norm_v;
-  const int32_t *cu, *cu4, *quad_seq;
-  int q_lo, quads, v_blocks;
-  uint16_t *kp, *vp;
+  const int32_t *cu, *cut, *tile_seq;
+  int t_lo, tiles;
+  uint16_t* img;
 };
 
-__global__ __launch_bounds__(256) void qkv_planes_kernel(QkvPlanesParams a) {
+constexpr int kTileImg = 3 * 32 * 256;  // bf16 per key or value image
+constexpr int kVtStride = 258;          // floats per LDS row of the value transpose (conflict-free column reads)
+
+// The key image of (tile, hk): wave w takes tokens w, w + 4, ..., 4 dims per
+// lane; rows past the sequence are clamped to its last token (every load
+// issued up front, none conditional) and written as zeros.
+__device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int wave, int lane) {
+  constexpr int D = 256, half = D / 2;
+  const int sq = a.tile_seq[tile];
+  const int t0 = 32 * (tile - a.cut[sq]);
+  const int n = min(32, a.cu[sq + 1] - a.cu[sq] - t0);
+  const int64_t r_first = a.cu[sq] - a.row0 + t0;  // qkv row of the tile's first token
+  const int width = (a.H + 2 * a.Hkv) * D;
+  uint16_t* kimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg);
+  const f32x4 gg = *reinterpret_cast<const f32x4*>(a.gk + lane * 4);
+  const int i0 = (lane & 31) * 4;
+  f32x4 v[8], c[8], sv[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int64_t row = r_first + min(wave + 4 * j, n - 1);
+    v[j] = *reinterpret_cast<const f32x4*>(a.qkv + row * width + (int64_t)(a.H + hk) * D + lane * 4);
+    const int t = a.pos[row];
+    c[j] = *reinterpret_cast<const f32x4*>(a.cs + (int64_t)t * half + i0);
+    sv[j] = *reinterpret_cast<const f32x4*>(a.sn + (int64_t)t * half + i0);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int k = wave + 4 * j;
+    f32x4 x[1] = {v[j]};
+    const float inv = rms_inv(sumsq<1>(x), D, a.eps);
+    x[0].x = x[0].x * inv * gg.x; x[0].y = x[0].y * inv * gg.y;
+    x[0].z = x[0].z * inv * gg.z; x[0].w = x[0].w * inv * gg.w;
+    f32x4 o;
+    o.x = __shfl_xor(x[0].x, 32, 64); o.y = __shfl_xor(x[0].y, 32, 64);
+    o.z = __shfl_xor(x[0].z, 32, 64); o.w = __shfl_xor(x[0].w, 32, 64);
+    f32x4 r;
+    if (lane < 32) {  // y_i = x_i c - x_{i+h} s
+      r.x = x[0].x * c[j].x - o.x * sv[j].x; r.y = x[0].y * c[j].y - o.y * sv[j].y;
+      r.z = x[0].z * c[j].z - o.z * sv[j].z; r.w = x[0].w * c[j].w - o.w * sv[j].w;
+    } else {  // y_{i+h} = x_i s + x_{i+h} c
+      r.x = o.x * sv[j].x + x[0].x * c[j].x; r.y = o.y * sv[j].y + x[0].y * c[j].y;
+      r.z = o.z * sv[j].z + x[0].z * c[j].z; r.w = o.w * sv[j].w + x[0].w * c[j].w;
+    }
+    if (k >= n) r = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint32_t th[4], tm[4], tl[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const Split3 sp = split3(r[e]);
+      th[e] = sp.h;
+      tm[e] = sp.m;
+      tl[e] = sp.l;
+    }
+    uint16_t* o16 = kimg + k * D + (((lane >> 1) ^ k) * 8) + (lane & 1) * 4;
+    *reinterpret_cast<uint2*>(o16) = make_uint2(pack_hi16(th[0], th[1]), pack_hi16(th[2], th[3]));
+    *reinterpret_cast<uint2*>(o16 + 32 * D) = make_uint2(pack_hi16(tm[0], tm[1]), pack_hi16(tm[2], tm[3]));
+    *reinterpret_cast<uint2*>(o16 + 64 * D) = make_uint2(pack_hi16(tl[0], tl[1]), pack_hi16(tl[2], tl[3]));
+  }
+}
+
+// The value image of (tile, hk): rows into LDS (clamped loads, zeros past
+// the sequence), then transposed, 16 bytes (8 slots of one dim and term) per
+// store.
+__device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int hk, int wave, int lane,
+                                           float (*Vt)[kVtStride]) {
+  constexpr int D = 256;
+  const int sq = a.tile_seq[tile];
+  const int t0 = 32 * (tile - a.cut[sq]);
+  const int n = min(32, a.cu[sq + 1] - a.cu[sq] - t0);
+  const int64_t r_first = a.cu[sq] - a.row0 + t0;
+  const int width = (a.H + 2 * a.Hkv) * D;
+  uint16_t* vimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg) + kTileImg;
+  f32x4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int64_t row = r_first + min(wave + 4 * j, n - 1);
+    v[j] = *reinterpret_cast<const f32x4*>(a.qkv + row * width + (int64_t)(a.H + a.Hkv + hk) * D + lane * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int k = wave + 4 * j;
+    const f32x4 x = k < n ? v[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<float2*>(&Vt[k][lane * 4]) = make_float2(x.x, x.y);
+    *reinterpret_cast<float2*>(&Vt[k][lane * 4 + 2]) = make_float2(x.z, x.w);
+  }
+  __syncthreads();
+  const int tid = wave * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int u = tid + 256 * i;
+    const int d = u >> 2, c = u & 3;  // dim, chunk of 8 slots: keys 4c .. 4c+3, 16 + 4c .. 16 + 4c+3
+    uint32_t th[8], tm[8], tl[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const Split3 sp = split3(Vt[(e >> 2) * 16 + 4 * c + (e & 3)][d]);
+      th[e] = sp.h;
+      tm[e] = sp.m;
+      tl[e] = sp.l;
+    }
+    uint16_t* o = vimg + d * 32 + ((c ^ ((d >> 1) & 3)) * 8);
+    *reinterpret_cast<uint4*>(o) = make_uint4(pack_hi16(th[0], th[1]), pack_hi16(th[2], th[3]),
+                                              pack_hi16(th[4], th[5]), pack_hi16(th[6], th[7]));
+    *reinterpret_cast<uint4*>(o + 32 * D) = make_uint4(pack_hi16(tm[0], tm[1]), pack_hi16(tm[2], tm[3]),
+                                                       pack_hi16(tm[4], tm[5]), pack_hi16(tm[6], tm[7]));
+    *reinterpret_cast<uint4*>(o + 64 * D) = make_uint4(pack_hi16(tl[0], tl[1]), pack_hi16(tl[2], tl[3]),
+                                                       pack_hi16(tl[4], tl[5]), pack_hi16(tl[6], tl[7]));
+  }
+}
+
+// Blocks 2i (key image) and 2i + 1 (value image) of (tile t_lo + i / Hkv,
+// kv head i % Hkv).
+__global__ __launch_bounds__(256) void kv_tiles_kernel(KvTilesParams a) {
+  __shared__ __attribute__((aligned(16))) float Vt[32][kVtStride];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t b = blockIdx.x;
-  if (b < a.v_blocks) {
-    const int qi = (int)(b / a.Hkv) * 4 + wave;
-    const int hv = (int)(b % a.Hkv);
-    if (qi < a.quads)
-      value_quad(a.qkv, a.row0, a.q_lo + qi, hv, lane, a.H, a.Hkv, a.eps, a.norm_v, a.cu, a.cu4, a.quad_seq, a.vp);
-    return;
-  }
-  const int64_t qb = b - a.v_blocks;
-  const int64_t row = qb / a.ny;
-  const int head = (int)(qb % a.ny) * 4 + wave;
-  if (head < a.H + a.Hkv) qk_planes_head(a.qkv, row, head, lane, a.H, a.Hkv, a.gq, a.gk, a.eps, a.pos, a.cs, a.sn, a.kp);
+  const int tile = a.t_lo + (int)(b / (2 * a.Hkv)), hk = (int)((b >> 1) % a.Hkv);
+  if (b & 1)
+    value_tile(a, tile, hk, wave, lane, Vt);
+  else
+    key_tile(a, tile, hk, wave, lane);
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, int64_t n) {
@@ -474,7 +478,8 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, int64_
   if (i < n) p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// y = the sum of `parts` partial products y_p = y + p * pstride (K-split
+// out[b, :dim] = y[b, :dim] / sqrt(sum(y[b, :dim]^2) + 1e-12), one wave per
+// row; y = the sum of `parts` partial products y_p = y + p * pstride (K-split
 // head product), added in part order.
 __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ y, int nseq, int width, int dim,
                                                      int parts, int64_t pstride, float* __restrict__ out) {
@@ -644,19 +649,15 @@ int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int3
   return FA_OK;
 }
 
-int launch_qkv_planes(fa_ctx* ctx, float* qkv, int64_t rows, int64_t row0, int32_t H, int32_t Hkv, const float* gq,
-                      const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
-                      bool norm_v, const int32_t* d_cu_seqlens, const int32_t* d_cu_quads, const int32_t* d_quad_seq,
-                      int32_t q_lo, int32_t quads, uint16_t* kp, uint16_t* vp, hipStream_t s) {
-  if (rows == 0) return FA_OK;
-  QkvPlanesParams a;
-  a.qkv = qkv; a.rows = rows; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.ny = (H + Hkv + 3) / 4;
-  a.gq = gq; a.gk = gk; a.eps = eps; a.pos = d_pos; a.cs = cos_t; a.sn = sin_t; a.norm_v = norm_v ? 1 : 0;
-  a.cu = d_cu_seqlens; a.cu4 = d_cu_quads; a.quad_seq = d_quad_seq; a.q_lo = q_lo; a.quads = quads;
-  a.kp = kp; a.vp = vp;
-  a.v_blocks = blocks_for(quads, 4) * Hkv;
-  const int64_t blocks = a.v_blocks + rows * a.ny;
-  hipLaunchKernelGGL(qkv_planes_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
+                    const int32_t* d_pos, const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
+                    const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
+                    hipStream_t s) {
+  if (tiles == 0) return FA_OK;
+  KvTilesParams a;
+  a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.pos = d_pos; a.cs = cos_t; a.sn = sin_t;
+  a.cu = d_cu_seqlens; a.cut = d_cu_tiles; a.tile_seq = d_tile_seq; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
+  hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(2 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }

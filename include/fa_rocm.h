@@ -35,7 +35,6 @@
  *   FA_GEMM_KSPLIT=1            no K split of the encoder's N = hidden products
  *   FA_MICROBATCH=0|<rows>      micro-batches off / from this many tokens (2048)
  *   FA_MICROBATCH_GROUPS=2..4   force the micro-batch count
- *   FA_ATTN_PLANES=0|1          force the fp32-MFMA / split-bf16 attention
  *   FA_ATTN_KEY_PARTS=1..8      force the key runs of the short-batch attention
  */
 #ifndef FA_ROCM_H

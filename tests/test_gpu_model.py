@@ -257,6 +257,21 @@ def test_key_split_attention_with_sliding_band(models):
     compare_states(gm, om, b.ids[:2], b.lengths[:2], [0], "C3[0:2] key-split states", layers=[1, 6, 24, -1])
 
 
+@pytest.mark.parametrize("L", [1100, 2048])
+def test_single_long_sequence_key_runs(models, L):
+    """One long sequence (above 1 024 tokens: the split-bf16 tile attention)
+    gives fewer work items than CUs, so each item's key tiles are cut into
+    runs summed by attention_combine_kernel (1 100: 26 items, 8 runs of 4-5
+    tiles; 2 048: 48 items, 5 runs). Against the oracle, layer by layer."""
+    gm, om = models
+    rng = np.random.default_rng(L)
+    ids = rng.integers(3, 262144, (1, L)).astype(np.int32)
+    ids[0, 0] = 2
+    lens = np.array([L], np.int32)
+    compare(gm.embed_ids(ids, lens), om.embed(ids, lens), f"single L={L}")
+    compare_states(gm, om, ids, lens, [0], f"single L={L} states", layers=[1, 6, 24, -1])
+
+
 def test_c4_long_sequences(models):
     """C4 (8 x 2048, lengths 1024..2048; four micro-batches, split-bf16
     attention with the 257 band on sliding layers and every key on global
