@@ -3,6 +3,7 @@
   python -m ai_amd.bench_gemm                 # the encoder's product shapes
   python -m ai_amd.bench_gemm --shape 32768,768,768 --reps 5 --no-check
   python -m ai_amd.bench_gemm --shape 128,2304,768 --shape 1,768,3072
+  python -m ai_amd.bench_gemm --library       # against the vendor bf16 GEMM
 
 One JSON line per shape: mean launch time over back-to-back calls, fp32-
 equivalent TFLOP/s (2*M*N*K / time) and the max |error| against a float64
@@ -136,6 +137,63 @@ def dropin(reps: int) -> None:
     ctx.close()
 
 
+def library(shapes, reps: int) -> None:
+    """The split product against the vendor bf16 GEMM on the same MFMA work.
+
+    The split-bf16 product A.W (A fp32 = hi + mid + lo, W bf16) is the plain
+    bf16 GEMM [A_hi | A_mid | A_lo] (M x 3K) . [W; W; W] (3K x N) with fp32
+    accumulation and output. For each shape this times fa_matmul_fused_dev
+    (split included) and torch.mm on bf16 operands of that (M, N, 3K) shape
+    with float32 output (hipBLASLt on ROCm; the planes are random here, only
+    the time matters), HIP events around `reps` back-to-back calls each."""
+    import torch
+    ctx = N.Context(0)
+    L = N.lib()
+    dev = torch.device("cuda")
+    for (M, Nn, K) in shapes:
+        rng = np.random.default_rng(M + Nn + K)
+        a = rng.standard_normal((M, K)).astype(np.float32)
+        wb = S.normal_bf16(3, "bench_gemm", 0.05, (Nn, K))
+        da, db, dc = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        for p, n in ((da, a.nbytes), (db, wb.nbytes), (dc, M * Nn * 4)):
+            N.check(ctx.h, L.fa_device_alloc(ctx.h, n, C.byref(p)))
+        N.check(ctx.h, L.fa_memcpy_h2d(ctx.h, da, a.ctypes.data, a.nbytes))
+        N.check(ctx.h, L.fa_memcpy_h2d(ctx.h, db, wb.ctypes.data, wb.nbytes))
+
+        def ours():
+            N.check(ctx.h, L.fa_matmul_fused_dev(ctx.h, M, Nn, K, da, K, db, K, N.FA_DT_BF16, N.FA_B_NK, None, dc, Nn))
+
+        a3 = torch.randn(M, 3 * K, device=dev, dtype=torch.bfloat16)
+        w3 = torch.randn(3 * K, Nn, device=dev, dtype=torch.bfloat16)
+        out_dtype = "float32"
+        try:
+            torch.mm(a3, w3, out_dtype=torch.float32)
+
+            def vendor():
+                torch.mm(a3, w3, out_dtype=torch.float32)
+        except (RuntimeError, TypeError):
+            out_dtype = "bfloat16"
+
+            def vendor():
+                torch.mm(a3, w3)
+        rec = dict(M=M, N=Nn, K=K, vendor_K=3 * K, vendor_out=out_dtype)
+        for label, fn, sync in (("split_kernel_us", ours, ctx.sync), ("vendor_bf16_us", vendor, torch.cuda.synchronize)):
+            for _ in range(3):
+                fn()
+            sync()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            sync()
+            rec[label] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+        rec["bf16_tflops_split_kernel"] = round(2 * M * Nn * 3 * K / (rec["split_kernel_us"] * 1e-6) / 1e12, 1)
+        rec["bf16_tflops_vendor"] = round(2 * M * Nn * 3 * K / (rec["vendor_bf16_us"] * 1e-6) / 1e12, 1)
+        print(json.dumps(rec), flush=True)
+        for p in (da, db, dc):
+            L.fa_device_free(ctx.h, p)
+    ctx.close()
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--shape", action="append",
@@ -144,11 +202,16 @@ def main() -> None:
     ap.add_argument("--no-check", action="store_true", help="skip the float64 comparison")
     ap.add_argument("--dropin", action="store_true",
                     help="time the MatMulFused drop-in at the gate shape with float32/bf16 weights in both layouts")
+    ap.add_argument("--library", action="store_true",
+                    help="time each shape against the vendor bf16 GEMM of the same MFMA work (M x 3K . 3K x N)")
     a = ap.parse_args()
     if a.dropin:
         dropin(a.reps)
         return
     shapes = [tuple(int(v) for v in sh.split(",")) for sh in a.shape] if a.shape else SHAPES
+    if a.library:
+        library(shapes, a.reps)
+        return
     run(shapes, a.reps, not a.no_check)
 
 
