@@ -348,6 +348,35 @@ def test_window_bound_at_sequence_length_masks_agree(ctx):
     assert d_band > 1e-3
 
 
+@pytest.mark.parametrize("heads", [(4, 2), (2, 2), (6, 1)])
+def test_tile_attention_other_head_groupings(ctx, heads):
+    """The tile attention's rows are (token, query head) pairs of one kv
+    head's group (G = H / Hkv query heads); EmbeddingGemma-300M has G = 3,
+    Hkv = 1. Four-layer variants with two kv heads of two query heads each,
+    plain multi-head attention (G = 1) and six query heads on one kv head,
+    over 1 158 tokens (the tile path; one sequence past the 257 band, one of
+    a single token), against the oracle: every row, and the hidden states
+    after the first and last layer."""
+    H, Hkv = heads
+    shape = _shape_variant(num_attention_heads=H, num_key_value_heads=Hkv, num_hidden_layers=4,
+                           sliding_window_pattern=2)
+    lens = np.array([300, 520, 77, 1, 260], np.int32)
+    rng = np.random.default_rng(H * 10 + Hkv)
+    ids = rng.integers(3, shape.vocab_size, (len(lens), int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    gm = G.Model(shape, ctx)
+    gm.load_synthetic()
+    om = O.OracleModel(shape)
+    om.load_synthetic()
+    try:
+        compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens), f"H={H} Hkv={Hkv}")
+        compare_states(gm, om, ids, lens, [1, 2], f"H={H} Hkv={Hkv} states", layers=[1, 4, -1])
+    finally:
+        gm.close()
+        om.close()
+
+
 def _topk_checked(s64, gi, oi, bound, what):
     """Identity of top-k lists wherever the float64 scores s64's k+1 best are
     separated by more than 2*bound per row (bound: how far either side's
