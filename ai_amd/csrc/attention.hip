@@ -633,9 +633,10 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
   // Software pipeline, iteration tt: [barrier: K(tt), V(tt-1) landed; every
   // wave done with iteration tt-1] load V(tt); S(tt) = K(tt).Q^T; [barrier:
   // every wave done with the keys] load K(tt+1) (the last again past the
-  // end); P.V of tile tt-1 and the softmax of tile tt in one block (the
-  // softmax's VALU work beside the MFMAs), then O's rescale, which must see
-  // tile tt-1's terms. Then P.V of the last tile. One key buffer and two
+  // end); P.V of tile tt-1 with the softmax of tile tt written between its
+  // blocks in four stages (each stage's results pinned where it is written,
+  // so the VALU work sits among the MFMAs instead of after them), then O's
+  // rescale, which must see tile tt-1's terms. Then P.V of the last tile. One key buffer and two
   // value buffers (144 KB).
   bf16x8 pb0, pb1, pb2;  // tile tt-1's probability terms
   // Tile tb + i's values go to Vs0 for even i, Vs1 for odd i: every LDS
@@ -650,13 +651,83 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
     dl_barrier<0xC07F>();  // every wave's key reads done (no wait for the loads)
     issue(img0 + min(tt + 1, te - 1) * tstride, Ks);
   };
+  // P.V of tile tt-1 (terms pb*) with the softmax of tile tt (scores sacc)
+  // written between its blocks of 16 dims, in four stages, so that the
+  // VALU work sits among the MFMAs; the new terms replace pb* at the end
+  auto pv_softmax = [&](const uint16_t* Vp, int tt, const f32x4 (&sacc)[2], float& alpha, bool& moved) {
+    const int vpos = (g ^ vsw) * 8;
+    float t[8];
+    float tmax = -INFINITY, mn = 0.f, psum = 0.f;
+    float pvv[8];
+    uint32_t ph[8], pm[8], pl[8];
+#pragma unroll
+    for (int db = 0; db < HD / 16; db++) {
+      const uint16_t* vr = Vp + (16 * db + lq) * 32 + vpos;
+      const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(vr);
+      const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(vr + TERM);
+      const bf16x8 v2 = *reinterpret_cast<const bf16x8*>(vr + 2 * TERM);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v2, pb0, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, pb2, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, pb1, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, pb0, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, pb1, oacc[db], 0, 0, 0);
+      oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, pb0, oacc[db], 0, 0, 0);
+      if (db == 1) {  // scaled, masked scores and the lane's maximum
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int j = tt * TL_KEYS + 16 * (e >> 2) + 4 * g + (e & 3);
+          const bool ok = (unsigned)(j - klo) < (unsigned)(khi - klo);
+          t[e] = ok ? sacc[e >> 2][e & 3] * p.scale : -INFINITY;
+          tmax = fmaxf(tmax, t[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) asm volatile("" ::"v"(t[e]));  // computed here, not sunk to the use
+        __builtin_amdgcn_sched_barrier(0);
+      } else if (db == 4) {  // the row's maximum and the offset
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const bool need = tmax > m_run + TL_TAU;
+        moved = __any(need);
+        mn = need ? tmax : m_run;
+        alpha = exp_flush(m_run - mn);  // 1 where the offset stays, 0 for the first valid tile
+        m_run = mn;
+        __builtin_amdgcn_sched_barrier(0);
+      } else if (db == 8) {  // weights (masked keys: -inf, flushed to 0)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          pvv[e] = exp_flush(t[e] - mn);
+          psum += pvv[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) asm volatile("" ::"v"(pvv[e]));
+        __builtin_amdgcn_sched_barrier(0);
+      } else if (db == 11) {  // their exact bf16 terms
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const Split3 sp = split3(pvv[e]);
+          ph[e] = sp.h;
+          pm[e] = sp.m;
+          pl[e] = sp.l;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) asm volatile("" ::"v"(ph[e]), "v"(pm[e]), "v"(pl[e]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    l_part = l_part * alpha + psum;
+    pb0 = as_bf16x8(u32x4{pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]), pack_hi16(ph[4], ph[5]),
+                          pack_hi16(ph[6], ph[7])});
+    pb1 = as_bf16x8(u32x4{pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]), pack_hi16(pm[4], pm[5]),
+                          pack_hi16(pm[6], pm[7])});
+    pb2 = as_bf16x8(u32x4{pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]), pack_hi16(pl[4], pl[5]),
+                          pack_hi16(pl[6], pl[7])});
+  };
   auto iter = [&](int tt, uint16_t* Vn, const uint16_t* Vp) {
     f32x4 sacc[2];
     front(tt, Vn, sacc);
-    pv(Vp, pb0, pb1, pb2);
     float alpha;
     bool moved;
-    softmax(tt, sacc, alpha, moved, pb0, pb1, pb2);
+    pv_softmax(Vp, tt, sacc, alpha, moved);
     if (moved) {
 #pragma unroll
       for (int db = 0; db < HD / 16; db++) oacc[db] *= alpha;
