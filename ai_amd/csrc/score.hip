@@ -152,7 +152,7 @@ __global__ __launch_bounds__(64) void topk_merge_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Fused scoring: similarities and top-k without a score matrix.
 //
-// Per block of up to 256 queries, four launches:
+// Per block of up to 256 queries, three launches:
 //  1. score_qsplit_kernel: each query row split into hi + mid bf16 planes
 //     (hi = the row with its low 16 bits cleared, mid the same of the
 //     remainder) and its float64 norm.
@@ -165,16 +165,14 @@ __global__ __launch_bounds__(64) void topk_merge_kernel(const float* __restrict_
 //     MFMA C layout gives a lane 16 docs of every 32-doc block); any doc a
 //     lane drops is no better than its list's fourth entry, which the lane
 //     reports as its discard bound. Doc norms are taken during the split.
-//  3. score_merge_kernel: one wave per query merges the 16 candidates of every
-//     workgroup to the best 16 by s', rescoring them exactly (float64 dot
-//     products rounded to float32) and ordering them by (value desc, index
-//     asc). The result is exact when the k-th rescored value exceeds every
-//     discard bound (lanes' and the merge's own 16th) plus eps * |q| *
-//     max|doc|: then no dropped doc can reach the top k. Otherwise the query
-//     is flagged.
-//  4. score_fallback_kernel: flagged queries (near-ties of more than a few
-//     docs around the k-th score, e.g. duplicated rows) are scanned exactly
-//     over every doc; the others return at once.
+//  3. score_merge_kernel: one workgroup per query merges the 16 candidates of
+//     every stage-1 workgroup to the best 16 by s', rescoring them exactly
+//     (float64 dot products rounded to float32) and ordering them by (value
+//     desc, index asc). The result is exact when the k-th rescored value
+//     exceeds every discard bound (lanes' and the merge's own 16th) plus eps
+//     * |q| * max|doc|: then no dropped doc can reach the top k. Otherwise
+//     (near-ties of more than a few docs around the k-th score, e.g.
+//     duplicated rows) the same workgroup scans every doc exactly.
 // The output is the exact top k by float32-rounded dot product, larger first,
 // equal values by lower index (tensor/reduce.go:269-297); NaN scores rank
 // below every number.
@@ -459,7 +457,7 @@ struct MergeParams {
   const float* q;
   int64_t ldq;
   const float* docs;
-  int64_t ldd;
+  int64_t ldd, nd;
   int nwg, d, k;
   float eps;  // score error bound of stage 1 per |q| |doc|
   int32_t* idx;
@@ -526,6 +524,7 @@ __global__ __launch_bounds__(256) void score_merge_kernel(MergeParams p) {
   __shared__ float sv[4][kSMerge];
   __shared__ int si[4][kSMerge];
   __shared__ float sx[4], sd[4];
+  __shared__ int s_flag;
   const int64_t q = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ncand = p.nwg * kSCand;  // at most kSMaxWG * kSCand = kSMerge per thread
@@ -568,102 +567,102 @@ __global__ __launch_bounds__(256) void score_merge_kernel(MergeParams p) {
     sd[wave] = dn2;
   }
   __syncthreads();
-  if (wave != 0) return;
-  for (int w2 = 1; w2 < 4; w2++) {
-    float bv[kSMerge];
-    int bi[kSMerge];
+  if (wave == 0) {
+    for (int w2 = 1; w2 < 4; w2++) {
+      float bv[kSMerge];
+      int bi[kSMerge];
+#pragma unroll
+      for (int u = 0; u < kSMerge; u++) {
+        bv[u] = sv[w2][u];
+        bi[u] = si[w2][u];
+      }
+      merge_lists(v, ix, bv, bi);
+      xb = fmaxf(xb, sx[w2]);
+      dn2 = fmaxf(dn2, sd[w2]);
+    }
+    xb = fmaxf(xb, v[kSMerge - 1]);  // the merge's own discards
+    // exact rescoring: float64 dot products of the query with the kSMerge
+    // candidates, the wave's lanes taking four columns each per 256, rounded to
+    // float32; lane u keeps candidate u's value
+    double part[kSMerge];
+#pragma unroll
+    for (int u = 0; u < kSMerge; u++) part[u] = 0.0;
+    const float* qrow = p.q + q * p.ldq;
+    for (int t = 4 * lane; t < p.d; t += 256) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(qrow + t);
+#pragma unroll
+      for (int u = 0; u < kSMerge; u++) {
+        // an empty slot reads doc 0 and is ignored below: no branch, so the
+        // loads of all slots are in flight together
+        const int64_t row = ix[u] == INT32_MAX ? 0 : ix[u];
+        const f32x4 y = *reinterpret_cast<const f32x4*>(p.docs + row * p.ldd + t);
+        part[u] = fma((double)x[0], (double)y[0], part[u]);
+        part[u] = fma((double)x[1], (double)y[1], part[u]);
+        part[u] = fma((double)x[2], (double)y[2], part[u]);
+        part[u] = fma((double)x[3], (double)y[3], part[u]);
+      }
+    }
+    float e = -INFINITY;
+    int me = INT32_MAX;
 #pragma unroll
     for (int u = 0; u < kSMerge; u++) {
-      bv[u] = sv[w2][u];
-      bi[u] = si[w2][u];
-    }
-    merge_lists(v, ix, bv, bi);
-    xb = fmaxf(xb, sx[w2]);
-    dn2 = fmaxf(dn2, sd[w2]);
-  }
-  xb = fmaxf(xb, v[kSMerge - 1]);  // the merge's own discards
-  // exact rescoring: float64 dot products of the query with the kSMerge
-  // candidates, the wave's lanes taking four columns each per 256, rounded to
-  // float32; lane u keeps candidate u's value
-  double part[kSMerge];
+      double t = part[u];
 #pragma unroll
-  for (int u = 0; u < kSMerge; u++) part[u] = 0.0;
-  const float* qrow = p.q + q * p.ldq;
-  for (int t = 4 * lane; t < p.d; t += 256) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(qrow + t);
+      for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+      if (lane == u && ix[u] != INT32_MAX) {
+        e = (float)t;
+        me = ix[u];
+      }
+    }
+    // rank of this lane's exact value among the kSMerge
+    int rank = 0;
 #pragma unroll
     for (int u = 0; u < kSMerge; u++) {
-      // an empty slot reads doc 0 and is ignored below: no branch, so the
-      // loads of all slots are in flight together
-      const int64_t row = ix[u] == INT32_MAX ? 0 : ix[u];
-      const f32x4 y = *reinterpret_cast<const f32x4*>(p.docs + row * p.ldd + t);
-      part[u] = fma((double)x[0], (double)y[0], part[u]);
-      part[u] = fma((double)x[1], (double)y[1], part[u]);
-      part[u] = fma((double)x[2], (double)y[2], part[u]);
-      part[u] = fma((double)x[3], (double)y[3], part[u]);
+      const float eu = __shfl(e, u, 64);
+      const int iu = __shfl(me, u, 64);
+      rank += better(eu, iu, e, me) ? 1 : 0;
     }
-  }
-  float e = -INFINITY;
-  int me = INT32_MAX;
-#pragma unroll
-  for (int u = 0; u < kSMerge; u++) {
-    double t = part[u];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-    if (lane == u && ix[u] != INT32_MAX) {
-      e = (float)t;
-      me = ix[u];
+    // the k-th best exact value: the lane of rank k-1
+    const uint64_t at = __ballot(lane < kSMerge && rank == p.k - 1);
+    const int src = at ? __ffsll((unsigned long long)at) - 1 : 0;
+    const float ek = __shfl(e, src, 64);
+    const int ik = __shfl(me, src, 64);
+    const float margin = p.eps * p.qnorm[q] * sqrtf(dn2) * (1.f + 1e-4f);
+    // no lane of rank k-1: fewer than k candidates stand for docs
+    const bool exact = at != 0 && ik != INT32_MAX && ek > xb + margin;  // false for NaN: flagged
+    if (exact && lane < kSMerge && rank < p.k) {
+      p.idx[q * p.k + rank] = me;
+      if (p.val) p.val[q * p.k + rank] = e;
     }
-  }
-  // rank of this lane's exact value among the kSMerge
-  int rank = 0;
-#pragma unroll
-  for (int u = 0; u < kSMerge; u++) {
-    const float eu = __shfl(e, u, 64);
-    const int iu = __shfl(me, u, 64);
-    rank += better(eu, iu, e, me) ? 1 : 0;
-  }
-  // the k-th best exact value: the lane of rank k-1
-  const uint64_t at = __ballot(lane < kSMerge && rank == p.k - 1);
-  const int src = at ? __ffsll((unsigned long long)at) - 1 : 0;
-  const float ek = __shfl(e, src, 64);
-  const int ik = __shfl(me, src, 64);
-  const float margin = p.eps * p.qnorm[q] * sqrtf(dn2) * (1.f + 1e-4f);
-  // no lane of rank k-1: fewer than k candidates stand for docs
-  const bool exact = at != 0 && ik != INT32_MAX && ek > xb + margin;  // false for NaN: flagged
-  if (exact && lane < kSMerge && rank < p.k) {
-    p.idx[q * p.k + rank] = me;
-    if (p.val) p.val[q * p.k + rank] = e;
-  }
-  if (lane == 0) p.flag[q] = exact ? 0 : 1;
-}
-
-// 4. Flagged queries: every doc's exact score, four waves' lists merged.
-__global__ __launch_bounds__(256) void score_fallback_kernel(const float* __restrict__ qs, int64_t ldq,
-                                                             const float* __restrict__ docs, int64_t ldd, int64_t nd,
-                                                             int d, int k, const int32_t* __restrict__ flag,
-                                                             int32_t* __restrict__ idx, float* __restrict__ val) {
-  const int64_t q = blockIdx.x;
-  if (flag[q] == 0) return;
-  __shared__ float sv[4][kSMaxK];
-  __shared__ int si[4][kSMaxK];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (lane == 0) {
+      p.flag[q] = exact ? 0 : 1;
+      s_flag = exact ? 0 : 1;
+    }
+  }  // wave 0
+  __syncthreads();
+  if (s_flag == 0) return;
+  // flagged (near-ties of more than a lane list, or fewer than k
+  // candidates): the exact scan, float64 dot products against every doc,
+  // each wave a list of the best k, merged into wave 0's in wave order
   WaveList W;
-  for (int64_t base = 0; base < nd; base += 256) {
+  const float* qrow = p.q + q * p.ldq;
+  for (int64_t base = 0; base < p.nd; base += 256) {
     const int64_t j = base + tid;
-    const bool ok = j < nd;
-    W.offer(k, lane, ok ? exact_dot(qs + q * ldq, docs + j * ldd, d) : NAN, ok ? (int)j : INT32_MAX);
+    const bool ok = j < p.nd;
+    W.offer(p.k, lane, ok ? exact_dot(qrow, p.docs + j * p.ldd, p.d) : NAN, ok ? (int)j : INT32_MAX);
   }
-  if (lane < k) {
+  __syncthreads();  // every wave is done with sv / si
+  if (lane < p.k) {
     sv[wave][lane] = W.lv;
     si[wave][lane] = W.li;
   }
   __syncthreads();
   if (wave == 0) {
-    for (int w2 = 1; w2 < 4; w2++) W.offer(k, lane, lane < k ? sv[w2][lane] : NAN, lane < k ? si[w2][lane] : INT32_MAX);
-    if (lane < k) {
-      idx[q * k + lane] = W.li == INT32_MAX ? -1 : W.li;
-      if (val) val[q * k + lane] = W.li == INT32_MAX ? NAN : W.lv;
+    for (int w2 = 1; w2 < 4; w2++)
+      W.offer(p.k, lane, lane < p.k ? sv[w2][lane] : NAN, lane < p.k ? si[w2][lane] : INT32_MAX);
+    if (lane < p.k) {
+      p.idx[q * p.k + lane] = W.li == INT32_MAX ? -1 : W.li;
+      if (p.val) p.val[q * p.k + lane] = W.li == INT32_MAX ? NAN : W.lv;
     }
   }
 }
@@ -733,9 +732,8 @@ int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, cons
     pm.cv = sc.cv; pm.ci = sc.ci; pm.bound = sc.bound; pm.wgnorm = sc.wgnorm; pm.qnorm = sc.qnorm; pm.q = qb;
     pm.ldq = ldq; pm.docs = docs; pm.ldd = ldd; pm.nwg = nwg; pm.d = d; pm.k = topk; pm.eps = eps;
     pm.idx = idx + q0 * topk; pm.val = val ? val + q0 * topk : nullptr; pm.flag = sc.flag;
+    pm.nd = nd;
     hipLaunchKernelGGL(score_merge_kernel, dim3(nb), dim3(256), 0, s, pm);
-    hipLaunchKernelGGL(score_fallback_kernel, dim3(nb), dim3(256), 0, s, qb, ldq, docs, ldd, nd, d, topk, sc.flag,
-                       idx + q0 * topk, val ? val + q0 * topk : nullptr);
   }
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
