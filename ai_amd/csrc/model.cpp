@@ -737,7 +737,9 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   // attention_varlen_qblock() queries per head.
   int64_t M_all = 0;
   for (int b = 0; b < B; b++) M_all += std::max(0, lengths[b]);
-  const bool tiles = !v2 && m->max_hd == H * 256 && M_all > fa::kAttnSplitRows;
+  // (batches of very short sequences, under 32 tokens on average, keep the
+  // fp32 kernel's 16-key tiles: a 32-key tile would be mostly padding)
+  const bool tiles = !v2 && m->max_hd == H * 256 && M_all > fa::kAttnSplitRows && M_all >= 32LL * B;
   const int tkeys = fa::attention_tiles_keys();
   const int G = H / c.num_key_value_heads;
   const int istep = tiles ? fa::attention_tiles_rows() : fa::attention_varlen_qblock();

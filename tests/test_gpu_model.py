@@ -272,6 +272,18 @@ def test_single_long_sequence_key_runs(models, L):
     compare_states(gm, om, ids, lens, [0], f"single L={L} states", layers=[1, 6, 24, -1])
 
 
+def test_many_short_sequences(models):
+    """150 sequences of 2-14 tokens (1 210 tokens, under 32 on average: the
+    fp32 attention with micro-batches) against the oracle, every row."""
+    gm, om = models
+    rng = np.random.default_rng(150)
+    lens = rng.integers(2, 15, 150).astype(np.int32)
+    ids = rng.integers(3, 262144, (150, int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=50), f"150 short (L {lens.min()}..{lens.max()})")
+
+
 def test_c4_long_sequences(models):
     """C4 (8 x 2048, lengths 1024..2048; four micro-batches, split-bf16
     attention with the 257 band on sliding layers and every key on global
