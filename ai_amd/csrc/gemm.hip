@@ -432,13 +432,18 @@ using X128x256w8 = XTile<128, 256, 4, 2>;  // 8 waves of 32x128 (80 KB of LDS: t
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// LDS rows of the split kernel are 32 bf16 (64 bytes, four 16-byte chunks)
-// without padding; chunk c of row r is stored at position c ^ lds_swz(r).
-// With this swizzle the 16-byte operand reads (32 consecutive rows, one chunk
-// each) and the 16-byte staging writes (four chunks of a row per four lanes)
-// touch distinct banks in every group of 8 lanes over 128 bytes and of 16
-// lanes over 256 bytes.
-__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// A slab of the split kernel (ROWS rows of 32 bf16: four 16-byte chunks per
+// row) is held chunk-major in LDS: chunk c of row r at 16-byte slot
+// c * ROWS + (r ^ 2c). gfx950's LDS serves 16-byte reads 16 lanes at a time
+// over 64 banks and 16-byte writes 8 lanes at a time over 32 banks (measured
+// with SQ_LDS_BANK_CONFLICT on single-pattern probes). The operand reads
+// (16 consecutive rows of one chunk per 16 lanes) then cover 16 distinct
+// slots mod 16, and the staging writes (lanes 4j..4j+3 write the four chunks
+// of one row, so 8 lanes hold two rows: r ^ 2c takes 8 distinct values mod 8)
+// are conflict-free too. Row-major rows with the chunks swizzled per row
+// measured 2-way conflicts on the reads (8 instead of 4 clocks per wave read).
+template <int ROWS>
+__device__ __forceinline__ int lds_chunk(int r, int c) { return (c * ROWS + (r ^ (2 * c))) * 8; }
 
 
 // Staging registers hold vector types (HIP's struct uint4 in an array was
@@ -486,13 +491,13 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
   for (int i = 0; i < NA; i++) {
     const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
     ga[i] = min(m0 + row, M - 1) * p.lda + k_off + c * 8;
-    la[i] = row * BK + ((c ^ lds_swz(row)) << 3);
+    la[i] = lds_chunk<BM>(row, c);
   }
 #pragma unroll
   for (int i = 0; i < NB; i++) {
     const int idx = tid + NT * i, row = idx >> 2, c = idx & 3;
     gb[i] = B + min(n0 + row, N - 1) * p.ldb + k_off + c * 8;
-    lb[i] = row * BK + ((c ^ lds_swz(row)) << 3);
+    lb[i] = lds_chunk<BN>(row, c);
   }
   auto load_global = [&](f32x4 (&ra)[2 * NA], u32x4 (&rb)[BT * NB], int kt) {
 #pragma unroll
@@ -533,24 +538,21 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
       for (int i = 0; i < NB; i++) *reinterpret_cast<u32x4*>(&Bs[buf][t][lb[i]]) = rb[t * NB + i];
   };
 
-  // Operand reads: lane half h takes chunk 2s+h of its row; every row read by
-  // a lane is (32-aligned base) + lane%32, so its swizzle is lds_swz(lane%32).
+  // Operand reads: lane half h takes chunk 2s+h of its row (32 consecutive
+  // rows of one chunk per half-wave; 32 rows further is 32 slots further).
   const int arow = wm * TL::TM + (lane & 31);
   const int brow = wn * TL::TN + (lane & 31);
-  const int sw = lds_swz(lane & 31);
   const int h = lane >> 5;
   auto read_ops = [&](int buf, int s, bf16x8 (&oa)[3][FM], bf16x8 (&ob)[BT][FN]) {
-    const int co = ((2 * s + h) ^ sw) << 3;
+    const int ca = lds_chunk<BM>(arow, 2 * s + h), cb = lds_chunk<BN>(brow, 2 * s + h);
 #pragma unroll
     for (int t = 0; t < 3; t++)
 #pragma unroll
-      for (int i = 0; i < FM; i++)
-        oa[t][i] = *reinterpret_cast<const bf16x8*>(&As[buf][t][(arow + 32 * i) * BK + co]);
+      for (int i = 0; i < FM; i++) oa[t][i] = *reinterpret_cast<const bf16x8*>(&As[buf][t][ca + 32 * 8 * i]);
 #pragma unroll
     for (int t = 0; t < BT; t++)
 #pragma unroll
-      for (int j = 0; j < FN; j++)
-        ob[t][j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][t][(brow + 32 * j) * BK + co]);
+      for (int j = 0; j < FN; j++) ob[t][j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][t][cb + 32 * 8 * j]);
   };
 
   f32x16 acc[FM][FN];

@@ -187,7 +187,12 @@ constexpr int kSMaxWG = 256;
 typedef __bf16 sbf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t su32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int s_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// LDS slabs (ROWS rows of 32 bf16) chunk-major: chunk c of row r at 16-byte
+// slot c * ROWS + (r ^ 2c), conflict-free for the 16-byte staging writes
+// (four lanes per row) and operand reads (consecutive rows of one chunk) on
+// gfx950's LDS (the layout of the split GEMM, gemm.hip).
+template <int ROWS>
+__device__ __forceinline__ int s_chunk(int r, int c) { return (c * ROWS + (r ^ (2 * c))) * 8; }
 
 // 1. One wave per query row of the block: hi/mid planes [kSQB x d] (zero rows
 // past nq) and |q| in float64 rounded up to float32.
@@ -271,7 +276,7 @@ __global__ __launch_bounds__(512) void score_stage1_kernel(Stage1Params p) {
       m[e] = sp.m;
       ss = fmaf(x, x, ss);
     }
-    const int o = srow * 32 + ((sc ^ s_swz(srow)) << 3);
+    const int o = s_chunk<kSDB>(srow, sc);
     *reinterpret_cast<uint4*>(&Dp[buf][0][o]) =
         make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
     *reinterpret_cast<uint4*>(&Dp[buf][1][o]) =
@@ -284,18 +289,20 @@ __global__ __launch_bounds__(512) void score_stage1_kernel(Stage1Params p) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int idx = tid + 512 * (i & 1), qr = idx >> 2, c = idx & 3;
-      *reinterpret_cast<su32x4*>(&Qp[buf][i >> 1][qr * 32 + ((c ^ s_swz(qr)) << 3)]) = g.b[i];
+      *reinterpret_cast<su32x4*>(&Qp[buf][i >> 1][s_chunk<kSQB>(qr, c)]) = g.b[i];
     }
   };
-  const int sw = s_swz(lane & 31), hh = lane >> 5;
+  const int hh = lane >> 5;
   auto read_ops = [&](int buf, int s, sbf16x8 (&oa)[2][2], sbf16x8 (&ob)[2][2]) {
-    const int co = ((2 * s + hh) ^ sw) << 3;
+    // 32 rows further is 32 slots further
+    const int ca = s_chunk<kSDB>(wd * 64 + (lane & 31), 2 * s + hh);
+    const int cb = s_chunk<kSQB>(wq * 64 + (lane & 31), 2 * s + hh);
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        oa[t][i] = *reinterpret_cast<const sbf16x8*>(&Dp[buf][t][(wd * 64 + i * 32 + (lane & 31)) * 32 + co]);
-        ob[t][i] = *reinterpret_cast<const sbf16x8*>(&Qp[buf][t][(wq * 64 + i * 32 + (lane & 31)) * 32 + co]);
+        oa[t][i] = *reinterpret_cast<const sbf16x8*>(&Dp[buf][t][ca + 32 * 8 * i]);
+        ob[t][i] = *reinterpret_cast<const sbf16x8*>(&Qp[buf][t][cb + 32 * 8 * i]);
       }
   };
   f32x16 acc[2][2];
