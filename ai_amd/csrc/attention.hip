@@ -89,6 +89,25 @@ __device__ __forceinline__ int dl_pos(int row, int chunk) { return chunk ^ (row 
 // instead of __syncthreads()'s release fence, which would also wait for the
 // next tile's loads to LDS. The signal fences keep the compiler from moving
 // LDS accesses across it.
+// Max and sum over lanes l, l^16, l^32 and l^48 (the four row groups of a
+// 16x16 MFMA column) with v_permlane16_swap / v_permlane32_swap: a swap of
+// a value with itself leaves the lane's own value in one result and its
+// partner's in the other, so no LDS round trip (ds_bpermute) is needed and
+// the reduction does not wait behind outstanding LDS reads.
+__device__ __forceinline__ float rows4_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// x_l + x_{l^16}, then the same over l^32 (each sum commutes exactly)
+__device__ __forceinline__ float rows4_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int WAIT>
 __device__ __forceinline__ void dl_barrier() {
   __builtin_amdgcn_s_waitcnt(WAIT);
@@ -223,8 +242,7 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
       sacc[r] = t;
       if (ok) tmax = fmaxf(tmax, t);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = rows4_max(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = exp_flush(m_run - m_new);
     m_run = m_new;
@@ -260,8 +278,7 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
     if (k0 + KT < kend) step(k0 + KT, K1, V1, K0, V0);
   }
 
-  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float l_tot = rows4_sum(l_part);
   const int OW = p.H * HD;
   if (p.kparts > 1) {
     // unnormalised O of this key run; lane lq < 16 of the first wave of the
@@ -479,8 +496,7 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
     for (int c = 0; c < HD / 32; c++)
 #pragma unroll
       for (int e = 0; e < 8; e++) ss = fmaf(x[c][e >> 2][e & 3], x[c][e >> 2][e & 3], ss);
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
+    ss = rows4_sum(ss);
     const float inv = rms_inv(ss, HD, p.eps);
     const float* gr = p.gq + 8 * g;
     const float* cr = p.cs + (int64_t)tok * (HD / 2) + 8 * g;
@@ -603,8 +619,7 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
       t[e] = ok ? sacc[e >> 2][e & 3] * p.scale : -INFINITY;
       tmax = fmaxf(tmax, t[e]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = rows4_max(tmax);
     const bool need = tmax > m_run + TL_TAU;
     moved = __any(need);
     const float mn = need ? tmax : m_run;
@@ -658,7 +673,6 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
     const int vpos = (g ^ vsw) * 8;
     float t[8];
     float tmax = -INFINITY, mn = 0.f, psum = 0.f;
-    float pvv[8];
     uint32_t ph[8], pm[8], pl[8];
 #pragma unroll
     for (int db = 0; db < HD / 16; db++) {
@@ -672,47 +686,36 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, pb0, oacc[db], 0, 0, 0);
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, pb1, oacc[db], 0, 0, 0);
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, pb0, oacc[db], 0, 0, 0);
-      if (db == 1) {  // scaled, masked scores and the lane's maximum
+      if (db < 2) {  // scaled, masked scores (four per block) and the lane's maximum
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
+        for (int e = 4 * db; e < 4 * db + 4; e++) {
           const int j = tt * TL_KEYS + 16 * (e >> 2) + 4 * g + (e & 3);
           const bool ok = (unsigned)(j - klo) < (unsigned)(khi - klo);
           t[e] = ok ? sacc[e >> 2][e & 3] * p.scale : -INFINITY;
           tmax = fmaxf(tmax, t[e]);
+          asm volatile("" ::"v"(t[e]));  // computed here, not sunk to the use
         }
-#pragma unroll
-        for (int e = 0; e < 8; e++) asm volatile("" ::"v"(t[e]));  // computed here, not sunk to the use
-        __builtin_amdgcn_sched_barrier(0);
-      } else if (db == 4) {  // the row's maximum and the offset
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      } else if (db == 2) {  // the row's maximum
+        tmax = rows4_max(tmax);
+        asm volatile("" ::"v"(tmax));
+      } else if (db == 3) {  // the offset
         const bool need = tmax > m_run + TL_TAU;
         moved = __any(need);
         mn = need ? tmax : m_run;
         alpha = exp_flush(m_run - mn);  // 1 where the offset stays, 0 for the first valid tile
         m_run = mn;
-        __builtin_amdgcn_sched_barrier(0);
-      } else if (db == 8) {  // weights (masked keys: -inf, flushed to 0)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          pvv[e] = exp_flush(t[e] - mn);
-          psum += pvv[e];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; e++) asm volatile("" ::"v"(pvv[e]));
-        __builtin_amdgcn_sched_barrier(0);
-      } else if (db == 11) {  // their exact bf16 terms
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const Split3 sp = split3(pvv[e]);
-          ph[e] = sp.h;
-          pm[e] = sp.m;
-          pl[e] = sp.l;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; e++) asm volatile("" ::"v"(ph[e]), "v"(pm[e]), "v"(pl[e]));
-        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::"v"(alpha), "v"(mn));
+      } else if (db >= 4 && db < 12) {  // one weight (masked keys: -inf, flushed to 0) and its exact bf16 terms
+        const int e = db - 4;
+        const float w = exp_flush(t[e] - mn);
+        psum += w;
+        const Split3 sp = split3(w);
+        ph[e] = sp.h;
+        pm[e] = sp.m;
+        pl[e] = sp.l;
+        asm volatile("" ::"v"(ph[e]), "v"(pm[e]), "v"(pl[e]), "v"(psum));
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     l_part = l_part * alpha + psum;
     pb0 = as_bf16x8(u32x4{pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]), pack_hi16(ph[4], ph[5]),
@@ -758,8 +761,7 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
     }
   }
 
-  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float l_tot = rows4_sum(l_part);
   if (!qvalid) return;
   const int OW = p.H * HD;
   if (p.kparts > 1) {

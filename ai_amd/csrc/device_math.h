@@ -40,9 +40,12 @@ __device__ __forceinline__ float gelu_tanh_ref(float x) {
 
 // exp with the reference's flush: inputs below -87 give exactly 0
 // (internal/kernel/generic.go:278-307), so masked softmax weights are exact
-// zeros. Computed as 2^(x*log2 e) on the hardware exp2.
+// zeros. Computed as 2^(x*log2 e) on the hardware exp2 (v_exp_f32) directly:
+// every input that is not flushed maps to at least 2^-125.6, a normal
+// float, where exp2f's guard for subnormal results (a range test, an offset
+// and an ldexp around the same instruction) changes nothing.
 __device__ __forceinline__ float exp_flush(float x) {
-  return x < -87.f ? 0.f : exp2f(x * 1.4426950408889634f);
+  return x < -87.f ? 0.f : __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
 // Sum over the 64 lanes of a wavefront (result in every lane).
