@@ -215,14 +215,15 @@ int microbatch_count_forced() {
 // Group count by the batch, from sweeps of 2, 3 and 4 groups on MI355X:
 // long sequences (the mean key count per token, sum L^2 / sum L, at least
 // 1 024) make the forward attention-bound and gain from a fourth stream
-// (C4, 8 x 1 024..2 048: 16.29 -> 15.27 ms); from 16 384 tokens the
-// products are large enough on their own and two groups keep their tiles
-// full (C3, 64 x 512: 34.25 -> 33.59 ms; C5 equal); else three (C2: 5.46 ms
-// against 5.81 with two and 5.76 with four).
+// (C4, 8 x 1 024..2 048: 11.80 ms against 11.84 with two and 11.97 with
+// three); from 24 576 tokens the products are large enough on their own and
+// two groups keep their tiles full (C3, 64 x 512: 27.45 ms against 28.0 with
+// three); else three (C2: 5.30 ms against 5.41 with two and 5.53 with four;
+// C5, 17 923 tokens: 13.74 against 13.91 and 14.26).
 int microbatch_count(int64_t tokens, double sum_l2) {
   if (const int f = microbatch_count_forced()) return f;
   if (sum_l2 >= 1024.0 * (double)tokens) return 4;
-  return tokens >= 16384 ? 2 : 3;
+  return tokens >= 24576 ? 2 : 3;
 }
 
 // Brackets one launch with events when profiling.
