@@ -8,13 +8,13 @@ namespace fa {
 // tanh as the reference computes it (internal/kernel/generic.go:313-359):
 // identity below |x| < 4e-4, +-1 from |x| >= 9, otherwise an odd degree-13
 // over even degree-6 rational after clamping to +-7.99881172180175781 (the
-// published Eigen float approximation).
+// published Eigen float approximation). The rational is evaluated for every
+// input and the three cases are selects (they exclude each other), so the
+// code has no branches: an epilogue holding many values per lane otherwise
+// became one divergent branch region per value.
 __device__ __forceinline__ float tanh_ref(float v) {
-  if (v > -0.0004f && v < 0.0004f) return v;
-  if (v >= 9.f) return 1.f;
-  if (v <= -9.f) return -1.f;
-  v = fminf(fmaxf(v, -7.99881172180175781f), 7.99881172180175781f);
-  const float v2 = v * v;
+  const float c = fminf(fmaxf(v, -7.99881172180175781f), 7.99881172180175781f);
+  const float v2 = c * c;
   float p = -2.76076847742355e-16f;
   p = fmaf(p, v2, 2.00018790482477e-13f);
   p = fmaf(p, v2, -8.60467152213735e-11f);
@@ -22,12 +22,15 @@ __device__ __forceinline__ float tanh_ref(float v) {
   p = fmaf(p, v2, 1.48572235717979e-05f);
   p = fmaf(p, v2, 6.37261928875436e-04f);
   p = fmaf(p, v2, 4.89352455891786e-03f);
-  p *= v;
+  p *= c;
   float q = 1.19825839466702e-06f;
   q = fmaf(q, v2, 1.18534705686654e-04f);
   q = fmaf(q, v2, 2.26843463243900e-03f);
   q = fmaf(q, v2, 4.89352518554385e-03f);
-  return p / q;
+  float r = p / q;
+  r = v >= 9.f ? 1.f : r;
+  r = v <= -9.f ? -1.f : r;
+  return (v > -0.0004f && v < 0.0004f) ? v : r;
 }
 
 // tanh-GELU, 0.5*x*(1 + tanh(sqrt(2/pi)*(x + 0.044715*x^3)))

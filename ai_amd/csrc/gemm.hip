@@ -134,7 +134,11 @@ __device__ __forceinline__ float epi_value(const GemmParams& p, float v, int64_t
 
 // Writes a wave's accumulators (FM x FN blocks of 32x32 in the MFMA C
 // layout) through the epilogue. Shared by the fp32 and split-bf16 kernels,
-// whose 32x32 MFMAs have the same C layout.
+// whose 32x32 MFMAs have the same C layout. Lane l holds rows
+// 8*(r/4) + 4*(l/32) + r%4 of column l%32 of each block. A wave whose
+// sub-tile lies inside C (every wave of an interior tile) stores without
+// per-element bounds tests, from one base address and 16 precomputed row
+// offsets; the tests made each of the lane's values a branch region.
 template <class TL, Epi EPI>
 __device__ __forceinline__ void store_c(const GemmParams& p, const f32x16 (&acc)[TL::FM][TL::FN], int64_t m0,
                                         int64_t n0, int wm, int wn, int lane) {
@@ -142,20 +146,28 @@ __device__ __forceinline__ void store_c(const GemmParams& p, const f32x16 (&acc)
   const int64_t M = p.m, N = p.n;
   const int lcol = lane & 31;
   const int lrow4 = (lane >> 5) * 4;
+  const int64_t r0 = m0 + wm * TL::TM, c0 = n0 + wn * TL::TN;
+  const bool inside = r0 + TL::TM <= M && c0 + TL::TN <= N;
+  int roff[16];  // element offsets of the lane's 16 rows in a block (ldc < 2^26: launch_gemm)
+#pragma unroll
+  for (int r = 0; r < 16; r++) roff[r] = EPI == Epi::Generic ? 0 : ((r >> 2) * 8 + lrow4 + (r & 3)) * (int)p.ldc;
   if constexpr (EPI == Epi::GeGLU) {
     static_assert(FN % 2 == 0, "GeGLU pairs column blocks");
     const int64_t F = N / 2;
 #pragma unroll
     for (int pj = 0; pj < FN / 2; pj++) {
-      const int64_t fcol = (n0 + wn * TL::TN) / 2 + pj * 32 + lcol;
+      const int64_t fcol = c0 / 2 + pj * 32 + lcol;
 #pragma unroll
       for (int i = 0; i < FM; i++) {
+        float* base = p.c + (r0 + i * 32) * p.ldc + fcol;
+        if (inside) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
-          if (row < M && fcol < F) {
-            const float g = acc[i][2 * pj][r], u = acc[i][2 * pj + 1][r];
-            p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
+          for (int r = 0; r < 16; r++) base[roff[r]] = gelu_tanh_ref(acc[i][2 * pj][r]) * acc[i][2 * pj + 1][r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int64_t row = r0 + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
+            if (row < M && fcol < F) base[roff[r]] = gelu_tanh_ref(acc[i][2 * pj][r]) * acc[i][2 * pj + 1][r];
           }
         }
       }
@@ -165,10 +177,20 @@ __device__ __forceinline__ void store_c(const GemmParams& p, const f32x16 (&acc)
     for (int i = 0; i < FM; i++) {
 #pragma unroll
       for (int j = 0; j < FN; j++) {
-        const int64_t col = n0 + wn * TL::TN + j * 32 + lcol;
+        const int64_t col = c0 + j * 32 + lcol;
+        if constexpr (EPI == Epi::None) {
+          float* base = p.c + (r0 + i * 32) * p.ldc + col;
+          if (inside) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) base[roff[r]] = acc[i][j][r];
+            continue;
+          }
+        }
+        // (the Generic epilogue keeps one checked path: its optional operands
+        // already hold many registers)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int64_t row = m0 + wm * TL::TM + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
+          const int64_t row = r0 + i * 32 + (r >> 2) * 8 + lrow4 + (r & 3);
           if (row < M && col < N) p.c[row * p.ldc + col] = epi_value<EPI>(p, acc[i][j][r], row, col);
         }
       }
@@ -1022,6 +1044,9 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   if (g.m == 0 || g.n == 0) return FA_OK;
   if (g.epi == Epi::GeGLU && (g.n % 64 != 0))
     return set_error(ctx, FA_ERR_ARG, "GeGLU product needs n (2F) divisible by 64, got %lld", (long long)g.n);
+  // the epilogue addresses a 32-row block with 32-bit offsets
+  if (g.ldc >= (1LL << 26))
+    return set_error(ctx, FA_ERR_ARG, "MatMul: ldc %lld above 2^26 elements", (long long)g.ldc);
   GemmParams p;
   std::memset(&p, 0, sizeof p);
   p.m = g.m; p.n = g.n; p.k = g.k;
