@@ -51,10 +51,36 @@ __device__ __forceinline__ float exp_flush(float x) {
   return x < -87.f ? 0.f : __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
-// Sum over the 64 lanes of a wavefront (result in every lane).
+// v of the lane 32 apart (lane ^ 32) by v_permlane32_swap, a VALU op: a
+// swap of v with itself leaves the lane's own value in one result and the
+// partner's in the other (the partner's is the second for lanes 0-31).
+__device__ __forceinline__ float lane_xor32(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 63) < 32 ? r[1] : r[0]);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront (result in every lane): the xor
+// butterfly over lane distances 32, 16, 8, 4, 2, 1, each step adding the
+// partner's value to the lane's own, without an LDS round trip per step
+// (ds_bpermute). 32 and 16: v_permlane32/16_swap (own and partner in the
+// two results); 8, 4, 2, 1: DPP row rotations by 8, 4, 2, 1, which after
+// the previous steps (the row's values repeat with period 2d) read exactly
+// the xor-d partner. Same additions in the same order as a shuffle
+// butterfly, so the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  v = v + dpp_f32<0x128>(v);  // row_ror:8
+  v = v + dpp_f32<0x124>(v);  // row_ror:4
+  v = v + dpp_f32<0x122>(v);  // row_ror:2
+  v = v + dpp_f32<0x121>(v);  // row_ror:1
   return v;
 }
 

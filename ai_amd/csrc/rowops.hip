@@ -272,8 +272,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   const f32x4 c = cv, sv = svv;
   if constexpr (D == 256) {
     f32x4 w;
-    w.x = __shfl_xor(v[0].x, 32, 64); w.y = __shfl_xor(v[0].y, 32, 64);
-    w.z = __shfl_xor(v[0].z, 32, 64); w.w = __shfl_xor(v[0].w, 32, 64);
+    w.x = lane_xor32(v[0].x); w.y = lane_xor32(v[0].y);
+    w.z = lane_xor32(v[0].z); w.w = lane_xor32(v[0].w);
     f32x4 r;
     if (lane < 32) {  // y_i = x_i c - x_{i+h} s
       r.x = v[0].x * c.x - w.x * sv.x; r.y = v[0].y * c.y - w.y * sv.y;
@@ -385,8 +385,8 @@ __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int h
     x[0].x = x[0].x * inv * gg.x; x[0].y = x[0].y * inv * gg.y;
     x[0].z = x[0].z * inv * gg.z; x[0].w = x[0].w * inv * gg.w;
     f32x4 o;
-    o.x = __shfl_xor(x[0].x, 32, 64); o.y = __shfl_xor(x[0].y, 32, 64);
-    o.z = __shfl_xor(x[0].z, 32, 64); o.w = __shfl_xor(x[0].w, 32, 64);
+    o.x = lane_xor32(x[0].x); o.y = lane_xor32(x[0].y);
+    o.z = lane_xor32(x[0].z); o.w = lane_xor32(x[0].w);
     f32x4 r;
     if (lane < 32) {  // y_i = x_i c - x_{i+h} s
       r.x = x[0].x * c[j].x - o.x * sv[j].x; r.y = x[0].y * c[j].y - o.y * sv[j].y;
