@@ -56,7 +56,7 @@ METRIC = "sentences/sec @ batch32×seq256 on 1 MI355X; GEMM % of fp32 MFMA peak"
 # 1 GiB copy kernel reads on the same counters (profiles/
 # gemm_gateup_c2_hbm_traffic.md). Re-measured whenever the kernel changes;
 # applies to the C2 workload only.
-GATEUP_TRAFFIC_C2 = {"bytes": (2 * 29701 + 30370) * 1024, "kernel_rev": "x3-128x256w8-vgpr128"}
+GATEUP_TRAFFIC_C2 = {"bytes": (2 * 30326 + 29578) * 1024, "kernel_rev": "x3-128x256w8-chunkmajor-lds"}
 
 
 def parse():
