@@ -4,6 +4,7 @@
   python -m ai_amd.bench_gemm --shape 32768,768,768 --reps 5 --no-check
   python -m ai_amd.bench_gemm --shape 128,2304,768 --shape 1,768,3072
   python -m ai_amd.bench_gemm --library       # against the vendor bf16 GEMM
+  python -m ai_amd.bench_gemm --a-data zeros  # same work on data that draws less power
 
 One JSON line per shape: mean launch time over back-to-back calls, fp32-
 equivalent TFLOP/s (2*M*N*K / time) and the max |error| against a float64
@@ -28,7 +29,19 @@ SHAPES = [(5517, 1280, 768), (5517, 768, 768), (5517, 2304, 768), (5517, 768, 11
           (32768, 1280, 768), (32768, 768, 768), (32768, 2304, 768), (32768, 768, 1152)]
 
 
-def run(shapes, reps: int, check: bool) -> list[dict]:
+def make_a(rng, M: int, K: int, kind: str) -> np.ndarray:
+    """The A operand: normal fp32 values (every split term busy), zeros, or
+    bf16-exact values (the mid and lo terms zero). Same MFMA work in every
+    case; the time differs only through the power the data draws."""
+    if kind == "zeros":
+        return np.zeros((M, K), np.float32)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    if kind == "bf16":
+        a = (a.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    return a
+
+
+def run(shapes, reps: int, check: bool, a_data: str = "normal") -> list[dict]:
     ctx = N.Context(0)
     L = N.lib()
     kernel = os.environ.get("FA_GEMM_XTILE", "auto")
@@ -37,7 +50,7 @@ def run(shapes, reps: int, check: bool) -> list[dict]:
     out = []
     for (M, Nn, K) in shapes:
         rng = np.random.default_rng(M + Nn + K)
-        a = rng.standard_normal((M, K)).astype(np.float32)
+        a = make_a(rng, M, K, a_data)
         wb = S.normal_bf16(3, "bench_gemm", 0.05, (Nn, K))
         da, db, dc = C.c_void_p(), C.c_void_p(), C.c_void_p()
         for p, n in ((da, a.nbytes), (db, wb.nbytes), (dc, M * Nn * 4)):
@@ -50,7 +63,7 @@ def run(shapes, reps: int, check: bool) -> list[dict]:
 
         call()
         ctx.sync()
-        rec = dict(kernel=kernel, M=M, N=Nn, K=K)
+        rec = dict(kernel=kernel, M=M, N=Nn, K=K, a_data=a_data)
         if check:
             c = np.empty((M, Nn), np.float32)
             N.check(ctx.h, L.fa_memcpy_d2h(ctx.h, c.ctypes.data, dc, c.nbytes))
@@ -203,6 +216,8 @@ def main() -> None:
                     help="time the MatMulFused drop-in at the gate shape with float32/bf16 weights in both layouts")
     ap.add_argument("--library", action="store_true",
                     help="time each shape against the vendor bf16 GEMM of the same MFMA work (M x 3K . 3K x N)")
+    ap.add_argument("--a-data", default="normal", choices=["normal", "zeros", "bf16"],
+                    help="values of A: normal fp32 (default), zeros, or bf16-exact (mid and lo split terms zero)")
     a = ap.parse_args()
     if a.dropin:
         dropin(a.reps)
@@ -211,7 +226,7 @@ def main() -> None:
     if a.library:
         library(shapes, a.reps)
         return
-    run(shapes, a.reps, not a.no_check)
+    run(shapes, a.reps, not a.no_check, a.a_data)
 
 
 if __name__ == "__main__":
