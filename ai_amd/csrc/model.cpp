@@ -226,6 +226,13 @@ int microbatch_count(int64_t tokens, double sum_l2) {
   return tokens >= 24576 ? 2 : 3;
 }
 
+// HBM bytes of one residual_norm launch: the product (and its second K
+// part when split) and x read, x written, and the next norm's input written
+// when there is a next norm.
+double resnorm_bytes(int64_t rows, int64_t d, const float* o2, const float* g_next) {
+  return (double)rows * d * 4.0 * (3.0 + (o2 ? 1.0 : 0.0) + (g_next ? 1.0 : 0.0));
+}
+
 // Brackets one launch with events when profiling.
 struct Probe {
   fa_model* m;
@@ -1022,7 +1029,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       pr.done();
     }
     {
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)rows * d * 16.0);
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, o2_o, L.g_pre_ffn));
       if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_attn, L.g_pre_ffn, eps, st, o2_o)))
         return rc;
       pr.done();
@@ -1047,7 +1054,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     const float* g_next = (l + 1 < NL) ? m->layers[l + 1].g_in : m->g_final;
     {
       // variant 2: the per-layer-input block reads x itself, so no norm here
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)rows * d * 16.0);
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, o2_dn, v2 ? nullptr : g_next));
       if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_ffn, v2 ? nullptr : g_next, eps, st,
                                          o2_dn)))
         return rc;
@@ -1072,7 +1079,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
         if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
         pr.done();
       }
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, (double)rows * d * 16.0);
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, o2_pl, g_next));
       if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_ple_post, g_next, eps, st, o2_pl, L.scalar)))
         return rc;
       pr.done();

@@ -353,12 +353,16 @@ struct KvTilesParams {
 };
 
 constexpr int kTileImg = 3 * 32 * 256;  // bf16 per key or value image
-constexpr int kVtStride = 258;          // floats per LDS row of the value transpose (conflict-free column reads)
+// floats per LDS row of the value transpose (128 dims): the column reads of
+// one wave (16 consecutive dims x keys 4c + const, c = 0..3) land on banks
+// 16c + dim mod 64, all distinct, since 4 * 132 = 16 (mod 64)
+constexpr int kVtStride = 132;
 
-// The key image of (tile, hk): wave w takes tokens w, w + 4, ..., 4 dims per
-// lane; rows past the sequence are clamped to its last token (every load
-// issued up front, none conditional) and written as zeros.
-__device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int wave, int lane) {
+// Keys 16*half .. 16*half + 15 of the key image of (tile, hk): wave w takes
+// keys 16*half + w, + 4, ..., 4 dims per lane; rows past the sequence are
+// clamped to its last token (every load issued up front, none conditional)
+// and written as zeros.
+__device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int half_, int wave, int lane) {
   constexpr int D = 256, half = D / 2;
   const int sq = a.tile_seq[tile];
   const int t0 = 32 * (tile - a.cut[sq]);
@@ -368,18 +372,18 @@ __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int h
   uint16_t* kimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg);
   const f32x4 gg = *reinterpret_cast<const f32x4*>(a.gk + lane * 4);
   const int i0 = (lane & 31) * 4;
-  f32x4 v[8], c[8], sv[8];
+  f32x4 v[4], c[4], sv[4];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int64_t row = r_first + min(wave + 4 * j, n - 1);
+  for (int j = 0; j < 4; j++) {
+    const int64_t row = r_first + min(16 * half_ + wave + 4 * j, n - 1);
     v[j] = *reinterpret_cast<const f32x4*>(a.qkv + row * width + (int64_t)(a.H + hk) * D + lane * 4);
     const int t = a.pos[row];
     c[j] = *reinterpret_cast<const f32x4*>(a.cs + (int64_t)t * half + i0);
     sv[j] = *reinterpret_cast<const f32x4*>(a.sn + (int64_t)t * half + i0);
   }
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int k = wave + 4 * j;
+  for (int j = 0; j < 4; j++) {
+    const int k = 16 * half_ + wave + 4 * j;
     f32x4 x[1] = {v[j]};
     const float inv = rms_inv(sumsq<1>(x), D, a.eps);
     x[0].x = x[0].x * inv * gg.x; x[0].y = x[0].y * inv * gg.y;
@@ -411,10 +415,10 @@ __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int h
   }
 }
 
-// The value image of (tile, hk): rows into LDS (clamped loads, zeros past
-// the sequence), then transposed, 16 bytes (8 slots of one dim and term) per
-// store.
-__device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int hk, int wave, int lane,
+// Dims 128*half .. 128*half + 127 of the value image of (tile, hk): rows
+// into LDS (clamped loads, zeros past the sequence), then transposed, 16
+// bytes (8 slots of one dim and term) per store.
+__device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int hk, int half_, int wave, int lane,
                                            float (*Vt)[kVtStride]) {
   constexpr int D = 256;
   const int sq = a.tile_seq[tile];
@@ -423,29 +427,29 @@ __device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int
   const int64_t r_first = a.cu[sq] - a.row0 + t0;
   const int width = (a.H + 2 * a.Hkv) * D;
   uint16_t* vimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg) + kTileImg;
-  f32x4 v[8];
+  float2 v[8];
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int64_t row = r_first + min(wave + 4 * j, n - 1);
-    v[j] = *reinterpret_cast<const f32x4*>(a.qkv + row * width + (int64_t)(a.H + a.Hkv + hk) * D + lane * 4);
+    v[j] = *reinterpret_cast<const float2*>(a.qkv + row * width + (int64_t)(a.H + a.Hkv + hk) * D + 128 * half_ +
+                                            lane * 2);
   }
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int k = wave + 4 * j;
-    const f32x4 x = k < n ? v[j] : f32x4{0.f, 0.f, 0.f, 0.f};
-    *reinterpret_cast<float2*>(&Vt[k][lane * 4]) = make_float2(x.x, x.y);
-    *reinterpret_cast<float2*>(&Vt[k][lane * 4 + 2]) = make_float2(x.z, x.w);
+    *reinterpret_cast<float2*>(&Vt[k][lane * 2]) = k < n ? v[j] : make_float2(0.f, 0.f);
   }
   __syncthreads();
   const int tid = wave * 64 + lane;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < 2; i++) {
     const int u = tid + 256 * i;
-    const int d = u >> 2, c = u & 3;  // dim, chunk of 8 slots: keys 4c .. 4c+3, 16 + 4c .. 16 + 4c+3
+    const int dl = u >> 2, c = u & 3;  // local dim, chunk of 8 slots: keys 4c .. 4c+3, 16 + 4c .. 16 + 4c+3
+    const int d = 128 * half_ + dl;
     uint32_t th[8], tm[8], tl[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      const Split3 sp = split3(Vt[(e >> 2) * 16 + 4 * c + (e & 3)][d]);
+      const Split3 sp = split3(Vt[(e >> 2) * 16 + 4 * c + (e & 3)][dl]);
       th[e] = sp.h;
       tm[e] = sp.m;
       tl[e] = sp.l;
@@ -460,17 +464,20 @@ __device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int
   }
 }
 
-// Blocks 2i (key image) and 2i + 1 (value image) of (tile t_lo + i / Hkv,
-// kv head i % Hkv).
+// Blocks 4i + j of (tile t_lo + i / Hkv, kv head i % Hkv): j = 0, 1 the
+// key image's two halves of 16 keys, j = 2, 3 the value image's two halves
+// of 128 dims (half-tile blocks: twice the blocks of whole-image ones, so
+// more of a launch's loads are in flight).
 __global__ __launch_bounds__(256) void kv_tiles_kernel(KvTilesParams a) {
   __shared__ __attribute__((aligned(16))) float Vt[32][kVtStride];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t b = blockIdx.x;
-  const int tile = a.t_lo + (int)(b / (2 * a.Hkv)), hk = (int)((b >> 1) % a.Hkv);
-  if (b & 1)
-    value_tile(a, tile, hk, wave, lane, Vt);
+  const int tile = a.t_lo + (int)(b / (4 * a.Hkv)), hk = (int)((b >> 2) % a.Hkv);
+  const int part = (int)(b & 3);
+  if (part >= 2)
+    value_tile(a, tile, hk, part - 2, wave, lane, Vt);
   else
-    key_tile(a, tile, hk, wave, lane);
+    key_tile(a, tile, hk, part, wave, lane);
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, int64_t n) {
@@ -657,7 +664,7 @@ int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int3
   KvTilesParams a;
   a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.pos = d_pos; a.cs = cos_t; a.sn = sin_t;
   a.cu = d_cu_seqlens; a.cut = d_cu_tiles; a.tile_seq = d_tile_seq; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
-  hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(2 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
