@@ -478,6 +478,51 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
   const int tok = (qvalid ? row : rb) / G;
   const int head = hk * G + (qvalid ? row : rb) % G;
 
+  // the item's key tiles: the union of its rows' windows
+  const int tok_lo = rb / G, tok_hi = (min(rb + TL_ROWS, nrows) - 1) / G;
+  int kbeg = 0, kend = L;
+  if (p.window > 0) {
+    kbeg = max(0, tok_lo - p.window + 1);
+    kend = min(L, tok_hi + p.window);
+  }
+  int tb = kbeg / TL_KEYS, te = (kend + TL_KEYS - 1) / TL_KEYS;
+  if (p.kparts > 1) {  // this part's run of tiles (possibly none)
+    const int per = (te - tb + p.kparts - 1) / p.kparts;
+    const int nb = tb + part * per;
+    te = min(te, nb + per);
+    tb = nb;
+  }
+
+  const uint16_t* img0 = p.img + ((int64_t)p.cut[seq] * p.Hkv + hk) * (2 * TL_IMG);
+  const int64_t tstride = (int64_t)p.Hkv * 2 * TL_IMG;
+  // 48 loads of 1 KB per image, six per wave
+  auto issue = [&](const uint16_t* src, uint16_t* dst) {
+#pragma unroll
+    for (int j = 0; j < 48 / TL_W; j++) {
+      const int c = wave + TL_W * j;
+      __builtin_amdgcn_global_load_lds(src + c * 512 + lane * 8, (__attribute__((address_space(3))) void*)&dst[c * 512],
+                                       16, 0, 0);
+    }
+  };
+
+  if (rb + 16 * wave >= nrows) {
+    // every row of this wave lies past the sequence's rows (the last item
+    // of a sequence): the wave issues its share of each image load and
+    // takes part in every barrier of the loop below, in the same order,
+    // and computes nothing
+    if (tb < te) {
+      issue(img0 + tb * tstride, Ks);
+      for (int tt = tb; tt < te; tt++) {
+        dl_barrier<0x0F70>();
+        issue(img0 + tt * tstride + TL_IMG, ((tt - tb) & 1) ? Vs1 : Vs0);
+        dl_barrier<0xC07F>();
+        issue(img0 + min(tt + 1, te - 1) * tstride, Ks);
+      }
+      dl_barrier<0x0F70>();
+    }
+    return;
+  }
+
   bf16x8 qt[3][HD / 32];
   {
     // q normed (RMSNorm, gain) and rotated (RoPE at the token's position)
@@ -525,33 +570,6 @@ __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesPara
       split_pack8(x[c][0], x[c][1], qt[0][c], qt[1][c], qt[2][c]);
     }
   }
-
-  // the item's key tiles: the union of its rows' windows
-  const int tok_lo = rb / G, tok_hi = (min(rb + TL_ROWS, nrows) - 1) / G;
-  int kbeg = 0, kend = L;
-  if (p.window > 0) {
-    kbeg = max(0, tok_lo - p.window + 1);
-    kend = min(L, tok_hi + p.window);
-  }
-  int tb = kbeg / TL_KEYS, te = (kend + TL_KEYS - 1) / TL_KEYS;
-  if (p.kparts > 1) {  // this part's run of tiles (possibly none)
-    const int per = (te - tb + p.kparts - 1) / p.kparts;
-    const int nb = tb + part * per;
-    te = min(te, nb + per);
-    tb = nb;
-  }
-
-  const uint16_t* img0 = p.img + ((int64_t)p.cut[seq] * p.Hkv + hk) * (2 * TL_IMG);
-  const int64_t tstride = (int64_t)p.Hkv * 2 * TL_IMG;
-  // 48 loads of 1 KB per image, six per wave
-  auto issue = [&](const uint16_t* src, uint16_t* dst) {
-#pragma unroll
-    for (int j = 0; j < 48 / TL_W; j++) {
-      const int c = wave + TL_W * j;
-      __builtin_amdgcn_global_load_lds(src + c * 512 + lane * 8, (__attribute__((address_space(3))) void*)&dst[c * 512],
-                                       16, 0, 0);
-    }
-  };
 
   f32x4 oacc[HD / 16];  // O^T: dims 16db + 4g + r of row lq
 #pragma unroll

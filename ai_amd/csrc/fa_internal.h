@@ -115,6 +115,10 @@ struct GemmArgs {
   // values, b_plane elements apart (fp32 weights that are not bf16-exact)
   int b_terms = 1;
   int64_t b_plane = 0;
+  // the launch runs beside other streams' kernels (the encoder's
+  // micro-batches): the tile choice can count on them to fill the CUs its
+  // own tiles leave idle
+  bool shared = false;
 };
 
 // B [k x n] (FA_B_KN) or [n x k] (FA_B_NK), leading dimension ldb -> bf16

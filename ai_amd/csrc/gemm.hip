@@ -912,10 +912,20 @@ bool use_f32_mfma() {
 // 1280, 2304; one pooled row against K = 3072, 15.9 vs 33.7 us; 512 x 768
 // x 1152, 12.3 vs 15.2 us. With more tiles it loses (256 x 2304 x 768: 14.7
 // vs 11.2 us): every tile re-splits its A rows and re-reads its B columns.
-XTileId pick_xtile(int64_t m, int64_t n, int64_t k, int ksplit, Epi epi, int cus) {
+//
+// A launch that shares the GPU with other streams' kernels (shared) takes
+// the 128x256 tile from 0.75 tiles per CU on: the other streams fill the
+// CUs it leaves idle, and it splits each A element half as often (per
+// forward: C5's micro-batch qkv products at about 6 000 rows, 13.36 ->
+// 13.17 ms; C4's gate|up at about 2 900 rows, 11.49 -> 11.37 ms; C3's o
+// and down products unchanged); at 0.3-0.5 tiles per CU (C2's
+// micro-batches, 1 840 rows) its longer per-tile chain loses (qkv: 5.10 ->
+// 5.40 ms, gate|up 5.10 -> 5.15).
+XTileId pick_xtile(int64_t m, int64_t n, int64_t k, int ksplit, Epi epi, int cus, bool shared) {
   if (((m + 31) / 32) * ((n + 63) / 64) * ksplit <= cus) return XTileId::small;
   const int64_t tiles256 = ((m + 127) / 128) * ((n + 255) / 256) * ksplit;
-  if (2 * tiles256 >= 3LL * cus && k / (32LL * ksplit) >= 24) return XTileId::x128x256w8;
+  const int64_t need = shared ? 3LL * cus : 6LL * cus;  // 4 x (0.75 or 1.5 tiles per CU)
+  if (4 * tiles256 >= need && k / (32LL * ksplit) >= 24) return XTileId::x128x256w8;
   const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128) * ksplit;
   if (2 * tiles128 < cus) return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
   if (tiles128 > 2 * cus && 4 * tiles128 <= 5 * 2 * cus) return XTileId::x64x128;
@@ -1081,7 +1091,7 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   } else if (fast && bf16 && !use_f32_mfma()) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     XTileId t = (XTileId)forced_xtile();
-    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.k, p.ksplit, g.epi, cus);
+    if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.k, p.ksplit, g.epi, cus, g.shared);
     dispatch_x3(t, p, g.epi, s);
   } else if (fast) {
     TileId t = (TileId)forced_tile();

@@ -963,6 +963,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     int rc;
     {
       fa::GemmArgs g;
+      g.shared = groups > 1;
       g.m = rows; g.n = L.width; g.k = d; g.a = xnr; g.lda = d; fa::set_b(g, L.wqkv); g.c = qkvr; g.ldc = L.width;
       fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * rows * L.width * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
@@ -1022,6 +1023,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::GemmArgs g;
+      g.shared = groups > 1;
       g.m = rows; g.n = d; g.k = H * D; g.a = attr; g.lda = H * D; fa::set_b(g, L.wo); g.c = or_;
       g.ldc = d; g.ksplit = ks_o; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_O, 2.0 * rows * d * H * D, 0);
@@ -1036,6 +1038,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::GemmArgs g;
+      g.shared = groups > 1;
       g.m = rows; g.n = 2 * F; g.k = d; g.a = xnr; g.lda = d; fa::set_b(g, L.wgu); g.c = gur; g.ldc = F;
       g.epi = fa::Epi::GeGLU;
       fa::Probe pr(m, FA_K_GEMM_GATEUP, 2.0 * rows * 2 * F * d, 0);
@@ -1044,6 +1047,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::GemmArgs g;
+      g.shared = groups > 1;
       g.m = rows; g.n = d; g.k = F; g.a = gur; g.lda = F; fa::set_b(g, L.wdown); g.c = or_; g.ldc = d;
       g.ksplit = ks_down; g.c_split = M * d;
       fa::Probe pr(m, FA_K_GEMM_DOWN, 2.0 * rows * d * F, 0);
@@ -1064,6 +1068,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       // x = (x + RMSNorm(gelu(x . Wg^T) * ple_l . Wp^T; g)) * scalar (embed.go:359-371)
       {
         fa::GemmArgs g;
+        g.shared = groups > 1;
         g.m = rows; g.n = P; g.k = d; g.a = xr; g.lda = d; fa::set_b(g, L.wple_gate); g.c = gur; g.ldc = P;
         g.epi = fa::Epi::Generic; g.act = FA_ACT_GELU; g.mul = ple + r0 * NL * P + (int64_t)l * P;
         g.ldm = (int64_t)NL * P;
@@ -1073,6 +1078,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       }
       {
         fa::GemmArgs g;
+        g.shared = groups > 1;
         g.m = rows; g.n = d; g.k = P; g.a = gur; g.lda = P; fa::set_b(g, L.wple_proj); g.c = or_; g.ldc = d;
         g.ksplit = ks_ple; g.c_split = M * d;
         fa::Probe pr(m, FA_K_GEMM_PLE, 2.0 * rows * d * P, 0);
