@@ -245,7 +245,7 @@ int attention_varlen_qblock();
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
                     const int32_t* d_pos, const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
                     const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
-                    hipStream_t s);
+                    hipStream_t s, bool norm_v = false);
 
 struct AttnTilesArgs {
   const float* qkv;       // raw q read here (rows of the launch start at packed row row0)

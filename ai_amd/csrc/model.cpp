@@ -737,34 +737,50 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   if (dim <= 0) dim = full;
   if (dim > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
   // ---- plan (host): cu_seqlens and attention work items ----
-  // Models whose layers all have head_dim 256 (EmbeddingGemma) take the
-  // split-bf16 tile attention: items of attention_tiles_rows() (token, query
-  // head) rows per kv head, keys and values as per-tile images (every
-  // sequence starts a tile of attention_tiles_keys() tokens: cu_tiles [B+1]
-  // and each tile's sequence). Others take the fp32-MFMA attention, items of
-  // attention_varlen_qblock() queries per head.
+  // Layers with head_dim 256 (every EmbeddingGemma layer, EmbeddingGemma
+  // 2's sliding layers) take the split-bf16 tile attention: items of
+  // attention_tiles_rows() (token, query head) rows per kv head, keys and
+  // values as per-tile images (every sequence starts a tile of
+  // attention_tiles_keys() tokens: cu_tiles [B+1] and each tile's
+  // sequence). Other layers take the fp32-MFMA attention, items of
+  // attention_varlen_qblock() queries per head. The two kinds of item sit
+  // in separate lists (tile items first), each ordered by group.
   int64_t M_all = 0;
   for (int b = 0; b < B; b++) M_all += std::max(0, lengths[b]);
   // (batches of very short sequences, under 32 tokens on average, keep the
   // fp32 kernel's 16-key tiles: a 32-key tile would be mostly padding)
-  const bool tiles = !v2 && m->max_hd == H * 256 && M_all > fa::kAttnSplitRows && M_all >= 32LL * B;
+  const bool tiles_ok = M_all > fa::kAttnSplitRows && M_all >= 32LL * B;
+  // the tile layers share one kv head count (the item rows and image slots
+  // depend on it); a model whose head_dim-256 layers differ in it keeps
+  // the fp32 kernel
+  int hkv_t = 0;
+  bool mixed_hkv = false;
+  for (const fa::Layer& L : m->layers) {
+    if (L.D != 256) continue;
+    if (hkv_t && L.Hkv != hkv_t) mixed_hkv = true;
+    hkv_t = L.Hkv;
+  }
+  auto layer_tiles = [&](const fa::Layer& L) { return tiles_ok && !mixed_hkv && L.D == 256; };
+  bool any_tiles = false, any_var = false;
+  for (int l = 0; l < n_run; l++) (layer_tiles(m->layers[l]) ? any_tiles : any_var) = true;
   const int tkeys = fa::attention_tiles_keys();
-  const int G = H / c.num_key_value_heads;
-  const int istep = tiles ? fa::attention_tiles_rows() : fa::attention_varlen_qblock();
-  const int iheads = tiles ? c.num_key_value_heads : H;  // items per row block
-  int64_t M = 0, n_items = 0, n_tiles = 0;
+  const int Gt = any_tiles ? H / hkv_t : 1;  // query heads per kv head of the tile layers
+  const int istep_t = fa::attention_tiles_rows(), istep_v = fa::attention_varlen_qblock();
+  int64_t M = 0, n_items_t = 0, n_items_v = 0, n_tiles = 0;
   for (int b = 0; b < B; b++) {
     if (lengths[b] < 1 || lengths[b] > T)
       return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
     M += lengths[b];
-    const int64_t rows_b = tiles ? (int64_t)G * lengths[b] : lengths[b];
-    n_items += (rows_b + istep - 1) / istep * iheads;
-    n_tiles += (lengths[b] + tkeys - 1) / tkeys;
+    if (any_tiles) {
+      n_items_t += ((int64_t)Gt * lengths[b] + istep_t - 1) / istep_t * hkv_t;
+      n_tiles += (lengths[b] + tkeys - 1) / tkeys;
+    }
+    if (any_var) n_items_v += ((int64_t)lengths[b] + istep_v - 1) / istep_v * H;
   }
+  const int64_t n_items = n_items_t + n_items_v;
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   double sum_l2 = 0;
   for (int i = 0; i < B; i++) sum_l2 += (double)lengths[i] * lengths[i];
-  if (!tiles) n_tiles = 0;
   const size_t plan_ints = 2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles;
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
@@ -785,7 +801,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   cut_h[0] = 0;
   for (int b = 0; b < B; b++) {
     cu_h[b + 1] = cu_h[b] + lengths[b];
-    cut_h[b + 1] = cut_h[b] + (tiles ? (lengths[b] + tkeys - 1) / tkeys : 0);
+    cut_h[b + 1] = cut_h[b] + (any_tiles ? (lengths[b] + tkeys - 1) / tkeys : 0);
     for (int q = cut_h[b]; q < cut_h[b + 1]; q++) tseq_h[q] = b;
   }
   // Micro-batches: with enough tokens the sequences are cut into groups of
@@ -816,47 +832,51 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   // heads) become 48 workgroups of two 16-key tiles, its 3 tile items 12
   // workgroups of one 32-key tile.
   const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  const int64_t n_items_all = n_items;
-  int kparts = 1;
-  if (!tiles && groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_all <= cus) {
-    kparts = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_all, 1));
-    kparts = std::max(1, std::min(kparts, (T + 31) / 32));  // at least two 16-key tiles per run
-    if (const int f = fa::attention_key_parts_forced()) kparts = f;
+  int kparts_v = 1, kparts_t = 1;  // key runs per fp32 item, per tile item
+  if (any_var && groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_v <= cus) {
+    kparts_v = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_v, 1));
+    kparts_v = std::max(1, std::min(kparts_v, (T + 31) / 32));  // at least two 16-key tiles per run
+    if (const int f = fa::attention_key_parts_forced()) kparts_v = f;
   }
-  if (tiles) {
+  if (any_tiles) {
     // fewer tile items than CUs (one or two long sequences): each item's key
     // tiles are cut into runs of at least four, one workgroup each
     const int max_tiles = (T + tkeys - 1) / tkeys;
-    if (n_items_all < cus) {
-      kparts = (int)std::min<int64_t>(fa::kMaxKeyParts, cus / std::max<int64_t>(n_items_all, 1));
-      kparts = std::max(1, std::min(kparts, max_tiles / 4));
+    if (n_items_t < cus) {
+      kparts_t = (int)std::min<int64_t>(fa::kMaxKeyParts, cus / std::max<int64_t>(n_items_t, 1));
+      kparts_t = std::max(1, std::min(kparts_t, max_tiles / 4));
     }
-    if (const int f = fa::attention_key_parts_forced()) kparts = std::min(f, max_tiles);
+    if (const int f = fa::attention_key_parts_forced()) kparts_t = std::min(f, max_tiles);
   }
   // Work items of each group, longest sequences first: an item's work grows
   // with its sequence's length, and dispatching the long ones first
   // shortens the tail. Tile items (sequence, first row, kv head); fp32
   // items (sequence, first query, head).
   std::vector<int>& order = m->seq_order;
-  int64_t it = 0, group_items[fa::kMaxMicrobatches] = {};
-  for (int gi = 0; gi < groups; gi++) {
-    const int b0 = gb[gi], b1 = gb[gi + 1];
-    order.resize(b1 - b0);
-    for (int b = b0; b < b1; b++) order[b - b0] = b;
-    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
-    const int64_t first = it;
-    for (int b : order) {
-      const int rows_b = tiles ? G * lengths[b] : lengths[b];
-      for (int q0 = 0; q0 < rows_b; q0 += istep) {
-        for (int h = 0; h < iheads; h++) {
-          items_h[3 * it] = b;
-          items_h[3 * it + 1] = q0;
-          items_h[3 * it + 2] = h;
-          it++;
+  int64_t it = 0, group_items_t[fa::kMaxMicrobatches] = {}, group_items_v[fa::kMaxMicrobatches] = {};
+  for (int list = 0; list < 2; list++) {
+    if (!(list == 0 ? any_tiles : any_var)) continue;
+    const int istep = list == 0 ? istep_t : istep_v;
+    const int iheads = list == 0 ? hkv_t : H;  // items per row block
+    for (int gi = 0; gi < groups; gi++) {
+      const int b0 = gb[gi], b1 = gb[gi + 1];
+      order.resize(b1 - b0);
+      for (int b = b0; b < b1; b++) order[b - b0] = b;
+      std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
+      const int64_t first = it;
+      for (int b : order) {
+        const int rows_b = list == 0 ? Gt * lengths[b] : lengths[b];
+        for (int q0 = 0; q0 < rows_b; q0 += istep) {
+          for (int h = 0; h < iheads; h++) {
+            items_h[3 * it] = b;
+            items_h[3 * it + 1] = q0;
+            items_h[3 * it + 2] = h;
+            it++;
+          }
         }
       }
+      (list == 0 ? group_items_t : group_items_v)[gi] = it - first;
     }
-    group_items[gi] = it - first;
   }
   int rc;
   if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
@@ -878,9 +898,10 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
                         (v2 ? (int64_t)NL * P : 0);
   int maxw = std::max(d, std::max(full, v2 ? m->E : d));
   for (int o : m->dense_out) maxw = std::max(maxw, o);
-  const int64_t part_floats = kparts > 1 ? fa::attention_part_floats(kparts, M, H, m->max_hd / H) : 0;
+  const int kparts_max = std::max(kparts_t, kparts_v);
+  const int64_t part_floats = kparts_max > 1 ? fa::attention_part_floats(kparts_max, M, H, m->max_hd / H) : 0;
   // key/value tile images: [tile][Hkv][key | value][3 * 32 * 256] bf16
-  const size_t img_bytes = (size_t)n_tiles * c.num_key_value_heads * 2 * (3 * 32 * 256) * 2;
+  const size_t img_bytes = (size_t)n_tiles * hkv_t * 2 * (3 * 32 * 256) * 2;
   const size_t f32_bytes = ((size_t)M * ncols + (size_t)B * (d + 2 * (size_t)maxw) + (size_t)part_floats) * 4 + 256;
   const size_t img_off = (f32_bytes + 255) & ~(size_t)255;
   const size_t ws_bytes = img_off + img_bytes + 4096;
@@ -930,12 +951,15 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     pr.done();
   }
   // one layer over rows [r0, r0 + rows) (the sequences of one group, whose
-  // attention items are items[0, n_it)) on stream st
-  auto run_layer = [&](int l, int b0, int b1, const int32_t* items, int64_t n_it, hipStream_t st) -> int {
+  // attention items are items_t[0, n_it_t) for a tile layer, items_v[0,
+  // n_it_v) otherwise) on stream st
+  auto run_layer = [&](int l, int b0, int b1, const int32_t* items_t, int64_t n_it_t, const int32_t* items_v,
+                       int64_t n_it_v, hipStream_t st) -> int {
     const int64_t r0 = cu_h[b0], rows = cu_h[b1] - r0;
     const fa::Layer& L = m->layers[l];
     const int D = L.D, Hkv = L.Hkv;
     const bool sliding = L.sliding;
+    const bool tiles = layer_tiles(L);
     // The N = hidden products (o, down, per-layer-input projection) split K
     // in two when their 128x128 tiles, counted over the concurrent groups,
     // give the CUs fewer than two each (C2: one stream 5 517 rows, or three
@@ -974,9 +998,12 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       // element each, tiles padded to 32 tokens); q is normed and rotated
       // by the attention as it loads it
       const int64_t ntl = cut_h[b1] - cut_h[b0];
-      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * 2 * Hkv * 4.0 * D + (double)ntl * Hkv * 2 * 3 * 32 * 256 * 2);
+      // (variant 2 norms the values too: each value half-block also reads
+      // the other half of its keys' values for the sum of squares)
+      fa::Probe pr(m, FA_K_QKNORM_ROPE, 0,
+                   (double)rows * (v2 ? 3 : 2) * Hkv * 4.0 * D + (double)ntl * Hkv * 2 * 3 * 32 * 256 * 2);
       if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t, cu_d, cut_d, tseq_d,
-                                    cut_h[b0], (int32_t)ntl, img, st)))
+                                    cut_h[b0], (int32_t)ntl, img, st, v2)))
         return rc;
       pr.done();
     } else {
@@ -991,8 +1018,8 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       a.qkv = qkvr; a.out = attr; a.row0 = r0; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
       a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
       a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
-      if (kparts > 1) {
-        a.kparts = kparts; a.rows = rows; a.part = attn_part;
+      if (kparts_v > 1) {
+        a.kparts = kparts_v; a.rows = rows; a.part = attn_part;
       }
       double pairs = 0;
       if (m->profiling) {
@@ -1012,12 +1039,12 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
         at.qkv = qkvr; at.img = img; at.out = attr; at.row0 = r0; at.cu_seqlens = cu_d; at.cu_tiles = cut_d;
         at.H = H; at.Hkv = Hkv; at.window = a.window; at.scale = a.scale;
         at.gq = L.g_q; at.eps = eps; at.cos_t = L.cos_t; at.sin_t = L.sin_t;
-        if (kparts > 1) {
-          at.kparts = kparts; at.rows = M; at.nrows = rows; at.part = attn_part;
+        if (kparts_t > 1) {
+          at.kparts = kparts_t; at.rows = M; at.nrows = rows; at.part = attn_part;
         }
-        if ((rc = fa::launch_attention_tiles(ctx, at, items, (int32_t)n_it, st))) return rc;
+        if ((rc = fa::launch_attention_tiles(ctx, at, items_t, (int32_t)n_it_t, st))) return rc;
       } else {
-        if ((rc = fa::launch_attention_varlen_items(ctx, a, items, (int32_t)n_it, st))) return rc;
+        if ((rc = fa::launch_attention_varlen_items(ctx, a, items_v, (int32_t)n_it_v, st))) return rc;
       }
       pr.done();
     }
@@ -1094,17 +1121,20 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   };
   if (groups == 1) {
     for (int l = 0; l < n_run; l++)
-      if ((rc = run_layer(l, 0, B, items_d, group_items[0], s))) return rc;
+      if ((rc = run_layer(l, 0, B, items_d, group_items_t[0], items_d + 3 * n_items_t, group_items_v[0], s)))
+        return rc;
   } else {
     // groups 1.. run on their own streams once the embeddings (and plan) are in
     FA_HIP_CHECK(ctx, hipEventRecord(m->ev_fork, s));
     for (int g = 1; g < groups; g++) FA_HIP_CHECK(ctx, hipStreamWaitEvent(m->mb_stream[g], m->ev_fork, 0));
     rc = FA_OK;
     for (int l = 0; l < n_run && !rc; l++) {
-      int64_t item0 = 0;
+      int64_t it0 = 0, iv0 = n_items_t;  // the group's first tile item, first fp32 item
       for (int g = 0; g < groups && !rc; g++) {
-        rc = run_layer(l, gb[g], gb[g + 1], items_d + 3 * item0, group_items[g], g ? m->mb_stream[g] : s);
-        item0 += group_items[g];
+        rc = run_layer(l, gb[g], gb[g + 1], items_d + 3 * it0, group_items_t[g], items_d + 3 * iv0, group_items_v[g],
+                       g ? m->mb_stream[g] : s);
+        it0 += group_items_t[g];
+        iv0 += group_items_v[g];
       }
     }
     // joined also after an error: later calls reuse the workspace on s

@@ -338,7 +338,9 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, 
 //   value image [term][dim][32 slots]: slot 8g + 4h + r holds key 16h + 4g +
 //   r (the order in which the attention's probabilities meet the values),
 //   the 16-byte chunk g of dim d at position g ^ ((d >> 1) & 3).
-// Tokens past the sequence are zeros.
+// Tokens past the sequence are zeros. With norm_v the values are first
+// RMS-normed over their 256 dims with unit gain (models/gemma/gemma2.go;
+// as qknorm_rope_kernel's value heads).
 struct KvTilesParams {
   const float* qkv;
   int64_t row0;
@@ -350,6 +352,7 @@ struct KvTilesParams {
   const int32_t *cu, *cut, *tile_seq;
   int t_lo, tiles;
   uint16_t* img;
+  int norm_v;  // values RMS-normed with unit gain first (EmbeddingGemma 2, gemma2.go)
 };
 
 constexpr int kTileImg = 3 * 32 * 256;  // bf16 per key or value image
@@ -428,11 +431,29 @@ __device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int
   const int width = (a.H + 2 * a.Hkv) * D;
   uint16_t* vimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg) + kTileImg;
   float2 v[8];
+  const float* vsrc = a.qkv + (int64_t)(a.H + a.Hkv + hk) * D + lane * 2;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     const int64_t row = r_first + min(wave + 4 * j, n - 1);
-    v[j] = *reinterpret_cast<const float2*>(a.qkv + row * width + (int64_t)(a.H + a.Hkv + hk) * D + 128 * half_ +
-                                            lane * 2);
+    v[j] = *reinterpret_cast<const float2*>(vsrc + row * width + 128 * half_);
+  }
+  if (a.norm_v) {
+    // the key's sum of squares over all 256 dims: this half's two per lane
+    // and the other half's, then the wave's sum (one key per j)
+    float2 w[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int64_t row = r_first + min(wave + 4 * j, n - 1);
+      w[j] = *reinterpret_cast<const float2*>(vsrc + row * width + 128 * (1 - half_));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float2 lo = half_ ? w[j] : v[j], hi = half_ ? v[j] : w[j];  // dims 2l, 2l+1 and 128 + 2l, 128 + 2l + 1
+      const float ss = wave_sum(fmaf(hi.y, hi.y, fmaf(hi.x, hi.x, fmaf(lo.y, lo.y, lo.x * lo.x))));
+      const float inv = rms_inv(ss, D, a.eps);
+      v[j].x *= inv;
+      v[j].y *= inv;
+    }
   }
 #pragma unroll
   for (int j = 0; j < 8; j++) {
@@ -659,11 +680,12 @@ int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int3
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
                     const int32_t* d_pos, const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
                     const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
-                    hipStream_t s) {
+                    hipStream_t s, bool norm_v) {
   if (tiles == 0) return FA_OK;
   KvTilesParams a;
   a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.pos = d_pos; a.cs = cos_t; a.sn = sin_t;
   a.cu = d_cu_seqlens; a.cut = d_cu_tiles; a.tile_seq = d_tile_seq; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
+  a.norm_v = norm_v ? 1 : 0;
   hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;

@@ -9,6 +9,9 @@
   heads, 2 key/value heads, head_dim 256 / 512 on full layers, per-layer
   input 512, embedding 768) with sequences longer than a small sliding
   radius, several batch shapes and Matryoshka Dim: cosine >= 0.9999.
+* The tile attention path (sliding layers of a batch over 1 024 tokens)
+  against the oracle at max |d| <= 5e-5 (the fp32 path's distance at
+  these widths is about 1.6e-5).
 * Batch invariance: a sequence's embedding does not depend on its batch.
 """
 import json
@@ -99,6 +102,32 @@ def test_gpu_matches_oracle(eg2, B, T, lo):
     assert got.shape == (B, shape.embedding_dim)
     assert c.min() >= 0.9999
     assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
+
+
+def test_gpu_tile_attention_matches_oracle(eg2):
+    """Over 1 024 tokens (32 or more per sequence) the sliding layers
+    (head_dim 256) run the split-bf16 tile attention, values normed in the
+    key/value image pass, and the full layers (head_dim 512) the fp32
+    kernel: every row against the oracle, and against its own
+    single-sequence run (fp32 kernel throughout)."""
+    shape, om, gm = eg2
+    ids, lengths = batch(4242, 6, 300, 150, shape.vocab_size)
+    assert int(lengths.sum()) > 1024
+    got = gm.embed_ids(ids, lengths)
+    want = om.embed(ids, lengths)
+    c = cos_rows(got, want)
+    d = np.abs(got - want).max()
+    print(f"EG2 tiles lengths {lengths.tolist()}: cosine min {c.min():.9f}, max|d| {d:.3g}", flush=True)
+    # the fp32 path's own distance to the oracle at these widths is about
+    # 1.6e-5 (test_gpu_matches_oracle)
+    assert c.min() >= 0.9999999
+    assert d <= 5e-5
+    for b in (0, 5):
+        n = int(lengths[b])
+        one = gm.embed_ids(ids[b:b + 1, :n], lengths[b:b + 1])
+        e = np.abs(one[0] - got[b]).max()
+        print(f"row {b}: tile path vs fp32 path max|d| {e:.3g}", flush=True)
+        assert e <= 5e-5, b
 
 
 def test_gpu_microbatches(eg2):
