@@ -370,8 +370,9 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 //
 // Rows. The query rows of kv head hk are the pairs (token t, query head
 // hk*G + g) of the G = H/Hkv heads that share it, numbered r = t*G + g. A
-// work item is (sequence, 128 consecutive rows, hk[, run of key tiles]); its
-// eight waves own 16 rows each, so one key/value tile in LDS serves every
+// work item is (sequence, 16 W consecutive rows, hk[, run of key tiles]);
+// its W waves (8, or 4 for some batches) own 16 rows each, so one
+// key/value tile in LDS serves every
 // query head of the group (and a short sequence fills an item's rows G
 // times sooner than with one head per item).
 //
@@ -381,8 +382,8 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 // a value image [term][dim][32 slots] whose slot 8g + 4h + r holds key 16h +
 // 4g + r (chunk g of dim d at position g ^ ((d >> 1) & 3)); 48 KB each,
 // copied to LDS unchanged by direct global->LDS loads (1 KB per wave
-// instruction). Two key buffers and one value buffer: 144 KB, one
-// workgroup per CU, two waves per SIMD.
+// instruction). One key buffer and two value buffers: 144 KB, one
+// workgroup per CU (two waves per SIMD with eight waves, one with four).
 //
 // Formulation (lane l: lq = l % 16, g = l / 16). The q terms stay in
 // registers: lane l holds row lq's dims 32c + 8g .. +7 (c = 0..7), three
@@ -409,8 +410,6 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 // (past the last tile: the last again, so no load is conditional), scores,
 // softmax, barrier (the values landed), P.V.
 constexpr int TL_KEYS = 32;              // keys per tile
-constexpr int TL_W = 8;                  // waves per workgroup
-constexpr int TL_ROWS = 16 * TL_W;       // query rows per work item
 constexpr int TL_IMG = 3 * 32 * 256;     // bf16 per key or value image
 constexpr float TL_TAU = 8.f;            // lazy-maximum slack
 
@@ -452,7 +451,14 @@ __device__ __forceinline__ void split_pack8(const f32x4& x0, const f32x4& x1, bf
   t2 = as_bf16x8(u32x4{pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7])});
 }
 
+// TL_W waves of 16 rows: 8 (128-row items, two waves per SIMD) or 4
+// (64-row items, one wave per SIMD: twice the items, each half as long,
+// for batches whose 128-row items fill between half a round and a round of
+// the CUs; the compiler then keeps what does not fit in 256 VGPRs in AGPRs
+// instead of scratch).
+template <int TL_W>
 __global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesParams p) {
+  constexpr int TL_ROWS = 16 * TL_W;  // query rows per work item
   constexpr int HD = 256;
   constexpr int TERM = TL_IMG / 3;  // bf16 per term of an image
   __shared__ __attribute__((aligned(16))) uint16_t Ks[TL_IMG];
@@ -902,6 +908,7 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
                            hipStream_t s) {
   if (a.Hkv <= 0 || a.H % a.Hkv != 0)
     return set_error(ctx, FA_ERR_ARG, "attention: %d query heads not a multiple of %d kv heads", a.H, a.Hkv);
+  if (a.waves != 4 && a.waves != 8) return set_error(ctx, FA_ERR_ARG, "attention: %d waves per item (4 or 8)", a.waves);
   if (n_items == 0) return FA_OK;
   if (a.kparts < 1 || a.kparts > kMaxKeyParts || (a.kparts > 1 && (!a.part || a.rows <= 0 || a.nrows <= 0)))
     return set_error(ctx, FA_ERR_ARG, "attention: %d key parts (1..%d, > 1 needs a partial buffer)", a.kparts,
@@ -911,7 +918,11 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
   p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
   p.gq = a.gq; p.cs = a.cos_t; p.sn = a.sin_t; p.eps = a.eps;
-  hipLaunchKernelGGL(attention_tiles_kernel, dim3((unsigned)((int64_t)n_items * a.kparts)), dim3(64 * TL_W), 0, s, p);
+  const dim3 grid((unsigned)((int64_t)n_items * a.kparts));
+  if (a.waves == 4)
+    hipLaunchKernelGGL(attention_tiles_kernel<4>, grid, dim3(64 * 4), 0, s, p);
+  else
+    hipLaunchKernelGGL(attention_tiles_kernel<8>, grid, dim3(64 * 8), 0, s, p);
   if (a.kparts > 1)
     hipLaunchKernelGGL(attention_combine_kernel<256>, dim3((unsigned)((a.nrows * a.H + 3) / 4)), dim3(256), 0, s,
                        a.part, a.kparts, a.rows, a.row0, a.nrows, a.H, a.out);
@@ -920,7 +931,7 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
 }
 
 int attention_varlen_qblock() { return QBLK; }
-int attention_tiles_rows() { return TL_ROWS; }
+int attention_tiles_rows(int waves) { return 16 * waves; }
 int attention_tiles_keys() { return TL_KEYS; }
 
 int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s) {

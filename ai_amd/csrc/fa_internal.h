@@ -268,13 +268,15 @@ struct AttnTilesArgs {
   const float* gq = nullptr;
   float eps = 0.f;
   const float *cos_t = nullptr, *sin_t = nullptr;
+  // waves per work item, 4 or 8 (items of attention_tiles_rows(waves) rows)
+  int32_t waves = 8;
 };
 // d_items holds n_items triples (sequence, first row, kv head): one item per
-// attention_tiles_rows() rows (token, query head of the kv head's group),
-// row r = token * (H / Hkv) + head - kv head * (H / Hkv).
+// attention_tiles_rows(a.waves) rows (token, query head of the kv head's
+// group), row r = token * (H / Hkv) + head - kv head * (H / Hkv).
 int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d_items, int32_t n_items,
                            hipStream_t s);
-int attention_tiles_rows();
+int attention_tiles_rows(int waves);
 int attention_tiles_keys();
 
 // Zeroes bytes (a multiple of 16, 16-byte aligned) with a fill kernel.

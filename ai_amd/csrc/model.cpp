@@ -739,7 +739,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   // ---- plan (host): cu_seqlens and attention work items ----
   // Layers with head_dim 256 (every EmbeddingGemma layer, EmbeddingGemma
   // 2's sliding layers) take the split-bf16 tile attention: items of
-  // attention_tiles_rows() (token, query head) rows per kv head, keys and
+  // attention_tiles_rows(waves) (token, query head) rows per kv head, keys and
   // values as per-tile images (every sequence starts a tile of
   // attention_tiles_keys() tokens: cu_tiles [B+1] and each tile's
   // sequence). Other layers take the fp32-MFMA attention, items of
@@ -765,7 +765,25 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   for (int l = 0; l < n_run; l++) (layer_tiles(m->layers[l]) ? any_tiles : any_var) = true;
   const int tkeys = fa::attention_tiles_keys();
   const int Gt = any_tiles ? H / hkv_t : 1;  // query heads per kv head of the tile layers
-  const int istep_t = fa::attention_tiles_rows(), istep_v = fa::attention_varlen_qblock();
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  // Tile items of eight waves (128 rows); of four (64 rows) when the
+  // 128-row items would fill more than half a round of the CUs but at most
+  // 0.6 of one: twice the items, each with half the rows and the same key
+  // loop, still about one round, shorten the attention's link in every
+  // layer's dependent chain. Measured per forward on MI355X (256 CUs),
+  // eight vs four waves: C2 (143 items of 128 rows) 5.22 vs 5.11 ms; 36 x
+  // 160 tokens (144 items) 5.09 vs 5.00; 40 x 160 (160) 5.61 vs 5.65; 48 x
+  // 160 (192) 6.34 vs 6.49; EmbeddingGemma 2 at C2 (202) 4.15 vs 4.17; C3,
+  // C4, C5 (from 271 items) 4-9 % slower with four. Below half a round the
+  // key runs spread the work instead.
+  int waves_t = 8;
+  if (any_tiles) {
+    const int r8 = fa::attention_tiles_rows(8);
+    int64_t n8 = 0;
+    for (int b = 0; b < B; b++) n8 += ((int64_t)Gt * std::max(0, lengths[b]) + r8 - 1) / r8 * hkv_t;
+    if (2 * n8 > cus && 5 * n8 <= 3LL * cus) waves_t = 4;
+  }
+  const int istep_t = fa::attention_tiles_rows(waves_t), istep_v = fa::attention_varlen_qblock();
   int64_t M = 0, n_items_t = 0, n_items_v = 0, n_tiles = 0;
   for (int b = 0; b < B; b++) {
     if (lengths[b] < 1 || lengths[b] > T)
@@ -831,7 +849,6 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   // that more CUs share the key loop: C1's 12 fp32 items (128 tokens, 3
   // heads) become 48 workgroups of two 16-key tiles, its 3 tile items 12
   // workgroups of one 32-key tile.
-  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int kparts_v = 1, kparts_t = 1;  // key runs per fp32 item, per tile item
   if (any_var && groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_v <= cus) {
     kparts_v = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_v, 1));
@@ -1038,7 +1055,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
         fa::AttnTilesArgs at;
         at.qkv = qkvr; at.img = img; at.out = attr; at.row0 = r0; at.cu_seqlens = cu_d; at.cu_tiles = cut_d;
         at.H = H; at.Hkv = Hkv; at.window = a.window; at.scale = a.scale;
-        at.gq = L.g_q; at.eps = eps; at.cos_t = L.cos_t; at.sin_t = L.sin_t;
+        at.gq = L.g_q; at.eps = eps; at.cos_t = L.cos_t; at.sin_t = L.sin_t; at.waves = waves_t;
         if (kparts_t > 1) {
           at.kparts = kparts_t; at.rows = M; at.nrows = rows; at.part = attn_part;
         }

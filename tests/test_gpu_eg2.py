@@ -104,15 +104,21 @@ def test_gpu_matches_oracle(eg2, B, T, lo):
     assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
 
 
-def test_gpu_tile_attention_matches_oracle(eg2):
+@pytest.mark.parametrize("B,T,lo", [(6, 300, 150), (20, 256, 150)])
+def test_gpu_tile_attention_matches_oracle(eg2, B, T, lo):
     """Over 1 024 tokens (32 or more per sequence) the sliding layers
     (head_dim 256) run the split-bf16 tile attention, values normed in the
     key/value image pass, and the full layers (head_dim 512) the fp32
     kernel: every row against the oracle, and against its own
-    single-sequence run (fp32 kernel throughout)."""
+    single-sequence run (fp32 kernel throughout). Six sequences give under
+    128 items of 128 rows (eight waves, keys cut into runs); twenty give
+    129-153, between half and 0.6 of a round of the 256 CUs (four-wave
+    items)."""
     shape, om, gm = eg2
-    ids, lengths = batch(4242, 6, 300, 150, shape.vocab_size)
+    ids, lengths = batch(4242 + B, B, T, lo, shape.vocab_size)
     assert int(lengths.sum()) > 1024
+    n8 = int(sum(-(-2 * int(n) // 128) * 2 for n in lengths))  # 128-row items over 2 kv heads
+    assert (n8 < 128) if B == 6 else (128 < n8 <= 153), n8
     got = gm.embed_ids(ids, lengths)
     want = om.embed(ids, lengths)
     c = cos_rows(got, want)
