@@ -78,7 +78,7 @@ def unit_rows(seed: int, name: str, n: int, d: int) -> np.ndarray:
 
 @dataclass
 class ModelShape:
-    """EmbeddingGemma-300M hyper-parameters (SURVEY-listed config.json values)."""
+    """EmbeddingGemma-300M hyper-parameters (its config.json values, as models/gemma/config.go reads them)."""
     hidden_size: int = 768
     num_hidden_layers: int = 24
     num_attention_heads: int = 3

@@ -171,7 +171,7 @@ def main():
         return
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {a.gpus}); data-parallel sharding over "
-              f"sentences is described in DESIGN.md but not run", file=sys.stderr)
+              f"sentences is not run", file=sys.stderr)
         sys.exit(2)
     from ai_amd import _native as N
     from ai_amd import gemma as G

@@ -211,7 +211,7 @@ def test_kmeans_empty_centre_restart_by_hand():
     r = O.cluster_kmeans(x, 4, 1, 0)
     # seeding (fixed by the PCG stream): rows 4 (e2), 6 (e3/4), 2 (e1), 6 again
     assert r["chosen"].tolist() == [4, 6, 2, 6]
-    # round 1: centres e2, e3, e1, e3; e0 rows score 0 everywhere -> centre 0
+    # first iteration: centres e2, e3, e1, e3; e0 rows score 0 everywhere -> centre 0
     assert r["assignment"].tolist() == [0, 0, 2, 2, 0, 1, 1, 0]
     assert r["sizes"].tolist() == [4, 2, 2, 0]
     # centre 3 restarts on the worst row: row 0 (similarity 0, first of the

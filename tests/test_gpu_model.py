@@ -319,7 +319,7 @@ def _shape_variant(**kw):
 
 
 def test_window_bound_at_sequence_length_masks_agree(ctx):
-    """Appendix C-1 of the build's survey: when the window bound is at least
+    """The masks-agree invariant: when the window bound is at least
     T the sliding layers apply no band, so at T = 512 a sliding_window whose
     bidirectional bound (512/2+1 = 257 by default) is raised to 1 025, or the
     unidirectional bound 512 (config.go:331-339: no mask when T <= w,
