@@ -33,12 +33,12 @@
 #include <vector>
 
 #include "fa_internal.h"
+#include "plan.h"
 
 namespace fa {
 
 namespace {
 
-constexpr int kMaxMicrobatches = 4;  // streams a forward may use (micro-batches)
 constexpr int64_t kAttnSplitRows = 1024;  // key-split attention only for batches up to this many tokens
 
 bool bf16_exact(float f, uint16_t* out) {
@@ -122,7 +122,8 @@ struct fa_model {
   // stream), the fork event and one join event per extra stream
   hipStream_t mb_stream[fa::kMaxMicrobatches] = {};
   hipEvent_t ev_fork = nullptr, ev_join[fa::kMaxMicrobatches] = {};
-  std::vector<int> seq_order;
+  std::vector<int> seq_order;                 // plan scratch
+  std::vector<int> plan_layer_D, plan_layer_Hkv;  // plan inputs: each layer's head dim, kv heads
   fa::DevBuf ids_dev, out_dev;
   // pinned staging of the host entry points' ids and results (asynchronous
   // copies; the entry points synchronise before returning)
@@ -736,69 +737,49 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   const int full = c.n_dense > 0 ? m->dense_out.back() : (v2 ? m->E : d);
   if (dim <= 0) dim = full;
   if (dim > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
-  // ---- plan (host): cu_seqlens and attention work items ----
-  // Layers with head_dim 256 (every EmbeddingGemma layer, EmbeddingGemma
-  // 2's sliding layers) take the split-bf16 tile attention: items of
-  // attention_tiles_rows(waves) (token, query head) rows per kv head, keys and
-  // values as per-tile images (every sequence starts a tile of
-  // attention_tiles_keys() tokens: cu_tiles [B+1] and each tile's
-  // sequence). Other layers take the fp32-MFMA attention, items of
-  // attention_varlen_qblock() queries per head. The two kinds of item sit
-  // in separate lists (tile items first), each ordered by group.
-  int64_t M_all = 0;
-  for (int b = 0; b < B; b++) M_all += std::max(0, lengths[b]);
-  // (batches of very short sequences, under 32 tokens on average, keep the
-  // fp32 kernel's 16-key tiles: a 32-key tile would be mostly padding)
-  const bool tiles_ok = M_all > fa::kAttnSplitRows && M_all >= 32LL * B;
-  // the tile layers share one kv head count (the item rows and image slots
-  // depend on it); a model whose head_dim-256 layers differ in it keeps
-  // the fp32 kernel
-  int hkv_t = 0;
-  bool mixed_hkv = false;
-  for (const fa::Layer& L : m->layers) {
-    if (L.D != 256) continue;
-    if (hkv_t && L.Hkv != hkv_t) mixed_hkv = true;
-    hkv_t = L.Hkv;
-  }
-  auto layer_tiles = [&](const fa::Layer& L) { return tiles_ok && !mixed_hkv && L.D == 256; };
-  bool any_tiles = false, any_var = false;
-  for (int l = 0; l < n_run; l++) (layer_tiles(m->layers[l]) ? any_tiles : any_var) = true;
-  const int tkeys = fa::attention_tiles_keys();
-  const int Gt = any_tiles ? H / hkv_t : 1;  // query heads per kv head of the tile layers
-  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  // Tile items of eight waves (128 rows); of four (64 rows) when the
-  // 128-row items would fill more than half a round of the CUs but at most
-  // 0.6 of one: twice the items, each with half the rows and the same key
-  // loop, still about one round, shorten the attention's link in every
-  // layer's dependent chain. Measured per forward on MI355X (256 CUs),
-  // eight vs four waves: C2 (143 items of 128 rows) 5.22 vs 5.11 ms; 36 x
-  // 160 tokens (144 items) 5.09 vs 5.00; 40 x 160 (160) 5.61 vs 5.65; 48 x
-  // 160 (192) 6.34 vs 6.49; EmbeddingGemma 2 at C2 (202) 4.15 vs 4.17; C3,
-  // C4, C5 (from 271 items) 4-9 % slower with four. Below half a round the
-  // key runs spread the work instead.
-  int waves_t = 8;
-  if (any_tiles) {
-    const int r8 = fa::attention_tiles_rows(8);
-    int64_t n8 = 0;
-    for (int b = 0; b < B; b++) n8 += ((int64_t)Gt * std::max(0, lengths[b]) + r8 - 1) / r8 * hkv_t;
-    if (2 * n8 > cus && 5 * n8 <= 3LL * cus) waves_t = 4;
-  }
-  const int istep_t = fa::attention_tiles_rows(waves_t), istep_v = fa::attention_varlen_qblock();
-  int64_t M = 0, n_items_t = 0, n_items_v = 0, n_tiles = 0;
+  // ---- plan (host): cu_seqlens, micro-batch groups, attention work items ----
+  int64_t M = 0;
+  double sum_l2 = 0;
   for (int b = 0; b < B; b++) {
     if (lengths[b] < 1 || lengths[b] > T)
       return set_error(ctx, FA_ERR_ARG, "gemma: length[%d] = %d outside 1..T=%d", b, lengths[b], T);
     M += lengths[b];
-    if (any_tiles) {
-      n_items_t += ((int64_t)Gt * lengths[b] + istep_t - 1) / istep_t * hkv_t;
-      n_tiles += (lengths[b] + tkeys - 1) / tkeys;
-    }
-    if (any_var) n_items_v += ((int64_t)lengths[b] + istep_v - 1) / istep_v * H;
+    sum_l2 += (double)lengths[b] * lengths[b];
   }
-  const int64_t n_items = n_items_t + n_items_v;
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
-  double sum_l2 = 0;
-  for (int i = 0; i < B; i++) sum_l2 += (double)lengths[i] * lengths[i];
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  // Micro-batches: with enough tokens the sequences are cut into groups of
+  // about equal token count (contiguous rows) whose layers run on separate
+  // streams, so that one group's kernels occupy the CUs the others leave
+  // idle (the last round of GEMM tiles and attention items, the norms'
+  // low-occupancy phases). Not while profiling: the probes time one stream.
+  // Group g holds sequences [gb[g], gb[g+1]).
+  int gb[fa::kMaxMicrobatches + 1] = {0, B};
+  int groups = 1;
+  if (M >= fa::microbatch_min_rows() && !m->profiling)
+    groups = fa::plan_groups(lengths, B, M, fa::microbatch_count(M, sum_l2), gb);
+  // each layer's attention path, the items and their key runs
+  std::vector<int>& layer_D = m->plan_layer_D;
+  std::vector<int>& layer_Hkv = m->plan_layer_Hkv;
+  layer_D.resize(m->layers.size());
+  layer_Hkv.resize(m->layers.size());
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    layer_D[l] = m->layers[l].D;
+    layer_Hkv[l] = m->layers[l].Hkv;
+  }
+  fa::AttnPlanIn pin;
+  pin.lengths = lengths; pin.B = B; pin.T = T; pin.H = H;
+  pin.layer_D = layer_D.data(); pin.layer_Hkv = layer_Hkv.data();
+  pin.n_layers = (int)m->layers.size(); pin.n_run = n_run;
+  pin.groups = groups; pin.gb = gb; pin.cus = cus;
+  pin.tile_keys = fa::attention_tiles_keys(); pin.varlen_qblock = fa::attention_varlen_qblock();
+  pin.max_key_parts = fa::kMaxKeyParts; pin.split_rows = fa::kAttnSplitRows;
+  pin.forced_key_parts = fa::attention_key_parts_forced();
+  fa::AttnPlan ap;
+  fa::plan_attention(pin, ap);
+  const int64_t n_items_t = ap.n_items_t, n_items = ap.n_items_t + ap.n_items_v, n_tiles = ap.n_tiles;
+  const int hkv_t = ap.hkv_t, kparts_t = ap.kparts_t, kparts_v = ap.kparts_v, waves_t = ap.waves_t;
+  const int tkeys = pin.tile_keys;
   const size_t plan_ints = 2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles;
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
@@ -819,82 +800,12 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   cut_h[0] = 0;
   for (int b = 0; b < B; b++) {
     cu_h[b + 1] = cu_h[b] + lengths[b];
-    cut_h[b + 1] = cut_h[b] + (any_tiles ? (lengths[b] + tkeys - 1) / tkeys : 0);
+    cut_h[b + 1] = cut_h[b] + (ap.any_tiles ? (lengths[b] + tkeys - 1) / tkeys : 0);
     for (int q = cut_h[b]; q < cut_h[b + 1]; q++) tseq_h[q] = b;
   }
-  // Micro-batches: with enough tokens the sequences are cut into groups of
-  // about equal token count (contiguous rows) whose layers run on separate
-  // streams, so that one group's kernels occupy the CUs the others leave
-  // idle (the last round of GEMM tiles and attention items, the norms'
-  // low-occupancy phases). Not while profiling: the probes time one stream.
-  // Group g holds sequences [gb[g], gb[g+1]).
-  int groups = 1;
-  int gb[fa::kMaxMicrobatches + 1] = {0, B};
-  if (M >= fa::microbatch_min_rows() && !m->profiling) {
-    const int want = std::min(fa::microbatch_count(M, sum_l2), B);
-    int b = 0;
-    int64_t cum = 0;
-    for (int g = 1; g < want; g++) {
-      // cut before the sequence that would take the groups so far past g/want of the
-      // tokens, keeping at least one sequence in this group and in each later one
-      while (b < B - (want - g) && (cum + lengths[b]) * want <= M * g) cum += lengths[b++];
-      if (b == gb[g - 1]) cum += lengths[b++];
-      gb[g] = b;
-    }
-    gb[want] = B;
-    groups = want;
-  }
-  // Attention over few items (a short batch on one stream) cuts each
-  // item's keys into up to four runs of whole tiles, one workgroup each, so
-  // that more CUs share the key loop: C1's 12 fp32 items (128 tokens, 3
-  // heads) become 48 workgroups of two 16-key tiles, its 3 tile items 12
-  // workgroups of one 32-key tile.
-  int kparts_v = 1, kparts_t = 1;  // key runs per fp32 item, per tile item
-  if (any_var && groups == 1 && M <= fa::kAttnSplitRows && 2 * n_items_v <= cus) {
-    kparts_v = (int)std::min<int64_t>(4, cus / std::max<int64_t>(n_items_v, 1));
-    kparts_v = std::max(1, std::min(kparts_v, (T + 31) / 32));  // at least two 16-key tiles per run
-    if (const int f = fa::attention_key_parts_forced()) kparts_v = f;
-  }
-  if (any_tiles) {
-    // fewer tile items than CUs (one or two long sequences): each item's key
-    // tiles are cut into runs of at least four, one workgroup each
-    const int max_tiles = (T + tkeys - 1) / tkeys;
-    if (n_items_t < cus) {
-      kparts_t = (int)std::min<int64_t>(fa::kMaxKeyParts, cus / std::max<int64_t>(n_items_t, 1));
-      kparts_t = std::max(1, std::min(kparts_t, max_tiles / 4));
-    }
-    if (const int f = fa::attention_key_parts_forced()) kparts_t = std::min(f, max_tiles);
-  }
-  // Work items of each group, longest sequences first: an item's work grows
-  // with its sequence's length, and dispatching the long ones first
-  // shortens the tail. Tile items (sequence, first row, kv head); fp32
-  // items (sequence, first query, head).
-  std::vector<int>& order = m->seq_order;
-  int64_t it = 0, group_items_t[fa::kMaxMicrobatches] = {}, group_items_v[fa::kMaxMicrobatches] = {};
-  for (int list = 0; list < 2; list++) {
-    if (!(list == 0 ? any_tiles : any_var)) continue;
-    const int istep = list == 0 ? istep_t : istep_v;
-    const int iheads = list == 0 ? hkv_t : H;  // items per row block
-    for (int gi = 0; gi < groups; gi++) {
-      const int b0 = gb[gi], b1 = gb[gi + 1];
-      order.resize(b1 - b0);
-      for (int b = b0; b < b1; b++) order[b - b0] = b;
-      std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return lengths[x] > lengths[y]; });
-      const int64_t first = it;
-      for (int b : order) {
-        const int rows_b = list == 0 ? Gt * lengths[b] : lengths[b];
-        for (int q0 = 0; q0 < rows_b; q0 += istep) {
-          for (int h = 0; h < iheads; h++) {
-            items_h[3 * it] = b;
-            items_h[3 * it + 1] = q0;
-            items_h[3 * it + 2] = h;
-            it++;
-          }
-        }
-      }
-      (list == 0 ? group_items_t : group_items_v)[gi] = it - first;
-    }
-  }
+  fa::plan_items(pin, ap, items_h, m->seq_order);
+  const int64_t* group_items_t = ap.group_items_t;
+  const int64_t* group_items_v = ap.group_items_v;
   int rc;
   if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
   int32_t* cu_d = m->plan_dev.as<int32_t>();
@@ -976,7 +887,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     const fa::Layer& L = m->layers[l];
     const int D = L.D, Hkv = L.Hkv;
     const bool sliding = L.sliding;
-    const bool tiles = layer_tiles(L);
+    const bool tiles = ap.layer_tiles(D);
     // The N = hidden products (o, down, per-layer-input projection) split K
     // in two when their 128x128 tiles, counted over the concurrent groups,
     // give the CUs fewer than two each (C2: one stream 5 517 rows, or three

@@ -1,0 +1,121 @@
+// Host-side planning of one encoder forward: micro-batch groups and
+// attention work items (plan.h).
+#include "plan.h"
+
+#include <algorithm>
+
+namespace fa {
+
+int plan_groups(const int32_t* lengths, int B, int64_t M, int want, int* gb) {
+  want = std::max(1, std::min(want, std::min(B, kMaxMicrobatches)));
+  gb[0] = 0;
+  int b = 0;
+  int64_t cum = 0;
+  for (int g = 1; g < want; g++) {
+    // cut before the sequence that would take the groups so far past g/want
+    // of the tokens, keeping at least one sequence in this group and in
+    // each later one
+    while (b < B - (want - g) && (cum + lengths[b]) * want <= M * g) cum += lengths[b++];
+    if (b == gb[g - 1]) cum += lengths[b++];
+    gb[g] = b;
+  }
+  gb[want] = B;
+  return want;
+}
+
+void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
+  p = AttnPlan{};
+  for (int b = 0; b < in.B; b++) p.M += in.lengths[b];
+  // Layers with head_dim 256 (every EmbeddingGemma layer, EmbeddingGemma
+  // 2's sliding layers) take the split-bf16 tile attention, from 1 025
+  // tokens with at least 32 per sequence on average (batches of shorter
+  // sequences keep the fp32 kernel's 16-key tiles: a 32-key tile would be
+  // mostly padding). The tile layers share one kv head count (the item
+  // rows and image slots depend on it); a model whose head_dim-256 layers
+  // differ in it keeps the fp32 kernel.
+  p.tiles_ok = p.M > in.split_rows && p.M >= 32LL * in.B;
+  for (int l = 0; l < in.n_layers; l++) {
+    if (in.layer_D[l] != 256) continue;
+    if (p.hkv_t && in.layer_Hkv[l] != p.hkv_t) p.mixed_hkv = true;
+    p.hkv_t = in.layer_Hkv[l];
+  }
+  for (int l = 0; l < in.n_run; l++) (p.layer_tiles(in.layer_D[l]) ? p.any_tiles : p.any_var) = true;
+  p.Gt = p.any_tiles ? in.H / p.hkv_t : 1;
+  // Tile items of eight waves (128 rows); of four (64 rows) when the
+  // 128-row items would fill more than half a round of the CUs but at most
+  // 0.6 of one: twice the items, each with half the rows and the same key
+  // loop, still about one round, shorten the attention's link in every
+  // layer's dependent chain. Measured per forward on MI355X (256 CUs),
+  // eight vs four waves: C2 (143 items of 128 rows) 5.22 vs 5.11 ms; 36 x
+  // 160 tokens (144 items) 5.09 vs 5.00; 40 x 160 (160) 5.61 vs 5.65; 48 x
+  // 160 (192) 6.34 vs 6.49; EmbeddingGemma 2 at C2 (202) 4.15 vs 4.17; C3,
+  // C4, C5 (from 271 items) 4-9 % slower with four. Below half a round the
+  // key runs spread the work instead.
+  if (p.any_tiles) {
+    int64_t n8 = 0;
+    for (int b = 0; b < in.B; b++) n8 += ((int64_t)p.Gt * in.lengths[b] + 127) / 128 * p.hkv_t;
+    if (2 * n8 > in.cus && 5 * n8 <= 3LL * in.cus) p.waves_t = 4;
+  }
+  const int istep_t = 16 * p.waves_t;
+  for (int b = 0; b < in.B; b++) {
+    const int L = in.lengths[b];
+    if (p.any_tiles) {
+      p.n_items_t += ((int64_t)p.Gt * L + istep_t - 1) / istep_t * p.hkv_t;
+      p.n_tiles += (L + in.tile_keys - 1) / in.tile_keys;
+    }
+    if (p.any_var) p.n_items_v += ((int64_t)L + in.varlen_qblock - 1) / in.varlen_qblock * in.H;
+  }
+  // Attention over few items (a short batch on one stream) cuts each
+  // item's keys into up to four runs of whole tiles, one workgroup each, so
+  // that more CUs share the key loop: C1's 12 fp32 items (128 tokens, 3
+  // heads) become 48 workgroups of two 16-key tiles.
+  if (p.any_var && in.groups == 1 && p.M <= in.split_rows && 2 * p.n_items_v <= in.cus) {
+    p.kparts_v = (int)std::min<int64_t>(4, in.cus / std::max<int64_t>(p.n_items_v, 1));
+    p.kparts_v = std::max(1, std::min(p.kparts_v, (in.T + 31) / 32));  // at least two 16-key tiles per run
+    if (in.forced_key_parts) p.kparts_v = in.forced_key_parts;
+  }
+  if (p.any_tiles) {
+    // fewer tile items than CUs (one or two long sequences): each item's
+    // key tiles are cut into runs of at least four, one workgroup each
+    const int max_tiles = (in.T + in.tile_keys - 1) / in.tile_keys;
+    if (p.n_items_t < in.cus) {
+      p.kparts_t = (int)std::min<int64_t>(in.max_key_parts, in.cus / std::max<int64_t>(p.n_items_t, 1));
+      p.kparts_t = std::max(1, std::min(p.kparts_t, max_tiles / 4));
+    }
+    if (in.forced_key_parts) p.kparts_t = std::min(in.forced_key_parts, max_tiles);
+  }
+}
+
+void plan_items(const AttnPlanIn& in, AttnPlan& p, int32_t* items, std::vector<int>& order) {
+  // Work items of each group, longest sequences first: an item's work grows
+  // with its sequence's length, and dispatching the long ones first
+  // shortens the tail.
+  int64_t it = 0;
+  for (int list = 0; list < 2; list++) {
+    const bool tiles = list == 0;
+    if (!(tiles ? p.any_tiles : p.any_var)) continue;
+    const int istep = tiles ? 16 * p.waves_t : in.varlen_qblock;
+    const int iheads = tiles ? p.hkv_t : in.H;  // items per row block
+    for (int gi = 0; gi < in.groups; gi++) {
+      const int b0 = in.gb[gi], b1 = in.gb[gi + 1];
+      order.resize(b1 - b0);
+      for (int b = b0; b < b1; b++) order[b - b0] = b;
+      std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return in.lengths[x] > in.lengths[y]; });
+      const int64_t first = it;
+      for (int b : order) {
+        const int rows_b = tiles ? p.Gt * in.lengths[b] : in.lengths[b];
+        for (int q0 = 0; q0 < rows_b; q0 += istep) {
+          for (int h = 0; h < iheads; h++) {
+            items[3 * it] = b;
+            items[3 * it + 1] = q0;
+            items[3 * it + 2] = h;
+            it++;
+          }
+        }
+      }
+      (tiles ? p.group_items_t : p.group_items_v)[gi] = it - first;
+    }
+  }
+}
+
+}  // namespace fa

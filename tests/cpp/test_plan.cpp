@@ -1,0 +1,230 @@
+// The encoder's host-side plan (ai_amd/csrc/plan.cpp) on the CPU: micro-batch
+// groups and attention work items for EmbeddingGemma-300M and EmbeddingGemma
+// 2 layer stacks at the configs' shapes. Checks what the kernels rely on:
+// every (row, kv head) or (query, head) of every sequence in exactly one
+// item, items of a group from that group's sequences only, groups
+// contiguous and token-balanced, and the path, wave-count and key-run
+// choices at their thresholds. Run by tests/test_cpp_host.py.
+#include <algorithm>
+#include <map>
+#include <numeric>
+#include <tuple>
+#include <vector>
+
+#include "plan.h"
+#include "testing.hpp"
+
+using fa::AttnPlan;
+using fa::AttnPlanIn;
+
+namespace {
+
+struct Stack {
+  std::vector<int> D, Hkv;
+  int H;
+};
+
+Stack eg300m() { return {std::vector<int>(24, 256), std::vector<int>(24, 1), 3}; }
+
+// EmbeddingGemma 2 (TestConfig2): 12 layers, full attention on 5 and 11
+// with head_dim 512 and one kv head, sliding layers head_dim 256, 2 kv heads
+Stack eg2() {
+  Stack s{std::vector<int>(12, 256), std::vector<int>(12, 2), 4};
+  for (int l : {5, 11}) {
+    s.D[l] = 512;
+    s.Hkv[l] = 1;
+  }
+  return s;
+}
+
+struct Case {
+  std::vector<int32_t> lengths;
+  int T = 0;
+  int groups = 1;
+  int gb[fa::kMaxMicrobatches + 1] = {};
+  AttnPlanIn in;
+  AttnPlan p;
+  std::vector<int32_t> items;
+};
+
+void run(Case& c, const Stack& s, int want_groups, int n_run = -1) {
+  const int B = (int)c.lengths.size();
+  c.T = *std::max_element(c.lengths.begin(), c.lengths.end());
+  const int64_t M = std::accumulate(c.lengths.begin(), c.lengths.end(), int64_t{0});
+  c.gb[0] = 0;
+  c.gb[1] = B;
+  c.groups = want_groups > 1 ? fa::plan_groups(c.lengths.data(), B, M, want_groups, c.gb) : 1;
+  c.in.lengths = c.lengths.data();
+  c.in.B = B;
+  c.in.T = c.T;
+  c.in.H = s.H;
+  c.in.layer_D = s.D.data();
+  c.in.layer_Hkv = s.Hkv.data();
+  c.in.n_layers = (int)s.D.size();
+  c.in.n_run = n_run < 0 ? (int)s.D.size() : n_run;
+  c.in.groups = c.groups;
+  c.in.gb = c.gb;
+  fa::plan_attention(c.in, c.p);
+  c.items.assign(3 * (c.p.n_items_t + c.p.n_items_v), -1);
+  std::vector<int> order;
+  fa::plan_items(c.in, c.p, c.items.data(), order);
+}
+
+// Every row block of every sequence (and head) in exactly one item of its
+// group's run; groups in order; within a group, longest sequences first.
+void check_items(const Case& c) {
+  const AttnPlan& p = c.p;
+  int64_t it = 0;
+  for (int list = 0; list < 2; list++) {
+    const bool tiles = list == 0;
+    if (!(tiles ? p.any_tiles : p.any_var)) {
+      for (int g = 0; g < c.groups; g++)
+        if ((tiles ? p.group_items_t : p.group_items_v)[g] != 0) FATAL("unused list %d has items", list);
+      continue;
+    }
+    const int istep = tiles ? 16 * p.waves_t : c.in.varlen_qblock;
+    const int iheads = tiles ? p.hkv_t : c.in.H;
+    std::map<std::tuple<int, int, int>, int> seen;
+    for (int g = 0; g < c.groups; g++) {
+      const int64_t n = (tiles ? p.group_items_t : p.group_items_v)[g];
+      int prev_len = 1 << 30;
+      for (int64_t k = 0; k < n; k++, it++) {
+        const int b = c.items[3 * it], q0 = c.items[3 * it + 1], h = c.items[3 * it + 2];
+        if (b < c.gb[g] || b >= c.gb[g + 1]) FATAL("item %lld of group %d: sequence %d outside [%d, %d)", (long long)it, g, b, c.gb[g], c.gb[g + 1]);
+        const int rows = tiles ? p.Gt * c.lengths[b] : c.lengths[b];
+        if (q0 < 0 || q0 >= rows || q0 % istep != 0) FATAL("item %lld: first row %d of %d (step %d)", (long long)it, q0, rows, istep);
+        if (h < 0 || h >= iheads) FATAL("item %lld: head %d of %d", (long long)it, h, iheads);
+        if (c.lengths[b] > prev_len) FATAL("group %d: sequence %d (length %d) after a shorter one", g, b, c.lengths[b]);
+        prev_len = c.lengths[b];
+        if (seen[{b, q0, h}]++) FATAL("item (%d, %d, %d) twice", b, q0, h);
+      }
+    }
+    int64_t want = 0;
+    for (size_t b = 0; b < c.lengths.size(); b++) {
+      const int rows = tiles ? p.Gt * c.lengths[b] : c.lengths[b];
+      want += (int64_t)((rows + istep - 1) / istep) * iheads;
+    }
+    if ((int64_t)seen.size() != want) FATAL("list %d: %zu distinct items, want %lld", list, seen.size(), (long long)want);
+    if (want != (tiles ? p.n_items_t : p.n_items_v)) FATAL("list %d: counted %lld items, wrote %lld", list, (long long)(tiles ? p.n_items_t : p.n_items_v), (long long)want);
+  }
+  if (it != p.n_items_t + p.n_items_v) FATAL("wrote %lld items of %lld", (long long)it, (long long)(p.n_items_t + p.n_items_v));
+}
+
+std::vector<int32_t> repeat(int n, int len) { return std::vector<int32_t>(n, len); }
+
+}  // namespace
+
+// plan_groups: contiguous, non-empty, every sequence once, and each group's
+// tokens within one sequence of its share
+TEST(TestGroupsBalanced) {
+  std::vector<int32_t> lengths;
+  uint32_t x = 12345;
+  for (int b = 0; b < 37; b++) {
+    x = x * 1664525u + 1013904223u;
+    lengths.push_back(20 + (int)(x >> 24));  // 20..275
+  }
+  const int B = (int)lengths.size();
+  const int64_t M = std::accumulate(lengths.begin(), lengths.end(), int64_t{0});
+  const int maxlen = *std::max_element(lengths.begin(), lengths.end());
+  for (int want = 1; want <= fa::kMaxMicrobatches; want++) {
+    int gb[fa::kMaxMicrobatches + 1];
+    const int g = fa::plan_groups(lengths.data(), B, M, want, gb);
+    if (g != want) FATAL("want %d groups, got %d", want, g);
+    if (gb[0] != 0 || gb[g] != B) FATAL("groups cover [%d, %d)", gb[0], gb[g]);
+    for (int i = 0; i < g; i++) {
+      if (gb[i + 1] <= gb[i]) FATAL("group %d empty", i);
+      int64_t tok = 0;
+      for (int b = gb[i]; b < gb[i + 1]; b++) tok += lengths[b];
+      if (std::abs((double)tok - (double)M / g) > maxlen) FATAL("group %d of %d: %lld tokens of %lld", i, g, (long long)tok, (long long)M);
+    }
+  }
+  // more groups than sequences: one sequence each
+  int gb[fa::kMaxMicrobatches + 1];
+  const int32_t two[] = {5, 900};
+  if (fa::plan_groups(two, 2, 905, 3, gb) != 2 || gb[1] != 1 || gb[2] != 2) FATAL("two sequences, three groups wanted");
+}
+
+// C1 (one 128-token sentence): the fp32 kernel, 12 items cut into 4 key runs
+TEST(TestC1FP32KeyRuns) {
+  Case c;
+  c.lengths = {128};
+  run(c, eg300m(), 1);
+  if (c.p.any_tiles || !c.p.any_var) FATAL("C1 takes the fp32 kernel");
+  if (c.p.n_items_v != 12 || c.p.kparts_v != 4) FATAL("items %lld key runs %d, want 12 and 4", (long long)c.p.n_items_v, c.p.kparts_v);
+  check_items(c);
+}
+
+// over 1 024 tokens at >= 32 per sequence: the tile attention; the wave
+// count by the 128-row item count against 256 CUs
+TEST(TestTileWaves) {
+  const struct {
+    int n, len, waves;
+    int64_t items;  // items of the chosen wave count
+  } cases[] = {
+      {36, 160, 4, 36 * 8},   // 144 items of 128 rows: 0.56 of a round
+      {40, 160, 8, 40 * 4},   // 160: 0.63
+      {48, 160, 8, 48 * 4},   // 192
+      {8, 2048, 8, 8 * 48},   // C4-like, one round and a half
+  };
+  for (const auto& tc : cases) {
+    Case c;
+    c.lengths = repeat(tc.n, tc.len);
+    run(c, eg300m(), 3);
+    if (!c.p.any_tiles || c.p.any_var) FATAL("%d x %d: tile attention on every layer", tc.n, tc.len);
+    if (c.p.waves_t != tc.waves) FATAL("%d x %d: %d waves, want %d", tc.n, tc.len, c.p.waves_t, tc.waves);
+    if (c.p.n_items_t != tc.items) FATAL("%d x %d: %lld items, want %lld", tc.n, tc.len, (long long)c.p.n_items_t, (long long)tc.items);
+    if (c.p.kparts_t != 1) FATAL("%d x %d: %d key runs", tc.n, tc.len, c.p.kparts_t);
+    if (c.p.n_tiles != (int64_t)tc.n * ((tc.len + 31) / 32)) FATAL("key tiles %lld", (long long)c.p.n_tiles);
+    check_items(c);
+  }
+}
+
+// one long sequence: 48 items of 128 rows, keys cut into 5 runs of 12-13 tiles
+TEST(TestTileKeyRuns) {
+  Case c;
+  c.lengths = {2048};
+  run(c, eg300m(), 1);
+  if (c.p.waves_t != 8 || c.p.n_items_t != 48 || c.p.kparts_t != 5)
+    FATAL("waves %d items %lld key runs %d, want 8, 48, 5", c.p.waves_t, (long long)c.p.n_items_t, c.p.kparts_t);
+  check_items(c);
+}
+
+// short sequences (under 32 tokens on average) keep the fp32 kernel
+TEST(TestShortSequencesFP32) {
+  Case c;
+  c.lengths = repeat(64, 20);  // 1 280 tokens
+  run(c, eg300m(), 1);
+  if (c.p.tiles_ok || c.p.any_tiles) FATAL("20-token sequences take the tile attention");
+  check_items(c);
+}
+
+// EmbeddingGemma 2: sliding layers on the tiles (2 kv heads, 2 query heads
+// each), full layers (head_dim 512) on the fp32 kernel; both lists by group
+TEST(TestEG2TwoLists) {
+  Case c;
+  c.lengths = {256, 131, 200, 77, 256, 160, 90, 199, 240, 64, 180, 222};
+  run(c, eg2(), 3);
+  if (!c.p.any_tiles || !c.p.any_var) FATAL("both paths expected");
+  if (c.p.hkv_t != 2 || c.p.Gt != 2) FATAL("kv heads %d, query heads per kv head %d", c.p.hkv_t, c.p.Gt);
+  if (!c.p.layer_tiles(256) || c.p.layer_tiles(512)) FATAL("per-layer path");
+  check_items(c);
+  // only the first five (sliding) layers run: no fp32 items
+  Case d;
+  d.lengths = c.lengths;
+  run(d, eg2(), 3, 5);
+  if (!d.p.any_tiles || d.p.any_var || d.p.n_items_v != 0) FATAL("five sliding layers: fp32 items %lld", (long long)d.p.n_items_v);
+  check_items(d);
+}
+
+// head_dim-256 layers with different kv head counts keep the fp32 kernel
+TEST(TestMixedKvHeads) {
+  Stack s = eg300m();
+  s.Hkv[3] = 3;
+  Case c;
+  c.lengths = repeat(16, 200);
+  run(c, s, 2);
+  if (!c.p.mixed_hkv || c.p.any_tiles || !c.p.any_var) FATAL("mixed kv heads must keep the fp32 kernel");
+  check_items(c);
+}
+
+int main(int argc, char** argv) { return ctest::run_all(argc, argv); }
