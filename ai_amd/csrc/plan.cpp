@@ -41,11 +41,13 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
   }
   for (int l = 0; l < in.n_run; l++) (p.layer_tiles(in.layer_D[l]) ? p.any_tiles : p.any_var) = true;
   p.Gt = p.any_tiles ? in.H / p.hkv_t : 1;
-  // Tile items of eight waves (128 rows); of four (64 rows) when the
-  // 128-row items would fill more than half a round of the CUs but at most
-  // 0.6 of one: twice the items, each with half the rows and the same key
-  // loop, still about one round, shorten the attention's link in every
-  // layer's dependent chain. Measured per forward on MI355X (256 CUs),
+  // Tile items of eight waves (128 rows); of four (64 rows) when the batch
+  // runs as micro-batches and its 128-row items would fill more than half
+  // a round of the CUs but at most 0.6 of one: twice the items, each with
+  // half the rows and the same key loop, still about one round, shorten
+  // the attention's link in every group's chain of dependent launches (on
+  // one stream the launch's own time decides: 49.0 µs with eight waves,
+  // 50.7 with four at C2). Measured per forward on MI355X (256 CUs),
   // eight vs four waves: C2 (143 items of 128 rows) 5.22 vs 5.11 ms; 36 x
   // 160 tokens (144 items) 5.09 vs 5.00; 40 x 160 (160) 5.61 vs 5.65; 48 x
   // 160 (192) 6.34 vs 6.49; EmbeddingGemma 2 at C2 (202) 4.15 vs 4.17; C3,
@@ -54,7 +56,7 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
   if (p.any_tiles) {
     int64_t n8 = 0;
     for (int b = 0; b < in.B; b++) n8 += ((int64_t)p.Gt * in.lengths[b] + 127) / 128 * p.hkv_t;
-    if (2 * n8 > in.cus && 5 * n8 <= 3LL * in.cus) p.waves_t = 4;
+    if (in.groups > 1 && 2 * n8 > in.cus && 5 * n8 <= 3LL * in.cus) p.waves_t = 4;
   }
   const int istep_t = 16 * p.waves_t;
   for (int b = 0; b < in.B; b++) {

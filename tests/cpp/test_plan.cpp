@@ -177,6 +177,12 @@ TEST(TestTileWaves) {
     if (c.p.n_tiles != (int64_t)tc.n * ((tc.len + 31) / 32)) FATAL("key tiles %lld", (long long)c.p.n_tiles);
     check_items(c);
   }
+  // the same batch on one stream (no micro-batches): eight waves
+  Case c;
+  c.lengths = repeat(36, 160);
+  run(c, eg300m(), 1);
+  if (c.p.waves_t != 8 || c.p.n_items_t != 36 * 4) FATAL("one stream: %d waves, %lld items", c.p.waves_t, (long long)c.p.n_items_t);
+  check_items(c);
 }
 
 // one long sequence: 48 items of 128 rows, keys cut into 5 runs of 12-13 tiles
