@@ -62,8 +62,10 @@ GATEUP_TRAFFIC_C2 = {"bytes": (2 * 30326 + 29578) * 1024, "kernel_rev": "x3-128x
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    # 50 steps: about 0.26 s of timed work per region at C2, so that one
+    # hiccup of the host moves the headline little
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--model", default="eg300m", choices=["eg300m", "eg2"],
                    help="eg300m: EmbeddingGemma-300M (the headline); eg2: the EmbeddingGemma 2 text tower at the "
