@@ -240,10 +240,10 @@ int attention_varlen_qblock();
 // rotated) and value image of each (tile, kv head) into img
 // [tile][Hkv][2][3*32*256] bf16. Tile tt of sequence b (d_cu_tiles[b] <= tt
 // < d_cu_tiles[b+1], every sequence starting a tile) holds its tokens 32 (tt
-// - d_cu_tiles[b]) .. +31; d_tile_seq[tt] = b. qkv and d_pos start at packed
-// row row0.
+// - d_cu_tiles[b]) .. +31 (their positions, for RoPE); d_tile_seq[tt] = b.
+// qkv starts at packed row row0.
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
-                    const int32_t* d_pos, const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
+                    const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
                     const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
                     hipStream_t s, bool norm_v = false);
 

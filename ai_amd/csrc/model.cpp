@@ -930,7 +930,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       // the other half of its keys' values for the sum of squares)
       fa::Probe pr(m, FA_K_QKNORM_ROPE, 0,
                    (double)rows * (v2 ? 3 : 2) * Hkv * 4.0 * D + (double)ntl * Hkv * 2 * 3 * 32 * 256 * 2);
-      if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t, cu_d, cut_d, tseq_d,
+      if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, L.cos_t, L.sin_t, cu_d, cut_d, tseq_d,
                                     cut_h[b0], (int32_t)ntl, img, st, v2)))
         return rc;
       pr.done();

@@ -347,7 +347,6 @@ struct KvTilesParams {
   int H, Hkv;
   const float* gk;
   float eps;
-  const int32_t* pos;
   const float *cs, *sn;
   const int32_t *cu, *cut, *tile_seq;
   int t_lo, tiles;
@@ -380,7 +379,7 @@ __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int h
   for (int j = 0; j < 4; j++) {
     const int64_t row = r_first + min(16 * half_ + wave + 4 * j, n - 1);
     v[j] = *reinterpret_cast<const f32x4*>(a.qkv + row * width + (int64_t)(a.H + hk) * D + lane * 4);
-    const int t = a.pos[row];
+    const int t = t0 + min(16 * half_ + wave + 4 * j, n - 1);  // the key's position in its sequence
     c[j] = *reinterpret_cast<const f32x4*>(a.cs + (int64_t)t * half + i0);
     sv[j] = *reinterpret_cast<const f32x4*>(a.sn + (int64_t)t * half + i0);
   }
@@ -678,12 +677,12 @@ int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int3
 }
 
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
-                    const int32_t* d_pos, const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
+                    const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
                     const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
                     hipStream_t s, bool norm_v) {
   if (tiles == 0) return FA_OK;
   KvTilesParams a;
-  a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.pos = d_pos; a.cs = cos_t; a.sn = sin_t;
+  a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.cs = cos_t; a.sn = sin_t;
   a.cu = d_cu_seqlens; a.cut = d_cu_tiles; a.tile_seq = d_tile_seq; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
   a.norm_v = norm_v ? 1 : 0;
   hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
