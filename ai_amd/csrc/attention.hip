@@ -372,9 +372,9 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 // hk*G + g) of the G = H/Hkv heads that share it, numbered r = t*G + g. A
 // work item is (sequence, 16 W consecutive rows, hk[, run of key tiles]);
 // its W waves (8, or 4 for some batches) own 16 rows each, so one
-// key/value tile in LDS serves every
-// query head of the group (and a short sequence fills an item's rows G
-// times sooner than with one head per item).
+// key/value tile in LDS serves every query head of the group (and a short
+// sequence fills an item's rows G times sooner than with one head per
+// item).
 //
 // Operands. Keys and values arrive as LDS images written once per layer by
 // kv_tiles_kernel: per (tile of 32 keys of one sequence, kv head) a key
@@ -405,10 +405,12 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 // flushes against the row's final maximum; the two differ only in weights
 // below e^-87 of the row's largest).
 //
-// Per tile: barrier (the tile's keys landed; every wave is done with the
-// previous values and keys), load the tile's values and the next tile's keys
-// (past the last tile: the last again, so no load is conditional), scores,
-// softmax, barrier (the values landed), P.V.
+// Per tile tt (software pipeline, detailed at the loop): barrier (keys of
+// tt and values of tt-1 landed; every wave done with iteration tt-1), load
+// the values of tt, scores of tt, barrier (every wave done reading the
+// keys), load the keys of tt+1 (past the last tile: the last again, so no
+// load is conditional), then P.V of tile tt-1 with tile tt's softmax spread
+// among its blocks.
 constexpr int TL_KEYS = 32;              // keys per tile
 constexpr int TL_IMG = 3 * 32 * 256;     // bf16 per key or value image
 constexpr float TL_TAU = 8.f;            // lazy-maximum slack
