@@ -5,9 +5,11 @@ raises, there is no CPU fallback.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 import re
+import weakref
 
 import numpy as np
 
@@ -163,6 +165,31 @@ def ptr(a: np.ndarray | None):
     return None if a is None else a.ctypes.data_as(vp)
 
 
+# Objects that own library handles (contexts, models), closed in reverse
+# creation order (models before the context they use) when the interpreter
+# exits: the HIP runtime's own teardown runs after Python's, and streams,
+# events or pinned buffers still live then (a program that never calls
+# close()) made it abort.
+_owners: list = []
+
+
+def own(obj) -> None:
+    """Registers obj (with a close() method) for closing at interpreter exit."""
+    _owners.append(weakref.ref(obj))
+
+
+@atexit.register
+def _close_owners() -> None:
+    for r in reversed(_owners):
+        o = r()
+        if o is not None:
+            try:
+                o.close()
+            except Exception:
+                pass
+    _owners.clear()
+
+
 class Context:
     """One GPU context (fa_ctx): a HIP stream plus scratch."""
 
@@ -172,6 +199,7 @@ class Context:
         if rc != FA_OK:
             raise FaError(rc, lib().fa_last_error(None).decode())
         self.h = h
+        own(self)
 
     def close(self) -> None:
         if self.h:

@@ -70,6 +70,7 @@ class Model:
         h = C.c_void_p()
         self._check(N.lib().fa_gemma_create(self.ctx.h, C.byref(self._cfg), C.byref(h)))
         self.h = h
+        N.own(self)
 
     def _check(self, rc: int) -> None:
         if rc != N.FA_OK:
@@ -77,7 +78,10 @@ class Model:
 
     def close(self) -> None:
         if getattr(self, "h", None):
-            N.lib().fa_gemma_destroy(self.h)
+            # a model outliving its context's close() cannot be destroyed
+            # through it any more (the library's model keeps the context)
+            if self.ctx.h:
+                N.lib().fa_gemma_destroy(self.h)
             self.h = None
 
     def __del__(self):
