@@ -175,6 +175,7 @@ _owners: list = []
 
 def own(obj) -> None:
     """Registers obj (with a close() method) for closing at interpreter exit."""
+    _owners[:] = [r for r in _owners if r() is not None]  # forget collected ones
     _owners.append(weakref.ref(obj))
 
 
