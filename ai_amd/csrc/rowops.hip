@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
                                                             const float* __restrict__ g_next, float eps,
                                                             float scale) {
   constexpr int d = NC * 256;
-  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // one wave per row
   int lane = threadIdx.x & 63;
   if (row >= rows) return;
   f32x4 ov[NC], xv[NC], gp[NC], gn[NC];
@@ -628,7 +628,13 @@ int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64
                          const float* g_post, const float* g_next, float eps, hipStream_t s, const float* o2,
                          float scale) {
   if (rows == 0) return FA_OK;
-  dim3 grid(blocks_for(rows, 4)), block(256);
+  // a short batch (C1: 128 rows) takes one row per workgroup, spread over
+  // four times the CUs: every launch of this chain of small kernels is
+  // latency, 1 % of C1's forward; from four rows per CU on, four per
+  // workgroup
+  const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const int per = rows <= 4LL * cus ? 1 : 4;
+  dim3 grid(blocks_for(rows, per)), block(64 * per);
   switch (d) {
     case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
     case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
