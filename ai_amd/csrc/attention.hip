@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
                                                                 float* __restrict__ out) {
   // rows: the partial buffers' row count; this launch sums rows row_off ..
   // row_off + n - 1 of them into out's rows 0 .. n - 1
-  const int64_t lid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // local row * H + head
+  const int64_t lid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // local row * H + head
   if (lid >= n * H) return;
   const int lane = threadIdx.x & 63;
   const int64_t OW = (int64_t)H * HD;
@@ -894,13 +894,17 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   else
     hipLaunchKernelGGL(attention_varlen_kernel<512>, grid, dim3(DL_NT), 0, s, p);
   if (a.kparts > 1) {
-    const dim3 g2((unsigned)((a.rows * a.H + 3) / 4));
+    // one (row, head) per wave; a short batch (C1: 384) one wave per
+    // workgroup, spread over more CUs
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int per = a.rows * a.H <= 4LL * cus ? 1 : 4;
+    const dim3 g2((unsigned)((a.rows * a.H + per - 1) / per)), b2(64 * per);
     if (a.D == 256)
-      hipLaunchKernelGGL(attention_combine_kernel<256>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, (int64_t)0,
-                         a.rows, a.H, a.out);
+      hipLaunchKernelGGL(attention_combine_kernel<256>, g2, b2, 0, s, a.part, a.kparts, a.rows, (int64_t)0, a.rows,
+                         a.H, a.out);
     else
-      hipLaunchKernelGGL(attention_combine_kernel<512>, g2, dim3(256), 0, s, a.part, a.kparts, a.rows, (int64_t)0,
-                         a.rows, a.H, a.out);
+      hipLaunchKernelGGL(attention_combine_kernel<512>, g2, b2, 0, s, a.part, a.kparts, a.rows, (int64_t)0, a.rows,
+                         a.H, a.out);
   }
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
