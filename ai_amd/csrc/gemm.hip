@@ -920,14 +920,17 @@ bool use_f32_mfma() {
 // 13.17 ms; C4's gate|up at about 2 900 rows, 11.49 -> 11.37 ms; C3's o
 // and down products unchanged); at 0.3-0.5 tiles per CU (C2's
 // micro-batches, 1 840 rows) its longer per-tile chain loses (qkv: 5.10 ->
-// 5.40 ms, gate|up 5.10 -> 5.15).
+// 5.40 ms, gate|up 5.10 -> 5.15). Below half a 128x128 tile per CU a
+// shared launch takes 64x128 tiles rather than 64x64: EmbeddingGemma 2's
+// micro-batch products of N = 512 (K split in two), 4.28 -> 4.15 ms per
+// forward on one box, 4.19 -> 4.17 on another.
 XTileId pick_xtile(int64_t m, int64_t n, int64_t k, int ksplit, Epi epi, int cus, bool shared) {
   if (((m + 31) / 32) * ((n + 63) / 64) * ksplit <= cus) return XTileId::small;
   const int64_t tiles256 = ((m + 127) / 128) * ((n + 255) / 256) * ksplit;
   const int64_t need = shared ? 3LL * cus : 6LL * cus;  // 4 x (0.75 or 1.5 tiles per CU)
   if (4 * tiles256 >= need && k / (32LL * ksplit) >= 24) return XTileId::x128x256w8;
   const int64_t tiles128 = ((m + 127) / 128) * ((n + 127) / 128) * ksplit;
-  if (2 * tiles128 < cus) return epi == Epi::GeGLU ? XTileId::x128x64v : XTileId::x64x64;
+  if (2 * tiles128 < cus) return epi == Epi::GeGLU ? XTileId::x128x64v : shared ? XTileId::x64x128 : XTileId::x64x64;
   if (tiles128 > 2 * cus && 4 * tiles128 <= 5 * 2 * cus) return XTileId::x64x128;
   return XTileId::x128x128w8;
 }
