@@ -161,6 +161,8 @@ TEST(TestTileWaves) {
     int n, len, waves;
     int64_t items;  // items of the chosen wave count
   } cases[] = {
+      {43, 128, 4, 43 * 6},   // 129 items of 128 rows: just over half a round
+      {52, 128, 8, 52 * 3},   // 156: just over 0.6 of a round
       {36, 160, 4, 36 * 8},   // 144 items of 128 rows: 0.56 of a round
       {40, 160, 8, 40 * 4},   // 160: 0.63
       {48, 160, 8, 48 * 4},   // 192

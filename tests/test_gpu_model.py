@@ -272,6 +272,20 @@ def test_single_long_sequence_key_runs(models, L):
     compare_states(gm, om, ids, lens, [0], f"single L={L} states", layers=[1, 6, 24, -1])
 
 
+@pytest.mark.parametrize("n", [43, 52])
+def test_tile_item_waves_at_the_threshold(models, n):
+    """n sequences of 128 tokens (three 128-row items each: 129 and 156
+    items for 256 CUs): 43 take the micro-batched forward's four-wave
+    64-row items (at most 0.6 of a round), 52 the eight-wave ones. Every row
+    against the oracle."""
+    gm, om = models
+    rng = np.random.default_rng(n)
+    lens = np.full(n, 128, np.int32)
+    ids = rng.integers(3, 262144, (n, 128)).astype(np.int32)
+    ids[:, 0] = 2
+    compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=16), f"{n} x 128 (tile items at the wave threshold)")
+
+
 def test_many_short_sequences(models):
     """150 sequences of 2-14 tokens (1 210 tokens, under 32 on average: the
     fp32 attention with micro-batches) against the oracle, every row."""
