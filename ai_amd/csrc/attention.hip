@@ -459,7 +459,7 @@ __device__ __forceinline__ void split_pack8(const f32x4& x0, const f32x4& x1, bf
 // the CUs; the compiler then keeps what does not fit in 256 VGPRs in AGPRs
 // instead of scratch).
 template <int TL_W>
-__global__ __launch_bounds__(64 * TL_W, 2) void attention_tiles_kernel(TilesParams p) {
+__global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_kernel(TilesParams p) {
   constexpr int TL_ROWS = 16 * TL_W;  // query rows per work item
   constexpr int HD = 256;
   constexpr int TERM = TL_IMG / 3;  // bf16 per term of an image
