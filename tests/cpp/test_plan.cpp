@@ -206,6 +206,30 @@ TEST(TestShortSequencesFP32) {
   check_items(c);
 }
 
+// the tile attention's two batch rules at their edges: more than 1 024
+// tokens, and at least 32 per sequence on average
+TEST(TestTilePathBoundaries) {
+  struct Edge {
+    std::vector<int32_t> lengths;
+    bool tiles;
+  };
+  std::vector<int32_t> l1025 = repeat(7, 128), l1055 = repeat(32, 32);
+  l1025.push_back(129);
+  l1055.push_back(31);
+  const Edge edges[] = {{repeat(8, 128), false}, {l1025, true}, {l1055, false}, {repeat(33, 32), true}};
+  for (const Edge& e : edges) {
+    for (int want : {1, 3}) {
+      Case c;
+      c.lengths = e.lengths;
+      run(c, eg300m(), want);
+      if (c.p.tiles_ok != e.tiles || c.p.any_tiles != e.tiles || c.p.any_var == e.tiles)
+        FATAL("%zu sequences, %lld tokens, %d groups: tiles %d, want %d", e.lengths.size(), (long long)c.p.M, c.groups,
+              (int)c.p.any_tiles, (int)e.tiles);
+      check_items(c);
+    }
+  }
+}
+
 // EmbeddingGemma 2: sliding layers on the tiles (2 kv heads, 2 query heads
 // each), full layers (head_dim 512) on the fp32 kernel; both lists by group
 TEST(TestEG2TwoLists) {

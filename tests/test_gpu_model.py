@@ -286,6 +286,22 @@ def test_tile_item_waves_at_the_threshold(models, n):
     compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=16), f"{n} x 128 (tile items at the wave threshold)")
 
 
+@pytest.mark.parametrize("n,L,last", [(8, 128, 128), (8, 128, 129), (33, 32, 31), (33, 32, 32)])
+def test_tile_path_boundaries(models, n, L, last):
+    """Batches on both sides of the tile attention's two batch rules (more
+    than 1 024 tokens; at least 32 per sequence on average): 1 024 tokens
+    and 1 055 over 33 sequences take the fp32 attention, 1 025 and 1 056
+    the split-bf16 tiles. Every row against the oracle."""
+    gm, om = models
+    rng = np.random.default_rng(1000 * n + last)
+    lens = np.full(n, L, np.int32)
+    lens[-1] = last
+    ids = rng.integers(3, 262144, (n, int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=11), f"{n} sequences, {lens.sum()} tokens")
+
+
 def test_many_short_sequences(models):
     """150 sequences of 2-14 tokens (1 210 tokens, under 32 on average: the
     fp32 attention with micro-batches) against the oracle, every row."""
