@@ -302,6 +302,21 @@ def test_tile_path_boundaries(models, n, L, last):
     compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=11), f"{n} sequences, {lens.sum()} tokens")
 
 
+@pytest.mark.parametrize("lengths", [[1], [1] * 5, [1, 2048, 1, 33]])
+def test_one_token_sequences(models, lengths):
+    """Sequences of a single token (only the BOS id): alone, five in a batch
+    (the fp32 attention, one key), and beside a 2 048-token sequence (the
+    tile attention, whose key tile is then almost all padding). Every row
+    against the oracle."""
+    gm, om = models
+    rng = np.random.default_rng(len(lengths) + sum(lengths))
+    lens = np.array(lengths, np.int32)
+    ids = rng.integers(3, 262144, (len(lens), int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=1), f"lengths {lengths}")
+
+
 def test_many_short_sequences(models):
     """150 sequences of 2-14 tokens (1 210 tokens, under 32 on average: the
     fp32 attention with micro-batches) against the oracle, every row."""
