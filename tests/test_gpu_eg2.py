@@ -3,12 +3,14 @@
 * Against the golden vectors of transformers' Gemma4TextModel
   (tests/golden/eg2_tiny.npz; 6 layers, full layer 5 with head_dim 512 and
   one key/value head, sliding radius 8 at T = 20): embeddings cosine >=
-  0.99999, max |d| <= 1e-4.
+  0.9999999, max |d| <= 2e-5 (measured about 6e-6).
 * Against the CPU oracle (orc_model2_*, pinned by tests/test_eg2_golden.py)
   at the reference's EmbeddingGemma 2 widths (TestConfig2: hidden 512, 4
   heads, 2 key/value heads, head_dim 256 / 512 on full layers, per-layer
   input 512, embedding 768) with sequences longer than a small sliding
-  radius, several batch shapes and Matryoshka Dim: cosine >= 0.9999.
+  radius, several batch shapes and Matryoshka Dim: cosine >= 0.9999999,
+  max |d| <= 5e-5 (the fp32 path's distance at these widths is about
+  1.6e-5), and a row batched or alone within 5e-5.
 * The tile attention path (sliding layers of a batch over 1 024 tokens)
   against the oracle at max |d| <= 5e-5 (the fp32 path's distance at
   these widths is about 1.6e-5).
@@ -48,8 +50,8 @@ def test_gpu_matches_transformers_golden(ctx):
     gm.close()
     c = cos_rows(got, emb)
     print(f"GPU vs {meta['source']}: cosine min {c.min():.9f}, max|d| {np.abs(got - emb).max():.3g}", flush=True)
-    assert c.min() >= 0.99999
-    assert np.abs(got - emb).max() <= 1e-4
+    assert c.min() >= 0.9999999
+    assert np.abs(got - emb).max() <= 2e-5
 
 
 def eg2_shape(**kw):
@@ -173,4 +175,4 @@ def test_gpu_dim_and_batch_invariance(eg2):
     for b in (0, 3):
         n = int(lengths[b])
         one = gm.embed_ids(ids[b:b + 1, :n], lengths[b:b + 1])
-        assert cos_rows(one, full[b:b + 1])[0] >= 0.99999
+        assert np.abs(one[0] - full[b]).max() <= 5e-5, b
