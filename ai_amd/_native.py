@@ -46,6 +46,14 @@ class Epilogue(C.Structure):
                 ("residual", vp), ("ldr", i64)]
 
 
+FA_MAX_BATCH_DIMS = 8
+
+
+class Matrix(C.Structure):
+    """fa_matrix: a strided operand (data, row/column strides, batch strides; elements)."""
+    _fields_ = [("data", vp), ("rs", i64), ("cs", i64), ("bstride", i64 * FA_MAX_BATCH_DIMS)]
+
+
 class GemmaConfig(C.Structure):
     _fields_ = [("hidden_size", i32), ("num_hidden_layers", i32), ("num_attention_heads", i32),
                 ("num_key_value_heads", i32), ("head_dim", i32), ("intermediate_size", i32), ("vocab_size", i32),
@@ -72,11 +80,17 @@ _SIGS = {
                                   i64]),
     "fa_matmul_fused_dev": (C.c_int, [vp, i64, i64, i64, vp, i64, vp, i64, C.c_int, C.c_int, C.POINTER(Epilogue),
                                       vp, i64]),
+    "fa_matmul_strided": (C.c_int, [vp, i32, P_i64, i64, i64, i64, C.POINTER(Matrix), C.POINTER(Matrix),
+                                    C.POINTER(Epilogue), vp]),
+    "fa_matmul_strided_dev": (C.c_int, [vp, i32, P_i64, i64, i64, i64, C.POINTER(Matrix), C.POINTER(Matrix),
+                                        C.POINTER(Epilogue), vp]),
     "fa_row_sum_squares": (C.c_int, [vp, vp, i64, i64, vp]),
     "fa_rmsnorm": (C.c_int, [vp, vp, vp, f32, i64, i64, vp]),
     "fa_rope": (C.c_int, [vp, vp, f64, vp, i64, i32, i32, vp]),
     "fa_attention": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, vp, i64, i64,
                                i64, i64, f32, vp]),
+    "fa_attention_dev": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, vp, i64,
+                                   i64, i64, i64, f32, vp]),
     "fa_similarities_topk": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
     "fa_similarities_topk_dev": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),
     "fa_similarities_topk_dev_noalloc": (C.c_int, [vp, vp, i64, vp, i64, i32, i32, vp, vp]),

@@ -36,7 +36,7 @@ HIP_FLAGS = [
     "-I", INCLUDE, "-I", CSRC,
 ]
 
-ROCM_SOURCES = ["context.cpp", "model.cpp", "plan.cpp", "gemm.hip", "rowops.hip", "attention.hip", "score.hip", "cluster.hip"]
+ROCM_SOURCES = ["context.cpp", "matmul.cpp", "model.cpp", "plan.cpp", "gemm.hip", "rowops.hip", "attention.hip", "score.hip", "cluster.hip"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -88,6 +88,7 @@ CPP_TESTS = ["test_tensor", "test_gemma", "test_tokenizer", "test_cluster", "tes
 CPP_CPU_TESTS = ["test_tokenizer", "test_config", "test_plan"]  # need no GPU
 CPP_PLAN_TEST = "test_plan"  # the encoder's host plan (csrc/plan.cpp) alone, no library
 CPP_DRIVERS = ["st_dump", "embed_dir"]  # programs the Python tests drive
+C_DRIVERS = ["exit_open"]  # C programs the Python tests drive
 CPP_TEST_BIN = os.path.join(BUILD, "cpp_tests")
 
 
@@ -111,6 +112,10 @@ def build_host(verbose: bool = False) -> str:
                      "-L", LIB, "-lfiber_host", "-lfa_rocm", "-lfa_synth", rpath])
     jobs.append([cxx, "-O2", "-std=c++17", "-Wall", "-I", CSRC, "-I", tdir, os.path.join(tdir, CPP_PLAN_TEST + ".cpp"),
                  os.path.join(CSRC, "plan.cpp"), "-o", os.path.join(CPP_TEST_BIN, CPP_PLAN_TEST)])
+    cc = shutil.which("gcc") or "gcc"
+    for t in C_DRIVERS:  # plain C callers of the C ABI
+        jobs.append([cc, "-O2", "-std=c99", "-Wall", "-I", INCLUDE, os.path.join(tdir, t + ".c"),
+                     "-o", os.path.join(CPP_TEST_BIN, t), "-L", LIB, "-lfa_rocm", "-lfa_synth", rpath])
     with cf.ThreadPoolExecutor(len(jobs)) as ex:
         for f in [ex.submit(_run, j, verbose) for j in jobs]:
             f.result()

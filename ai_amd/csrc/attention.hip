@@ -807,6 +807,188 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   for (int db = 0; db < HD / 16; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db] * inv;
 }
 
+// ---- dense attention on the MFMA (the tensor.AttentionScaled drop-in) ----------
+// attention_dense_kernel<HD, DSPLIT> computes fa_attention's result for
+// head_dim HD in {64, 128, 256, 512}: q [B,H,T,HD], k/v [B,H,S,HD] with
+// arbitrary (16-byte multiple) batch and head strides (stride 0 for GQA's
+// Expand) and rows of HD contiguous, and any additive mask tensor read
+// through its broadcast strides. The reference's algebra
+// (internal/blas/attention.go:105-122): raw scores s = q.k, with scale > 0
+// row = s + mask/scale, weights exp(scale*row - scale*max(row)) with the
+// flush below -87 (generic.go:278-307), so masked keys get weight exactly 0;
+// with scale <= 0 the scores are scaled first and the mask added as is.
+//
+// Formulation as attention_varlen_kernel's (v_mfma_f32_16x16x4_f32): a wave
+// owns 16 queries and HD/DSPLIT head dimensions, computes S^T = K.Q^T for a
+// tile of 16 keys (lane l: query l%16 against keys 4(l/16)+r) and O += P.V
+// with its probabilities as the A operand. DSPLIT = 1 (HD <= 256): four
+// waves own 64 queries and the full head each, no exchange; DSPLIT = 2 (HD =
+// 512): wave pairs split the head and add their partial scores through LDS.
+// A work item is (batch, head, block of queries); K and V tiles are the
+// contiguous 16*HD floats of 16 key rows, loaded straight into two LDS
+// buffers (global_load_lds, 1 KB per wave instruction, 16-byte chunks
+// XOR-swizzled by row), the next tile loading during the current one.
+struct DenseParams {
+  const float *q, *k, *v, *mask;
+  float* out;
+  int32_t H, T, S;
+  int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, m_sb, m_sh, m_sr, m_sc;
+  float scale;
+  int32_t qblocks;  // query blocks per (batch, head)
+};
+
+template <int HD, int DSPLIT>
+__global__ __launch_bounds__(DL_NT) void attention_dense_kernel(DenseParams p) {
+  constexpr int DW = HD / DSPLIT;  // head dimensions per wave
+  constexpr int QB = 16 * (4 / DSPLIT);  // queries per item
+  constexpr int ROWF = HD;
+  constexpr int LOADS = KT * HD / 256 / 4;  // 1 KB loads per wave per K (or V) tile
+  static_assert(HD >= 64 && LOADS >= 1, "head dimension");
+  __shared__ __attribute__((aligned(16))) float K0[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float V0[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float K1[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float V1[KT * ROWF];
+  __shared__ __attribute__((aligned(16))) float Sx[DSPLIT == 2 ? 4 : 1][64 * 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = wave / DSPLIT, half = wave % DSPLIT;
+  const int g = lane >> 4;
+  const int lq = lane & 15;
+
+  const int bh = blockIdx.x / p.qblocks, qblk = blockIdx.x % p.qblocks;
+  const int b = bh / p.H, h = bh % p.H;
+  const int dofs = half * DW;
+  const float* kbase = p.k + b * p.k_sb + h * p.k_sh;
+  const float* vbase = p.v + b * p.v_sb + h * p.v_sh;
+  const int S = p.S;
+
+  const int qi = qblk * QB + grp * 16 + lq;
+  const bool qvalid = qi < p.T;
+  const int qc = qvalid ? qi : p.T - 1;
+  f32x4 qreg[DW / 16];
+  {
+    const float* qr = p.q + b * p.q_sb + h * p.q_sh + (int64_t)qc * HD + dofs;
+#pragma unroll
+    for (int sg = 0; sg < DW / 16; sg++) qreg[sg] = *reinterpret_cast<const f32x4*>(qr + sg * 16 + g * 4);
+  }
+  const float* mrow = p.mask ? p.mask + b * p.m_sb + h * p.m_sh + (int64_t)qc * p.m_sr : nullptr;
+  const bool pos = p.scale > 0.f;
+  const float sa = pos ? p.scale : 1.f, inv_scale = pos ? 1.f / p.scale : 1.f;
+
+  f32x4 oacc[DW / 16];
+#pragma unroll
+  for (int db = 0; db < DW / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegBig;
+  float l_part = 0.f;
+
+  // load j of wave w covers floats (4 LOADS w + j) * 256 .. +255 of the tile
+  auto issue_tile = [&](int k0, float* Kb, float* Vb) {
+#pragma unroll
+    for (int j = 0; j < LOADS; j++) {
+      const int f0 = (wave * LOADS + j) * 256;
+      const int r = (f0 + lane * 4) / HD;              // tile row of this lane's chunk
+      const int cpos = ((f0 + lane * 4) % HD) >> 2;    // its LDS chunk position in the row
+      const int64_t key = min(k0 + r, S - 1);
+      const int chunk = dl_pos(r, cpos);               // the global chunk that lands there
+      __builtin_amdgcn_global_load_lds(kbase + key * HD + chunk * 4,
+                                       (__attribute__((address_space(3))) void*)&Kb[f0], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + key * HD + chunk * 4,
+                                       (__attribute__((address_space(3))) void*)&Vb[f0], 16, 0, 0);
+    }
+  };
+  issue_tile(0, K0, V0);
+
+  auto step = [&](int k0, const float* Kc, const float* Vc, float* Kn, float* Vn) {
+    dl_barrier<0x0070>();  // this tile landed everywhere; the other buffer is free
+    if (k0 + KT < S) issue_tile(k0 + KT, Kn, Vn);
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      const float* krow = &Kc[lq * ROWF];
+      auto kfrag = [&](int sg) {
+        return *reinterpret_cast<const f32x4*>(krow + dl_pos(lq, (dofs + sg * 16 + g * 4) >> 2) * 4);
+      };
+      f32x4 a = kfrag(0);
+#pragma unroll
+      for (int sg = 0; sg < DW / 16; sg++) {
+        const f32x4 an = sg + 1 < DW / 16 ? kfrag(sg + 1) : a;
+#pragma unroll
+        for (int c = 0; c < 4; c++) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], qreg[sg][c], sacc, 0, 0, 0);
+        a = an;
+      }
+    }
+    if constexpr (DSPLIT == 2) {
+      *reinterpret_cast<f32x4*>(&Sx[wave][lane * 4]) = sacc;
+      dl_barrier<0xC07F>();  // lgkmcnt(0) only: the next tile's loads stay in flight
+      const f32x4 other = *reinterpret_cast<const f32x4*>(&Sx[wave ^ 1][lane * 4]);
+      const f32x4 lo = half == 0 ? sacc : other, hi = half == 0 ? other : sacc;
+#pragma unroll
+      for (int r = 0; r < 4; r++) sacc[r] = lo[r] + hi[r];
+    }
+    float tmax = kNegBig;
+    bool valid[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int j = k0 + g * 4 + r;
+      valid[r] = j < S;
+      float row = sacc[r];
+      if (!pos) row = __fmul_rn(row, p.scale);
+      if (mrow && valid[r]) row = __fadd_rn(__fmul_rn(inv_scale, mrow[(int64_t)j * p.m_sc]), row);
+      const float t = sa * row;
+      sacc[r] = t;
+      if (valid[r]) tmax = fmaxf(tmax, t);
+    }
+    tmax = rows4_max(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = exp_flush(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float pv = valid[r] ? exp_flush(sacc[r] - m_new) : 0.f;
+      sacc[r] = pv;
+      psum += pv;
+    }
+    l_part = l_part * alpha + psum;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+      for (int db = 0; db < DW / 16; db++) oacc[db][r] *= ar;
+    }
+#pragma unroll
+    for (int db = 0; db < DW / 16; db++) {
+      const int f = dofs + db * 16 + lq;
+      f32x4 bv;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int row = 4 * g + c;
+        bv[c] = Vc[row * ROWF + dl_pos(row, f >> 2) * 4 + (f & 3)];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(sacc[c], bv[c], oacc[db], 0, 0, 0);
+    }
+  };
+  for (int k0 = 0; k0 < S; k0 += 2 * KT) {
+    step(k0, K0, V0, K1, V1);
+    if (k0 + KT < S) step(k0 + KT, K1, V1, K0, V0);
+  }
+
+  const float l_tot = rows4_sum(l_part);
+  float* obase = p.out + ((int64_t)bh * p.T + qblk * QB + grp * 16) * HD + dofs;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int qr = 4 * g + r;
+    const float inv = 1.f / __shfl(l_tot, qr, 64);
+    if (qblk * QB + grp * 16 + qr < p.T) {
+      float* orow = obase + (int64_t)qr * HD;
+#pragma unroll
+      for (int db = 0; db < DW / 16; db++) orow[db * 16 + lq] = oacc[db][r] * inv;
+    }
+  }
+}
+
 // ---- generic attention (per-op drop-in) ------------------------------------------
 constexpr int GMAXD = 512;
 
@@ -939,6 +1121,39 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
 int attention_varlen_qblock() { return QBLK; }
 int attention_tiles_rows(int waves) { return 16 * waves; }
 int attention_tiles_keys() { return TL_KEYS; }
+
+bool attention_dense_ok(const AttnGenericArgs& a) {
+  static const bool off = [] {
+    const char* e = std::getenv("FA_ATTN_DENSE");
+    return e && e[0] == '0';
+  }();
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int64_t qblocks = (a.T + 63) / 64;
+  return !off && (a.D == 64 || a.D == 128 || a.D == 256 || a.D == 512) && a.T > 0 && a.S > 0 && al(a.q) &&
+         al(a.k) && al(a.v) && a.q_sb % 4 == 0 && a.q_sh % 4 == 0 && a.k_sb % 4 == 0 && a.k_sh % 4 == 0 &&
+         a.v_sb % 4 == 0 && a.v_sh % 4 == 0 && (int64_t)a.B * a.H * qblocks * 2 < INT32_MAX;
+}
+
+int launch_attention_dense(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s) {
+  if (!attention_dense_ok(a)) return set_error(ctx, FA_ERR_UNSUPPORTED, "Attention: no MFMA path for these operands");
+  DenseParams p;
+  p.q = a.q; p.k = a.k; p.v = a.v; p.mask = a.mask; p.out = a.out;
+  p.H = a.H; p.T = a.T; p.S = a.S;
+  p.q_sb = a.q_sb; p.q_sh = a.q_sh; p.k_sb = a.k_sb; p.k_sh = a.k_sh; p.v_sb = a.v_sb; p.v_sh = a.v_sh;
+  p.m_sb = a.m_sb; p.m_sh = a.m_sh; p.m_sr = a.m_sr; p.m_sc = a.m_sc;
+  p.scale = a.scale;
+  const int qb = a.D >= 256 ? 32 : 64;  // DSPLIT = 2 from head_dim 256: wave pairs share 16 queries
+  p.qblocks = (a.T + qb - 1) / qb;
+  const dim3 grid((unsigned)((int64_t)a.B * a.H * p.qblocks)), block(DL_NT);
+  switch (a.D) {
+    case 64: hipLaunchKernelGGL((attention_dense_kernel<64, 1>), grid, block, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((attention_dense_kernel<128, 1>), grid, block, 0, s, p); break;
+    case 256: hipLaunchKernelGGL((attention_dense_kernel<256, 2>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((attention_dense_kernel<512, 2>), grid, block, 0, s, p); break;
+  }
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
 
 int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s) {
   if (a.D > GMAXD) return set_error(ctx, FA_ERR_UNSUPPORTED, "Attention: head dimension %d > %d", a.D, GMAXD);

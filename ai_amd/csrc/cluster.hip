@@ -513,6 +513,10 @@ int fa_cluster_normalize_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, 
   if (!ctx) return set_error(ctx, FA_ERR_ARG, "cluster: ctx is NULL");
   int rc;
   if ((rc = fa::check_rows(ctx, "Normalize", n, d))) return rc;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "cluster");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   return fa::launch_normalize(ctx, x, n, d, out);
 }
@@ -522,6 +526,10 @@ int fa_cluster_normalize(fa_ctx* ctx, const float* x, int64_t n, int32_t d, floa
   int rc;
   if ((rc = fa::check_rows(ctx, "Normalize", n, d))) return rc;
   if (n == 0 || d == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "cluster");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void* dx;
   const size_t bytes = (size_t)n * d * 4;
@@ -542,6 +550,10 @@ int fa_cluster_nearest_dev(fa_ctx* ctx, const float* x, int64_t n, const float* 
                      (long long)k);
   if (d <= 0) return set_error(ctx, FA_ERR_ARG, "Nearest: rows of length %d", d);
   if (n == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "Nearest");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   fa::DevBuf& ws = ctx->slot(S_CL_WORK);
   if ((rc = ws.ensure(ctx, (size_t)n * k * 4))) return rc;
@@ -563,6 +575,10 @@ int fa_cluster_nearest(fa_ctx* ctx, const float* x, int64_t n, const float* cent
                      (long long)k);
   if (d <= 0) return set_error(ctx, FA_ERR_ARG, "Nearest: rows of length %d", d);
   if (n == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "Nearest");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void *dx, *dc;
   if ((rc = fa::stage_h2d(ctx, S_CL_X, x, (size_t)n * d * 4, &dx))) return rc;
@@ -587,6 +603,10 @@ int fa_cluster_kmeans_dev(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int
   if (k <= 0 || k > n) return set_error(ctx, FA_ERR_ARG, "cluster: k must be between 1 and the number of rows");
   if (d <= 0) return set_error(ctx, FA_ERR_ARG, "KMeans: rows of length %d", d);
   if (!iterations) return set_error(ctx, FA_ERR_ARG, "KMeans: iterations is NULL");
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "cluster");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   hipStream_t st = ctx->stream;
   const int nchunks = (int)((n + fa::kChunk - 1) / fa::kChunk);
@@ -694,6 +714,10 @@ int fa_cluster_kmeans(fa_ctx* ctx, const float* x, int64_t n, int32_t d, int32_t
   if ((rc = fa::check_rows(ctx, "KMeans", n, d))) return rc;
   if (k <= 0 || k > n) return set_error(ctx, FA_ERR_ARG, "cluster: k must be between 1 and the number of rows");
   if (d <= 0) return set_error(ctx, FA_ERR_ARG, "KMeans: rows of length %d", d);
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "cluster");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void* dx;
   if ((rc = fa::stage_h2d(ctx, S_CL_X, x, (size_t)n * d * 4, &dx))) return rc;

@@ -1,6 +1,7 @@
 // Context, errors, device buffers and the tensor-level C-ABI entry points
 // (host pointers in, host pointers out).
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -11,6 +12,74 @@ namespace fa {
 
 namespace {
 thread_local std::string tls_error;
+
+// Live handles. A process that exits with a context or model still open
+// would otherwise leave streams, events, pinned host buffers and device
+// memory to the HIP runtime's own teardown, which then aborts ("terminate
+// called after throwing an instance of 'std::bad_variant_access'", seen with
+// a model left open). close_at_exit() is registered with atexit() on the
+// first fa_create, after the runtime has initialised (and registered its
+// teardown), so it runs first and releases what is still open, models
+// before contexts. The containers are never destroyed (no static destructor
+// runs after the handler).
+std::mutex g_reg_mu;
+std::vector<fa_ctx*>* g_ctxs = new std::vector<fa_ctx*>();
+std::vector<std::pair<fa_model*, fa_ctx*>>* g_models = new std::vector<std::pair<fa_model*, fa_ctx*>>();
+bool g_exit_hook = false;
+
+void ctx_release(fa_ctx* ctx) {
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (auto& b : ctx->scratch) b.release();
+  (void)hipStreamDestroy(ctx->stream);
+  noalloc_release(ctx);
+  delete ctx;
+}
+
+void close_at_exit() {
+  std::vector<std::pair<fa_model*, fa_ctx*>> models;
+  std::vector<fa_ctx*> ctxs;
+  {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    models.swap(*g_models);
+    ctxs.swap(*g_ctxs);
+  }
+  for (auto it = models.rbegin(); it != models.rend(); ++it) model_release(it->first);
+  for (auto it = ctxs.rbegin(); it != ctxs.rend(); ++it) ctx_release(*it);
+}
+
+// Removes x from v; whether it was there.
+template <class V, class F>
+bool take(V& v, F match) {
+  for (size_t i = 0; i < v.size(); i++)
+    if (match(v[i])) {
+      v.erase(v.begin() + (long)i);
+      return true;
+    }
+  return false;
+}
+}  // namespace
+
+void register_model(fa_model* m, fa_ctx* ctx) {
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  g_models->push_back({m, ctx});
+}
+
+bool unregister_model(fa_model* m) {
+  std::lock_guard<std::mutex> lk(g_reg_mu);
+  return take(*g_models, [m](const std::pair<fa_model*, fa_ctx*>& e) { return e.first == m; });
+}
+
+int refuse_capture(fa_ctx* ctx, hipStream_t s, const char* op) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(s, &st);
+  if (e != hipSuccess) return set_error(ctx, FA_ERR_HIP, "%s: hipStreamIsCapturing: %s", op, hipGetErrorString(e));
+  if (st != hipStreamCaptureStatusNone)
+    return set_error(ctx, FA_ERR_STATE,
+                     "%s: the context's stream is being captured into a HIP graph; this entry point may allocate "
+                     "and upload per-call data and cannot be captured (fa_similarities_topk_dev_noalloc can)",
+                     op);
+  return FA_OK;
 }
 
 int set_error(fa_ctx* ctx, int code, const char* fmt, ...) {
@@ -113,17 +182,33 @@ int fa_create(int device, fa_ctx** out) {
     delete c;
     return set_error(nullptr, rc, "%s", msg.c_str());
   }
+  {
+    std::lock_guard<std::mutex> lk(fa::g_reg_mu);
+    fa::g_ctxs->push_back(c);
+    if (!fa::g_exit_hook) fa::g_exit_hook = std::atexit(fa::close_at_exit) == 0;
+  }
   *out = c;
   return FA_OK;
 }
 
 void fa_destroy(fa_ctx* ctx) {
   if (!ctx) return;
-  (void)hipSetDevice(ctx->device);
-  (void)hipStreamSynchronize(ctx->stream);
-  for (auto& b : ctx->scratch) b.release();
-  (void)hipStreamDestroy(ctx->stream);
-  delete ctx;
+  std::vector<std::pair<fa_model*, fa_ctx*>> models;
+  {
+    std::lock_guard<std::mutex> lk(fa::g_reg_mu);
+    // unknown, or already closed at exit: nothing to do
+    if (!fa::take(*fa::g_ctxs, [ctx](fa_ctx* c) { return c == ctx; })) return;
+    // models still open on this context go first (they use its stream)
+    for (size_t i = 0; i < fa::g_models->size();)
+      if ((*fa::g_models)[i].second == ctx) {
+        models.push_back((*fa::g_models)[i]);
+        fa::g_models->erase(fa::g_models->begin() + (long)i);
+      } else {
+        i++;
+      }
+  }
+  for (auto& e : models) fa::model_release(e.first);
+  fa::ctx_release(ctx);
 }
 
 const char* fa_last_error(const fa_ctx* ctx) {
@@ -221,6 +306,10 @@ int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a
   if (e && e->residual && e->ldr < n)
     return set_error(ctx, FA_ERR_ARG, "MatMulFused: Residual leading dimension < n");
   if (m == 0 || n == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "MatMulFused");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   const size_t esz = b_dtype == FA_DT_BF16 ? 2 : 4;
   void *da = nullptr, *db = nullptr, *dc = nullptr;
@@ -271,6 +360,10 @@ int fa_matmul_fused_dev(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const floa
   if (e && (e->act < FA_ACT_NONE || e->act > FA_ACT_TANH))
     return set_error(ctx, FA_ERR_ARG, "MatMulFused: unknown activation %d", e->act);
   if (m == 0 || n == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "MatMulFused");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   fa::GemmArgs g;
   g.m = m; g.n = n; g.k = k;
@@ -290,6 +383,10 @@ int fa_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float*
   if (!ctx) return set_error(ctx, FA_ERR_ARG, "RowSumSquares: ctx is NULL");
   if (m < 0 || n < 0) return set_error(ctx, FA_ERR_ARG, "RowSumSquares: negative shape");
   if (m == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "RowSumSquares");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void *dx, *dout;
   int rc;
@@ -308,6 +405,10 @@ int fa_rmsnorm(fa_ctx* ctx, const float* x, const float* g, float eps, int64_t r
   if (rows < 0) return set_error(ctx, FA_ERR_ARG, "RMSNorm: negative row count");
   if (!g) return set_error(ctx, FA_ERR_ARG, "RMSNorm: g must have %lld elements", (long long)n);
   if (rows == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "RMSNorm");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void *dx, *dg, *dout;
   int rc;
@@ -330,6 +431,10 @@ int fa_rope(fa_ctx* ctx, const float* x, double base, const int32_t* positions, 
   if (rows % T != 0) return set_error(ctx, FA_ERR_ARG, "RoPE: %lld rows are not a multiple of T=%d", (long long)rows, T);
   if (!positions) return set_error(ctx, FA_ERR_ARG, "RoPE: got 0 positions for %d slots", T);
   if (rows == 0) return FA_OK;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "RoPE");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   std::vector<float> cs, sn;
   fa::rope_tables_host(base, positions, T, D, cs, sn);
@@ -355,21 +460,59 @@ static size_t span4(int32_t B, int32_t H, int32_t R, int32_t C, int64_t sb, int6
   return (size_t)(last + 1) * 4;
 }
 
+namespace {
+int attention_check(fa_ctx* ctx, int32_t B, int32_t H, int32_t T, int32_t S, int32_t D, int64_t q_sb, int64_t q_sh,
+                    int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh, int64_t m_sb, int64_t m_sh, int64_t m_sr,
+                    int64_t m_sc) {
+  if (!ctx) return set_error(ctx, FA_ERR_ARG, "Attention: ctx is NULL");
+  if (B < 0 || H < 0 || T < 0 || S < 0 || D < 0) return set_error(ctx, FA_ERR_ARG, "Attention: negative shape");
+  if (q_sb < 0 || q_sh < 0 || k_sb < 0 || k_sh < 0 || v_sb < 0 || v_sh < 0 || m_sb < 0 || m_sh < 0 || m_sr < 0 ||
+      m_sc < 0)
+    return set_error(ctx, FA_ERR_ARG, "Attention: negative stride");
+  if ((int64_t)B * H * T > 0 && D > 0 && S == 0) return set_error(ctx, FA_ERR_ARG, "Attention: no keys (S = 0)");
+  return FA_OK;
+}
+
+int attention_launch(fa_ctx* ctx, const fa::AttnGenericArgs& a) {
+  // the MFMA kernel for the head dims it covers, the per-row kernel otherwise
+  if (fa::attention_dense_ok(a)) return fa::launch_attention_dense(ctx, a, ctx->stream);
+  return fa::launch_attention_generic(ctx, a, ctx->stream);
+}
+}  // namespace
+
+int fa_attention_dev(fa_ctx* ctx, const float* q, const float* k, const float* v, int32_t B, int32_t H, int32_t T,
+                     int32_t S, int32_t D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t v_sb,
+                     int64_t v_sh, const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_sr, int64_t m_sc,
+                     float scale, float* out) {
+  int rc = attention_check(ctx, B, H, T, S, D, q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, m_sb, m_sh, m_sr, m_sc);
+  if (rc) return rc;
+  if ((int64_t)B * H * T == 0 || D == 0) return FA_OK;
+  if (!q || !k || !v || !out) return set_error(ctx, FA_ERR_ARG, "Attention: NULL buffer");
+  if ((rc = fa::refuse_capture(ctx, ctx->stream, "Attention"))) return rc;
+  FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
+  fa::AttnGenericArgs a;
+  a.q = q; a.k = k; a.v = v; a.mask = mask;
+  a.B = B; a.H = H; a.T = T; a.S = S; a.D = D;
+  a.q_sb = q_sb; a.q_sh = q_sh; a.k_sb = k_sb; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sh = v_sh;
+  a.m_sb = m_sb; a.m_sh = m_sh; a.m_sr = m_sr; a.m_sc = m_sc;
+  a.scale = scale;
+  a.out = out;
+  return attention_launch(ctx, a);
+}
+
 int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, int32_t B, int32_t H, int32_t T,
                  int32_t S, int32_t D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t v_sb,
                  int64_t v_sh, const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_sr, int64_t m_sc, float scale,
                  float* out) {
-  if (!ctx) return set_error(ctx, FA_ERR_ARG, "Attention: ctx is NULL");
-  if (B < 0 || H < 0 || T < 0 || S < 0 || D < 0)
-    return set_error(ctx, FA_ERR_ARG, "Attention: negative shape");
-  if (q_sb < 0 || q_sh < 0 || k_sb < 0 || k_sh < 0 || v_sb < 0 || v_sh < 0 || m_sb < 0 || m_sh < 0 || m_sr < 0 ||
-      m_sc < 0)
-    return set_error(ctx, FA_ERR_ARG, "Attention: negative stride");
+  int rc = attention_check(ctx, B, H, T, S, D, q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, m_sb, m_sh, m_sr, m_sc);
+  if (rc) return rc;
   if ((int64_t)B * H * T == 0 || D == 0) return FA_OK;
-  if (S == 0) return set_error(ctx, FA_ERR_ARG, "Attention: no keys (S = 0)");
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "Attention");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void *dq, *dk, *dv, *dm = nullptr, *dout;
-  int rc;
   if ((rc = fa::stage_h2d(ctx, S_Q, q, span4(B, H, T, D, q_sb, q_sh, D, 1), &dq))) return rc;
   if ((rc = fa::stage_h2d(ctx, S_K, k, span4(B, H, S, D, k_sb, k_sh, D, 1), &dk))) return rc;
   if ((rc = fa::stage_h2d(ctx, S_V, v, span4(B, H, S, D, v_sb, v_sh, D, 1), &dv))) return rc;
@@ -384,7 +527,7 @@ int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, in
   a.m_sb = m_sb; a.m_sh = m_sh; a.m_sr = m_sr; a.m_sc = m_sc;
   a.scale = scale;
   a.out = (float*)dout;
-  if ((rc = fa::launch_attention_generic(ctx, a, ctx->stream))) return rc;
+  if ((rc = attention_launch(ctx, a))) return rc;
   FA_HIP_CHECK(ctx, hipMemcpyAsync(out, dout, obytes, hipMemcpyDeviceToHost, ctx->stream));
   FA_HIP_CHECK(ctx, hipStreamSynchronize(ctx->stream));
   return FA_OK;
@@ -400,12 +543,17 @@ int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, cons
     return set_error(ctx, FA_ERR_ARG, "Similarities top-k: k=%d outside 1..min(32, %lld)", topk, (long long)nd);
   if (nq == 0) return FA_OK;
   if (nq > 65535) return set_error(ctx, FA_ERR_ARG, "Similarities top-k: %lld queries > 65535", (long long)nq);
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "Similarities");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   int rc;
   // Batches of queries: the fused kernels (no score matrix; blocks of 256
-  // queries share each pass over the docs). Few queries: the fp32-MFMA
-  // product and the two-pass top-k, which read the docs once without
-  // computing a 256-query block.
+  // queries share each pass over the docs; exact float32-rounded scores).
+  // Few queries: the fp32-MFMA product and the two-pass top-k, which read the
+  // docs once without computing a 256-query block (the fused stage computes
+  // whole blocks: one query would cost what 256 do).
   if (nq >= 128 && fa::score_fused_ok(queries, d, docs, d, d, topk)) {
     const int nwg = fa::score_workgroups(nd, ctx->cu_count);
     fa::DevBuf& ws = ctx->slot(S_TOPK);
@@ -434,6 +582,10 @@ int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const fl
     return set_error(ctx, FA_ERR_ARG, "Similarities top-k: k=%d outside 1..min(32, %lld)", topk, (long long)nd);
   if (nq == 0) return FA_OK;
   if (nq > 65535) return set_error(ctx, FA_ERR_ARG, "Similarities top-k: %lld queries > 65535", (long long)nq);
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "Similarities");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   void *dq, *dd;
   int rc;

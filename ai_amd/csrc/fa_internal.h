@@ -56,6 +56,7 @@ enum : size_t {
   S_CL_WORK, S_CL_X, S_CL_C, S_CL_OUT,  // cluster entry points
   S_TOPK,                               // top-k candidates
   S_BPLANES,                            // B operand as bf16 [n x k] planes (matmul drop-in)
+  S_APACK,                              // A operand packed to [nb][m][kp] (strided matmul)
   S_COUNT
 };
 }  // namespace slots
@@ -74,6 +75,18 @@ struct fa_ctx {
 };
 
 namespace fa {
+
+// Handle registry (context.cpp): models are tracked with their context so
+// that fa_destroy and the exit handler release them first. unregister_model
+// returns whether m was live.
+void register_model(fa_model* m, fa_ctx* ctx);
+bool unregister_model(fa_model* m);
+// Releases every resource of a model (model.cpp); m must not be registered.
+void model_release(fa_model* m);
+
+// FA_ERR_STATE when stream s is being captured into a HIP graph: the entry
+// points that grow buffers or upload per-call plans cannot be captured.
+int refuse_capture(fa_ctx* ctx, hipStream_t s, const char* op);
 
 // Copies host data into scratch slot `slot` (grown as needed) and returns
 // the device pointer via *out.
@@ -119,7 +132,33 @@ struct GemmArgs {
   // micro-batches): the tile choice can count on them to fill the CUs its
   // own tiles leave idle
   bool shared = false;
+  // nbatch > 1 (b_terms = 3 only, at most kMaxGridZ): entry z computes
+  // C + z*c_bs = A + z*a_bs times the planes at B + z*b_bs (bf16 elements)
+  int64_t nbatch = 1;
+  int64_t a_bs = 0, b_bs = 0, c_bs = 0;
 };
+
+constexpr int kMaxGridZ = 65535;
+
+// Batch dimensions of a strided operand (tensor.MatMul's broadcast, the
+// reference's walkRows over broadcast strides, tensor/matmul.go:92-98):
+// entry z (row-major over dim[0..nd-1]) starts at sum_d idx_d * stride[d].
+struct BatchMap {
+  int nd = 0;
+  int dim[FA_MAX_BATCH_DIMS] = {};
+  int64_t stride[FA_MAX_BATCH_DIMS] = {};
+};
+// A view [nb][m][k] (element (z, i, p) at src[off(z) + i*rs + p*cs]) ->
+// contiguous fp32 [nb][m][kp] with columns k..kp-1 zero (kp % 4 == 0).
+// Entries z0 .. z0 + nb - 1 of the view.
+int launch_pack_a(fa_ctx* ctx, const float* src, const BatchMap& bm, int z0, int64_t rs, int64_t cs, int64_t nb,
+                  int64_t m, int64_t k, int64_t kp, float* dst, hipStream_t s);
+// B view, logical [k x n] per entry (element (z, p, j) at src[off(z) + p*rs +
+// j*cs]) -> three bf16 planes hi, mid, lo [n][kp] per entry, entry z at
+// planes + 3*(z - z0)*n*kp for entries z0 .. z0 + nb - 1, columns k..kp-1
+// zero (kp % 8 == 0).
+int launch_split_b_view(fa_ctx* ctx, const float* src, const BatchMap& bm, int z0, int64_t rs, int64_t cs,
+                        int64_t nb, int64_t n, int64_t k, int64_t kp, uint16_t* planes, hipStream_t s);
 
 // B [k x n] (FA_B_KN) or [n x k] (FA_B_NK), leading dimension ldb -> bf16
 // planes [n][k] at planes (k % 8 == 0): fp32 B as three planes hi, mid, lo
@@ -150,6 +189,11 @@ struct AttnGenericArgs {
   float* out;
 };
 int launch_attention_generic(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s);
+// The MFMA kernel for head_dim 64/128/256/512 with 16-byte aligned q/k/v rows
+// (base pointers and batch/head strides): whether it applies (FA_ATTN_DENSE=0
+// turns it off, for comparisons), and its launch.
+bool attention_dense_ok(const AttnGenericArgs& a);
+int launch_attention_dense(fa_ctx* ctx, const AttnGenericArgs& a, hipStream_t s);
 
 // Per-row top-k of scores [nq x nd] (1 <= topk <= 32, nq <= 65535) into
 // idx/val [nq x topk]; scratch holds topk_scratch_bytes(nq, nd, topk) bytes
@@ -164,6 +208,8 @@ int score_workgroups(int64_t nd, int cus);
 // Records the device address of the no-alloc entry point's fixed scratch
 // array for ctx's device (current); once per device.
 int noalloc_scratch_init(fa_ctx* ctx);
+// Gives up ctx's claim on its device's no-alloc array (context release).
+void noalloc_release(const fa_ctx* ctx);
 size_t score_scratch_bytes(int d, int nwg);
 bool score_fused_ok(const float* q, int64_t ldq, const float* docs, int64_t ldd, int d, int topk);
 int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, const float* docs, int64_t nd,

@@ -100,6 +100,10 @@ struct GemmParams {
   // split-bf16 kernel with BT = 3: B is three bf16 planes (hi, mid, lo of
   // fp32 weights) b_plane elements apart
   int64_t b_plane;
+  // batched products (grid.z = batch entries, BT = 3 only): entry z reads A
+  // at a + z * a_bs, B at b + z * b_bs (bf16 elements) and writes c + z * c_bs
+  int64_t a_bs, b_bs, c_bs;
+  int nbatch;
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -491,6 +495,11 @@ __global__ __launch_bounds__(TL::NT, TL::MINW) void gemm_x3_kernel(GemmParams p)
   const int wave = tid >> 6;
   const int wm = wave / TL::WN, wn = wave % TL::WN;
   const int64_t M = p.m, N = p.n;
+  if constexpr (BT == 3) {  // batch entry blockIdx.z (0 and zero strides when not batched)
+    p.a += blockIdx.z * p.a_bs;
+    p.b = static_cast<const uint16_t*>(p.b) + blockIdx.z * p.b_bs;
+    p.c += blockIdx.z * p.c_bs;
+  }
   const float* __restrict__ A = p.a;
   const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.b);
 
@@ -656,7 +665,8 @@ void launch_x3(GemmParams p, hipStream_t s) {
   p.tiles_n = (int)((p.n + TL::BN - 1) / TL::BN);
   p.nk = (int)(p.k / TL::BK);
   if (p.ksplit < 1) p.ksplit = 1;
-  dim3 grid(p.tiles_m * p.tiles_n, p.ksplit), block(TL::NT);
+  if (p.nbatch < 1 || BT != 3) p.nbatch = 1;
+  dim3 grid(p.tiles_m * p.tiles_n, p.ksplit, p.nbatch), block(TL::NT);
   hipLaunchKernelGGL((gemm_x3_kernel<TL, EPI, BT>), grid, block, 0, s, p);
 }
 
@@ -967,7 +977,8 @@ void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
 // of LDS: one workgroup per CU) once they give every CU half a tile, else
 // 64x64 tiles (128x64 for GeGLU) of four waves.
 void dispatch_x3_bt3(const GemmParams& p, Epi epi, int cus, hipStream_t s) {
-  const int64_t tiles128 = ((p.m + 127) / 128) * ((p.n + 127) / 128) * std::max(p.ksplit, 1);
+  const int64_t tiles128 =
+      ((p.m + 127) / 128) * ((p.n + 127) / 128) * std::max(p.ksplit, 1) * std::max(p.nbatch, 1);
   const bool big = 2 * tiles128 >= cus;
   switch (epi) {
     case Epi::None:
@@ -1029,7 +1040,103 @@ __global__ __launch_bounds__(256) void split_b_kernel(const void* __restrict__ b
 
 bool x3_has_geglu(XTileId t) { return t != XTileId::x64x64; }
 
+// ---- strided and batched operands (tensor.MatMul's views) ---------------------
+// Element offset of batch entry z (row-major over the batch dimensions) in a
+// strided operand; 32-bit index arithmetic (entries < 2^31).
+__device__ __forceinline__ int64_t batch_offset(const BatchMap& bm, int z) {
+  int64_t off = 0;
+  for (int d = bm.nd - 1; d >= 0; d--) {
+    const int q = z / bm.dim[d];
+    off += (int64_t)(z - q * bm.dim[d]) * bm.stride[d];
+    z = q;
+  }
+  return off;
+}
+
+// A view [nb][m][k] with element (z, i, p) at src[off(z) + i*rs + p*cs] ->
+// contiguous [nb][m][kp], columns k..kp-1 zero. One thread per 4 columns.
+__global__ __launch_bounds__(256) void pack_a_kernel(const float* __restrict__ src, BatchMap bm, int z0, int64_t rs,
+                                                     int64_t cs, int64_t m, int64_t k, int64_t kp, int64_t total,
+                                                     float* __restrict__ dst) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int64_t kq = kp / 4;
+  const int64_t row = t / kq;  // z * m + i
+  const int64_t p0 = (t - row * kq) * 4;
+  const int z = (int)(row / m);
+  const float* s = src + batch_offset(bm, z0 + z) + (row - (int64_t)z * m) * rs;
+  f32x4 v;
+#pragma unroll
+  for (int e = 0; e < 4; e++) v[e] = p0 + e < k ? s[(p0 + e) * cs] : 0.f;
+  *reinterpret_cast<f32x4*>(dst + row * kp + p0) = v;
+}
+
+// B view, logical [k x n] per entry with element (z, p, j) at src[off(z) +
+// p*rs + j*cs] -> three bf16 planes hi, mid, lo of [n][kp] per entry
+// (planes + (3 z + term) * n * kp), columns k..kp-1 zero. One thread per
+// (entry, column, 8 k values); consecutive threads take consecutive 8-value
+// chunks of one column when p is the unit-stride index (k_major), else
+// consecutive columns of one chunk.
+__global__ __launch_bounds__(256) void split_b_view_kernel(const float* __restrict__ src, BatchMap bm, int z0, int64_t rs,
+                                                           int64_t cs, int64_t n, int64_t k, int64_t kp, int k_major,
+                                                           int64_t total, uint16_t* __restrict__ planes) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int64_t kc_n = kp / 8, per = n * kc_n;
+  const int z = (int)(t / per);
+  const int64_t r = t - (int64_t)z * per;
+  int64_t col, kc;
+  if (k_major) {
+    col = r / kc_n;
+    kc = r - col * kc_n;
+  } else {
+    kc = r / n;
+    col = r - kc * n;
+  }
+  const float* s = src + batch_offset(bm, z0 + z) + col * cs;
+  uint32_t h[8], md[8], l[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int64_t p = kc * 8 + e;
+    const Split3 sp = split3(p < k ? s[p * rs] : 0.f);
+    h[e] = sp.h;
+    md[e] = sp.m;
+    l[e] = sp.l;
+  }
+  const int64_t plane = n * kp;
+  uint16_t* o = planes + (int64_t)z * 3 * plane + col * kp + kc * 8;
+  *reinterpret_cast<uint4*>(o) =
+      make_uint4(pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7]));
+  *reinterpret_cast<uint4*>(o + plane) =
+      make_uint4(pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3]), pack_hi16(md[4], md[5]), pack_hi16(md[6], md[7]));
+  *reinterpret_cast<uint4*>(o + 2 * plane) =
+      make_uint4(pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]), pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7]));
+}
+
 }  // namespace
+
+int launch_pack_a(fa_ctx* ctx, const float* src, const BatchMap& bm, int z0, int64_t rs, int64_t cs, int64_t nb,
+                  int64_t m, int64_t k, int64_t kp, float* dst, hipStream_t s) {
+  if (kp % 4 != 0 || kp < k) return set_error(ctx, FA_ERR_ARG, "MatMul: packed width %lld", (long long)kp);
+  const int64_t total = nb * m * (kp / 4);
+  if (total == 0) return FA_OK;
+  hipLaunchKernelGGL(pack_a_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, bm, z0, rs, cs, m,
+                     k, kp, total, dst);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
+
+int launch_split_b_view(fa_ctx* ctx, const float* src, const BatchMap& bm, int z0, int64_t rs, int64_t cs,
+                        int64_t nb, int64_t n, int64_t k, int64_t kp, uint16_t* planes, hipStream_t s) {
+  if (kp % 8 != 0 || kp < k) return set_error(ctx, FA_ERR_ARG, "MatMul: packed width %lld", (long long)kp);
+  const int64_t total = nb * n * (kp / 8);
+  if (total == 0) return FA_OK;
+  const int k_major = (rs == 1 && cs != 1) ? 1 : 0;
+  hipLaunchKernelGGL(split_b_view_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, bm, z0, rs, cs,
+                     n, k, kp, k_major, total, planes);
+  FA_CHECK_LAUNCH(ctx);
+  return FA_OK;
+}
 
 int gemm_ksplit() {
   static const int v = [] {
@@ -1068,7 +1175,18 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
   p.residual = g.residual; p.ldr = g.ldr; p.act = g.act;
   p.ksplit = 1;
   p.b_plane = g.b_plane;
+  p.nbatch = 1;
   if (g.b_terms != 1 && g.b_terms != 3) return set_error(ctx, FA_ERR_ARG, "MatMul: %d B planes", g.b_terms);
+  if (g.nbatch > 1) {
+    // batch entries on grid.z: the three-plane kernel only, one K range
+    if (g.b_terms != 3 || g.ksplit > 1 || g.nbatch > kMaxGridZ)
+      return set_error(ctx, FA_ERR_ARG, "MatMul: a batch of %lld needs three B planes, no K split and <= %d entries",
+                       (long long)g.nbatch, kMaxGridZ);
+    p.nbatch = (int)g.nbatch;
+    p.a_bs = g.a_bs;
+    p.b_bs = g.b_bs;
+    p.c_bs = g.c_bs;
+  }
   if (((g.m + 63) / 64) * ((g.n + 63) / 64) > INT32_MAX / 4) return set_error(ctx, FA_ERR_ARG, "MatMul: too many tiles");
   const bool bf16 = g.b_dtype == FA_DT_BF16;
   const bool nk = g.b_layout == FA_B_NK;

@@ -451,15 +451,23 @@ int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out) {
       rc = set_error(ctx, FA_ERR_HIP, "hipStreamCreate failed");
   }
   if (rc) {
-    fa_gemma_destroy(m);
+    fa::model_release(m);
     return rc;
   }
+  fa::register_model(m, ctx);
   *out = m;
   return FA_OK;
 }
 
 void fa_gemma_destroy(fa_model* m) {
-  if (!m) return;
+  // unknown, already closed with its context, or at exit: nothing to do
+  if (!m || !fa::unregister_model(m)) return;
+  fa::model_release(m);
+}
+
+}  // extern "C"
+
+void fa::model_release(fa_model* m) {
   (void)hipSetDevice(m->ctx->device);
   (void)hipStreamSynchronize(m->ctx->stream);
   for (hipStream_t st : m->mb_stream)
@@ -485,11 +493,17 @@ void fa_gemma_destroy(fa_model* m) {
   delete m;
 }
 
+extern "C" {
+
 int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t* shape, int32_t ndim,
                         const void* data) {
   if (!m || !name || !data || (ndim > 0 && !shape)) return set_error(m ? m->ctx : nullptr, FA_ERR_ARG, "gemma: NULL argument");
   fa_ctx* ctx = m->ctx;
   if (dtype != FA_DT_F32 && dtype != FA_DT_BF16) return set_error(ctx, FA_ERR_ARG, "gemma: weight %s: dtype %d", name, dtype);
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "gemma");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   const fa_gemma_config& c = m->cfg;
   const bool v2 = m->variant == 2;
@@ -546,6 +560,14 @@ int fa_gemma_set_weight(fa_model* m, const char* name, int dtype, const int64_t*
       }
       src16 = tmp.data();
     }
+    // the six-term kernel of a three-plane matrix takes whole 32-wide K slabs
+    // (the one-plane case has the fp32-MFMA kernel for other widths): refuse
+    // here rather than at the first embed
+    if (!exact && cols % 32 != 0)
+      return set_error(ctx, FA_ERR_UNSUPPORTED,
+                       "gemma: weight %s: a float32 matrix with values bfloat16 cannot hold needs an input width "
+                       "that is a multiple of 32, got %lld",
+                       name, (long long)cols);
     if (!exact && dst.terms == 1) {
       // promote to three planes: the rows set so far become hi, mid = lo = 0
       void* np = nullptr;
@@ -687,6 +709,10 @@ int fa_gemma_finalize(fa_model* m) {
                                           : 2 + (size_t)c.n_dense + 13 * (size_t)c.num_hidden_layers;
   if (m->seen.size() != expected)
     return set_error(ctx, FA_ERR_STATE, "gemma: %zu of %zu weights set", m->seen.size(), expected);
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "gemma");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   std::vector<int32_t> pos(c.max_tokens);
   for (int t = 0; t < c.max_tokens; t++) pos[t] = t;
@@ -723,6 +749,10 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   fa_ctx* ctx = m->ctx;
   const fa_gemma_config& c = m->cfg;
   if (!m->finalized) return set_error(ctx, FA_ERR_STATE, "gemma: embed before every weight was set (finalize)");
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "gemma");
+    if (rc_) return rc_;
+  }
   if (B < 0 || T < 0) return set_error(ctx, FA_ERR_ARG, "gemma: negative batch shape [%d x %d]", B, T);
   if (B == 0) return FA_OK;
   if (!d_ids || !lengths || !(hidden ? hidden : d_out)) return set_error(ctx, FA_ERR_ARG, "gemma: NULL buffer");
@@ -1160,6 +1190,10 @@ int fa_gemma_encode_ids(fa_model* m, const int32_t* ids, const int32_t* lengths,
   int64_t M = 0;
   for (int b = 0; b < B; b++) M += lengths[b];
   const int d = m->cfg.hidden_size;
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "gemma");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
   if ((rc = m->out_dev.ensure(ctx, (size_t)M * d * 4))) return rc;
@@ -1189,6 +1223,10 @@ int fa_gemma_embed_ids(fa_model* m, const int32_t* ids, const int32_t* lengths, 
   int rc;
   if ((rc = fa::check_ids(m, ids, lengths, B, T))) return rc;
   if (dd > full) return set_error(ctx, FA_ERR_ARG, "gemma: Dim(%d) outside 1..%d", dim, full);
+  {
+    const int rc_ = fa::refuse_capture(ctx, ctx->stream, "gemma");
+    if (rc_) return rc_;
+  }
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   if ((rc = m->ids_dev.ensure(ctx, (size_t)B * T * 4))) return rc;
   if ((rc = m->out_dev.ensure(ctx, (size_t)B * dd * 4))) return rc;

@@ -752,9 +752,12 @@ int launch_score_topk(fa_ctx* ctx, const float* q, int64_t nq, int64_t ldq, cons
 // queries, in a fixed array of each device (held until the process ends). Its
 // device address comes from hipGetSymbolAddress once per device, at context
 // creation on that device; host code never passes the array's name itself.
-// Calls on one device share the array: calls that overlap on one GPU race.
-// No kernel relies on its previous contents (every value read in a call is
-// written earlier in the same call).
+// The array of a device belongs to the first context that calls the entry
+// point there, until that context is destroyed: calls from other contexts
+// on that device are refused (FA_ERR_STATE) instead of racing on it, and the
+// owner's calls are ordered by its one stream. No kernel relies on the
+// array's previous contents (every value read in a call is written earlier
+// in the same call).
 constexpr size_t kNoAllocScratchBytes = (size_t)12 << 20;
 __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
@@ -762,7 +765,27 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+const fa_ctx* g_scratch_owner[kMaxDevices] = {};
 }  // namespace
+
+void noalloc_release(const fa_ctx* ctx) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  for (auto& o : g_scratch_owner)
+    if (o == ctx) o = nullptr;
+}
+
+// Claims the device's array for ctx (or finds it already ctx's).
+int noalloc_claim(fa_ctx* ctx) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  const fa_ctx*& o = g_scratch_owner[ctx->device];
+  if (o && o != ctx)
+    return set_error(ctx, FA_ERR_STATE,
+                     "Similarities (no-alloc): the fixed scratch of device %d belongs to another context until that "
+                     "context is destroyed (calls from two contexts would race on it)",
+                     ctx->device);
+  o = ctx;
+  return FA_OK;
+}
 
 int noalloc_scratch_init(fa_ctx* ctx) {
   const int dev = ctx->device;
@@ -830,6 +853,7 @@ extern "C" int fa_similarities_topk_dev_noalloc(fa_ctx* ctx, const float* querie
   void* ptr = ctx->device >= 0 && ctx->device < fa::kMaxDevices ? fa::g_scratch_ptr[ctx->device] : nullptr;
   if (!ptr) return set_error(ctx, FA_ERR_STATE, "Similarities (no-alloc): scratch address of device %d unknown",
                              ctx->device);
+  if (const int rc = fa::noalloc_claim(ctx)) return rc;
   FA_HIP_CHECK(ctx, hipSetDevice(ctx->device));
   return fa::launch_score_topk(ctx, queries, nq, d, docs, nd, d, d, topk, idx, val, ptr, nwg, ctx->stream);
 }

@@ -156,6 +156,67 @@ Tensor Tensor::T() const {
   return t;
 }
 
+static int norm_dim(const char* op, int dim, int nd) {
+  const int d = dim < 0 ? dim + nd : dim;
+  if (d < 0 || d >= nd) throw Error(op, "dimension " + std::to_string(dim) + " out of range for rank " + std::to_string(nd));
+  return d;
+}
+
+Tensor Tensor::Transpose(int d0, int d1) const {
+  const int a = norm_dim("Transpose", d0, Dims()), b = norm_dim("Transpose", d1, Dims());
+  Tensor t = *this;
+  std::swap(t.shape_[a], t.shape_[b]);
+  std::swap(t.strides_[a], t.strides_[b]);
+  return t;
+}
+
+Tensor Tensor::Select(int dim, int64_t index) const {
+  const int d = norm_dim("Select", dim, Dims());
+  if (index < 0 || index >= shape_[d])
+    fail("Select", "index " + std::to_string(index) + " out of range for dimension of size " + std::to_string(shape_[d]));
+  Tensor t = *this;
+  t.offset_ += index * strides_[d];
+  t.shape_.erase(t.shape_.begin() + d);
+  t.strides_.erase(t.strides_.begin() + d);
+  return t;
+}
+
+Tensor Tensor::Narrow(int dim, int64_t start, int64_t length) const {
+  const int d = norm_dim("Narrow", dim, Dims());
+  if (start < 0 || length < 0 || start + length > shape_[d])
+    fail("Narrow", "range [" + std::to_string(start) + ", " + std::to_string(start + length) + ") outside dimension of size " +
+                       std::to_string(shape_[d]));
+  Tensor t = *this;
+  if (length > 0) t.offset_ += start * strides_[d];
+  t.shape_[d] = length;
+  return t;
+}
+
+Tensor Tensor::Unsqueeze(int dim) const {
+  const int nd = Dims();
+  const int d = dim < 0 ? dim + nd + 1 : dim;
+  if (d < 0 || d > nd) fail("Unsqueeze", "dimension " + std::to_string(dim) + " out of range for rank " + std::to_string(nd));
+  Tensor t = *this;
+  const int64_t st = d < nd ? strides_[d] * shape_[d] : 1;
+  t.shape_.insert(t.shape_.begin() + d, 1);
+  t.strides_.insert(t.strides_.begin() + d, st);
+  return t;
+}
+
+Tensor Tensor::Squeeze(int dim) const {
+  const int d = norm_dim("Squeeze", dim, Dims());
+  if (shape_[d] != 1) fail("Squeeze", "dimension " + std::to_string(dim) + " has size " + std::to_string(shape_[d]));
+  Tensor t = *this;
+  t.shape_.erase(t.shape_.begin() + d);
+  t.strides_.erase(t.strides_.begin() + d);
+  return t;
+}
+
+float Tensor::Item() const {
+  if (Size() != 1) fail("Item", "tensor of shape " + shape_str(shape_) + " has " + std::to_string(Size()) + " elements");
+  return Float32s()[0];
+}
+
 std::vector<float> Tensor::RowSumSquares() const {
   if (shape_.size() != 2) fail("RowSumSquares", "expected a 2-D tensor, got " + shape_str(shape_));
   Tensor x = Contiguous();
@@ -164,6 +225,77 @@ std::vector<float> Tensor::RowSumSquares() const {
   call("RowSumSquares", fa_row_sum_squares(device(), x.base(), shape_[0], shape_[1], out.data()));
   return out;
 }
+
+namespace {
+
+fa_matrix view2d(const Tensor& t) {
+  fa_matrix v{};
+  const int nd = t.Dims();
+  v.data = t.base();
+  v.rs = t.strides()[nd - 2];
+  v.cs = t.strides()[nd - 1];
+  return v;
+}
+
+// broadcastShapes (tensor/shape.go:94-118)
+Shape broadcast_shapes(const char* op, const Shape& a, const Shape& b) {
+  const size_t n = std::max(a.size(), b.size());
+  Shape out(n);
+  for (size_t i = 1; i <= n; i++) {
+    const int64_t da = i <= a.size() ? a[a.size() - i] : 1, db = i <= b.size() ? b[b.size() - i] : 1;
+    if (da == db || db == 1) out[n - i] = da;
+    else if (da == 1) out[n - i] = db;
+    else fail(op, "shapes " + shape_str(a) + " and " + shape_str(b) + " are not broadcastable");
+  }
+  return out;
+}
+
+Tensor matmul2d(const Tensor& x, const Tensor& y) {
+  const int64_t m = x.Dim(0), k = x.Dim(1), n = y.Dim(1);
+  if (k != y.Dim(0)) fail("MatMul", "shape mismatch " + shape_str(x.shape()) + " · " + shape_str(y.shape()));
+  Tensor out = Tensor::Zeros({m, n});
+  if (m == 0 || n == 0) return out;
+  const fa_matrix a = view2d(x), b = view2d(y);
+  call("MatMul", fa_matmul_strided(device(), 0, nullptr, m, n, k, &a, &b, nullptr, const_cast<float*>(out.base())));
+  return out;
+}
+
+// matmulBatched (tensor/matmul.go:74-127)
+Tensor matmul_batched(const Tensor& x, const Tensor& y) {
+  const int nx = x.Dims(), ny = y.Dims();
+  const int64_t m = x.Dim(nx - 2), k = x.Dim(nx - 1), n = y.Dim(ny - 1);
+  if (k != y.Dim(ny - 2)) fail("MatMul", "shape mismatch " + shape_str(x.shape()) + " · " + shape_str(y.shape()));
+  const Shape xb(x.shape().begin(), x.shape().end() - 2), yb(y.shape().begin(), y.shape().end() - 2);
+  if (ny == 2 && x.IsContiguous()) {  // [B..., m, k] . [k, n]: the batch folds into M
+    Shape shape = xb;
+    shape.push_back(m);
+    shape.push_back(n);
+    int64_t rows = m;
+    for (int64_t v : xb) rows *= v;
+    return MatMul(x.Reshape({rows, k}), y).Reshape(shape);
+  }
+  const Shape batch = broadcast_shapes("MatMul", xb, yb);
+  if (batch.size() > FA_MAX_BATCH_DIMS)
+    fail("MatMul", std::to_string(batch.size()) + " batch dimensions, at most " + std::to_string(FA_MAX_BATCH_DIMS));
+  Shape shape = batch;
+  shape.push_back(m);
+  shape.push_back(n);
+  Tensor out = Tensor::Zeros(shape);
+  if (out.Size() == 0) return out;
+  fa_matrix a = view2d(x), b = view2d(y);
+  // broadcastStrides (tensor/shape.go:122-131): stride 0 where a dimension is broadcast
+  const size_t nb = batch.size();
+  for (size_t d = 0; d < nb; d++) {
+    const size_t offx = nb - xb.size(), offy = nb - yb.size();
+    a.bstride[d] = d >= offx && xb[d - offx] != 1 ? x.strides()[d - offx] : 0;
+    b.bstride[d] = d >= offy && yb[d - offy] != 1 ? y.strides()[d - offy] : 0;
+  }
+  call("MatMul", fa_matmul_strided(device(), (int32_t)nb, batch.data(), m, n, k, &a, &b, nullptr,
+                                   const_cast<float*>(out.base())));
+  return out;
+}
+
+}  // namespace
 
 Tensor MatMulFused(const Tensor& x, const Tensor& w, const Fused& f) {
   if (x.Dims() != 2 || w.Dims() != 2)
@@ -180,19 +312,9 @@ Tensor MatMulFused(const Tensor& x, const Tensor& w, const Fused& f) {
                               shape_str(t->shape()));
   Tensor out = Tensor::Zeros({m, n});
   if (m == 0 || n == 0) return out;
-  const Tensor xc = x.Contiguous();
-  // A transposed view of a contiguous [n, k] operand is consumed in place
-  // (the reference reads strided views without a copy, matmul.go:10-36).
-  int layout = FA_B_KN;
-  Tensor wc;
-  int64_t ldb = n;
-  if (!w.IsContiguous() && w.strides()[0] == 1 && w.strides()[1] == k) {
-    wc = w;
-    layout = FA_B_NK;
-    ldb = k;
-  } else {
-    wc = w.Contiguous();
-  }
+  // x and w are read through their strides (transposed views included, as
+  // the reference's GemmZeroEpilogue reads blas.Mat views); the element-wise
+  // operands are made contiguous as the reference does (matmul_fused.go:79-84)
   fa_epilogue e{};
   Tensor bias, mul, res;
   if (f.Bias) { bias = f.Bias->Contiguous(); e.bias = bias.base(); }
@@ -200,16 +322,35 @@ Tensor MatMulFused(const Tensor& x, const Tensor& w, const Fused& f) {
   e.act = f.Act;
   if (f.Mul) { mul = f.Mul->Contiguous(); e.mul = mul.base(); e.ldm = n; }
   if (f.Residual) { res = f.Residual->Contiguous(); e.residual = res.base(); e.ldr = n; }
-  call("MatMulFused", fa_matmul_fused(device(), m, n, k, xc.base(), k, wc.base(), ldb, FA_DT_F32, layout, &e,
-                                      const_cast<float*>(out.base()), n));
+  const fa_matrix a = view2d(x), b = view2d(w);
+  call("MatMulFused", fa_matmul_strided(device(), 0, nullptr, m, n, k, &a, &b, &e, const_cast<float*>(out.base())));
   return out;
 }
 
 Tensor MatMul(const Tensor& x, const Tensor& w) {
-  if (x.Dims() != 2 || w.Dims() != 2)
-    fail("MatMul", "this mirror covers the 2-D product, got " + shape_str(x.shape()) + " and " + shape_str(w.shape()));
-  if (x.Dim(1) != w.Dim(0)) fail("MatMul", "shape mismatch " + shape_str(x.shape()) + " · " + shape_str(w.shape()));
-  return MatMulFused(x, w, Fused{});
+  const int nx = x.Dims(), nw = w.Dims();
+  if (nx == 0 || nw == 0)
+    fail("MatMul", "operands must be at least 1-D, got " + shape_str(x.shape()) + " and " + shape_str(w.shape()));
+  if (nx == 1 && nw == 1) {
+    if (x.Dim(0) != w.Dim(0)) fail("MatMul", "shape mismatch " + shape_str(x.shape()) + " · " + shape_str(w.shape()));
+    return MatMul(x.Unsqueeze(0), w.Unsqueeze(1)).Reshape({});
+  }
+  if (nx == 1) return MatMul(x.Unsqueeze(0), w).Squeeze(-2);
+  if (nw == 1) return MatMul(x, w.Unsqueeze(1)).Squeeze(-1);
+  if (nx == 2 && nw == 2) return matmul2d(x, w);
+  return matmul_batched(x, w);
+}
+
+Tensor Dot(const Tensor& x, const Tensor& y) {
+  if (x.Dims() != 1 || y.Dims() != 1)
+    fail("Dot", "expected 1-D tensors, got " + shape_str(x.shape()) + " and " + shape_str(y.shape()));
+  return MatMul(x, y);
+}
+
+Tensor Outer(const Tensor& x, const Tensor& y) {
+  if (x.Dims() != 1 || y.Dims() != 1)
+    fail("Outer", "expected 1-D tensors, got " + shape_str(x.shape()) + " and " + shape_str(y.shape()));
+  return MatMul(x.Unsqueeze(1), y.Unsqueeze(0));
 }
 
 Tensor RMSNorm(const Tensor& x, const Tensor& g, float eps) {
@@ -642,7 +783,7 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
     if (o.MaxTokens > 0) cfg.MaxTokens = std::min(o.MaxTokens, cfg.Variant == 2 ? 8192 : 2048);
     if (o.BatchTokens <= 0) throw Error("gemma: BatchTokens must be positive");
     // sentence-transformers head (model.go:236-310): mean pooling, Dense
-    // layers without bias, identity or Tanh, Normalize
+    // layers (linear.weight; identity or Tanh), Normalize
     struct DenseMod {
       std::string path;
       int in, out, act;
@@ -664,8 +805,10 @@ std::unique_ptr<Model> Model::Load(const std::string& dir, const LoadOpts& o) {
               (mode.empty() && !pc.get_bool("pooling_mode_mean_tokens", true)))
             throw Error("gemma: only mean pooling is supported");
         } else if (type == "sentence_transformers.models.Dense") {
+          // the reference reads the "bias" flag and loads linear.weight only
+          // (model.go:277-304): a bias tensor is present but not applied
           const json::Value dc = read_json(mdir + "/config.json", "Dense config");
-          if (dc.get_bool("bias")) throw Error("gemma: Dense layers with bias are not supported");
+          (void)dc.get_bool("bias");
           const std::string act = dc.get_string("activation_function");
           int a = FA_ACT_NONE;
           if (act == "torch.nn.modules.activation.Tanh") a = FA_ACT_TANH;

@@ -74,6 +74,17 @@ class Tensor {
   Tensor Expand(Shape shape) const;
   // Transposed view of a 2-D tensor (T).
   Tensor T() const;
+  // Views (tensor/view.go): dimensions d0 and d1 swapped (negative dims count
+  // from the end); the slice at index of dimension dim, which is removed;
+  // length elements of dimension dim from start; a new dimension of size 1
+  // at dim; dimension dim (of size 1) removed.
+  Tensor Transpose(int d0, int d1) const;
+  Tensor Select(int dim, int64_t index) const;
+  Tensor Narrow(int dim, int64_t start, int64_t length) const;
+  Tensor Unsqueeze(int dim) const;
+  Tensor Squeeze(int dim) const;
+  // The single value of a tensor with one element (Item).
+  float Item() const;
 
   // (*Tensor).RowSumSquares: sum of squares of each row of a 2-D tensor.
   std::vector<float> RowSumSquares() const;
@@ -100,7 +111,16 @@ struct Fused {
   const Tensor* Residual = nullptr;
 };
 
+// tensor.MatMul (tensor/matmul.go:10-36): NumPy semantics. 2-D x 2-D is the
+// matrix product; a 1-D operand is promoted to a row (left) or column
+// (right) and the added dimension removed; with more dimensions the batch
+// dimensions broadcast. Strided views (T, Transpose, Select, Narrow,
+// Expand) are read through their strides on the device, not copied.
 Tensor MatMul(const Tensor& x, const Tensor& w);
+// Inner product of two 1-D tensors as a 0-D tensor; outer product of two
+// 1-D tensors (tensor/matmul.go:131-150).
+Tensor Dot(const Tensor& x, const Tensor& y);
+Tensor Outer(const Tensor& x, const Tensor& y);
 Tensor MatMulFused(const Tensor& x, const Tensor& w, const Fused& f);
 Tensor RMSNorm(const Tensor& x, const Tensor& g, float eps);
 Tensor RoPE(const Tensor& x, double base, const std::vector<int>& positions);

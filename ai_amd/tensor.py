@@ -123,9 +123,94 @@ def MatMulFused(x, w, f: Fused | None = None, *, w_layout: int = N.FA_B_KN, ctx:
     return out
 
 
+def _view(a: np.ndarray) -> np.ndarray:
+    """a as float32 whose strides are non-negative multiples of 4 bytes (a
+    view unchanged when it already is; a copy otherwise)."""
+    if a.dtype != np.float32:
+        return a.astype(np.float32)
+    if any(s < 0 or s % 4 for s in a.strides):
+        return np.ascontiguousarray(a)
+    return a
+
+
+def _broadcast_shapes(a: tuple, b: tuple) -> tuple:
+    """broadcastShapes (tensor/shape.go:94-118)."""
+    n = max(len(a), len(b))
+    out = []
+    for i in range(n, 0, -1):
+        da = a[len(a) - i] if i <= len(a) else 1
+        db = b[len(b) - i] if i <= len(b) else 1
+        if da == db or db == 1:
+            out.append(da)
+        elif da == 1:
+            out.append(db)
+        else:
+            _fail("MatMul", f"shapes {list(a)} and {list(b)} are not broadcastable")
+    return tuple(out)
+
+
+def _matrix(a: np.ndarray, batch: tuple) -> N.Matrix:
+    """fa_matrix of a's last two dimensions, with broadcastStrides over batch
+    (tensor/shape.go:122-131: stride 0 where a batch dimension is broadcast)."""
+    v = N.Matrix()
+    v.data = a.ctypes.data
+    v.rs, v.cs = a.strides[-2] // 4, a.strides[-1] // 4
+    lead = a.shape[:-2]
+    off = len(batch) - len(lead)
+    for d in range(len(batch)):
+        if d >= off and lead[d - off] != 1:
+            v.bstride[d] = a.strides[d - off] // 4
+    return v
+
+
+def _matmul_views(x: np.ndarray, w: np.ndarray, batch: tuple, ctx: N.Context) -> np.ndarray:
+    m, k, n = x.shape[-2], x.shape[-1], w.shape[-1]
+    out = np.empty(batch + (m, n), np.float32)
+    if out.size == 0:
+        return out
+    if len(batch) > N.FA_MAX_BATCH_DIMS:
+        _fail("MatMul", f"{len(batch)} batch dimensions, at most {N.FA_MAX_BATCH_DIMS}")
+    a, b = _matrix(x, batch), _matrix(w, batch)
+    bshape = (N.i64 * max(len(batch), 1))(*batch)
+    _call("MatMul", ctx, N.lib().fa_matmul_strided(ctx.h, len(batch), bshape, m, n, k, N.C.byref(a), N.C.byref(b),
+                                                   None, N.ptr(out)))
+    return out
+
+
 def MatMul(x, w, *, w_layout: int = N.FA_B_KN, ctx: N.Context | None = None):
-    """2-D matrix product (the 2-D case of tensor.MatMul, tensor/matmul.go:19-72)."""
-    return MatMulFused(x, w, None, w_layout=w_layout, ctx=ctx)
+    """tensor.MatMul (tensor/matmul.go:10-127): NumPy semantics. 2-D x 2-D is
+    the matrix product; a 1-D operand is promoted to a row (left) or a column
+    (right) and the added dimension removed; with more dimensions the batch
+    dimensions broadcast (stride 0). Strided numpy views (transposes, slices,
+    broadcast_to) are read through their strides on the device, not copied.
+
+    A bfloat16 w (uint16 bits) or w_layout=FA_B_NK ([n x k] storage) takes the
+    2-D weight path of MatMulFused.
+    """
+    ctx = ctx or default_context()
+    x, w = np.asarray(x), np.asarray(w)
+    if w.dtype == np.uint16 or w_layout != N.FA_B_KN:
+        return MatMulFused(x, w, None, w_layout=w_layout, ctx=ctx)
+    if x.ndim == 0 or w.ndim == 0:
+        _fail("MatMul", f"operands must be at least 1-D, got {list(x.shape)} and {list(w.shape)}")
+    if x.ndim == 1 and w.ndim == 1:
+        if x.shape[0] != w.shape[0]:
+            _fail("MatMul", f"shape mismatch {list(x.shape)} · {list(w.shape)}")
+        return MatMul(x[None, :], w[:, None], ctx=ctx).reshape(())
+    if x.ndim == 1:
+        return MatMul(x[None, :], w, ctx=ctx)[..., 0, :]
+    if w.ndim == 1:
+        return MatMul(x, w[:, None], ctx=ctx)[..., 0]
+    x, w = _view(x), _view(w)
+    m, k, n = x.shape[-2], x.shape[-1], w.shape[-1]
+    if k != w.shape[-2]:
+        _fail("MatMul", f"shape mismatch {list(x.shape)} · {list(w.shape)}")
+    if x.ndim == 2 and w.ndim == 2:
+        return _matmul_views(x, w, (), ctx)
+    if w.ndim == 2 and x.flags.c_contiguous:  # [B..., m, k] . [k, n]: the batch folds into M
+        rows = int(np.prod(x.shape[:-2], dtype=np.int64)) * m
+        return _matmul_views(x.reshape(rows, k), w, (), ctx).reshape(x.shape[:-2] + (m, n))
+    return _matmul_views(x, w, _broadcast_shapes(x.shape[:-2], w.shape[:-2]), ctx)
 
 
 def RowSumSquares(x, *, ctx: N.Context | None = None):

@@ -22,9 +22,11 @@
  * contexts may be used from distinct threads.
  *
  * HIP graphs: fa_similarities_topk_dev_noalloc is the entry point meant for
- * capture. The others are not capture-safe: they may grow device buffers on
+ * capture. The others are not capture-safe (they may grow device buffers on
  * a call, and fa_gemma_embed_ids_dev uploads its per-call plan from a pinned
- * host buffer that the next call rewrites and records events of the model.
+ * host buffer that the next call rewrites and records events of the model):
+ * they check hipStreamIsCapturing on the context's stream and return
+ * FA_ERR_STATE while it is being captured.
  *
  * Tuning switches (environment, read once per process; unset = the measured
  * defaults; for A/B measurements only, results stay within the parity bars):
@@ -81,6 +83,11 @@ typedef struct fa_model fa_model;
 
 /* Create a context on HIP device `device` (one stream, default priority). */
 int fa_create(int device, fa_ctx** out);
+/* Destroy a context, after the models still open on it (fa_gemma_destroy).
+ * NULL, or a handle already destroyed, is ignored. Contexts and models still
+ * open when the process exits are destroyed by an exit handler the library
+ * registers with atexit() at the first fa_create (after the HIP runtime has
+ * initialised, so before the runtime's own teardown). */
 void fa_destroy(fa_ctx* ctx);
 /* Last error message of ctx, or of the calling thread when ctx is NULL
  * (for fa_create failures). Never NULL. */
@@ -126,6 +133,42 @@ int fa_matmul_fused(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a
 int fa_matmul_fused_dev(fa_ctx* ctx, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const void* b,
                         int64_t ldb, int b_dtype, int b_layout, const fa_epilogue* e, float* c, int64_t ldc);
 
+/* A matrix operand of tensor.MatMul as the strided view the reference hands
+ * its GEMM driver (blas.Mat{Data, Rows, Cols, RS, CS}, tensor/matmul.go:38-40)
+ * plus the broadcast batch strides of matmulBatched (tensor/matmul.go:92-98):
+ * element [i, j] of batch entry (z_0, ..., z_{nb-1}) is
+ *   data[z_0*bstride[0] + ... + z_{nb-1}*bstride[nb-1] + i*rs + j*cs].
+ * Strides are in elements and >= 0; a broadcast batch dimension has stride
+ * 0, a transposed view has rs == 1 (tensor.T, Transpose(-2, -1)). */
+#define FA_MAX_BATCH_DIMS 8
+typedef struct fa_matrix {
+  const float* data;
+  int64_t rs, cs;
+  int64_t bstride[FA_MAX_BATCH_DIMS];
+} fa_matrix;
+
+/* tensor.MatMul / MatMulFused on strided operands, the general case of
+ * tensor/matmul.go:19-127: for every entry of the broadcast batch shape
+ * batch[0..nbatch-1] (nbatch = 0: one 2-D product),
+ *   out[z] = epilogue(A_z [m x k] . B_z [k x n]),
+ * out contiguous [batch..., m, n] (the reference's fresh output tensor). A
+ * and B are float32 views as described at fa_matrix; nothing is copied on
+ * the host, the operands are read through their strides on the device
+ * (transposed, offset, stride-0 broadcast views included). e (NULL for
+ * none) is MatMulFused's epilogue and needs nbatch == 0. k == 0 gives
+ * epilogue(0). Products are fp32-accurate (each fp32 value the exact sum of
+ * three bf16 terms, fp32 accumulation on the bf16 MFMA). The caller does
+ * 1-D promotion as the reference does (matmul.go:24-30): a 1-D left operand
+ * is the row [1 x k], a 1-D right operand the column [k x 1]. Host pointers;
+ * returns when out is filled. */
+int fa_matmul_strided(fa_ctx* ctx, int32_t nbatch, const int64_t* batch, int64_t m, int64_t n, int64_t k,
+                      const fa_matrix* a, const fa_matrix* b, const fa_epilogue* e, float* out);
+/* Device-pointer variant (a->data, b->data, out and the epilogue's arrays on
+ * the device; batch and the fa_matrix structs on the host); enqueues on
+ * fa_stream(ctx). */
+int fa_matmul_strided_dev(fa_ctx* ctx, int32_t nbatch, const int64_t* batch, int64_t m, int64_t n, int64_t k,
+                          const fa_matrix* a, const fa_matrix* b, const fa_epilogue* e, float* out);
+
 /* out[i] = sum_j x[i,j]^2 for row-major x [m x n].
  * Replaces (*Tensor).RowSumSquares (tensor/matmul_fused.go:125-143). */
 int fa_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out);
@@ -149,12 +192,20 @@ int fa_rope(fa_ctx* ctx, const float* x, double base, const int32_t* positions, 
  * reference's Expand). mask: additive, NULL or strides (m_sb, m_sh, m_sr,
  * m_sc) over [B, H, T, S] (0 where broadcast). out: [B, H, T, D]
  * contiguous. Masked weights are exactly 0 (exp of inputs below -87 flushes
- * to 0, internal/kernel/generic.go:278-307).
+ * to 0, internal/kernel/generic.go:278-307). Head dims 64, 128, 256 and
+ * 512 with 16-byte aligned rows (batch and head strides multiples of 4) run
+ * on the fp32 MFMA; other shapes on a per-row kernel (D <= 512).
  * Replaces tensor.AttentionScaled (tensor/attention.go:67-83,130-287). */
 int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, int32_t B, int32_t H, int32_t T,
                  int32_t S, int32_t D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t v_sb,
                  int64_t v_sh, const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_sr, int64_t m_sc, float scale,
                  float* out);
+/* Device-pointer variant of fa_attention (q, k, v, mask, out on the device;
+ * enqueues on fa_stream(ctx)). */
+int fa_attention_dev(fa_ctx* ctx, const float* q, const float* k, const float* v, int32_t B, int32_t H, int32_t T,
+                     int32_t S, int32_t D, int64_t q_sb, int64_t q_sh, int64_t k_sb, int64_t k_sh, int64_t v_sb,
+                     int64_t v_sh, const float* mask, int64_t m_sb, int64_t m_sh, int64_t m_sr, int64_t m_sc,
+                     float scale, float* out);
 
 /* Scores queries [nq x d] against docs [nd x d] (dot products, the rows
  * being unit length as cluster.Similarities requires, cluster.go:180-190) and
@@ -166,8 +217,12 @@ int fa_attention(fa_ctx* ctx, const float* q, const float* k, const float* v, in
  * selects one); slots past a row's non-NaN scores get index -1 and value NaN.
  * From 128 queries with d % 32 == 0, topk <= 16 and 16-byte aligned rows the
  * scores are the exact dot products rounded to float32 and no score matrix is
- * formed (blocks of 256 queries); otherwise an fp32-MFMA product is followed
- * by a two-pass top-k. */
+ * formed (blocks of 256 queries); otherwise an fp32-MFMA product (fp32
+ * accumulation, within a few units of the last place of the exact score) is
+ * followed by a two-pass top-k. A query's scores, and its order among
+ * candidates whose scores agree to that precision, can therefore differ
+ * between a call with fewer than 128 queries (or topk > 16) and one with
+ * more; fa_similarities_topk_dev_noalloc takes the exact path for any nq. */
 int fa_similarities_topk(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd, int32_t d,
                          int32_t topk, int32_t* idx, float* val);
 
@@ -181,8 +236,11 @@ int fa_similarities_topk_dev(fa_ctx* ctx, const float* queries, int64_t nq, cons
  * nq), with its scratch in a fixed 12 MiB array per device instead of the
  * context's buffers: d % 32 == 0 and d <= 2048, 1 <= topk <= 16, 16-byte
  * aligned rows, else FA_ERR_ARG. Device pointers; enqueues on
- * fa_stream(ctx). Calls on one GPU share the array: calls that overlap on one
- * GPU (other contexts, other streams) race. */
+ * fa_stream(ctx). The array of a GPU belongs to the first context that calls
+ * this entry point on it, until fa_destroy of that context: calls from other
+ * contexts on that GPU return FA_ERR_STATE instead of racing on it. The
+ * owner's calls are ordered by its stream; graphs captured from them share
+ * the array too, so their replays must not overlap each other. */
 int fa_similarities_topk_dev_noalloc(fa_ctx* ctx, const float* queries, int64_t nq, const float* docs, int64_t nd,
                                      int32_t d, int32_t topk, int32_t* idx, float* val);
 
@@ -273,6 +331,8 @@ typedef struct fa_gemma_config {
 /* Create an empty model on ctx (no weights yet). Replaces the allocation
  * part of gemma.Load (models/gemma/model.go:76-232). */
 int fa_gemma_create(fa_ctx* ctx, const fa_gemma_config* cfg, fa_model** out);
+/* Release a model (gemma's Close, model.go:381). NULL, or a model already
+ * released (with its context, or at exit), is ignored. */
 void fa_gemma_destroy(fa_model* m);
 
 /* Upload one checkpoint tensor by its Hugging Face name, as gemma.Load

@@ -128,6 +128,132 @@ TEST(TestMatMulAgainstFloat64) {
   }
 }
 
+// naiveMatMul (tensor/tensor_test.go:355-368): float64 sums over At(), so
+// any 2-D view works.
+static Tensor naive_matmul(const Tensor& a, const Tensor& b) {
+  const int64_t m = a.Dim(0), k = a.Dim(1), n = b.Dim(1);
+  std::vector<float> out(m * n);
+  for (int64_t i = 0; i < m; i++)
+    for (int64_t j = 0; j < n; j++) {
+      double s = 0;
+      for (int64_t p = 0; p < k; p++) s += (double)a.At({i, p}) * (double)b.At({p, j});
+      out[i * n + j] = (float)s;
+    }
+  return Tensor::New(std::move(out), {m, n});
+}
+
+// assertClose (tensor/tensor_test.go:10-26): |got - want| <= tol (1 + |want|)
+static void assert_close(const char* name, const Tensor& got, const Tensor& want, double tol) {
+  if (got.shape() != want.shape()) FATAL("%s: shape of rank %d, want rank %d", name, got.Dims(), want.Dims());
+  auto g = got.Float32s(), w = want.Float32s();
+  for (size_t i = 0; i < g.size(); i++)
+    if (!(std::fabs((double)g[i] - w[i]) <= tol * (1 + std::fabs((double)w[i]))))
+      FATAL("%s: element %zu = %.9g, want %.9g", name, i, g[i], w[i]);
+}
+
+template <class F>
+static void expect_tensor_error(const char* name, F fn) {
+  try {
+    fn();
+  } catch (const Error&) {
+    return;
+  }
+  FATAL("%s: expected a tensor error", name);
+}
+
+// tensor/tensor_test.go:370-433 (TestMatMul), restated: plain and transposed
+// operands at the reference's shapes, the vector forms, batched products
+// with broadcasting, the fold of a batch into M, strided batch operands and
+// many small products; then offset, stride-0 and empty views.
+TEST(TestMatMul) {
+  std::mt19937_64 rng(56);
+  const int64_t shapes[][3] = {{1, 1, 1}, {2, 3, 4}, {7, 5, 9}, {64, 64, 64}, {33, 17, 65}, {1, 40, 50}, {50, 40, 1}, {130, 70, 90}};
+  for (auto& s : shapes) {
+    const int64_t m = s[0], k = s[1], n = s[2];
+    Tensor a = randn(rng, {m, k}), b = randn(rng, {k, n});
+    assert_close("MatMul", MatMul(a, b), naive_matmul(a, b), 1e-4);
+    Tensor at = randn(rng, {k, m}).T(), bt = randn(rng, {n, k}).T();  // transposed views, not copied
+    assert_close("MatMul AtB", MatMul(at, b), naive_matmul(at, b), 1e-4);
+    assert_close("MatMul ABt", MatMul(a, bt), naive_matmul(a, bt), 1e-4);
+    assert_close("MatMul AtBt", MatMul(at, bt), naive_matmul(at, bt), 1e-4);
+  }
+  // vector forms
+  Tensor v = Tensor::New({1, 2, 3}, {3});
+  Tensor mm = Tensor::New({1, 2, 3, 4, 5, 6}, {2, 3});
+  Tensor d = Dot(v, v);
+  if (d.Dims() != 0 || d.Item() != 14) FATAL("Dot: rank %d value %g", d.Dims(), d.Item());
+  assert_close("M.v", MatMul(mm, v), Tensor::New({14, 32}, {2}), 0);
+  assert_close("v.Mt", MatMul(v, mm.T()), Tensor::New({14, 32}, {2}), 0);
+  assert_close("Outer", Outer(Tensor::New({1, 2}, {2}), v), Tensor::New({1, 2, 3, 2, 4, 6}, {2, 3}), 0);
+  // batched with broadcasting
+  Tensor a = randn(rng, {3, 2, 4, 5}), b = randn(rng, {2, 5, 6});
+  Tensor got = MatMul(a, b);
+  if (got.shape() != Shape{3, 2, 4, 6}) FATAL("batched shape of rank %d", got.Dims());
+  for (int64_t i = 0; i < 3; i++)
+    for (int64_t j = 0; j < 2; j++)
+      assert_close("batched", got.Select(0, i).Select(0, j), naive_matmul(a.Select(0, i).Select(0, j), b.Select(0, j)),
+                   1e-4);
+  // batched x 2-D folds the batch into M
+  Tensor c = randn(rng, {5, 7});
+  got = MatMul(a, c);
+  for (int64_t i = 0; i < 3; i++)
+    for (int64_t j = 0; j < 2; j++)
+      assert_close("batched 2D", got.Select(0, i).Select(0, j), naive_matmul(a.Select(0, i).Select(0, j), c), 1e-4);
+  // batched with strided (transposed) batch operands
+  Tensor bt = randn(rng, {2, 6, 5}).Transpose(1, 2);
+  got = MatMul(a, bt);
+  for (int64_t i = 0; i < 3; i++)
+    for (int64_t j = 0; j < 2; j++)
+      assert_close("batched transposed", got.Select(0, i).Select(0, j),
+                   naive_matmul(a.Select(0, i).Select(0, j), bt.Select(0, j)), 1e-4);
+  // many small products over the batch
+  Tensor x = randn(rng, {64, 8, 8}), y = randn(rng, {64, 8, 8});
+  got = MatMul(x, y);
+  for (int64_t i = 0; i < 64; i += 7)
+    assert_close("small batch", got.Select(0, i), naive_matmul(x.Select(0, i), y.Select(0, i)), 1e-4);
+  // a strided (non-contiguous) batched left operand against a 2-D right
+  // operand: no fold into M, the batch broadcasts the 2-D operand
+  Tensor xt = randn(rng, {3, 9, 4}).Transpose(1, 2);  // [3, 4, 9], rows strided
+  Tensor w2 = randn(rng, {9, 33});
+  got = MatMul(xt, w2);
+  for (int64_t i = 0; i < 3; i++) assert_close("strided batch x 2-D", got.Select(0, i), naive_matmul(xt.Select(0, i), w2), 1e-4);
+  // offset views (Narrow, Select) and stride-0 broadcasts (Expand)
+  Tensor big = randn(rng, {70, 90});
+  Tensor an = big.Narrow(0, 3, 40).Narrow(1, 5, 64);   // offset rows and columns, row stride 90
+  Tensor bn = randn(rng, {100, 50}).Narrow(0, 17, 64);  // offset rows
+  assert_close("narrowed", MatMul(an, bn), naive_matmul(an, bn), 1e-4);
+  Tensor brow = randn(rng, {1, 50}).Expand({64, 50});    // every row the same (row stride 0)
+  assert_close("expanded", MatMul(an, brow), naive_matmul(an, brow), 1e-4);
+  Tensor e3 = randn(rng, {4, 8}).Expand({5, 4, 8});      // batch stride 0 on the left
+  Tensor r3 = randn(rng, {5, 8, 3});
+  got = MatMul(e3, r3);
+  for (int64_t i = 0; i < 5; i++) assert_close("expanded batch", got.Select(0, i), naive_matmul(e3.Select(0, i), r3.Select(0, i)), 1e-4);
+  // empty operands: k = 0 gives zeros, m = 0 an empty result
+  assert_close("k = 0", MatMul(Tensor::Zeros({3, 0}), Tensor::Zeros({0, 4})), Tensor::Zeros({3, 4}), 0);
+  assert_close("m = 0", MatMul(Tensor::Zeros({0, 5}), randn(rng, {5, 4})), Tensor::Zeros({0, 4}), 0);
+  expect_tensor_error("shape", [] { MatMul(Tensor::Zeros({2, 3}), Tensor::Zeros({2, 3})); });
+  expect_tensor_error("scalar", [] { MatMul(Tensor::Zeros({}), Tensor::Zeros({2})); });
+  expect_tensor_error("batch broadcast", [] { MatMul(Tensor::Zeros({2, 3, 4}), Tensor::Zeros({3, 4, 5})); });
+}
+
+// MatMulFused reads strided operands as the reference's GemmZeroEpilogue
+// does (blas.Mat views, tensor/matmul_fused.go:86-89): a transposed x and w
+// give the product of their values.
+TEST(TestMatMulFusedStridedOperands) {
+  std::mt19937_64 rng(57);
+  Tensor x = randn(rng, {48, 33}).T(), w = randn(rng, {70, 48}).T();  // x [33 x 48], w [48 x 70]
+  Tensor bias = randn(rng, {70});
+  Fused f;
+  f.Bias = &bias;
+  f.Act = ReLUAct;
+  Tensor got = MatMulFused(x, w, f);
+  Tensor base = naive_matmul(x, w);
+  auto bv = bias.Float32s(), pv = base.Float32s();
+  std::vector<float> want(pv.size());
+  for (size_t i = 0; i < pv.size(); i++) want[i] = std::max(0.f, pv[i] + bv[i % 70]);
+  assert_close("fused strided", got, Tensor::New(want, {33, 70}), 1e-4);
+}
+
 // tensor/matmul_fused_test.go:8-44: MatMulFused equals the composed
 // operations for every epilogue combination.
 TEST(TestMatMulFusedMatchesComposed) {

@@ -138,3 +138,32 @@ def test_weight_specs_complete():
     names = [s[0] for s in specs]
     assert len(names) == len(set(names)) == 2 + 2 + 13 * 24
     assert sum(int(np.prod(s[1])) for s in specs) == 307_581_696
+
+
+# ---- tensor.MatMul's views in the Python mirror (host logic only) -------------
+
+def test_matmul_view_strides_and_broadcast():
+    """The fa_matrix the mirror builds for numpy views: element strides of
+    the matrix dimensions and broadcastStrides over the batch
+    (tensor/shape.go:94-131); no device call."""
+    from ai_amd import tensor as T
+    a = np.zeros((3, 1, 4, 5), np.float32)
+    b = np.zeros((2, 6, 5), np.float32).swapaxes(1, 2)  # [2, 5, 6], rows of stride 1
+    batch = T._broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    assert batch == (3, 2)
+    ma, mb = T._matrix(a, batch), T._matrix(b, batch)
+    assert (ma.rs, ma.cs, list(ma.bstride[:2])) == (5, 1, [20, 0])  # a's size-1 dim broadcasts: stride 0
+    assert (mb.rs, mb.cs, list(mb.bstride[:2])) == (1, 5, [0, 30])  # b has no first batch dim
+    c = np.broadcast_to(np.zeros((1, 8), np.float32), (7, 8))
+    mc = T._matrix(c, ())
+    assert (mc.rs, mc.cs) == (0, 1)
+    with pytest.raises(T.TensorError, match="not broadcastable"):
+        T._broadcast_shapes((2, 3), (3, 3))
+    # negative or odd byte strides are copied, float64 converted
+    assert T._view(np.zeros((4, 4), np.float32)[::-1]).strides == (16, 4)
+    assert T._view(np.zeros((4, 4))).dtype == np.float32
+
+
+def test_matmul_strided_rejects_without_context():
+    assert N.lib().fa_matmul_strided(None, 0, None, 1, 1, 1, None, None, None, None) == N.FA_ERR_ARG
+    assert N.lib().fa_matmul_strided_dev(None, 0, None, 1, 1, 1, None, None, None, None) == N.FA_ERR_ARG

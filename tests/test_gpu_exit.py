@@ -35,3 +35,18 @@ def test_exit_with_handles_open():
     assert "embedded (2, 768)" in r.stdout
     assert "terminate called" not in r.stdout
     assert r.returncode == 0, r.returncode
+
+
+def test_c_program_exits_with_model_and_context_open():
+    """The library's own exit handler (registered at fa_create) closes the
+    model and context a C caller left open, before the HIP runtime's teardown
+    (tests/cpp/exit_open.c)."""
+    from ai_amd import build as B
+    binary = os.path.join(B.CPP_TEST_BIN, "exit_open")
+    assert os.path.exists(binary), "run __graft_entry__.build() first"
+    print(f"running {binary}", flush=True)
+    r = subprocess.run([binary], cwd=ROOT, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=100)
+    print(r.stdout, flush=True)
+    assert "embedded 2 x 768" in r.stdout
+    assert "terminate called" not in r.stdout
+    assert r.returncode == 0, r.returncode

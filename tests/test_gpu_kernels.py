@@ -324,3 +324,75 @@ def test_similarities_topk_dev_fresh_context():
             if p.value:
                 L.fa_device_free(c.h, p)
         c.close()
+
+
+# ---- the MFMA path of fa_attention (head dims 64, 128, 256, 512) -----------------
+
+@pytest.mark.parametrize("D", [64, 128, 256, 512])
+@pytest.mark.parametrize("B,H,Hkv,Tq,Sk", [(2, 4, 4, 70, 70), (1, 3, 1, 130, 33), (2, 2, 1, 17, 200)])
+def test_attention_mfma_vs_oracle(ctx, D, B, H, Hkv, Tq, Sk):
+    """fa_attention's MFMA kernel against the oracle (the reference's
+    AttentionBlock algebra) at the reference's 1e-4 bar
+    (tensor/attention_test.go:64-91): GQA as stride-0 head views (Expand),
+    padding masks [B,1,1,S], window and causal masks [T,S] broadcast over
+    batch and head, T != S, lengths that are not whole tiles."""
+    r = rng(D * 7 + B * H + Tq + Sk)
+    q = r.standard_normal((B, H, Tq, D)).astype(np.float32)
+    k1 = r.standard_normal((B, Hkv, Sk, D)).astype(np.float32)
+    v1 = r.standard_normal((B, Hkv, Sk, D)).astype(np.float32)
+    assert Hkv in (1, H)
+    k = np.broadcast_to(k1, (B, H, Sk, D))  # head stride 0 when Hkv == 1 (the reference's Expand)
+    v = np.broadcast_to(v1, (B, H, Sk, D))
+    lengths = [Sk] + [max(1, Sk // 3)] * (B - 1)
+    masks = [None, T.PaddingMask(lengths, Sk)]
+    if Tq == Sk:
+        masks.append(T.WindowMask(Tq, 9).reshape(1, 1, Tq, Tq))
+        masks.append(T.CausalMask(Tq))
+    for mask in masks:
+        for scale in (1.0 / np.sqrt(D), -0.03):
+            got = T.AttentionScaled(q, k, v, mask, scale, ctx=ctx)
+            want = O.attention(q, k, v, mask, scale)
+            close(got, want, what=f"MFMA attention D={D} B={B} H={H}/{Hkv} T={Tq} S={Sk} "
+                                  f"mask={None if mask is None else mask.shape} scale={scale:.3g}")
+
+
+def test_attention_mfma_masked_weights_are_exact_zeros(ctx):
+    """tensor/attention_test.go:266-285 on the MFMA path (D = 64): causal
+    position 0 reproduces v[0], and keys behind the mask carry weight exactly
+    0 (values of 1e30 there change nothing)."""
+    r = rng(12)
+    n, d = 64, 64
+    q, k, v = (r.standard_normal((1, 1, n, d)).astype(np.float32) for _ in range(3))
+    out = T.Attention(q, k, v, T.CausalMask(n), ctx=ctx)
+    assert np.abs(out[0, 0, 0] - v[0, 0, 0]).max() <= 1e-6
+    lengths = [40]
+    pad = T.PaddingMask(lengths, n)
+    base = T.Attention(q, k, v, pad, ctx=ctx)
+    vv = v.copy()
+    vv[:, :, 40:] = 1e30
+    got = T.Attention(q, k, vv, pad, ctx=ctx)
+    assert np.isfinite(got).all()
+    assert np.array_equal(got, base)
+
+
+def test_attention_mfma_dev_entry_point(ctx):
+    """fa_attention_dev on device buffers equals fa_attention (host)."""
+    r = rng(13)
+    B, H, Tq, D = 2, 3, 96, 128
+    q, k, v = (r.standard_normal((B, H, Tq, D)).astype(np.float32) for _ in range(3))
+    want = T.AttentionScaled(q, k, v, None, 0.1, ctx=ctx)
+    L = N.lib()
+    ptrs = []
+    for a in (q, k, v, np.empty_like(q)):
+        p = C.c_void_p()
+        N.check(ctx.h, L.fa_device_alloc(ctx.h, a.nbytes, C.byref(p)))
+        N.check(ctx.h, L.fa_memcpy_h2d(ctx.h, p, a.ctypes.data, a.nbytes))
+        ptrs.append(p)
+    st = Tq * D
+    N.check(ctx.h, L.fa_attention_dev(ctx.h, ptrs[0], ptrs[1], ptrs[2], B, H, Tq, Tq, D, H * st, st, H * st, st, H * st,
+                                      st, None, 0, 0, 0, 0, 0.1, ptrs[3]))
+    got = np.empty_like(q)
+    N.check(ctx.h, L.fa_memcpy_d2h(ctx.h, got.ctypes.data, ptrs[3], got.nbytes))
+    for p in ptrs:
+        L.fa_device_free(ctx.h, p)
+    assert np.array_equal(got, want)

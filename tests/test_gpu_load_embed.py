@@ -135,6 +135,32 @@ def test_load_and_embed_texts(model_dir, tmp_path, prompt, dim):
     assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
 
 
+def test_dense_bias_flag_is_read_and_the_bias_not_applied(model_dir, tmp_path):
+    """The reference's Load reads a Dense module's "bias" flag but loads only
+    linear.weight (models/gemma/model.go:277-304): a directory whose Dense
+    layers declare a bias, and hold a nonzero linear.bias, loads and gives
+    the same embeddings as the same directory without one."""
+    import shutil
+    from safetensors.torch import load_file
+    d, _ = model_dir
+    d2 = tmp_path / "with_bias"
+    shutil.copytree(d, d2)
+    for p in sorted(d2.glob("*_Dense")):
+        cfg = json.loads((p / "config.json").read_text())
+        cfg["bias"] = True
+        (p / "config.json").write_text(json.dumps(cfg))
+        t = load_file(str(p / "model.safetensors"))
+        t["linear.bias"] = torch.full((cfg["out_features"],), 0.5)
+        save_file(t, str(p / "model.safetensors"))
+    r1, of1 = run(d, tmp_path, TEXTS)
+    assert r1.returncode == 0, r1.stdout
+    a = np.fromfile(of1, np.float32).copy()
+    r2, of2 = run(d2, tmp_path, TEXTS)
+    assert r2.returncode == 0, r2.stdout
+    b = np.fromfile(of2, np.float32)
+    assert np.array_equal(a, b)
+
+
 def test_load_errors(model_dir, tmp_path):
     d, _ = model_dir
     r, _ = run(d, tmp_path, ["x"], "nope")

@@ -182,3 +182,20 @@ def test_matmul_tanh_activation(ctx):
     got = T.MatMulFused(a, w, e, ctx=ctx)
     want = O.tanh(O.gemm(a, w))
     assert np.abs(got - want).max() <= 1e-5
+
+
+def test_three_plane_matrix_needs_whole_k_slabs(ctx):
+    """A float32 matrix bfloat16 cannot hold runs on the six-term kernel,
+    which takes 32-wide K slabs: an input width that is not a multiple of 32
+    is refused when the weight is set (FA_ERR_UNSUPPORTED), not at the first
+    embed; the same matrix with bf16-exact values is accepted (the fp32-MFMA
+    kernel takes any width)."""
+    shape = S.ModelShape(num_hidden_layers=1, vocab_size=256, dense_out=[100, 768])
+    m = G.Model(shape, ctx)
+    try:
+        w = np.random.default_rng(5).standard_normal((768, 100)).astype(np.float32) * 0.02
+        with pytest.raises(G.GemmaError, match=r"\[5\].*multiple of 32"):
+            m.set_weight("dense.1.linear.weight", w)
+        m.set_weight("dense.1.linear.weight", S.bf16_to_f32(S.f32_to_bf16(w)))
+    finally:
+        m.close()

@@ -81,3 +81,59 @@ def test_noalloc_refuses_what_the_scratch_cannot_hold(nctx):
     assert L.fa_similarities_topk_dev_noalloc(nctx.h, dq, 4, dq, 4, 48, 1, out, out) == N.FA_ERR_ARG
     L.fa_device_free(nctx.h, dq)
     L.fa_device_free(nctx.h, out)
+
+
+def test_noalloc_allocates_no_device_memory(nctx):
+    """The point of the entry point: calls of several sizes (after one warm-up
+    call that loads the kernels) leave the device's free memory unchanged."""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L = N.lib()
+    r = np.random.default_rng(78)
+    q = unit(r.standard_normal((260, 512)))
+    docs = unit(r.standard_normal((9000, 512)))
+    dq, dd = dev(nctx, q), dev(nctx, docs)
+    di, dv = C.c_void_p(), C.c_void_p()
+    N.check(nctx.h, L.fa_device_alloc(nctx.h, 260 * 16 * 4, C.byref(di)))
+    N.check(nctx.h, L.fa_device_alloc(nctx.h, 260 * 16 * 4, C.byref(dv)))
+    N.check(nctx.h, L.fa_similarities_topk_dev_noalloc(nctx.h, dq, 260, dd, 9000, 512, 16, di, dv))
+    nctx.sync()
+    free0, free1, total = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    assert hip.hipMemGetInfo(C.byref(free0), C.byref(total)) == 0
+    for nq, nd, k in ((260, 9000, 16), (7, 300, 3), (129, 9000, 10), (1, 17, 1)):
+        N.check(nctx.h, L.fa_similarities_topk_dev_noalloc(nctx.h, dq, nq, dd, nd, 512, k, di, dv))
+    nctx.sync()
+    assert hip.hipMemGetInfo(C.byref(free1), C.byref(total)) == 0
+    print(f"free device memory before {free0.value} after {free1.value}", flush=True)
+    assert free1.value == free0.value
+    for p in (dq, dd, di, dv):
+        L.fa_device_free(nctx.h, p)
+
+
+def test_noalloc_array_belongs_to_one_context(nctx):
+    """A second context on the same GPU is refused (FA_ERR_STATE) while the
+    first owns the array, instead of racing on it; once the owner is
+    destroyed the other context may claim it."""
+    L = N.lib()
+    r = np.random.default_rng(79)
+    q = unit(r.standard_normal((8, 256)))
+    other = N.Context(0)
+    dq = dev(other, q)
+    out = C.c_void_p()
+    N.check(other.h, L.fa_device_alloc(other.h, 8 * 4 * 2, C.byref(out)))
+    N.check(nctx.h, L.fa_similarities_topk_dev_noalloc(nctx.h, dq, 8, dq, 8, 256, 1, out, out))  # nctx owns it
+    nctx.sync()
+    assert L.fa_similarities_topk_dev_noalloc(other.h, dq, 8, dq, 8, 256, 1, out, out) == N.FA_ERR_STATE
+    assert b"another context" in L.fa_last_error(other.h)
+    third = N.Context(0)
+    third.close()  # destroying a context that never claimed the array leaves nctx's claim
+    assert L.fa_similarities_topk_dev_noalloc(other.h, dq, 8, dq, 8, 256, 1, out, out) == N.FA_ERR_STATE
+    nctx.close()  # the owner goes: the array is free again
+    N.check(other.h, L.fa_similarities_topk_dev_noalloc(other.h, dq, 8, dq, 8, 256, 1, out, out))
+    other.sync()
+    idx = np.empty(8, np.int32)
+    N.check(other.h, L.fa_memcpy_d2h(other.h, idx.ctypes.data, out, 32))
+    assert idx.tolist() == list(range(8))  # each unit row is its own best match
+    L.fa_device_free(other.h, dq)
+    L.fa_device_free(other.h, out)
+    other.close()
