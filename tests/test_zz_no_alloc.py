@@ -129,7 +129,7 @@ def test_noalloc_array_belongs_to_one_context(nctx):
     third.close()  # destroying a context that never claimed the array leaves nctx's claim
     assert L.fa_similarities_topk_dev_noalloc(other.h, dq, 8, dq, 8, 256, 1, out, out) == N.FA_ERR_STATE
     nctx.close()  # the owner goes: the array is free again
-    N.check(other.h, L.fa_similarities_topk_dev_noalloc(other.h, dq, 8, dq, 8, 256, 1, out, out))
+    N.check(other.h, L.fa_similarities_topk_dev_noalloc(other.h, dq, 8, dq, 8, 256, 1, out, None))  # indices only
     other.sync()
     idx = np.empty(8, np.int32)
     N.check(other.h, L.fa_memcpy_d2h(other.h, idx.ctypes.data, out, 32))
