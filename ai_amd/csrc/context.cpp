@@ -264,7 +264,7 @@ namespace {
 // take keep the fp32-MFMA kernel with its checked loader.
 int prepare_b(fa_ctx* ctx, GemmArgs& g) {
   const bool a_ok = (reinterpret_cast<uintptr_t>(g.a) & 15) == 0 && g.lda % 4 == 0;
-  if (!(g.k > 0 && g.k % 32 == 0 && a_ok)) return FA_OK;
+  if (!(g.k > 0 && g.k % 32 == 0 && a_ok) || gemm_f32_mfma_forced()) return FA_OK;
   if (g.b_dtype == FA_DT_BF16 && g.b_layout == FA_B_NK) return FA_OK;  // already the fast form (when aligned)
   const int terms = g.b_dtype == FA_DT_F32 ? 3 : 1;
   DevBuf& pb = ctx->slot(slots::S_BPLANES);

@@ -171,6 +171,11 @@ int launch_split_b(fa_ctx* ctx, const void* b, int b_dtype, int64_t ldb, int lay
 // [m x F] = gelu(gate) * up.
 int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t stream);
 
+// FA_GEMM_MFMA=f32 (comparisons): every product on the fp32-MFMA kernel, bf16
+// weights widened and float32 weights taken as they are (no three-plane
+// rewrite).
+bool gemm_f32_mfma_forced();
+
 // K-split factor the encoder uses for its N = hidden products (o, down):
 // FA_GEMM_KSPLIT=1 or 2 (default 2).
 int gemm_ksplit();

@@ -1138,6 +1138,8 @@ int launch_split_b_view(fa_ctx* ctx, const float* src, const BatchMap& bm, int z
   return FA_OK;
 }
 
+bool gemm_f32_mfma_forced() { return use_f32_mfma(); }
+
 int gemm_ksplit() {
   static const int v = [] {
     const char* e = std::getenv("FA_GEMM_KSPLIT");

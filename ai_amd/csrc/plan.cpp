@@ -88,6 +88,26 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
   }
 }
 
+namespace {
+
+// Estimated time of a launch whose workgroup i (cost cost(i)) runs on XCD
+// i % 8, each XCD's slots taking its workgroups in order as slots free up.
+template <class Cost>
+double launch_span(int64_t n, int slots, Cost cost) {
+  const int per = std::max(1, slots / kXcds);
+  std::vector<std::vector<double>> free_at(kXcds, std::vector<double>(per, 0.0));
+  double span = 0;
+  for (int64_t i = 0; i < n; i++) {
+    auto& f = free_at[i % kXcds];
+    auto it = std::min_element(f.begin(), f.end());
+    *it += cost(i);
+    span = std::max(span, *it);
+  }
+  return span;
+}
+
+}  // namespace
+
 void plan_items(const AttnPlanIn& in, AttnPlan& p, int32_t* items, std::vector<int>& order) {
   // Work items of each group, longest sequences first: an item's work grows
   // with its sequence's length, and dispatching the long ones first
@@ -104,14 +124,97 @@ void plan_items(const AttnPlanIn& in, AttnPlan& p, int32_t* items, std::vector<i
       for (int b = b0; b < b1; b++) order[b - b0] = b;
       std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return in.lengths[x] > in.lengths[y]; });
       const int64_t first = it;
-      for (int b : order) {
-        const int rows_b = tiles ? p.Gt * in.lengths[b] : in.lengths[b];
-        for (int q0 = 0; q0 < rows_b; q0 += istep) {
-          for (int h = 0; h < iheads; h++) {
-            items[3 * it] = b;
-            items[3 * it + 1] = q0;
-            items[3 * it + 2] = h;
-            it++;
+      if (tiles ? p.kparts_t == 1 : p.kparts_v == 1) {
+        // XCD-local items: workgroup i of a launch runs on XCD i % 8, and
+        // every item of a sequence reads the same keys and values (the tile
+        // path's images, the fp32 path's rows of q|k|v). Queue x of the
+        // group's n items takes positions x, x + 8, ... : n / 8 of them,
+        // plus one for x < n % 8. A sequence's items (sequences longest
+        // first) fill the queue with the most room and move to the next
+        // only when it is full, so its keys and values are fetched into as
+        // few XCD L2s as the balance allows; each queue ends exactly full.
+        int64_t n = 0;
+        for (int b : order) n += ((int64_t)(tiles ? p.Gt : 1) * in.lengths[b] + istep - 1) / istep * iheads;
+        std::vector<std::vector<int64_t>> q(kXcds);  // packed (sequence, first row, head)
+        std::vector<int64_t> room(kXcds);
+        for (int x = 0; x < kXcds; x++) room[x] = n / kXcds + (x < n % kXcds ? 1 : 0);
+        for (int b : order) {
+          const int rows_b = tiles ? p.Gt * in.lengths[b] : in.lengths[b];
+          int x = -1;
+          for (int q0 = 0; q0 < rows_b; q0 += istep)
+            for (int h = 0; h < iheads; h++) {
+              if (x < 0 || room[x] == 0) {
+                x = 0;
+                for (int y = 1; y < kXcds; y++)
+                  if (room[y] > room[x]) x = y;
+              }
+              q[x].push_back(((int64_t)b << 32) | ((int64_t)q0 << 8) | h);
+              room[x]--;
+            }
+        }
+        // Equal item counts per XCD are not equal work when sequence lengths
+        // differ and the launch takes more than one round: keep this order
+        // only where its estimated span (an item costs its key tiles plus
+        // two for its prologue; one workgroup per CU, as the tile attention
+        // and the head_dim-512 fp32 kernel run) is within 3 % of the plain
+        // longest-first order's (C4 on
+        // one stream: 281 items of 1 024-2 048 tokens, +14 % measured for
+        // the attention with XCD-local queues; C3, equal lengths: -4.7 %).
+        const int keys = tiles ? in.tile_keys : 16;
+        auto cost_of = [&](int b) { return 2.0 + (double)((in.lengths[b] + keys - 1) / keys); };
+        std::vector<int32_t> plain;
+        for (int b : order) {
+          const int rows_b = tiles ? p.Gt * in.lengths[b] : in.lengths[b];
+          for (int q0 = 0; q0 < rows_b; q0 += istep)
+            for (int h = 0; h < iheads; h++) plain.push_back(b);
+        }
+        const int slots = in.cus;
+        const double span_plain = launch_span(n, slots, [&](int64_t i) { return cost_of(plain[i]); });
+        const double span_xcd =
+            launch_span(n, slots, [&](int64_t i) { return cost_of((int)(q[i % kXcds][i / kXcds] >> 32)); });
+        // and only for long key loops (a group's mean length at least 12
+        // key tiles of 32): C3's 512-token sequences -1.7 % per forward
+        // (attention -4 %), while C2's micro-batches (mean 172 tokens) ran
+        // 0.7 % slower with the XCD-local order and C5 (mean 72) equal,
+        // though it cut the C2 launch's HBM fetch of the images 2.7 times
+        int64_t keys_sum = 0;
+        for (int b : order) keys_sum += in.lengths[b];
+        const bool long_keys = keys_sum >= 384LL * (int64_t)order.size();
+        const bool local = long_keys && span_xcd <= 1.03 * span_plain;
+        for (int64_t i = 0; i < n; i++) {
+          if (local) {
+            const int64_t e = q[i % kXcds][i / kXcds];
+            items[3 * it] = (int32_t)(e >> 32);
+            items[3 * it + 1] = (int32_t)((e >> 8) & 0xFFFFFF);
+            items[3 * it + 2] = (int32_t)(e & 0xFF);
+          } else {
+            items[3 * it] = plain[i];
+          }
+          it++;
+        }
+        if (!local) {  // the plain order's rows and heads
+          it -= n;
+          for (int b : order) {
+            const int rows_b = tiles ? p.Gt * in.lengths[b] : in.lengths[b];
+            for (int q0 = 0; q0 < rows_b; q0 += istep)
+              for (int h = 0; h < iheads; h++) {
+                items[3 * it + 1] = q0;
+                items[3 * it + 2] = h;
+                it++;
+              }
+          }
+        }
+        (tiles ? p.xcd_local_t : p.xcd_local_v)[gi] = local;
+      } else {
+        for (int b : order) {
+          const int rows_b = tiles ? p.Gt * in.lengths[b] : in.lengths[b];
+          for (int q0 = 0; q0 < rows_b; q0 += istep) {
+            for (int h = 0; h < iheads; h++) {
+              items[3 * it] = b;
+              items[3 * it + 1] = q0;
+              items[3 * it + 2] = h;
+              it++;
+            }
           }
         }
       }

@@ -10,6 +10,7 @@
 namespace fa {
 
 constexpr int kMaxMicrobatches = 4;  // streams a forward may use (micro-batches)
+constexpr int kXcds = 8;             // MI355X: a launch's workgroup i runs on XCD i % 8
 
 // Cuts B sequences (M tokens in all) into min(want, B) contiguous groups of
 // about equal token count, each holding at least one sequence: group g is
@@ -47,6 +48,8 @@ struct AttnPlan {
   int64_t n_items_t = 0, n_items_v = 0;
   int64_t n_tiles = 0;                // key tiles over the batch (tile layers)
   int64_t group_items_t[kMaxMicrobatches] = {}, group_items_v[kMaxMicrobatches] = {};
+  // whether each group's items took the XCD-local order (plan_items)
+  bool xcd_local_t[kMaxMicrobatches] = {}, xcd_local_v[kMaxMicrobatches] = {};
   // does a layer of head_dim D take the tile attention?
   bool layer_tiles(int D) const { return tiles_ok && !mixed_hkv && D == 256; }
 };
@@ -57,7 +60,11 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p);
 
 // Writes the items, 3 ints each: first the tile items (sequence, first row,
 // kv head), then the fp32 items (sequence, first query, head), each list
-// ordered by group and, within a group, longest sequences first; fills
+// ordered by group and, within a group, longest sequences first; items of
+// one workgroup each (kparts == 1) instead go to per-XCD queues, a
+// sequence's items together where the queues' balance allows (longest first
+// within a queue), interleaved by position, where that order's estimated
+// span is within 3 % of the plain order's (p.xcd_local_t / _v); fills
 // p.group_items_t and p.group_items_v. items holds 3 * (p.n_items_t +
 // p.n_items_v) ints; order is scratch.
 void plan_items(const AttnPlanIn& in, AttnPlan& p, int32_t* items, std::vector<int>& order);

@@ -33,7 +33,10 @@
  *   FA_GEMM_XTILE=128x64v|64x128|64x64|128x128w8|128x256w8|small
  *                               force a split-bf16 product tile
  *   FA_GEMM_TILE=128x128|64x64|128x64v   force an fp32-MFMA product tile
- *   FA_GEMM_MFMA=f32            bf16 weights through the fp32-MFMA kernel
+ *   FA_GEMM_MFMA=f32            the model's and fa_matmul_fused's products on the fp32-MFMA
+ *                               kernel (bf16 weights widened, float32 weights without the
+ *                               three-plane rewrite)
+ *   FA_ATTN_DENSE=0             fa_attention on the per-row kernel for every head dim
  *   FA_GEMM_KSPLIT=1            no K split of the encoder's N = hidden products
  *   FA_MICROBATCH=0|<rows>      micro-batches off / from this many tokens (2048)
  *   FA_MICROBATCH_GROUPS=2..4   force the micro-batch count

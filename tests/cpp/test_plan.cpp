@@ -7,6 +7,7 @@
 // choices at their thresholds. Run by tests/test_cpp_host.py.
 #include <algorithm>
 #include <map>
+#include <set>
 #include <numeric>
 #include <tuple>
 #include <vector>
@@ -71,7 +72,11 @@ void run(Case& c, const Stack& s, int want_groups, int n_run = -1) {
 }
 
 // Every row block of every sequence (and head) in exactly one item of its
-// group's run; groups in order; within a group, longest sequences first.
+// group's run; groups in order; within a group, longest sequences first —
+// for items of one workgroup each, within each XCD's positions (i % 8),
+// and sequences spread over more than one XCD only where a queue filled
+// up, which each of the 8 queues does once: at most 8 extra XCDs over the
+// group's sequences.
 void check_items(const Case& c) {
   const AttnPlan& p = c.p;
   int64_t it = 0;
@@ -86,15 +91,32 @@ void check_items(const Case& c) {
     const int iheads = tiles ? p.hkv_t : c.in.H;
     std::map<std::tuple<int, int, int>, int> seen;
     for (int g = 0; g < c.groups; g++) {
+      const bool xcd = (tiles ? p.kparts_t == 1 : p.kparts_v == 1) && (tiles ? p.xcd_local_t : p.xcd_local_v)[g];
       const int64_t n = (tiles ? p.group_items_t : p.group_items_v)[g];
       int prev_len = 1 << 30;
+      if (xcd) {
+        int prev_x[fa::kXcds];
+        for (int& v : prev_x) v = 1 << 30;
+        std::map<int, std::set<int>> residues;
+        for (int64_t k = 0; k < n; k++) {
+          const int b = c.items[3 * (it + k)], x = (int)(k % fa::kXcds);
+          residues[b].insert(x);
+          if (c.lengths[b] > prev_x[x]) FATAL("group %d, XCD %d: sequence %d (length %d) after a shorter one", g, x, b, c.lengths[b]);
+          prev_x[x] = c.lengths[b];
+        }
+        // a sequence moves to another queue only when its queue is full
+        int64_t spills = 0;
+        for (auto& [b, r] : residues) spills += (int64_t)r.size() - 1;
+        if (spills > fa::kXcds)
+          FATAL("group %d: sequences spread over %lld extra XCDs", g, (long long)spills);
+      }
       for (int64_t k = 0; k < n; k++, it++) {
         const int b = c.items[3 * it], q0 = c.items[3 * it + 1], h = c.items[3 * it + 2];
         if (b < c.gb[g] || b >= c.gb[g + 1]) FATAL("item %lld of group %d: sequence %d outside [%d, %d)", (long long)it, g, b, c.gb[g], c.gb[g + 1]);
         const int rows = tiles ? p.Gt * c.lengths[b] : c.lengths[b];
         if (q0 < 0 || q0 >= rows || q0 % istep != 0) FATAL("item %lld: first row %d of %d (step %d)", (long long)it, q0, rows, istep);
         if (h < 0 || h >= iheads) FATAL("item %lld: head %d of %d", (long long)it, h, iheads);
-        if (c.lengths[b] > prev_len) FATAL("group %d: sequence %d (length %d) after a shorter one", g, b, c.lengths[b]);
+        if (!xcd && c.lengths[b] > prev_len) FATAL("group %d: sequence %d (length %d) after a shorter one", g, b, c.lengths[b]);
         prev_len = c.lengths[b];
         if (seen[{b, q0, h}]++) FATAL("item (%d, %d, %d) twice", b, q0, h);
       }
@@ -260,3 +282,49 @@ TEST(TestMixedKvHeads) {
 }
 
 int main(int argc, char** argv) { return ctest::run_all(argc, argv); }
+
+// The XCD-local order for long key loops where it does not lengthen the
+// launch: equal lengths (C3-like, several rounds) take it; a C4-like batch
+// on one stream (281 items of 1 024-2 048 tokens, more than one round)
+// keeps the plain longest-first order, whose second round holds only the
+// shortest sequence's items, and so does a C2-like batch (mean length 172:
+// short key loops).
+TEST(TestXcdLocalChoice) {
+  {
+    Case c;
+    c.lengths = repeat(64, 512);
+    run(c, eg300m(), 1);
+    if (!c.p.xcd_local_t[0]) FATAL("C3-like, one stream: plain order");
+    check_items(c);
+  }
+  {
+    Case c;
+    c.lengths = {2048, 1900, 1700, 1500, 1300, 1200, 1100, 1024};
+    run(c, eg300m(), 1);
+    if (c.p.kparts_t != 1) FATAL("C4-like: %d key runs", c.p.kparts_t);
+    if (c.p.xcd_local_t[0]) FATAL("C4-like, one stream: XCD-local order");
+    check_items(c);
+  }
+  {
+    Case c;
+    uint32_t x = 7;
+    for (int b = 0; b < 32; b++) {
+      x = x * 1664525u + 1013904223u;
+      c.lengths.push_back(64 + (int)((x >> 8) % 193));  // U[64, 256]
+    }
+    for (int groups : {1, 3}) {
+      run(c, eg300m(), groups);
+      for (int g = 0; g < groups; g++)
+        if (c.p.xcd_local_t[g]) FATAL("C2-like, %d groups: group %d in XCD-local order", groups, g);
+      check_items(c);
+    }
+  }
+  {
+    Case c;  // C4-like in four micro-batches: two sequences per group, one round each
+    c.lengths = {2048, 1900, 1700, 1500, 1300, 1200, 1100, 1024};
+    run(c, eg300m(), 4);
+    for (int g = 0; g < 4; g++)
+      if (!c.p.xcd_local_t[g]) FATAL("C4-like, 4 groups: group %d in plain order", g);
+    check_items(c);
+  }
+}
