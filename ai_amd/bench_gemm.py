@@ -94,7 +94,8 @@ def dropin(reps: int) -> None:
     GELU and Mul, W float32 in the reference's [k x n] layout (and bf16, and
     [n x k]). Host entry point (fa_matmul_fused: copies in and out included,
     as the cgo shim calls it) and device-pointer entry point
-    (fa_matmul_fused_dev, operands resident)."""
+    (fa_matmul_fused_dev, operands resident); for float32 weights also the
+    strided entry point the Go binding uses (fa_matmul_strided_dev)."""
     ctx = N.Context(0)
     L = N.lib()
     m, k, n = 5517, 768, 1152
@@ -144,6 +145,26 @@ def dropin(reps: int) -> None:
             ctx.sync()
             out[label] = round((time.perf_counter() - t0) / reps * 1e6, 1)
         out["dev_tflops_fp32_equiv"] = round(2 * m * n * k / (out["dev_us"] * 1e-6) / 1e12, 1)
+        if dt == N.FA_DT_F32:
+            # the Go binding's route since it takes strided views
+            # (fa_matmul_strided_dev): W as a [k x n] array, or the [n x k]
+            # array read as its transposed view (row stride 1)
+            av, wv = N.Matrix(), N.Matrix()
+            av.data, av.rs, av.cs = ptrs["a"].value, k, 1
+            wv.data = ptrs["w"].value
+            wv.rs, wv.cs = (n, 1) if layout == N.FA_B_KN else (1, k)
+
+            def strided():
+                N.check(ctx.h, L.fa_matmul_strided_dev(ctx.h, 0, None, m, n, k, C.byref(av), C.byref(wv),
+                                                       C.byref(ed), ptrs["c"]))
+            for _ in range(3):
+                strided()
+            ctx.sync()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                strided()
+            ctx.sync()
+            out["strided_dev_us"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
         print(json.dumps(out), flush=True)
         for p in ptrs.values():
             L.fa_device_free(ctx.h, p)

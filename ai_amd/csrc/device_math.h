@@ -120,4 +120,80 @@ __device__ __forceinline__ Split3 split3(float a) {
 // Two bf16 high halves packed as one dword, element `lo` first in memory.
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t lo, uint32_t hi) { return (lo >> 16) | (hi & 0xFFFF0000u); }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Sum over the wave of the squares of a lane's NC float4 (a row of NC * 256
+// values spread 4 per lane per 256), fixed order per lane then wave_sum.
+template <int NC>
+__device__ __forceinline__ float sumsq(const f32x4 (&v)[NC]) {
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    s = fmaf(v[c].x, v[c].x, s);
+    s = fmaf(v[c].y, v[c].y, s);
+    s = fmaf(v[c].z, v[c].z, s);
+    s = fmaf(v[c].w, v[c].w, s);
+  }
+  return wave_sum(s);
+}
+
+// One row of the encoder's residual step, by one wave (lane: columns
+// 256 c + 4 lane .. +3): x = (x + RMSNorm(o [+ o2]; g_post)) * scale, then
+// xn = RMSNorm(x; g_next) when g_next != null (models/gemma/embed.go:
+// 217-237). o2 is a K-split product's second partial, added after o.
+// Shared by residual_norm_kernel and the small-M product's fused tail, so
+// both give the same bits.
+template <int NC>
+__device__ __forceinline__ void residual_norm_row(const float* __restrict__ o, const float* __restrict__ o2,
+                                                  float* __restrict__ x, float* __restrict__ xn, int64_t row,
+                                                  const float* __restrict__ g_post, const float* __restrict__ g_next,
+                                                  float eps, float scale, int lane) {
+  constexpr int d = NC * 256;
+  f32x4 ov[NC], xv[NC], gp[NC], gn[NC];
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    ov[c] = *reinterpret_cast<const f32x4*>(o + row * d + col);
+    xv[c] = *reinterpret_cast<const f32x4*>(x + row * d + col);
+  }
+  // the gains load with the rows, not after the reductions
+#pragma unroll
+  for (int c = 0; c < NC; c++) gp[c] = *reinterpret_cast<const f32x4*>(g_post + c * 256 + lane * 4);
+  if (g_next) {
+#pragma unroll
+    for (int c = 0; c < NC; c++) gn[c] = *reinterpret_cast<const f32x4*>(g_next + c * 256 + lane * 4);
+  }
+  if (o2) {
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + row * d + c * 256 + lane * 4);
+      ov[c].x = ov[c].x + p2.x; ov[c].y = ov[c].y + p2.y; ov[c].z = ov[c].z + p2.z; ov[c].w = ov[c].w + p2.w;
+    }
+  }
+  const float inv = rms_inv(sumsq<NC>(ov), d, eps);
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    const f32x4 gg = gp[c];
+    xv[c].x = xv[c].x + ov[c].x * inv * gg.x;
+    xv[c].y = xv[c].y + ov[c].y * inv * gg.y;
+    xv[c].z = xv[c].z + ov[c].z * inv * gg.z;
+    xv[c].w = xv[c].w + ov[c].w * inv * gg.w;
+    if (scale != 1.f) {
+      xv[c].x = xv[c].x * scale; xv[c].y = xv[c].y * scale; xv[c].z = xv[c].z * scale; xv[c].w = xv[c].w * scale;
+    }
+    *reinterpret_cast<f32x4*>(x + row * d + col) = xv[c];
+  }
+  if (g_next == nullptr) return;
+  const float inv2 = rms_inv(sumsq<NC>(xv), d, eps);
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int col = c * 256 + lane * 4;
+    const f32x4 gg = gn[c];
+    f32x4 r;
+    r.x = xv[c].x * inv2 * gg.x; r.y = xv[c].y * inv2 * gg.y; r.z = xv[c].z * inv2 * gg.z; r.w = xv[c].w * inv2 * gg.w;
+    *reinterpret_cast<f32x4*>(xn + row * d + col) = r;
+  }
+}
+
 }  // namespace fa

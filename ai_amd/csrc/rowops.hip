@@ -89,18 +89,6 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, 
 // ---- model-path kernels (hidden size a multiple of 256, at most 1024) -----------
 // NC = hidden/256 float4 chunks per lane.
 
-template <int NC>
-__device__ __forceinline__ float sumsq(const f32x4 (&v)[NC]) {
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < NC; c++) {
-    s = fmaf(v[c].x, v[c].x, s);
-    s = fmaf(v[c].y, v[c].y, s);
-    s = fmaf(v[c].z, v[c].z, s);
-    s = fmaf(v[c].w, v[c].w, s);
-  }
-  return wave_sum(s);
-}
 
 // x[r] = E[ids[src[r]]] * scale; xn[r] = x[r] * rms_inv(x[r]) * g.
 template <int NC>
@@ -163,55 +151,9 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
                                                             int64_t rows, const float* __restrict__ g_post,
                                                             const float* __restrict__ g_next, float eps,
                                                             float scale) {
-  constexpr int d = NC * 256;
   int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // one wave per row
-  int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  f32x4 ov[NC], xv[NC], gp[NC], gn[NC];
-#pragma unroll
-  for (int c = 0; c < NC; c++) {
-    const int col = c * 256 + lane * 4;
-    ov[c] = *reinterpret_cast<const f32x4*>(o + row * d + col);
-    xv[c] = *reinterpret_cast<const f32x4*>(x + row * d + col);
-  }
-  // the gains load with the rows, not after the reductions
-#pragma unroll
-  for (int c = 0; c < NC; c++) gp[c] = *reinterpret_cast<const f32x4*>(g_post + c * 256 + lane * 4);
-  if (g_next) {
-#pragma unroll
-    for (int c = 0; c < NC; c++) gn[c] = *reinterpret_cast<const f32x4*>(g_next + c * 256 + lane * 4);
-  }
-  if (o2) {
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-      const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + row * d + c * 256 + lane * 4);
-      ov[c].x = ov[c].x + p2.x; ov[c].y = ov[c].y + p2.y; ov[c].z = ov[c].z + p2.z; ov[c].w = ov[c].w + p2.w;
-    }
-  }
-  const float inv = rms_inv(sumsq<NC>(ov), d, eps);
-#pragma unroll
-  for (int c = 0; c < NC; c++) {
-    const int col = c * 256 + lane * 4;
-    const f32x4 gg = gp[c];
-    xv[c].x = xv[c].x + ov[c].x * inv * gg.x;
-    xv[c].y = xv[c].y + ov[c].y * inv * gg.y;
-    xv[c].z = xv[c].z + ov[c].z * inv * gg.z;
-    xv[c].w = xv[c].w + ov[c].w * inv * gg.w;
-    if (scale != 1.f) {
-      xv[c].x = xv[c].x * scale; xv[c].y = xv[c].y * scale; xv[c].z = xv[c].z * scale; xv[c].w = xv[c].w * scale;
-    }
-    *reinterpret_cast<f32x4*>(x + row * d + col) = xv[c];
-  }
-  if (g_next == nullptr) return;
-  const float inv2 = rms_inv(sumsq<NC>(xv), d, eps);
-#pragma unroll
-  for (int c = 0; c < NC; c++) {
-    const int col = c * 256 + lane * 4;
-    const f32x4 gg = gn[c];
-    f32x4 r;
-    r.x = xv[c].x * inv2 * gg.x; r.y = xv[c].y * inv2 * gg.y; r.z = xv[c].z * inv2 * gg.z; r.w = xv[c].w * inv2 * gg.w;
-    *reinterpret_cast<f32x4*>(xn + row * d + col) = r;
-  }
+  residual_norm_row<NC>(o, o2, x, xn, row, g_post, g_next, eps, scale, threadIdx.x & 63);
 }
 
 // Per (token, head): RMSNorm over D (256 or 512) with the head's gain vector
