@@ -237,36 +237,36 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   }
 }
 
-// pooled[b, c] = (sum over the sequence's rows of h[., c]) * (1/L_b). A
-// block covers 64 columns of one sequence: its 4 waves take every 4th row
-// (coalesced 256-byte row segments) and the 4 partial sums are added in wave
-// order, so the result does not depend on scheduling.
-__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ cu,
-                                                   int d, float* __restrict__ pooled) {
-  __shared__ float part[4][64];
+// pooled[b, c] = (sum over the sequence's rows of h[., c]) * (1/L_b). One
+// workgroup of 16 waves per (sequence, 256 columns): wave w adds rows w, w +
+// 16, ... in order (lane: four columns, 16-byte loads, eight rows in
+// flight), then the 16 wave sums are added in wave order, so the result does
+// not depend on scheduling.
+__global__ __launch_bounds__(1024) void pool_kernel(const float* __restrict__ h, const int32_t* __restrict__ cu,
+                                                    int d, float* __restrict__ pooled) {
+  __shared__ f32x4 part[16][64];
   const int b = blockIdx.x;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int c = blockIdx.y * 64 + tx;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.y * 256 + lane * 4;
   const int r0 = cu[b], r1 = cu[b + 1];
-  float s = 0.f;
-  if (c < d) {
-    // rows ty, ty + 4, ... added in order, eight loads in flight
-    int r = r0 + ty;
-    for (; r + 28 < r1; r += 32) {
-      float v[8];
+  f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+  int r = r0 + w;
+  for (; r + 112 < r1; r += 128) {
+    f32x4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = h[(int64_t)(r + 4 * u) * d + c];
+    for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const f32x4*>(h + (int64_t)(r + 16 * u) * d + c);
 #pragma unroll
-      for (int u = 0; u < 8; u++) s += v[u];
-    }
-    for (; r < r1; r += 4) s += h[(int64_t)r * d + c];
+    for (int u = 0; u < 8; u++) s += v[u];
   }
-  part[ty][tx] = s;
+  for (; r < r1; r += 16) s += *reinterpret_cast<const f32x4*>(h + (int64_t)r * d + c);
+  part[w][lane] = s;
   __syncthreads();
-  if (ty == 0 && c < d) {
-    const float tot = ((part[0][tx] + part[1][tx]) + part[2][tx]) + part[3][tx];
+  if (w == 0) {
+    f32x4 tot = part[0][lane];
+#pragma unroll
+    for (int i = 1; i < 16; i++) tot += part[i][lane];
     const int n = r1 - r0 > 0 ? r1 - r0 : 1;
-    pooled[(int64_t)b * d + c] = tot * (1.f / (float)n);
+    *reinterpret_cast<f32x4*>(pooled + (int64_t)b * d + c) = tot * (1.f / (float)n);
   }
 }
 
@@ -608,7 +608,8 @@ int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t
 int launch_pool(fa_ctx* ctx, const float* h, const int32_t* cu_seqlens, int32_t nseq, int32_t d, float* pooled,
                 hipStream_t s) {
   if (nseq == 0) return FA_OK;
-  dim3 grid(nseq, (d + 63) / 64), block(256);
+  if (d % 256 != 0) return set_error(ctx, FA_ERR_UNSUPPORTED, "pool: width %d not a multiple of 256", d);
+  dim3 grid(nseq, d / 256), block(1024);
   hipLaunchKernelGGL(pool_kernel, grid, block, 0, s, h, cu_seqlens, d, pooled);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
