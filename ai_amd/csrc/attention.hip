@@ -458,18 +458,33 @@ __device__ __forceinline__ void split_pack8(const f32x4& x0, const f32x4& x1, bf
 // for batches whose 128-row items fill between half a round and a round of
 // the CUs; the compiler then keeps what does not fit in 256 VGPRs in AGPRs
 // instead of scratch).
-template <int TL_W>
+// DS = 2 (with TL_W = 8): 64-row items whose head dimension is split over
+// a pair of waves, waves w and w + 4 owning the same 16 rows and dims
+// [0, 128) and [128, 256) of q (for the scores) and of O (for P.V). Each
+// wave's partial scores over its 128 dims go to LDS before the barrier
+// that follows the score step, and both waves of the pair add them as
+// own + partner's (the same fp32 sum in both: addition commutes exactly),
+// so they compute identical probabilities. Per wave: half the MFMAs,
+// q terms and O of a four-wave item, at two waves per SIMD.
+template <int TL_W, int DS>
 __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_kernel(TilesParams p) {
-  constexpr int TL_ROWS = 16 * TL_W;  // query rows per work item
+  static_assert(DS == 1 || (DS == 2 && TL_W == 8), "dim split: eight waves in pairs");
+  constexpr int RB = TL_W / DS;       // row blocks of 16 per item
+  constexpr int TL_ROWS = 16 * RB;    // query rows per work item
   constexpr int HD = 256;
+  constexpr int NC = HD / 32 / DS;    // q chunks of 32 dims per wave
+  constexpr int NDB = HD / 16 / DS;   // blocks of 16 O dims per wave
   constexpr int TERM = TL_IMG / 3;  // bf16 per term of an image
   __shared__ __attribute__((aligned(16))) uint16_t Ks[TL_IMG];
   __shared__ __attribute__((aligned(16))) uint16_t Vs0[TL_IMG];
   __shared__ __attribute__((aligned(16))) uint16_t Vs1[TL_IMG];
+  // partial scores of each wave (two 16-key blocks x 64 lanes), DS = 2
+  __shared__ f32x4 Xs[DS == 2 ? TL_W * 2 * 64 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rbw = wave % RB, hf = wave / RB;  // the wave's row block and dim half
   const int lq = lane & 15, g = lane >> 4;
 
   const int item = blockIdx.x / p.kparts, part = blockIdx.x % p.kparts;
@@ -481,7 +496,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   const int64_t start = p.cu[seq] - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
   const int nrows = G * L;
-  const int row = rb + 16 * wave + lq;
+  const int row = rb + 16 * rbw + lq;
   const bool qvalid = row < nrows;
   const int tok = (qvalid ? row : rb) / G;
   const int head = hk * G + (qvalid ? row : rb) % G;
@@ -513,7 +528,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     }
   };
 
-  if (rb + 16 * wave >= nrows) {
+  if (rb + 16 * rbw >= nrows) {
     // every row of this wave lies past the sequence's rows (the last item
     // of a sequence): the wave issues its share of each image load and
     // takes part in every barrier of the loop below, in the same order,
@@ -531,7 +546,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     return;
   }
 
-  bf16x8 qt[3][HD / 32];
+  bf16x8 qt[3][NC];
   {
     // q normed (RMSNorm, gain) and rotated (RoPE at the token's position)
     // as it is loaded: the row's dims are spread over the four lanes with
@@ -573,15 +588,23 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
       }
     }
 #pragma unroll
-    for (int c = 0; c < HD / 32; c++) {
-      if (!qvalid) x[c][0] = x[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      split_pack8(x[c][0], x[c][1], qt[0][c], qt[1][c], qt[2][c]);
+    for (int c = 0; c < NC; c++) {
+      // the wave's dim half (chunks NC * hf ..)
+      f32x4 x0 = x[c][0], x1 = x[c][1];
+      if constexpr (DS == 2) {
+        if (hf) {
+          x0 = x[NC + c][0];
+          x1 = x[NC + c][1];
+        }
+      }
+      if (!qvalid) x0 = x1 = f32x4{0.f, 0.f, 0.f, 0.f};
+      split_pack8(x0, x1, qt[0][c], qt[1][c], qt[2][c]);
     }
   }
 
-  f32x4 oacc[HD / 16];  // O^T: dims 16db + 4g + r of row lq
+  f32x4 oacc[NDB];  // O^T: dims 16(NDB hf + db) + 4g + r of row lq
 #pragma unroll
-  for (int db = 0; db < HD / 16; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < NDB; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegBig;
   float l_part = 0.f;
   const int vsw = (lq >> 1) & 3;
@@ -599,8 +622,8 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
       const int key = 16 * kb + lq;
       const uint16_t* kr = Kc + key * HD;
 #pragma unroll
-      for (int c = 0; c < HD / 32; c++) {
-        const int pos = ((4 * c + g) ^ key) * 8;
+      for (int c = 0; c < NC; c++) {
+        const int pos = ((4 * (NC * hf + c) + g) ^ key) * 8;
         const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kr + pos);
         const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kr + TERM + pos);
         const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(kr + 2 * TERM + pos);
@@ -618,8 +641,8 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   auto pv = [&](const uint16_t* Vc, const bf16x8& b0, const bf16x8& b1, const bf16x8& b2) {
     const int vpos = (g ^ vsw) * 8;
 #pragma unroll
-    for (int db = 0; db < HD / 16; db++) {
-      const uint16_t* vr = Vc + (16 * db + lq) * 32 + vpos;
+    for (int db = 0; db < NDB; db++) {
+      const uint16_t* vr = Vc + (16 * (NDB * hf + db) + lq) * 32 + vpos;
       const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(vr);
       const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(vr + TERM);
       const bf16x8 v2 = *reinterpret_cast<const bf16x8*>(vr + 2 * TERM);
@@ -689,8 +712,17 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     dl_barrier<0x0F70>();  // vmcnt(0): K(tt), V(tt-1) landed (own loads, then everyone's)
     issue(img0 + tt * tstride + TL_IMG, Vn);
     qk(Ks, sacc);
-    dl_barrier<0xC07F>();  // every wave's key reads done (no wait for the loads)
+    if constexpr (DS == 2) {
+      Xs[(2 * wave) * 64 + lane] = sacc[0];
+      Xs[(2 * wave + 1) * 64 + lane] = sacc[1];
+    }
+    dl_barrier<0xC07F>();  // every wave's key reads (and partial-score writes) done; no wait for the loads
     issue(img0 + min(tt + 1, te - 1) * tstride, Ks);
+    if constexpr (DS == 2) {  // the partner's half (it writes again only after the next barrier)
+      const int pw = wave ^ RB;
+      sacc[0] = sacc[0] + Xs[(2 * pw) * 64 + lane];
+      sacc[1] = sacc[1] + Xs[(2 * pw + 1) * 64 + lane];
+    }
   };
   // P.V of tile tt-1 (terms pb*) with the softmax of tile tt (scores sacc)
   // written between its blocks of 16 dims, in four stages, so that the
@@ -700,9 +732,10 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     float t[8];
     float tmax = -INFINITY, mn = 0.f, psum = 0.f;
     uint32_t ph[8], pm[8], pl[8];
+    constexpr int WPS = DS == 2 ? 2 : 1;  // weights per block in the last stage
 #pragma unroll
-    for (int db = 0; db < HD / 16; db++) {
-      const uint16_t* vr = Vp + (16 * db + lq) * 32 + vpos;
+    for (int db = 0; db < NDB; db++) {
+      const uint16_t* vr = Vp + (16 * (NDB * hf + db) + lq) * 32 + vpos;
       const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(vr);
       const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(vr + TERM);
       const bf16x8 v2 = *reinterpret_cast<const bf16x8*>(vr + 2 * TERM);
@@ -731,15 +764,18 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
         alpha = exp_flush(m_run - mn);  // 1 where the offset stays, 0 for the first valid tile
         m_run = mn;
         asm volatile("" ::"v"(alpha), "v"(mn));
-      } else if (db >= 4 && db < 12) {  // one weight (masked keys: -inf, flushed to 0) and its exact bf16 terms
-        const int e = db - 4;
-        const float w = exp_flush(t[e] - mn);
-        psum += w;
-        const Split3 sp = split3(w);
-        ph[e] = sp.h;
-        pm[e] = sp.m;
-        pl[e] = sp.l;
-        asm volatile("" ::"v"(ph[e]), "v"(pm[e]), "v"(pl[e]), "v"(psum));
+      } else if (db >= 4 && db < 4 + 8 / WPS) {  // WPS weights (masked keys: -inf, flushed to 0) and their exact bf16 terms
+#pragma unroll
+        for (int u = 0; u < WPS; u++) {
+          const int e = (db - 4) * WPS + u;
+          const float w = exp_flush(t[e] - mn);
+          psum += w;
+          const Split3 sp = split3(w);
+          ph[e] = sp.h;
+          pm[e] = sp.m;
+          pl[e] = sp.l;
+          asm volatile("" ::"v"(ph[e]), "v"(pm[e]), "v"(pl[e]), "v"(psum));
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -759,7 +795,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     pv_softmax(Vp, tt, sacc, alpha, moved);
     if (moved) {
 #pragma unroll
-      for (int db = 0; db < HD / 16; db++) oacc[db] *= alpha;
+      for (int db = 0; db < NDB; db++) oacc[db] *= alpha;
     }
   };
   if (tb < te) {
@@ -792,19 +828,19 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   const int OW = p.H * HD;
   if (p.kparts > 1) {
     const int64_t arow = p.cu[seq] + tok;  // absolute packed row
-    float* orow = p.part + ((int64_t)part * p.rows + arow) * OW + (int64_t)head * HD + 4 * g;
+    float* orow = p.part + ((int64_t)part * p.rows + arow) * OW + (int64_t)head * HD + 16 * NDB * hf + 4 * g;
 #pragma unroll
-    for (int db = 0; db < HD / 16; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db];
-    if (g == 0) {
+    for (int db = 0; db < NDB; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db];
+    if (g == 0 && hf == 0) {
       float2* pml = reinterpret_cast<float2*>(p.part + (int64_t)p.kparts * p.rows * OW);
       pml[((int64_t)part * p.rows + arow) * p.H + head] = make_float2(m_run, l_tot);
     }
     return;
   }
   const float inv = 1.f / l_tot;
-  float* orow = p.out + (start + tok) * OW + (int64_t)head * HD + 4 * g;
+  float* orow = p.out + (start + tok) * OW + (int64_t)head * HD + 16 * NDB * hf + 4 * g;
 #pragma unroll
-  for (int db = 0; db < HD / 16; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db] * inv;
+  for (int db = 0; db < NDB; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db] * inv;
 }
 
 // ---- dense attention on the MFMA (the tensor.AttentionScaled drop-in) ----------
@@ -1092,6 +1128,16 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
   return FA_OK;
 }
 
+// 64-row items on eight waves in dim-split pairs (attention_tiles_kernel<8,
+// 2>) instead of four waves; FA_ATTN_PAIRS=0 selects the four-wave kernel.
+static bool tiles_pairs() {
+  static const bool on = [] {
+    const char* e = std::getenv("FA_ATTN_PAIRS");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d_items, int32_t n_items,
                            hipStream_t s) {
   if (a.Hkv <= 0 || a.H % a.Hkv != 0)
@@ -1107,10 +1153,12 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
   p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
   p.gq = a.gq; p.cs = a.cos_t; p.sn = a.sin_t; p.eps = a.eps;
   const dim3 grid((unsigned)((int64_t)n_items * a.kparts));
-  if (a.waves == 4)
-    hipLaunchKernelGGL(attention_tiles_kernel<4>, grid, dim3(64 * 4), 0, s, p);
+  if (a.waves == 4 && tiles_pairs())
+    hipLaunchKernelGGL((attention_tiles_kernel<8, 2>), grid, dim3(64 * 8), 0, s, p);
+  else if (a.waves == 4)
+    hipLaunchKernelGGL((attention_tiles_kernel<4, 1>), grid, dim3(64 * 4), 0, s, p);
   else
-    hipLaunchKernelGGL(attention_tiles_kernel<8>, grid, dim3(64 * 8), 0, s, p);
+    hipLaunchKernelGGL((attention_tiles_kernel<8, 1>), grid, dim3(64 * 8), 0, s, p);
   if (a.kparts > 1)
     hipLaunchKernelGGL(attention_combine_kernel<256>, dim3((unsigned)((a.nrows * a.H + 3) / 4)), dim3(256), 0, s,
                        a.part, a.kparts, a.rows, a.row0, a.nrows, a.H, a.out);

@@ -203,6 +203,29 @@ int attention_key_parts_forced() {
   return v;
 }
 
+// FA_ATTN_ROWS=64|128 forces the tile attention's rows per item (tuning);
+// 0 when unset.
+int attention_rows_forced() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_ATTN_ROWS");
+    if (!e) return 0;
+    const int r = std::atoi(e);
+    return r == 64 || r == 128 ? r : 0;
+  }();
+  return v;
+}
+
+// FA_ATTN_XCD=1|0 forces the XCD-local attention item order on or off
+// (tuning); 0 when unset (chosen per group).
+int attention_xcd_forced() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_ATTN_XCD");
+    if (!e) return 0;
+    return e[0] == '0' ? -1 : 1;
+  }();
+  return v;
+}
+
 // FA_MICROBATCH_GROUPS=<2..4> forces the group count (tuning); 0 when unset.
 int microbatch_count_forced() {
   static const int v = [] {
@@ -805,6 +828,8 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   pin.tile_keys = fa::attention_tiles_keys(); pin.varlen_qblock = fa::attention_varlen_qblock();
   pin.max_key_parts = fa::kMaxKeyParts; pin.split_rows = fa::kAttnSplitRows;
   pin.forced_key_parts = fa::attention_key_parts_forced();
+  pin.forced_rows = fa::attention_rows_forced();
+  pin.forced_xcd = fa::attention_xcd_forced();
   fa::AttnPlan ap;
   fa::plan_attention(pin, ap);
   const int64_t n_items_t = ap.n_items_t, n_items = ap.n_items_t + ap.n_items_v, n_tiles = ap.n_tiles;

@@ -57,6 +57,7 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
     int64_t n8 = 0;
     for (int b = 0; b < in.B; b++) n8 += ((int64_t)p.Gt * in.lengths[b] + 127) / 128 * p.hkv_t;
     if (in.groups > 1 && 2 * n8 > in.cus && 5 * n8 <= 3LL * in.cus) p.waves_t = 4;
+    if (in.forced_rows) p.waves_t = in.forced_rows / 16;
   }
   const int istep_t = 16 * p.waves_t;
   for (int b = 0; b < in.B; b++) {
@@ -180,7 +181,7 @@ void plan_items(const AttnPlanIn& in, AttnPlan& p, int32_t* items, std::vector<i
         int64_t keys_sum = 0;
         for (int b : order) keys_sum += in.lengths[b];
         const bool long_keys = keys_sum >= 384LL * (int64_t)order.size();
-        const bool local = long_keys && span_xcd <= 1.03 * span_plain;
+        const bool local = in.forced_xcd ? in.forced_xcd > 0 : long_keys && span_xcd <= 1.03 * span_plain;
         for (int64_t i = 0; i < n; i++) {
           if (local) {
             const int64_t e = q[i % kXcds][i / kXcds];

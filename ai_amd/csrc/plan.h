@@ -34,6 +34,8 @@ struct AttnPlanIn {
   int tile_keys = 32, varlen_qblock = 32, max_key_parts = 8;
   int64_t split_rows = 1024;
   int forced_key_parts = 0;          // tuning: key runs forced (0: chosen)
+  int forced_rows = 0;               // tuning: tile item rows forced, 64 or 128 (0: chosen)
+  int forced_xcd = 0;                // tuning: XCD-local item order forced on (1) or off (-1)
 };
 
 struct AttnPlan {
