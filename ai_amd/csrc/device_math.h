@@ -138,13 +138,13 @@ __device__ __forceinline__ float sumsq(const f32x4 (&v)[NC]) {
 }
 
 // One row of the encoder's residual step, by one wave (lane: columns
-// 256 c + 4 lane .. +3): x = (x + RMSNorm(o [+ o2]; g_post)) * scale, then
-// xn = RMSNorm(x; g_next) when g_next != null (models/gemma/embed.go:
-// 217-237). o2 is a K-split product's second partial, added after o.
-// Shared by residual_norm_kernel and the small-M product's fused tail, so
-// both give the same bits.
+// 256 c + 4 lane .. +3): x = (x + RMSNorm(o [+ parts]; g_post)) * scale,
+// then xn = RMSNorm(x; g_next) when g_next != null (models/gemma/embed.go:
+// 217-237). With o2 != null, a K-split product's other n2 partials sit at
+// o2 + j * pstride (j < n2) and are added to o in part order.
 template <int NC>
 __device__ __forceinline__ void residual_norm_row(const float* __restrict__ o, const float* __restrict__ o2,
+                                                  int n2, int64_t pstride,
                                                   float* __restrict__ x, float* __restrict__ xn, int64_t row,
                                                   const float* __restrict__ g_post, const float* __restrict__ g_next,
                                                   float eps, float scale, int lane) {
@@ -163,10 +163,11 @@ __device__ __forceinline__ void residual_norm_row(const float* __restrict__ o, c
 #pragma unroll
     for (int c = 0; c < NC; c++) gn[c] = *reinterpret_cast<const f32x4*>(g_next + c * 256 + lane * 4);
   }
-  if (o2) {
+  // the other K parts, added in part order
+  for (int j = 0; o2 && j < n2; j++) {
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-      const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + row * d + c * 256 + lane * 4);
+      const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + j * pstride + row * d + c * 256 + lane * 4);
       ov[c].x = ov[c].x + p2.x; ov[c].y = ov[c].y + p2.y; ov[c].z = ov[c].z + p2.z; ov[c].w = ov[c].w + p2.w;
     }
   }

@@ -241,10 +241,11 @@ int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_
 // q/k RMSNorm with (1+g) and RoPE on the packed qkv buffer [rows x (H+2*Hkv)*D],
 // in place; positions from d_pos.
 // With norm_v, the Hkv value heads are RMS-normalised too (unit gain, no
-// rotation). D is 256 or 512.
+// rotation). D is 256 or 512. qkv2 (optional): the second K part of a
+// K-split q|k|v product (same layout), added to qkv first, values included.
 int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t Hkv, int32_t D, const float* gq,
                        const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
-                       hipStream_t s, bool norm_v = false);
+                       hipStream_t s, bool norm_v = false, const float* qkv2 = nullptr);
 
 // pl [rows, nl*P] in place: each P-wide piece becomes RMSNorm(pl * scale; g).
 int launch_ple_norm(fa_ctx* ctx, float* pl, int64_t rows, int32_t nl, int32_t P, float scale, const float* g,
@@ -252,10 +253,11 @@ int launch_ple_norm(fa_ctx* ctx, float* pl, int64_t rows, int32_t nl, int32_t P,
 
 // x = (x + RMSNorm(o; g_post)) * scale; then xn = RMSNorm(x; g_next)
 // (g_next may be null: then xn is not written).
-// o2 (optional): second partial product of a K-split GEMM, added to o.
+// o2 (optional): the other n2 (1..3) partial products of a K-split GEMM,
+// planes pstride floats apart, added to o in part order.
 int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
                          const float* g_post, const float* g_next, float eps, hipStream_t s,
-                         const float* o2 = nullptr, float scale = 1.f);
+                         const float* o2 = nullptr, float scale = 1.f, int n2 = 1, int64_t pstride = 0);
 
 // Fused varlen attention over packed tokens. qkv [rows x (H+2Hkv)*D]; out
 // [rows x H*D]; cu_seqlens [nseq+1]; window: keys with |i-j| >= window are

@@ -226,6 +226,36 @@ int attention_xcd_forced() {
   return v;
 }
 
+// K parts of the N = hidden products (o, down) for a few-row batch whose
+// small-M tiles, times four parts, still fit one per CU (FA_SMALL_KSPLIT=2
+// or 4, default 4). A small-M workgroup's time is its operand loads: with
+// four parts each loads half the bytes of two (at 128 rows: o 8.5 -> 7.4
+// us, down 9.8 -> 8.4 us per launch; C1 1.30 -> 1.28 ms per forward, 64
+// tokens 1.25 -> 1.22 ms on MI355X), for two more partial planes read by
+// the residual step.
+int small_ksplit() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_SMALL_KSPLIT");
+    if (!e) return 4;
+    return std::atoi(e) >= 4 ? 4 : 2;
+  }();
+  return v;
+}
+
+// K parts of a few-row batch's q|k|v product on the fp32 attention path,
+// added by the q/k norm pass (FA_QKV_KSPLIT=1 or 2, default 2): 160 instead
+// of 80 workgroups at 128 rows, each loading half the operands (11.1 ->
+// 9.0 us per launch; C1 1.28 -> 1.24 ms, 64 tokens 1.22 -> 1.17 ms per
+// forward on MI355X), for one more read of the product in the norm pass.
+int qkv_ksplit() {
+  static const int v = [] {
+    const char* e = std::getenv("FA_QKV_KSPLIT");
+    if (!e) return 2;
+    return std::atoi(e) >= 2 ? 2 : 1;
+  }();
+  return v;
+}
+
 // FA_MICROBATCH_GROUPS=<2..4> forces the group count (tuning); 0 when unset.
 int microbatch_count_forced() {
   static const int v = [] {
@@ -250,11 +280,11 @@ int microbatch_count(int64_t tokens, double sum_l2) {
   return tokens >= 24576 ? 2 : 3;
 }
 
-// HBM bytes of one residual_norm launch: the product (and its second K
-// part when split) and x read, x written, and the next norm's input written
-// when there is a next norm.
-double resnorm_bytes(int64_t rows, int64_t d, const float* o2, const float* g_next) {
-  return (double)rows * d * 4.0 * (3.0 + (o2 ? 1.0 : 0.0) + (g_next ? 1.0 : 0.0));
+// HBM bytes of one residual_norm launch: the product's K parts and x
+// read, x written, and the next norm's input written when there is a next
+// norm.
+double resnorm_bytes(int64_t rows, int64_t d, int parts, const float* g_next) {
+  return (double)rows * d * 4.0 * (2.0 + parts + (g_next ? 1.0 : 0.0));
 }
 
 // Brackets one launch with events when profiling.
@@ -877,7 +907,10 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   // variant 2 adds the per-layer inputs [M, layers*P]; its [M, P] gate
   // output reuses gu (free after the down product)
   const int ksplit = fa::gemm_ksplit();
-  const int64_t ncols = 2LL * d + m->max_width + m->max_hd + (int64_t)ksplit * d + std::max(F, P) +
+  // a few-row batch on one stream may split those products in four
+  const bool few_rows = groups == 1 && ksplit > 1 && ((M + 31) / 32) * ((d + 63) / 64) * 4 <= cus;
+  const int ks_max = few_rows ? std::max(ksplit, fa::small_ksplit()) : ksplit;
+  const int64_t ncols = 2LL * d + m->max_width + m->max_hd + (int64_t)ks_max * d + std::max(F, P) +
                         (v2 ? (int64_t)NL * P : 0);
   int maxw = std::max(d, std::max(full, v2 ? m->E : d));
   for (int o : m->dense_out) maxw = std::max(maxw, o);
@@ -895,7 +928,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   float* qkv = xn + M * d;
   float* att = qkv + M * m->max_width;
   float* o = att + M * m->max_hd;
-  float* gu = o + (int64_t)ksplit * M * d;
+  float* gu = o + (int64_t)ks_max * M * d;
   float* ple = gu + M * std::max(F, P);
   float* pooled = ple + (v2 ? M * NL * P : 0);
   float* hbuf0 = pooled + (size_t)B * d;
@@ -950,10 +983,15 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     // partial's writes and reads cost more than the fill gains (C5's three
     // groups of about 5 970 rows: 4.7 % faster unsplit).
     const int64_t n_tiles = ((rows + 127) / 128) * ((d + 127) / 128) * groups;
-    const int ks = n_tiles < 2LL * cus ? ksplit : 1;
-    // per product: split only when K divides into whole 32-wide slabs
-    const int ks_o = (H * D) % (32 * ks) == 0 ? ks : 1, ks_down = F % (32 * ks) == 0 ? ks : 1,
-              ks_ple = P % (32 * ks) == 0 ? ks : 1;
+    const int ks = n_tiles < 2LL * cus ? ks_max : 1;
+    // per product: the most parts (ks, halved as needed) that divide K into
+    // whole 32-wide slabs
+    auto parts = [&](int64_t K) {
+      int k = ks;
+      while (k > 1 && K % (32 * k) != 0) k /= 2;
+      return k;
+    };
+    const int ks_o = parts(H * D), ks_down = parts(F), ks_ple = parts(P);
     const float* o2_o = ks_o > 1 ? o + M * d + r0 * d : nullptr;
     const float* o2_dn = ks_down > 1 ? o + M * d + r0 * d : nullptr;
     const float* o2_pl = ks_ple > 1 ? o + M * d + r0 * d : nullptr;
@@ -968,10 +1006,20 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     float* const gur = gu + r0 * std::max(F, P);
     float* const or_ = o + r0 * d;
     int rc;
+    // a few-row batch on the fp32 attention path splits the q|k|v product
+    // in K: its second part goes to o's planes (free until the o product)
+    // and the q/k norm pass adds it
+    const bool qkv_split = few_rows && !tiles && fa::qkv_ksplit() > 1 && d % 64 == 0 &&
+                           (int64_t)ks_max * d >= m->max_width;
+    const float* qkv2 = qkv_split ? o : nullptr;
     {
       fa::GemmArgs g;
       g.shared = groups > 1;
       g.m = rows; g.n = L.width; g.k = d; g.a = xnr; g.lda = d; fa::set_b(g, L.wqkv); g.c = qkvr; g.ldc = L.width;
+      if (qkv_split) {
+        g.ksplit = 2;
+        g.c_split = o - qkvr;
+      }
       fa::Probe pr(m, FA_K_GEMM_QKV, 2.0 * rows * L.width * d, 0);
       if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
       pr.done();
@@ -992,7 +1040,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     } else {
       fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * (H + (v2 ? 2 : 1) * Hkv) * D * 8.0);
       if ((rc = fa::launch_qknorm_rope(ctx, qkvr, rows, H, Hkv, D, L.g_q, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t,
-                                       st, v2)))
+                                       st, v2, qkv2)))
         return rc;
       pr.done();
     }
@@ -1041,8 +1089,9 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       pr.done();
     }
     {
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, o2_o, L.g_pre_ffn));
-      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_attn, L.g_pre_ffn, eps, st, o2_o)))
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, ks_o, L.g_pre_ffn));
+      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_attn, L.g_pre_ffn, eps, st, o2_o, 1.f,
+                                         ks_o - 1, M * d)))
         return rc;
       pr.done();
     }
@@ -1068,9 +1117,9 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     const float* g_next = (l + 1 < NL) ? m->layers[l + 1].g_in : m->g_final;
     {
       // variant 2: the per-layer-input block reads x itself, so no norm here
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, o2_dn, v2 ? nullptr : g_next));
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, ks_down, v2 ? nullptr : g_next));
       if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_post_ffn, v2 ? nullptr : g_next, eps, st,
-                                         o2_dn)))
+                                         o2_dn, 1.f, ks_down - 1, M * d)))
         return rc;
       pr.done();
     }
@@ -1095,8 +1144,9 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
         if ((rc = fa::launch_gemm(ctx, g, st))) return rc;
         pr.done();
       }
-      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, o2_pl, g_next));
-      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_ple_post, g_next, eps, st, o2_pl, L.scalar)))
+      fa::Probe pr(m, FA_K_RESIDUAL_NORM, 0, fa::resnorm_bytes(rows, d, ks_ple, g_next));
+      if ((rc = fa::launch_residual_norm(ctx, or_, xr, xnr, rows, d, L.g_ple_post, g_next, eps, st, o2_pl, L.scalar,
+                                         ks_ple - 1, M * d)))
         return rc;
       pr.done();
     }

@@ -142,18 +142,20 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* __rest
 }
 
 // x = (x + RMSNorm(o; g_post)) * scale; xn = RMSNorm(x; g_next) when
-// g_next != null. With o2 != null, o is the sum of two partial products
-// o + o2 (in that order) of a K-split GEMM. scale is EmbeddingGemma 2's
-// layer scalar after its per-layer-input block (embed.go:367-370), else 1.
+// g_next != null. With o2 != null, o is the sum of a K-split GEMM's
+// partial products o + o2[0] + ... + o2[n2 - 1] (planes pstride apart, in
+// that order). scale is EmbeddingGemma 2's layer scalar after its
+// per-layer-input block (embed.go:367-370), else 1.
 template <int NC>
 __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restrict__ o, const float* __restrict__ o2,
+                                                            int n2, int64_t pstride,
                                                             float* __restrict__ x, float* __restrict__ xn,
                                                             int64_t rows, const float* __restrict__ g_post,
                                                             const float* __restrict__ g_next, float eps,
                                                             float scale) {
   int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // one wave per row
   if (row >= rows) return;
-  residual_norm_row<NC>(o, o2, x, xn, row, g_post, g_next, eps, scale, threadIdx.x & 63);
+  residual_norm_row<NC>(o, o2, n2, pstride, x, xn, row, g_post, g_next, eps, scale, threadIdx.x & 63);
 }
 
 // Per (token, head): RMSNorm over D (256 or 512) with the head's gain vector
@@ -164,9 +166,13 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const float* __restr
 // 4 per lane per 256: at D=256 the rotation partner of element i (< 128) is
 // i+128, held by lane+32; at D=512 the partner of i (< 256) is i+256, held
 // by the same lane. Block = one token: waves 0..H-1 are the query heads,
-// H..H+Hkv-1 the keys, then the values.
+// H..H+Hkv-1 the keys, then the values. With qkv2 != null the q|k|v product
+// was split in K and qkv2 holds its second part (same layout): every head,
+// the values included, is the sum qkv + qkv2 (in that order), written back
+// to qkv (the values unnormed unless norm_v).
 template <int D>
-__global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qkv, int64_t rows, int H, int Hkv,
+__global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qkv, const float* __restrict__ qkv2,
+                                                          int64_t rows, int H, int Hkv,
                                                           const float* __restrict__ gq, const float* __restrict__ gk,
                                                           float eps, const int32_t* __restrict__ pos,
                                                           const float* __restrict__ cs, const float* __restrict__ sn,
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   const int64_t row = blockIdx.x;
   const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= rows || head >= H + Hkv + (norm_v ? Hkv : 0)) return;
+  if (row >= rows || head >= H + Hkv + (norm_v || qkv2 ? Hkv : 0)) return;
   const int width = (H + 2 * Hkv) * D;
   float* p = qkv + row * width + (int64_t)head * D;
   // every load is issued before the reduction: the head's values, its gains
@@ -185,6 +191,19 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   const bool rot = head < H + Hkv;
 #pragma unroll
   for (int c = 0; c < NQ; c++) v[c] = *reinterpret_cast<const f32x4*>(p + c * 256 + lane * 4);
+  if (qkv2) {
+    const float* p2 = qkv2 + row * width + (int64_t)head * D;
+#pragma unroll
+    for (int c = 0; c < NQ; c++) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(p2 + c * 256 + lane * 4);
+      v[c].x = v[c].x + w.x; v[c].y = v[c].y + w.y; v[c].z = v[c].z + w.z; v[c].w = v[c].w + w.w;
+    }
+    if (!rot && !norm_v) {  // a value head: the sum only
+#pragma unroll
+      for (int c = 0; c < NQ; c++) *reinterpret_cast<f32x4*>(p + c * 256 + lane * 4) = v[c];
+      return;
+    }
+  }
   if (rot) {
 #pragma unroll
     for (int c = 0; c < NQ; c++) gg[c] = *reinterpret_cast<const f32x4*>(g + c * 256 + lane * 4);
@@ -568,8 +587,9 @@ int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_
 
 int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64_t rows, int32_t d,
                          const float* g_post, const float* g_next, float eps, hipStream_t s, const float* o2,
-                         float scale) {
+                         float scale, int n2, int64_t pstride) {
   if (rows == 0) return FA_OK;
+  if (o2 && (n2 < 1 || n2 > 3)) return set_error(ctx, FA_ERR_ARG, "residual norm: %d extra K parts (1..3)", n2);
   // a short batch (C1: 128 rows) takes one row per workgroup, spread over
   // four times the CUs: every launch of this chain of small kernels is
   // latency, 1 % of C1's forward; from four rows per CU on, four per
@@ -578,10 +598,10 @@ int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64
   const int per = rows <= 4LL * cus ? 1 : 4;
   dim3 grid(blocks_for(rows, per)), block(64 * per);
   switch (d) {
-    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
-    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
-    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
-    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, o2, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 256: hipLaunchKernelGGL(residual_norm_kernel<1>, grid, block, 0, s, o, o2, n2, pstride, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 512: hipLaunchKernelGGL(residual_norm_kernel<2>, grid, block, 0, s, o, o2, n2, pstride, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 768: hipLaunchKernelGGL(residual_norm_kernel<3>, grid, block, 0, s, o, o2, n2, pstride, x, xn, rows, g_post, g_next, eps, scale); break;
+    case 1024: hipLaunchKernelGGL(residual_norm_kernel<4>, grid, block, 0, s, o, o2, n2, pstride, x, xn, rows, g_post, g_next, eps, scale); break;
     default: return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: hidden size %d not in {256,512,768,1024}", d);
   }
   FA_CHECK_LAUNCH(ctx);
@@ -590,17 +610,17 @@ int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64
 
 int launch_qknorm_rope(fa_ctx* ctx, float* qkv, int64_t rows, int32_t H, int32_t Hkv, int32_t D, const float* gq,
                        const float* gk, float eps, const int32_t* d_pos, const float* cos_t, const float* sin_t,
-                       hipStream_t s, bool norm_v) {
+                       hipStream_t s, bool norm_v, const float* qkv2) {
   if (D != 256 && D != 512) return set_error(ctx, FA_ERR_UNSUPPORTED, "gemma: head_dim %d not 256 or 512", D);
   if (rows == 0) return FA_OK;
-  const int heads = H + Hkv + (norm_v ? Hkv : 0);
+  const int heads = H + Hkv + (norm_v || qkv2 ? Hkv : 0);
   dim3 grid((unsigned)rows, (unsigned)((heads + 3) / 4)), block(256);
   if (D == 256)
-    hipLaunchKernelGGL(qknorm_rope_kernel<256>, grid, block, 0, s, qkv, rows, H, Hkv, gq, gk, eps, d_pos, cos_t,
-                       sin_t, norm_v ? 1 : 0);
+    hipLaunchKernelGGL(qknorm_rope_kernel<256>, grid, block, 0, s, qkv, qkv2, rows, H, Hkv, gq, gk, eps, d_pos,
+                       cos_t, sin_t, norm_v ? 1 : 0);
   else
-    hipLaunchKernelGGL(qknorm_rope_kernel<512>, grid, block, 0, s, qkv, rows, H, Hkv, gq, gk, eps, d_pos, cos_t,
-                       sin_t, norm_v ? 1 : 0);
+    hipLaunchKernelGGL(qknorm_rope_kernel<512>, grid, block, 0, s, qkv, qkv2, rows, H, Hkv, gq, gk, eps, d_pos,
+                       cos_t, sin_t, norm_v ? 1 : 0);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
