@@ -684,11 +684,16 @@ void launch_x3(GemmParams p, hipStream_t s) {
 // on timing) and the workgroup's threads apply the epilogue. With K split
 // across grid.y (p.ksplit > 1) each part writes its partial product to
 // c + part * c_split without epilogue, as gemm_x3_kernel does.
+// NB = 1 (GeGLU only): a 32 x 32 tile holding 16 features, its columns
+// 0-15 the gate and 16-31 the up rows of those features (the weight's
+// 32-row gate and up groups, read half a group at a time): twice the
+// workgroups of the 32 x 64 tile, each loading half the weight columns.
 constexpr int kSmallNW = 8;
 
-template <int NW, Epi EPI>
+template <int NW, Epi EPI, int NB = 2>
 __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) float red[NW][2][16][64];
+  static_assert(NB == 2 || (NB == 1 && EPI == Epi::GeGLU), "narrow tiles: GeGLU only");
+  __shared__ __attribute__((aligned(16))) float red[NW][NB][16][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -696,7 +701,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
   const float* __restrict__ A = p.a;
   const uint16_t* __restrict__ B = static_cast<const uint16_t*>(p.b);
   const int64_t m0 = (int64_t)(blockIdx.x / p.tiles_n) * 32;
-  const int64_t n0 = (int64_t)(blockIdx.x % p.tiles_n) * 64;
+  const int64_t n0 = (int64_t)(blockIdx.x % p.tiles_n) * 32 * NB;
   const int nk = p.nk / p.ksplit;  // slabs of this K part
   const int s0 = (int)((int64_t)wave * nk / NW), s1 = (int)((int64_t)(wave + 1) * nk / NW);
   const int64_t k_off = (int64_t)blockIdx.y * nk * 32 + (lane >> 5) * 8;
@@ -704,12 +709,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
   // lane l supplies row l%32 of A and column l%32 of each B block, k values
   // 8*(l/32) .. +7 of each 16-wide step (the bijection of gemm_x3_kernel)
   const float* arow = A + min(m0 + (lane & 31), M - 1) * p.lda + k_off;
-  const uint16_t* brow0 = B + min(n0 + (lane & 31), N - 1) * p.ldb + k_off;
+  // NB = 1: features f0 .. f0 + 15 (f0 = n0 / 2), gate rows in lanes 0-15,
+  // up rows (32 further) in lanes 16-31
+  const int64_t brow_n = NB == 2 ? n0 + (lane & 31)
+                                 : (n0 / 64) * 64 + (n0 / 2) % 32 + (lane & 15) + ((lane & 16) ? 32 : 0);
+  const uint16_t* brow0 = B + min(brow_n, N - 1) * p.ldb + k_off;
   const uint16_t* brow1 = B + min(n0 + 32 + (lane & 31), N - 1) * p.ldb + k_off;
 
-  f32x16 acc[2];
+  f32x16 acc[NB];
 #pragma unroll
-  for (int j = 0; j < 2; j++)
+  for (int j = 0; j < NB; j++)
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[j][r] = 0.f;
 
@@ -717,7 +726,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
   // vector of each B block
   struct Regs {
     f32x4 a[4];
-    u32x4 b[4];
+    u32x4 b[2 * NB];
   };
   auto load = [&](Regs& g, int kt) {
     const int64_t o = (int64_t)kt * 32;
@@ -725,8 +734,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
     for (int st = 0; st < 2; st++) {
       g.a[2 * st] = *reinterpret_cast<const f32x4*>(arow + o + 16 * st);
       g.a[2 * st + 1] = *reinterpret_cast<const f32x4*>(arow + o + 16 * st + 4);
-      g.b[2 * st] = *reinterpret_cast<const u32x4*>(brow0 + o + 16 * st);
-      g.b[2 * st + 1] = *reinterpret_cast<const u32x4*>(brow1 + o + 16 * st);
+      g.b[NB * st] = *reinterpret_cast<const u32x4*>(brow0 + o + 16 * st);
+      if constexpr (NB == 2) g.b[2 * st + 1] = *reinterpret_cast<const u32x4*>(brow1 + o + 16 * st);
     }
   };
   auto compute = [&](const Regs& g) {
@@ -747,13 +756,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
                                                  pack_hi16(m[4], m[5]), pack_hi16(m[6], m[7])});
       oa[2] = __builtin_bit_cast(bf16x8, (u32x4){pack_hi16(l[0], l[1]), pack_hi16(l[2], l[3]),
                                                  pack_hi16(l[4], l[5]), pack_hi16(l[6], l[7])});
-      const bf16x8 b0 = __builtin_bit_cast(bf16x8, g.b[2 * st]);
-      const bf16x8 b1 = __builtin_bit_cast(bf16x8, g.b[2 * st + 1]);
       // smallest terms first, as gemm_x3_kernel
 #pragma unroll
       for (int t = 2; t >= 0; t--) {
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t], b0, acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t], b1, acc[1], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[t], __builtin_bit_cast(bf16x8, g.b[NB * st + j]),
+                                                           acc[j], 0, 0, 0);
       }
     }
   };
@@ -777,7 +786,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
     }
   }
 #pragma unroll
-  for (int j = 0; j < 2; j++)
+  for (int j = 0; j < NB; j++)
 #pragma unroll
     for (int r = 0; r < 16; r++) red[wave][j][r][lane] = acc[j][r];
   __syncthreads();
@@ -785,7 +794,25 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
   // C element (j, r, l): row 8*(r/4) + 4*(l/32) + r%4, column 32*j + l%32
   GemmParams q = p;
   if (p.ksplit > 1) q.c = p.c + blockIdx.y * p.c_split;
-  if constexpr (EPI == Epi::GeGLU) {
+  if constexpr (EPI == Epi::GeGLU && NB == 1) {
+    // gate in columns 0-15 (lanes l % 32 < 16), up 16 columns further
+    const int64_t F = N / 2;
+    for (int e = tid; e < 16 * 32; e += NW * 64) {
+      const int r = e >> 5, lq = e & 31;
+      const int l = (lq & 15) | ((lq & 16) << 1);
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) {
+        g += red[w][0][r][l];
+        u += red[w][0][r][l + 16];
+      }
+      const int64_t row = m0 + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
+      const int64_t fcol = n0 / 2 + (l & 15);
+      if (row < M && fcol < F) p.c[row * p.ldc + fcol] = gelu_tanh_ref(g) * u;
+    }
+    return;
+  }
+  if constexpr (EPI == Epi::GeGLU && NB == 2) {
     if (p.ksplit == 1) {
       // gate block 0 and up block 1 hold the same 32 features
       const int64_t F = N / 2;
@@ -795,7 +822,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
 #pragma unroll
         for (int w = 0; w < NW; w++) {
           g += red[w][0][r][l];
-          u += red[w][1][r][l];
+          u += red[w][NB - 1][r][l];
         }
         const int64_t row = m0 + (r >> 2) * 8 + (l >> 5) * 4 + (r & 3);
         const int64_t fcol = n0 / 2 + (l & 31);
@@ -804,7 +831,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
       return;
     }
   }
-  for (int e = tid; e < 2 * 16 * 64; e += NW * 64) {
+  for (int e = tid; e < NB * 16 * 64; e += NW * 64) {
     const int j = e >> 10, r = (e >> 6) & 15, l = e & 63;
     float v = 0.f;
 #pragma unroll
@@ -816,12 +843,33 @@ __global__ __launch_bounds__(NW * 64) void gemm_x3_small_kernel(GemmParams p) {
   }
 }
 
+// Narrow GeGLU tiles (16 features) while they fit one per CU
+// (FA_SMALL_NARROW=0 turns them off): gate|up at 64 rows (144 narrow
+// tiles), 11.4 -> 9.7 us per launch, 1.17 -> 1.12 ms per forward on
+// MI355X; at 128 rows (288 narrow tiles, a second round on some CUs)
+// 11.3 -> 13.6 us, so the 32 x 64 tiles stay there.
+static bool small_narrow(const GemmParams& p, int cus) {
+  static const bool on = [] {
+    const char* e = std::getenv("FA_SMALL_NARROW");
+    return !(e && e[0] == '0');
+  }();
+  return on && p.ksplit == 1 && p.n % 64 == 0 && ((p.m + 31) / 32) * (p.n / 32) <= cus;
+}
+
 template <Epi EPI>
-void launch_x3_small(GemmParams p, hipStream_t s) {
+void launch_x3_small(GemmParams p, hipStream_t s, int cus = 256) {
   p.tiles_m = (int)((p.m + 31) / 32);
-  p.tiles_n = (int)((p.n + 63) / 64);
   p.nk = (int)(p.k / 32);
   if (p.ksplit < 1) p.ksplit = 1;
+  if constexpr (EPI == Epi::GeGLU) {
+    if (small_narrow(p, cus)) {
+      p.tiles_n = (int)(p.n / 32);
+      dim3 grid(p.tiles_m * p.tiles_n, 1), block(kSmallNW * 64);
+      hipLaunchKernelGGL((gemm_x3_small_kernel<kSmallNW, EPI, 1>), grid, block, 0, s, p);
+      return;
+    }
+  }
+  p.tiles_n = (int)((p.n + 63) / 64);
   dim3 grid(p.tiles_m * p.tiles_n, p.ksplit), block(kSmallNW * 64);
   hipLaunchKernelGGL((gemm_x3_small_kernel<kSmallNW, EPI>), grid, block, 0, s, p);
 }
@@ -956,13 +1004,13 @@ void dispatch_x3_epi(const GemmParams& p, Epi epi, hipStream_t s) {
   }
 }
 
-void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s) {
+void dispatch_x3(XTileId t, const GemmParams& p, Epi epi, hipStream_t s, int cus = 256) {
   switch (t) {
     case XTileId::small:
       switch (epi) {
-        case Epi::None: launch_x3_small<Epi::None>(p, s); break;
-        case Epi::Generic: launch_x3_small<Epi::Generic>(p, s); break;
-        case Epi::GeGLU: launch_x3_small<Epi::GeGLU>(p, s); break;
+        case Epi::None: launch_x3_small<Epi::None>(p, s, cus); break;
+        case Epi::Generic: launch_x3_small<Epi::Generic>(p, s, cus); break;
+        case Epi::GeGLU: launch_x3_small<Epi::GeGLU>(p, s, cus); break;
       }
       break;
     case XTileId::x128x64v: dispatch_x3_epi<X128x64v>(p, epi, s); break;
@@ -1215,7 +1263,7 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t s) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     XTileId t = (XTileId)forced_xtile();
     if ((int)t < 0 || (g.epi == Epi::GeGLU && !x3_has_geglu(t))) t = pick_xtile(g.m, g.n, g.k, p.ksplit, g.epi, cus, g.shared);
-    dispatch_x3(t, p, g.epi, s);
+    dispatch_x3(t, p, g.epi, s, cus);
   } else if (fast) {
     TileId t = (TileId)forced_tile();
     if ((int)t < 0 || (g.epi == Epi::GeGLU && t == TileId::k64x64))
