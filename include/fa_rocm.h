@@ -41,6 +41,13 @@
  *   FA_MICROBATCH=0|<rows>      micro-batches off / from this many tokens (2048)
  *   FA_MICROBATCH_GROUPS=2..4   force the micro-batch count
  *   FA_ATTN_KEY_PARTS=1..8      force the key runs of the short-batch attention
+ *   FA_ATTN_ROWS=64|128         force the tile attention's rows per work item
+ *   FA_ATTN_PAIRS=0             64-row tile items on four single waves instead of
+ *                               eight waves in head-dimension pairs
+ *   FA_ATTN_XCD=1|0             force the XCD-local attention item order on / off
+ *   FA_SMALL_KSPLIT=2           two (not four) K parts for a few-row batch's o/down
+ *   FA_QKV_KSPLIT=1             no K split of a few-row batch's q|k|v product
+ *   FA_SMALL_NARROW=0           no 16-feature tiles for the few-row gate|up product
  */
 #ifndef FA_ROCM_H
 #define FA_ROCM_H
