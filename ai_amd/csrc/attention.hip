@@ -813,14 +813,11 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
       __builtin_amdgcn_sched_barrier(0);  // no code motion between the two halves (register pressure)
       iter(tt + 1, Vs0, Vs1);
     }
-    if (tt < te) {
-      iter(tt, Vs1, Vs0);
-      dl_barrier<0x0F70>();  // V(te-1) landed everywhere
-      pv(Vs1, pb0, pb1, pb2);
-    } else {
-      dl_barrier<0x0F70>();
-      pv(Vs0, pb0, pb1, pb2);
-    }
+    if (tt < te) iter(tt, Vs1, Vs0);
+    dl_barrier<0x0F70>();  // V(te-1) landed everywhere
+    // the last tile's values: one P.V for either parity (no loads follow,
+    // so the buffer need not be named statically here)
+    pv(((te - 1 - tb) & 1) ? Vs1 : Vs0, pb0, pb1, pb2);
   }
 
   const float l_tot = rows4_sum(l_part);
