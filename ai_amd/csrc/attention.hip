@@ -528,13 +528,30 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     }
   };
 
+  // The first tile's key image: issued whole by the second wave of each
+  // SIMD (waves TL_W/2 ..) before anything else. Those waves get their q
+  // rows after the first waves' anyway (the CU's memory pipeline serves
+  // the first waves' loads first), so the image lands while the first
+  // waves prepare q, and no wave's q wait covers it but theirs. A run
+  // without tiles loads the last tile of the range and waits for it
+  // before the exit.
+  const bool k_first = wave >= TL_W / 2;
+  if (k_first) {
+    const uint16_t* src = img0 + min(tb, te - 1) * tstride;
+#pragma unroll
+    for (int j = 0; j < 96 / TL_W; j++) {
+      const int c = (wave - TL_W / 2) + (TL_W / 2) * j;
+      __builtin_amdgcn_global_load_lds(src + c * 512 + lane * 8, (__attribute__((address_space(3))) void*)&Ks[c * 512],
+                                       16, 0, 0);
+    }
+  }
+
   if (rb + 16 * rbw >= nrows) {
     // every row of this wave lies past the sequence's rows (the last item
     // of a sequence): the wave issues its share of each image load and
     // takes part in every barrier of the loop below, in the same order,
     // and computes nothing
     if (tb < te) {
-      issue(img0 + tb * tstride, Ks);
       for (int tt = tb; tt < te; tt++) {
         dl_barrier<0x0F70>();
         issue(img0 + tt * tstride + TL_IMG, ((tt - tb) & 1) ? Vs1 : Vs0);
@@ -543,6 +560,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
       }
       dl_barrier<0x0F70>();
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): a first image issued above
     return;
   }
 
@@ -799,7 +817,6 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     }
   };
   if (tb < te) {
-    issue(img0 + tb * tstride, Ks);
     {
       f32x4 sacc[2];
       front(tb, Vs0, sacc);
@@ -818,6 +835,8 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     // the last tile's values: one P.V for either parity (no loads follow,
     // so the buffer need not be named statically here)
     pv(((te - 1 - tb) & 1) ? Vs1 : Vs0, pb0, pb1, pb2);
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first image issued above
   }
 
   const float l_tot = rows4_sum(l_part);
