@@ -169,19 +169,24 @@ void plan_items(const AttnPlanIn& in, AttnPlan& p, int32_t* items, std::vector<i
           for (int q0 = 0; q0 < rows_b; q0 += istep)
             for (int h = 0; h < iheads; h++) plain.push_back(b);
         }
-        const int slots = in.cus;
-        const double span_plain = launch_span(n, slots, [&](int64_t i) { return cost_of(plain[i]); });
-        const double span_xcd =
-            launch_span(n, slots, [&](int64_t i) { return cost_of((int)(q[i % kXcds][i / kXcds] >> 32)); });
         // and only for long key loops (a group's mean length at least 12
         // key tiles of 32): C3's 512-token sequences -1.7 % per forward
         // (attention -4 %), while C2's micro-batches (mean 172 tokens) ran
         // 0.7 % slower with the XCD-local order and C5 (mean 72) equal,
         // though it cut the C2 launch's HBM fetch of the images 2.7 times
+        // (the spans are estimated only where that rule leaves a choice)
         int64_t keys_sum = 0;
         for (int b : order) keys_sum += in.lengths[b];
         const bool long_keys = keys_sum >= 384LL * (int64_t)order.size();
-        const bool local = in.forced_xcd ? in.forced_xcd > 0 : long_keys && span_xcd <= 1.03 * span_plain;
+        bool local = long_keys;
+        if (long_keys && !in.forced_xcd) {
+          const int slots = in.cus;
+          const double span_plain = launch_span(n, slots, [&](int64_t i) { return cost_of(plain[i]); });
+          const double span_xcd =
+              launch_span(n, slots, [&](int64_t i) { return cost_of((int)(q[i % kXcds][i / kXcds] >> 32)); });
+          local = span_xcd <= 1.03 * span_plain;
+        }
+        if (in.forced_xcd) local = in.forced_xcd > 0;
         for (int64_t i = 0; i < n; i++) {
           if (local) {
             const int64_t e = q[i % kXcds][i / kXcds];
