@@ -41,22 +41,37 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
   }
   for (int l = 0; l < in.n_run; l++) (p.layer_tiles(in.layer_D[l]) ? p.any_tiles : p.any_var) = true;
   p.Gt = p.any_tiles ? in.H / p.hkv_t : 1;
-  // Tile items of eight waves (128 rows); of four (64 rows) when the batch
+  // Tile items of 128 rows (eight waves); of 64 rows (waves_t = 4: eight
+  // waves in head-dimension pairs, or four single waves) when the batch
   // runs as micro-batches and its 128-row items would fill more than half
   // a round of the CUs but at most 0.6 of one: twice the items, each with
   // half the rows and the same key loop, still about one round, shorten
   // the attention's link in every group's chain of dependent launches (on
-  // one stream the launch's own time decides: 49.0 µs with eight waves,
-  // 50.7 with four at C2). Measured per forward on MI355X (256 CUs),
-  // eight vs four waves: C2 (143 items of 128 rows) 5.22 vs 5.11 ms; 36 x
+  // one stream the launch's own time decides: at C2 1.19 ms of attention
+  // per forward with 128-row items, 1.22 with 64-row pairs). Measured per
+  // forward on MI355X (256 CUs), 128- vs 64-row items (then four single
+  // waves): C2 (143 items of 128 rows) 5.22 vs 5.11 ms; 36 x
   // 160 tokens (144 items) 5.09 vs 5.00; 40 x 160 (160) 5.61 vs 5.65; 48 x
   // 160 (192) 6.34 vs 6.49; EmbeddingGemma 2 at C2 (202) 4.15 vs 4.17; C3,
   // C4, C5 (from 271 items) 4-9 % slower with four. Below half a round the
   // key runs spread the work instead.
+  // On one stream with at most half a round of 128-row items (the key runs'
+  // regime), 64-row items on eight waves in head-dimension pairs win while
+  // the sequences stay under 1 536 tokens (MI355X, per forward: 1 025
+  // tokens -5.6 %, one 1 100-token sequence -4.3 %, 8 x 160 -8.5 %, 5 x 300
+  // -7.4 %, 3 x 512 -2.9 %, 3 x 600 -1.2 %, 6 x 200 + 100 -10 %): twice
+  // the items fill more CUs, each with two waves per SIMD. One 2 048-token
+  // sequence loses 2 % (its items' key runs halve: 2 of 32 tiles instead of
+  // 5 of 13), so it keeps 128-row items.
   if (p.any_tiles) {
     int64_t n8 = 0;
-    for (int b = 0; b < in.B; b++) n8 += ((int64_t)p.Gt * in.lengths[b] + 127) / 128 * p.hkv_t;
+    int max_len = 0;
+    for (int b = 0; b < in.B; b++) {
+      n8 += ((int64_t)p.Gt * in.lengths[b] + 127) / 128 * p.hkv_t;
+      max_len = std::max(max_len, (int)in.lengths[b]);
+    }
     if (in.groups > 1 && 2 * n8 > in.cus && 5 * n8 <= 3LL * in.cus) p.waves_t = 4;
+    if (in.groups == 1 && 2 * n8 <= in.cus && max_len < 1536) p.waves_t = 4;
     if (in.forced_rows) p.waves_t = in.forced_rows / 16;
   }
   const int istep_t = 16 * p.waves_t;

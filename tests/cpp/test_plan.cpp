@@ -209,6 +209,22 @@ TEST(TestTileWaves) {
   check_items(c);
 }
 
+// one stream, at most half a round of 128-row items, sequences under 1 536
+// tokens: 64-row items (waves_t 4), key runs by the doubled item count
+TEST(TestOneStreamFewItems) {
+  Case c;
+  c.lengths = {1100};  // 26 items of 128 rows -> 52 of 64
+  run(c, eg300m(), 1);
+  if (c.p.waves_t != 4 || c.p.n_items_t != 52 || c.p.kparts_t != 4)
+    FATAL("waves %d items %lld key runs %d, want 4, 52, 4", c.p.waves_t, (long long)c.p.n_items_t, c.p.kparts_t);
+  check_items(c);
+  Case d;
+  d.lengths = repeat(8, 160);  // 32 items of 128 rows
+  run(d, eg300m(), 1);
+  if (d.p.waves_t != 4 || d.p.n_items_t != 64) FATAL("8 x 160: waves %d items %lld", d.p.waves_t, (long long)d.p.n_items_t);
+  check_items(d);
+}
+
 // one long sequence: 48 items of 128 rows, keys cut into 5 runs of 12-13 tiles
 TEST(TestTileKeyRuns) {
   Case c;
