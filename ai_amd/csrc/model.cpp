@@ -256,6 +256,17 @@ int qkv_ksplit() {
   return v;
 }
 
+// FA_TILE_MIN_ROWS=<tokens>: the tile attention from more tokens than this
+// (tuning; 1 024 when unset).
+int64_t tile_min_rows() {
+  static const int64_t v = [] {
+    const char* e = std::getenv("FA_TILE_MIN_ROWS");
+    if (!e) return (int64_t)1024;
+    return (int64_t)std::max(0LL, std::atoll(e));
+  }();
+  return v;
+}
+
 // FA_MICROBATCH_GROUPS=<2..4> forces the group count (tuning); 0 when unset.
 int microbatch_count_forced() {
   static const int v = [] {
@@ -860,6 +871,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   pin.forced_key_parts = fa::attention_key_parts_forced();
   pin.forced_rows = fa::attention_rows_forced();
   pin.forced_xcd = fa::attention_xcd_forced();
+  pin.tile_min_rows = fa::tile_min_rows();
   fa::AttnPlan ap;
   fa::plan_attention(pin, ap);
   const int64_t n_items_t = ap.n_items_t, n_items = ap.n_items_t + ap.n_items_v, n_tiles = ap.n_tiles;

@@ -28,12 +28,20 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
   for (int b = 0; b < in.B; b++) p.M += in.lengths[b];
   // Layers with head_dim 256 (every EmbeddingGemma layer, EmbeddingGemma
   // 2's sliding layers) take the split-bf16 tile attention, from 1 025
-  // tokens with at least 32 per sequence on average (batches of shorter
-  // sequences keep the fp32 kernel's 16-key tiles: a 32-key tile would be
-  // mostly padding). The tile layers share one kv head count (the item
-  // rows and image slots depend on it); a model whose head_dim-256 layers
-  // differ in it keeps the fp32 kernel.
-  p.tiles_ok = p.M > in.split_rows && p.M >= 32LL * in.B;
+  // tokens, or from 448·1 024 query-key pairs per head (sum of L^2) in a
+  // smaller batch, with at least 32 tokens per sequence on average
+  // (batches of shorter sequences keep the fp32 kernel's 16-key tiles: a
+  // 32-key tile would be mostly padding). Below 1 025 tokens the pairs
+  // decide (MI355X, per forward, tile vs fp32 kernel): 2 x 512 tokens
+  // 2.30 vs 2.56 ms, 768 + 200 2.33 vs 2.65, one 768-token sequence 2.18
+  // vs 2.30, one 1 000-token sequence 2.37 vs 2.73; but 640 tokens 2.08 vs
+  // 2.06, 2 x 384 2.13 vs 2.08, 5 x 200 2.30 vs 2.14, 4 x 128 1.87 vs 1.67.
+  // The tile layers share one kv head count (the item rows and image slots
+  // depend on it); a model whose head_dim-256 layers differ in it keeps the
+  // fp32 kernel.
+  double pairs = 0;
+  for (int b = 0; b < in.B; b++) pairs += (double)in.lengths[b] * in.lengths[b];
+  p.tiles_ok = (p.M > in.tile_min_rows || pairs >= (double)in.tile_min_pairs) && p.M >= 32LL * in.B;
   for (int l = 0; l < in.n_layers; l++) {
     if (in.layer_D[l] != 256) continue;
     if (p.hkv_t && in.layer_Hkv[l] != p.hkv_t) p.mixed_hkv = true;

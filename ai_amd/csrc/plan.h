@@ -36,6 +36,8 @@ struct AttnPlanIn {
   int forced_key_parts = 0;          // tuning: key runs forced (0: chosen)
   int forced_rows = 0;               // tuning: tile item rows forced, 64 or 128 (0: chosen)
   int forced_xcd = 0;                // tuning: XCD-local item order forced on (1) or off (-1)
+  int64_t tile_min_rows = 1024;      // the tile attention from more tokens than this,
+  int64_t tile_min_pairs = 458752;   // or from this many query-key pairs per head (sum L^2)
 };
 
 struct AttnPlan {

@@ -244,8 +244,9 @@ TEST(TestShortSequencesFP32) {
   check_items(c);
 }
 
-// the tile attention's two batch rules at their edges: more than 1 024
-// tokens, and at least 32 per sequence on average
+// the tile attention's batch rules at their edges: more than 1 024 tokens
+// or at least 458 752 query-key pairs per head, and at least 32 tokens per
+// sequence on average
 TEST(TestTilePathBoundaries) {
   struct Edge {
     std::vector<int32_t> lengths;
@@ -254,7 +255,12 @@ TEST(TestTilePathBoundaries) {
   std::vector<int32_t> l1025 = repeat(7, 128), l1055 = repeat(32, 32);
   l1025.push_back(129);
   l1055.push_back(31);
-  const Edge edges[] = {{repeat(8, 128), false}, {l1025, true}, {l1055, false}, {repeat(33, 32), true}};
+  const Edge edges[] = {{repeat(8, 128), false}, {l1025, true}, {l1055, false}, {repeat(33, 32), true},
+                        {{512, 512}, true},    // 524 288 pairs
+                        {{384, 384}, false},   // 294 912
+                        {{640}, false},        // 409 600
+                        {{678}, true},         // 459 684
+                        {{677}, false}};       // 458 329
   for (const Edge& e : edges) {
     for (int want : {1, 3}) {
       Case c;

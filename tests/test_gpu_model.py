@@ -262,8 +262,9 @@ def test_key_split_attention_with_sliding_band(models):
 def test_single_long_sequence_key_runs(models, L):
     """One long sequence (above 1 024 tokens: the split-bf16 tile attention)
     gives fewer work items than CUs, so each item's key tiles are cut into
-    runs summed by attention_combine_kernel (1 100: 26 items, 8 runs of 4-5
-    tiles; 2 048: 48 items, 5 runs). Against the oracle, layer by layer."""
+    runs summed by attention_combine_kernel (1 100: 52 items of 64 rows on
+    head-dimension wave pairs, 4 runs of 8-9 tiles; 2 048: 48 items of 128
+    rows, 5 runs). Against the oracle, layer by layer."""
     gm, om = models
     rng = np.random.default_rng(L)
     ids = rng.integers(3, 262144, (1, L)).astype(np.int32)
@@ -301,6 +302,22 @@ def test_tile_path_boundaries(models, n, L, last):
     ids[:, 0] = 2
     ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
     compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens, group=11), f"{n} sequences, {lens.sum()} tokens")
+
+
+@pytest.mark.parametrize("lengths", [[512, 512], [768, 200], [640]])
+def test_tile_path_by_pairs(models, lengths):
+    """Batches of at most 1 024 tokens take the tile attention when their
+    query-key pairs per head (sum of L^2) reach 458 752: 2 x 512 and 768 +
+    200 on the tiles (one stream, 64-row items, key runs), 640 on the fp32
+    kernel. Every row and three layers' states against the oracle."""
+    gm, om = models
+    rng = np.random.default_rng(sum(lengths))
+    lens = np.array(lengths, np.int32)
+    ids = rng.integers(3, 262144, (len(lengths), int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    compare(gm.embed_ids(ids, lens), om.embed(ids, lens), f"{lengths} (pairs rule)")
+    compare_states(gm, om, ids, lens, sorted({0, len(lengths) - 1}), f"{lengths} states", layers=[1, 12, -1])
 
 
 @pytest.mark.parametrize("lengths", [[1], [1] * 5, [1, 2048, 1, 33]])
