@@ -320,6 +320,27 @@ def test_tile_path_by_pairs(models, lengths):
     compare_states(gm, om, ids, lens, sorted({0, len(lengths) - 1}), f"{lengths} states", layers=[1, 12, -1])
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_batches_across_plan_rules(models, seed):
+    """Seeded random batches (1-12 sequences of 1-700 tokens) that land on
+    either side of the plan's rules: fp32 or tile attention (tokens, pairs,
+    mean length), 64- or 128-row tile items, key runs, the few-row K splits
+    and narrow gate|up tiles, micro-batches from 2 048 tokens. Every row
+    against the oracle."""
+    gm, om = models
+    rng = np.random.default_rng(7000 + seed)
+    B = int(rng.integers(1, 13))
+    lens = rng.integers(1, 701, B).astype(np.int32)
+    if seed % 3 == 0:
+        lens[0] = int(rng.integers(500, 701))  # at least one long sequence
+    ids = rng.integers(3, 262144, (B, int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    print(f"seed {seed}: {B} sequences, {int(lens.sum())} tokens, sum L^2 {int((lens.astype(np.int64) ** 2).sum())}",
+          flush=True)
+    compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens), f"random batch {seed}")
+
+
 @pytest.mark.parametrize("lengths", [[1], [1] * 5, [1, 2048, 1, 33]])
 def test_one_token_sequences(models, lengths):
     """Sequences of a single token (only the BOS id): alone, five in a batch
