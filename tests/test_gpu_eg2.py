@@ -115,9 +115,9 @@ def test_gpu_tile_attention_matches_oracle(eg2, B, T, lo):
     key/value image pass, and the full layers (head_dim 512) the fp32
     kernel: every row against the oracle, and against its own
     single-sequence run (fp32 kernel throughout). Six sequences give under
-    128 items of 128 rows (eight waves, keys cut into runs); twenty give
-    129-153, between half and 0.6 of a round of the 256 CUs (four-wave
-    items)."""
+    128 items of 128 rows on one stream: 64-row items on head-dimension wave
+    pairs, keys cut into runs; twenty give 129-153, between half and 0.6 of
+    a round of the 256 CUs, in micro-batches: 64-row items as well."""
     shape, om, gm = eg2
     ids, lengths = batch(4242 + B, B, T, lo, shape.vocab_size)
     assert int(lengths.sum()) > 1024
