@@ -177,7 +177,7 @@ int launch_gemm(fa_ctx* ctx, const GemmArgs& g, hipStream_t stream);
 bool gemm_f32_mfma_forced();
 
 // K-split factor the encoder uses for its N = hidden products (o, down):
-// FA_GEMM_KSPLIT=1 or 2 (default 2).
+// FA_GEMM_KSPLIT=1 or 2 (default 2); 1 under FA_GEMM_MFMA=f32.
 int gemm_ksplit();
 
 int launch_row_sum_squares(fa_ctx* ctx, const float* x, int64_t m, int64_t n, float* out, hipStream_t s);

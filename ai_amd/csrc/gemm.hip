@@ -1190,6 +1190,7 @@ bool gemm_f32_mfma_forced() { return use_f32_mfma(); }
 
 int gemm_ksplit() {
   static const int v = [] {
+    if (use_f32_mfma()) return 1;  // the fp32-MFMA kernel computes whole K ranges only
     const char* e = std::getenv("FA_GEMM_KSPLIT");
     return (e && std::strcmp(e, "1") == 0) ? 1 : 2;
   }();

@@ -1217,7 +1217,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   // the last dense product splits K (its few rows give few tiles: 3072 -> 768
   // for one pooled row is 12 of them) and the L2 norm adds the partials,
   // unless a Tanh follows it (model.go:296-301, embed.go:415-418: applied in
-  // the product's epilogue, so on the whole sum)
+  // the product's epilogue, so on the whole sum) or K splits are off
   int head_parts = 1;
   for (int i = 0; i < c.n_dense; i++) {
     fa::GemmArgs g;
@@ -1226,7 +1226,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     if (m->dense_act[i] == FA_ACT_TANH) {
       g.epi = fa::Epi::Generic;
       g.act = FA_ACT_TANH;
-    } else if (i + 1 == c.n_dense) {
+    } else if (i + 1 == c.n_dense && ksplit > 1) {
       for (int ks : {4, 2})
         if (cur_w % (32 * ks) == 0 && (int64_t)ks * m->dense_out[i] <= maxw) {
           head_parts = ks;
