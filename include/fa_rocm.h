@@ -37,7 +37,8 @@
  *                               kernel (bf16 weights widened, float32 weights without the
  *                               three-plane rewrite)
  *   FA_ATTN_DENSE=0             fa_attention on the per-row kernel for every head dim
- *   FA_GEMM_KSPLIT=1            no K split of the encoder's N = hidden products
+ *   FA_GEMM_KSPLIT=1            no K-split products in the encoder (also implied by
+ *                               FA_GEMM_MFMA=f32)
  *   FA_MICROBATCH=0|<rows>      micro-batches off / from this many tokens (2048)
  *   FA_MICROBATCH_GROUPS=2..4   force the micro-batch count
  *   FA_ATTN_KEY_PARTS=1..8      force the key runs of the short-batch attention
