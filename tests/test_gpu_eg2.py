@@ -108,6 +108,24 @@ def test_gpu_matches_oracle(eg2, B, T, lo):
     assert np.allclose(np.linalg.norm(got, axis=1), 1, atol=1e-5)
 
 
+@pytest.mark.parametrize("B,T", [(3, 400), (2, 512)])
+def test_gpu_few_sequences_tile_items(eg2, B, T):
+    """A few long sequences on one stream: 3 x 400 tokens (more than 1 024)
+    and 2 x 512 (524 288 query-key pairs per head) take the tile attention
+    on the sliding layers, as 64-row items on head-dimension wave pairs
+    with their keys cut into runs (two kv heads); the full layers keep the
+    fp32 kernel. Every row against the oracle."""
+    shape, om, gm = eg2
+    ids, lengths = batch(5150 + B * T, B, T, T, shape.vocab_size)
+    got = gm.embed_ids(ids, lengths)
+    want = om.embed(ids, lengths)
+    c = cos_rows(got, want)
+    d = np.abs(got - want).max()
+    print(f"EG2 {B} x {T}: cosine {c.min():.9f}, max|d| {d:.3g}", flush=True)
+    assert c.min() >= 0.9999999
+    assert d <= 5e-5
+
+
 @pytest.mark.parametrize("B,T,lo", [(6, 300, 150), (20, 256, 150)])
 def test_gpu_tile_attention_matches_oracle(eg2, B, T, lo):
     """Over 1 024 tokens (32 or more per sequence) the sliding layers
