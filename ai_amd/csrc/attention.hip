@@ -370,11 +370,12 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 //
 // Rows. The query rows of kv head hk are the pairs (token t, query head
 // hk*G + g) of the G = H/Hkv heads that share it, numbered r = t*G + g. A
-// work item is (sequence, 16 W consecutive rows, hk[, run of key tiles]);
-// its W waves (8, or 4 for some batches) own 16 rows each, so one
-// key/value tile in LDS serves every query head of the group (and a short
-// sequence fills an item's rows G times sooner than with one head per
-// item).
+// work item is (sequence, 128 or 64 consecutive rows, hk[, run of key
+// tiles]); its waves own 16 rows each (eight waves for 128 rows; for 64
+// rows eight waves in pairs that split the head dimension, or four), so
+// one key/value tile in LDS serves every query head of the group (and a
+// short sequence fills an item's rows G times sooner than with one head
+// per item).
 //
 // Operands. Keys and values arrive as LDS images written once per layer by
 // kv_tiles_kernel: per (tile of 32 keys of one sequence, kv head) a key
@@ -382,8 +383,9 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return *reinterpret_cast<
 // a value image [term][dim][32 slots] whose slot 8g + 4h + r holds key 16h +
 // 4g + r (chunk g of dim d at position g ^ ((d >> 1) & 3)); 48 KB each,
 // copied to LDS unchanged by direct global->LDS loads (1 KB per wave
-// instruction). One key buffer and two value buffers: 144 KB, one
-// workgroup per CU (two waves per SIMD with eight waves, one with four).
+// instruction). One key buffer and two value buffers: 144 KB (160 KB with
+// the wave pairs' partial-score exchange), one workgroup per CU (two waves
+// per SIMD with eight waves, one with four).
 //
 // Formulation (lane l: lq = l % 16, g = l / 16). The q terms stay in
 // registers: lane l holds row lq's dims 32c + 8g .. +7 (c = 0..7), three
