@@ -321,7 +321,8 @@ struct AttnTilesArgs {
   const float* gq = nullptr;
   float eps = 0.f;
   const float *cos_t = nullptr, *sin_t = nullptr;
-  // waves per work item, 4 or 8 (items of attention_tiles_rows(waves) rows)
+  // 16-row blocks per work item, 4 or 8 (64 or 128 rows; 64-row items run
+  // on eight waves in head-dimension pairs unless FA_ATTN_PAIRS=0)
   int32_t waves = 8;
 };
 // d_items holds n_items triples (sequence, first row, kv head): one item per

@@ -47,7 +47,7 @@ struct AttnPlan {
   bool any_tiles = false, any_var = false;  // some run layer takes each path
   int hkv_t = 0;                      // kv heads of the tile layers
   int Gt = 1;                         // query heads per kv head of the tile layers
-  int waves_t = 8;                    // waves per tile item (rows: 16 per wave)
+  int waves_t = 8;                    // 16-row blocks per tile item: 8 (128 rows) or 4 (64 rows)
   int kparts_t = 1, kparts_v = 1;     // key runs per tile item, per fp32 item
   int64_t n_items_t = 0, n_items_v = 0;
   int64_t n_tiles = 0;                // key tiles over the batch (tile layers)
