@@ -27,7 +27,17 @@ __device__ __forceinline__ float tanh_ref(float v) {
   q = fmaf(q, v2, 1.18534705686654e-04f);
   q = fmaf(q, v2, 2.26843463243900e-03f);
   q = fmaf(q, v2, 4.89352518554385e-03f);
-  float r = p / q;
+  // p / q from the hardware reciprocal: one Newton step on 1/q, then one
+  // correction of the quotient (p - q r is exact in an fma). q lies in
+  // [4.9e-3, 0.95] and |p| < q, so no scaling or special case applies, and
+  // the result equals the correctly rounded quotient: checked on 2 million
+  // points of the clamped range with the reciprocal off by up to one unit
+  // in the last place either way. Six VALU instructions instead of the
+  // general division's ten (v_div_scale, v_div_fmas, v_div_fixup).
+  float rq = __builtin_amdgcn_rcpf(q);
+  rq = fmaf(fmaf(-q, rq, 1.f), rq, rq);
+  float r = p * rq;
+  r = fmaf(fmaf(-q, r, p), rq, r);
   r = v >= 9.f ? 1.f : r;
   r = v <= -9.f ? -1.f : r;
   return (v > -0.0004f && v < 0.0004f) ? v : r;
