@@ -476,6 +476,9 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   constexpr int HD = 256;
   constexpr int NC = HD / 32 / DS;    // q chunks of 32 dims per wave
   constexpr int NDB = HD / 16 / DS;   // blocks of 16 O dims per wave
+  // operand reads one step ahead of the MFMAs that use them (12 more
+  // VGPRs): the wave pairs' kernel has the registers to spare
+  constexpr bool TL_PF = DS == 2;
   constexpr int TERM = TL_IMG / 3;  // bf16 per term of an image
   __shared__ __attribute__((aligned(16))) uint16_t Ks[TL_IMG];
   __shared__ __attribute__((aligned(16))) uint16_t Vs0[TL_IMG];
@@ -635,37 +638,89 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     khi = min(L, tok + p.window);
   }
 
+  // The six term products of one 16-key block and one 32-dim chunk, in a
+  // fixed order (smallest terms first), accumulated into s.
+  auto qk_chunk = [&](f32x4& s, const bf16x8& k0, const bf16x8& k1, const bf16x8& k2, int c) {
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qt[0][c], s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[2][c], s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qt[1][c], s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qt[0][c], s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[1][c], s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[0][c], s, 0, 0, 0);
+  };
   auto qk = [&](const uint16_t* Kc, f32x4 (&sacc)[2]) {
+    if constexpr (TL_PF) {
+      // The two key blocks' chains interleaved (each MFMA's accumulator was
+      // written two MFMAs earlier, not one), and the key terms of chunk c + 1
+      // read while chunk c's products run. Each block's products keep the
+      // order above, so the scores are the same bits.
+      sacc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      bf16x8 kt[2][2][3];  // [chunk parity][key block][term]
+      auto rd = [&](int c, bf16x8 (&dst)[2][3]) {
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
-      sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int key = 16 * kb + lq;
-      const uint16_t* kr = Kc + key * HD;
+        for (int kb = 0; kb < 2; kb++) {
+          const int key = 16 * kb + lq;
+          const uint16_t* kr = Kc + key * HD + ((4 * (NC * hf + c) + g) ^ key) * 8;
+#pragma unroll
+          for (int t = 0; t < 3; t++) dst[kb][t] = *reinterpret_cast<const bf16x8*>(kr + t * TERM);
+        }
+      };
+      rd(0, kt[0]);
 #pragma unroll
       for (int c = 0; c < NC; c++) {
-        const int pos = ((4 * (NC * hf + c) + g) ^ key) * 8;
-        const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kr + pos);
-        const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kr + TERM + pos);
-        const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(kr + 2 * TERM + pos);
-        // smallest terms first
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qt[0][c], sacc[kb], 0, 0, 0);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[2][c], sacc[kb], 0, 0, 0);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qt[1][c], sacc[kb], 0, 0, 0);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qt[0][c], sacc[kb], 0, 0, 0);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[1][c], sacc[kb], 0, 0, 0);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qt[0][c], sacc[kb], 0, 0, 0);
+        if (c + 1 < NC) rd(c + 1, kt[(c + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);  // the next chunk's reads issue before this chunk's products
+        const int b = c & 1;
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][0][2], qt[0][c], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][1][2], qt[0][c], sacc[1], 0, 0, 0);
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][0][0], qt[2][c], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][1][0], qt[2][c], sacc[1], 0, 0, 0);
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][0][1], qt[1][c], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][1][1], qt[1][c], sacc[1], 0, 0, 0);
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][0][1], qt[0][c], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][1][1], qt[0][c], sacc[1], 0, 0, 0);
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][0][0], qt[1][c], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][1][0], qt[1][c], sacc[1], 0, 0, 0);
+        sacc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][0][0], qt[0][c], sacc[0], 0, 0, 0);
+        sacc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[b][1][0], qt[0][c], sacc[1], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int key = 16 * kb + lq;
+        const uint16_t* kr = Kc + key * HD;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          const int pos = ((4 * (NC * hf + c) + g) ^ key) * 8;
+          const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kr + pos);
+          const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kr + TERM + pos);
+          const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(kr + 2 * TERM + pos);
+          qk_chunk(sacc[kb], k0, k1, k2, c);
+        }
       }
     }
   };
   // O^T += V^T . P^T for one tile (terms b0, b1, b2 of the probabilities)
+  // the value terms of block db (with TL_PF read one block ahead)
+  auto vread = [&](const uint16_t* Vc, int db, bf16x8 (&dst)[3]) {
+    const uint16_t* vr = Vc + (16 * (NDB * hf + db) + lq) * 32 + (g ^ vsw) * 8;
+#pragma unroll
+    for (int t = 0; t < 3; t++) dst[t] = *reinterpret_cast<const bf16x8*>(vr + t * TERM);
+  };
   auto pv = [&](const uint16_t* Vc, const bf16x8& b0, const bf16x8& b1, const bf16x8& b2) {
-    const int vpos = (g ^ vsw) * 8;
+    bf16x8 vt[2][3];
+    if constexpr (TL_PF) vread(Vc, 0, vt[0]);
 #pragma unroll
     for (int db = 0; db < NDB; db++) {
-      const uint16_t* vr = Vc + (16 * (NDB * hf + db) + lq) * 32 + vpos;
-      const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(vr);
-      const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(vr + TERM);
-      const bf16x8 v2 = *reinterpret_cast<const bf16x8*>(vr + 2 * TERM);
+      if constexpr (TL_PF) {
+        if (db + 1 < NDB) vread(Vc, db + 1, vt[(db + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        vread(Vc, db, vt[db & 1]);
+      }
+      const bf16x8 v0 = vt[db & 1][0], v1 = vt[db & 1][1], v2 = vt[db & 1][2];
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v2, b0, oacc[db], 0, 0, 0);
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, b2, oacc[db], 0, 0, 0);
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, b1, oacc[db], 0, 0, 0);
@@ -748,17 +803,21 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   // written between its blocks of 16 dims, in four stages, so that the
   // VALU work sits among the MFMAs; the new terms replace pb* at the end
   auto pv_softmax = [&](const uint16_t* Vp, int tt, const f32x4 (&sacc)[2], float& alpha, bool& moved) {
-    const int vpos = (g ^ vsw) * 8;
     float t[8];
     float tmax = -INFINITY, mn = 0.f, psum = 0.f;
     uint32_t ph[8], pm[8], pl[8];
     constexpr int WPS = DS == 2 ? 2 : 1;  // weights per block in the last stage
+    bf16x8 vt[2][3];
+    if constexpr (TL_PF) vread(Vp, 0, vt[0]);
 #pragma unroll
     for (int db = 0; db < NDB; db++) {
-      const uint16_t* vr = Vp + (16 * (NDB * hf + db) + lq) * 32 + vpos;
-      const bf16x8 v0 = *reinterpret_cast<const bf16x8*>(vr);
-      const bf16x8 v1 = *reinterpret_cast<const bf16x8*>(vr + TERM);
-      const bf16x8 v2 = *reinterpret_cast<const bf16x8*>(vr + 2 * TERM);
+      if constexpr (TL_PF) {
+        if (db + 1 < NDB) vread(Vp, db + 1, vt[(db + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        vread(Vp, db, vt[db & 1]);
+      }
+      const bf16x8 v0 = vt[db & 1][0], v1 = vt[db & 1][1], v2 = vt[db & 1][2];
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v2, pb0, oacc[db], 0, 0, 0);
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, pb2, oacc[db], 0, 0, 0);
       oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, pb1, oacc[db], 0, 0, 0);
