@@ -480,14 +480,27 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ y
     for (int p = 1; p < parts; p++) v += r[p * pstride + i];
     return v;
   };
-  constexpr int kHeld = 16;  // values per lane kept in registers (dim <= 1 024)
+  constexpr int kHeld = 16;      // values per lane kept in registers (dim <= 1 024)
+  constexpr int kHeldParts = 4;  // partial products loaded together (the head's K parts)
   float s = 0.f;
-  if (dim <= kWave * kHeld) {
+  if (dim <= kWave * kHeld && parts <= kHeldParts) {
+    // every part's values loaded before the first sum (one round trip
+    // instead of one per part and value), then added in part order
+    float w[kHeldParts][kHeld];
+#pragma unroll
+    for (int p = 0; p < kHeldParts; p++)
+#pragma unroll
+      for (int t = 0; t < kHeld; t++) {
+        const int i = lane + kWave * t;
+        w[p][t] = (p < parts && i < dim) ? r[p * pstride + i] : 0.f;
+      }
     float v[kHeld];
 #pragma unroll
     for (int t = 0; t < kHeld; t++) {
-      const int i = lane + kWave * t;
-      v[t] = i < dim ? value(i) : 0.f;
+      v[t] = w[0][t];
+#pragma unroll
+      for (int p = 1; p < kHeldParts; p++)
+        if (p < parts) v[t] += w[p][t];
     }
 #pragma unroll
     for (int t = 0; t < kHeld; t++) s = fmaf(v[t], v[t], s);
