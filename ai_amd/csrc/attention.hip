@@ -327,22 +327,37 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __r
   const int64_t lrow = lid / H, h = lid % H;
   const int64_t row = row_off + lrow, id = row * H + h;
   const float2* ml = reinterpret_cast<const float2*>(part + (int64_t)kparts * rows * OW);
+  // every run's (max, sum) and partial O loaded before the first use (one
+  // round trip instead of one per run; kparts <= kMaxKeyParts, checked by
+  // the launchers), then combined in run order
+  float2 mlv[kMaxKeyParts];
+  f32x4 ov[kMaxKeyParts][HD / 256];
+#pragma unroll
+  for (int q = 0; q < kMaxKeyParts; q++) {
+    if (q < kparts) {
+      mlv[q] = ml[q * rows * H + id];
+      const float* src = part + (q * rows + row) * OW + h * HD + lane * 4;
+#pragma unroll
+      for (int c = 0; c < HD / 256; c++) ov[q][c] = *reinterpret_cast<const f32x4*>(src + c * 256);
+    }
+  }
   float M = kNegBig;
-  for (int q = 0; q < kparts; q++) M = fmaxf(M, ml[q * rows * H + id].x);
+#pragma unroll
+  for (int q = 0; q < kMaxKeyParts; q++)
+    if (q < kparts) M = fmaxf(M, mlv[q].x);
   float Lsum = 0.f;
   f32x4 acc[HD / 256];
 #pragma unroll
   for (int c = 0; c < HD / 256; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < kparts; q++) {
-    const float2 v = ml[q * rows * H + id];
-    const float w = exp_flush(v.x - M);
-    Lsum += w * v.y;
-    const float* src = part + (q * rows + row) * OW + h * HD + lane * 4;
 #pragma unroll
-    for (int c = 0; c < HD / 256; c++) {
-      const f32x4 o = *reinterpret_cast<const f32x4*>(src + c * 256);
+  for (int q = 0; q < kMaxKeyParts; q++) {
+    if (q < kparts) {
+      const float w = exp_flush(mlv[q].x - M);
+      Lsum += w * mlv[q].y;
 #pragma unroll
-      for (int e = 0; e < 4; e++) acc[c][e] += w * o[e];
+      for (int c = 0; c < HD / 256; c++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[c][e] += w * ov[q][c][e];
     }
   }
   const float inv = 1.f / Lsum;

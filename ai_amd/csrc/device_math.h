@@ -173,12 +173,34 @@ __device__ __forceinline__ void residual_norm_row(const float* __restrict__ o, c
 #pragma unroll
     for (int c = 0; c < NC; c++) gn[c] = *reinterpret_cast<const f32x4*>(g_next + c * 256 + lane * 4);
   }
-  // the other K parts, added in part order
-  for (int j = 0; o2 && j < n2; j++) {
+  // the other K parts, added in part order; up to kHeldParts of them all
+  // loaded before the first sum (one round trip instead of one per part)
+  constexpr int kHeldParts = 3;
+  if (o2 && n2 <= kHeldParts) {
+    f32x4 p2[kHeldParts][NC];
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-      const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + j * pstride + row * d + c * 256 + lane * 4);
-      ov[c].x = ov[c].x + p2.x; ov[c].y = ov[c].y + p2.y; ov[c].z = ov[c].z + p2.z; ov[c].w = ov[c].w + p2.w;
+    for (int j = 0; j < kHeldParts; j++)
+      if (j < n2) {
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+          p2[j][c] = *reinterpret_cast<const f32x4*>(o2 + j * pstride + row * d + c * 256 + lane * 4);
+      }
+#pragma unroll
+    for (int j = 0; j < kHeldParts; j++)
+      if (j < n2) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          ov[c].x = ov[c].x + p2[j][c].x; ov[c].y = ov[c].y + p2[j][c].y;
+          ov[c].z = ov[c].z + p2[j][c].z; ov[c].w = ov[c].w + p2[j][c].w;
+        }
+      }
+  } else {
+    for (int j = 0; o2 && j < n2; j++) {
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const f32x4 p2 = *reinterpret_cast<const f32x4*>(o2 + j * pstride + row * d + c * 256 + lane * 4);
+        ov[c].x = ov[c].x + p2.x; ov[c].y = ov[c].y + p2.y; ov[c].z = ov[c].z + p2.z; ov[c].w = ov[c].w + p2.w;
+      }
     }
   }
   const float inv = rms_inv(sumsq<NC>(ov), d, eps);
