@@ -92,12 +92,22 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
     if (p.any_var) p.n_items_v += ((int64_t)L + in.varlen_qblock - 1) / in.varlen_qblock * in.H;
   }
   // Attention over few items (a short batch on one stream) cuts each
-  // item's keys into up to four runs of whole tiles, one workgroup each, so
+  // item's keys into up to eight runs of whole tiles, one workgroup each, so
   // that more CUs share the key loop: C1's 12 fp32 items (128 tokens, 3
-  // heads) become 48 workgroups of two 16-key tiles.
+  // heads) become 96 workgroups of one 16-key tile. Per forward on MI355X
+  // against the earlier rule (at most four runs of at least two tiles):
+  // 128 tokens 1.171 -> 1.140 ms, 64 1.071 -> 1.038, 200 1.380 -> 1.294,
+  // 300 1.678 -> 1.584, 400 1.838 -> 1.760, 500 1.913 -> 1.900; 4 x 128
+  // (runs capped at four by their length) unchanged; 32 tokens keep one run.
   if (p.any_var && in.groups == 1 && p.M <= in.split_rows && 2 * p.n_items_v <= in.cus) {
-    p.kparts_v = (int)std::min<int64_t>(4, in.cus / std::max<int64_t>(p.n_items_v, 1));
-    p.kparts_v = std::max(1, std::min(p.kparts_v, (in.T + 31) / 32));  // at least two 16-key tiles per run
+    p.kparts_v = (int)std::min<int64_t>(in.max_key_parts, in.cus / std::max<int64_t>(p.n_items_v, 1));
+    const int tiles16 = (in.T + 15) / 16;  // the longest sequence's 16-key tiles
+    p.kparts_v = std::max(1, std::min(p.kparts_v, tiles16));  // at least one tile per run
+    // no more runs than its run length needs (8 tiles in 5 runs are runs of
+    // 2, 2, 2, 2 and an empty one: 4 runs)
+    const int per = (tiles16 + p.kparts_v - 1) / p.kparts_v;
+    p.kparts_v = (tiles16 + per - 1) / per;
+    if (in.T <= 32) p.kparts_v = 1;  // two tiles: the combine launch costs more than a tile
     if (in.forced_key_parts) p.kparts_v = in.forced_key_parts;
   }
   if (p.any_tiles) {

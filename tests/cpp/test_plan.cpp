@@ -166,14 +166,39 @@ TEST(TestGroupsBalanced) {
   if (fa::plan_groups(two, 2, 905, 3, gb) != 2 || gb[1] != 1 || gb[2] != 2) FATAL("two sequences, three groups wanted");
 }
 
-// C1 (one 128-token sentence): the fp32 kernel, 12 items cut into 4 key runs
+// C1 (one 128-token sentence): the fp32 kernel, 12 items cut into 8 key
+// runs of one 16-key tile
 TEST(TestC1FP32KeyRuns) {
   Case c;
   c.lengths = {128};
   run(c, eg300m(), 1);
   if (c.p.any_tiles || !c.p.any_var) FATAL("C1 takes the fp32 kernel");
-  if (c.p.n_items_v != 12 || c.p.kparts_v != 4) FATAL("items %lld key runs %d, want 12 and 4", (long long)c.p.n_items_v, c.p.kparts_v);
+  if (c.p.n_items_v != 12 || c.p.kparts_v != 8) FATAL("items %lld key runs %d, want 12 and 8", (long long)c.p.n_items_v, c.p.kparts_v);
   check_items(c);
+}
+
+// The fp32 items' key runs: at most one per 16-key tile and per CU share,
+// no more than the run length needs, none from two tiles down
+TEST(TestFP32KeyRunCounts) {
+  struct K { std::vector<int32_t> lengths; int items, runs; };
+  const K cases[] = {
+      {{32}, 3, 1},                 // two tiles: no runs (no combine launch)
+      {{48}, 6, 3},                 // three tiles of one key run each
+      {{64}, 6, 4},
+      {{300}, 30, 7},               // 8 CU shares of 19 tiles: runs of 3 tiles, 7 of them
+      {{500}, 48, 5},               // 5 CU shares of 32 tiles: runs of 7 tiles
+      {{128, 128, 128, 128}, 48, 4}, // 5 CU shares of 8 tiles: runs of 2, 4 of them
+  };
+  for (const K& k : cases) {
+    Case c;
+    c.lengths = k.lengths;
+    run(c, eg300m(), 1);
+    if (c.p.any_tiles || !c.p.any_var) FATAL("%d tokens: the fp32 kernel expected", (int)k.lengths[0]);
+    if (c.p.n_items_v != k.items || c.p.kparts_v != k.runs)
+      FATAL("%zu x %d: items %lld key runs %d, want %d and %d", k.lengths.size(), (int)k.lengths[0],
+            (long long)c.p.n_items_v, c.p.kparts_v, k.items, k.runs);
+    check_items(c);
+  }
 }
 
 // over 1 024 tokens at >= 32 per sequence: the tile attention; the wave
