@@ -320,6 +320,25 @@ def test_tile_path_by_pairs(models, lengths):
     compare_states(gm, om, ids, lens, sorted({0, len(lengths) - 1}), f"{lengths} states", layers=[1, 12, -1])
 
 
+@pytest.mark.parametrize("lengths", [[33], [48], [300], [500], [128, 128, 128, 128], [200, 17, 3]])
+def test_fp32_key_run_counts(models, lengths):
+    """Short batches on the fp32 attention with the key runs their plan
+    gives (tests/cpp/test_plan.cpp): 3 runs of one 16-key tile at 33 and 48
+    tokens, 7 runs of three tiles at 300, 5 of seven at 500, 4 of two for
+    four 128-token sequences, and a ragged batch whose short sequences
+    leave most of their runs empty (a run without keys contributes weight
+    0 to the combine). Every row and three layers' states against the
+    oracle."""
+    gm, om = models
+    rng = np.random.default_rng(90 + sum(lengths))
+    lens = np.array(lengths, np.int32)
+    ids = rng.integers(3, 262144, (len(lengths), int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    compare(gm.embed_ids(ids, lens), om.embed(ids, lens), f"{lengths} (fp32 key runs)")
+    compare_states(gm, om, ids, lens, sorted({0, len(lengths) - 1}), f"{lengths} states", layers=[1, 12, -1])
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_random_batches_across_plan_rules(models, seed):
     """Seeded random batches (1-12 sequences of 1-700 tokens) that land on
