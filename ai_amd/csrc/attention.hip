@@ -571,6 +571,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     // of a sequence): the wave issues its share of each image load and
     // takes part in every barrier of the loop below, in the same order,
     // and computes nothing
+    if constexpr (DS == 2) dl_barrier<0xC07F>();  // the q halves' exchange below
     if (tb < te) {
       for (int tt = tb; tt < te; tt++) {
         dl_barrier<0x0F70>();
@@ -593,10 +594,52 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     const float* qr = p.qkv + (start + tok) * W + (int64_t)head * HD + 8 * g;
     f32x4 x[HD / 32][2];
     float ss = 0.f;
+    if constexpr (DS == 2) {
+      // Wave pairs: each wave loads its own half of the rows' dims (chunks
+      // NC * hf ..) and the halves swap through LDS (the value buffers, free
+      // until the first tile's value loads, which follow that tile's first
+      // barrier): half the q bytes from memory at the launch's start, where
+      // every workgroup loads its q rows at once. Same values, same sums.
+      f32x4* xs = reinterpret_cast<f32x4*>((wave < 6 ? Vs0 : Vs1) + (wave % 6) * 4096);  // 8 KB per wave
+      const int pw = wave ^ RB;
+      const f32x4* xp = reinterpret_cast<const f32x4*>((pw < 6 ? Vs0 : Vs1) + (pw % 6) * 4096);
+      if (hf == 0) {
 #pragma unroll
-    for (int c = 0; c < HD / 32; c++) {
-      x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
-      x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
+        for (int c = 0; c < NC; c++) {
+          x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
+          x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
+          xs[(2 * c) * 64 + lane] = x[c][0];
+          xs[(2 * c + 1) * 64 + lane] = x[c][1];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          x[NC + c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * (NC + c));
+          x[NC + c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * (NC + c) + 4);
+          xs[(2 * c) * 64 + lane] = x[NC + c][0];
+          xs[(2 * c + 1) * 64 + lane] = x[NC + c][1];
+        }
+      }
+      dl_barrier<0xC07F>();  // lgkmcnt(0): every half written; the first key image stays in flight
+      if (hf == 0) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          x[NC + c][0] = xp[(2 * c) * 64 + lane];
+          x[NC + c][1] = xp[(2 * c + 1) * 64 + lane];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+          x[c][0] = xp[(2 * c) * 64 + lane];
+          x[c][1] = xp[(2 * c + 1) * 64 + lane];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < HD / 32; c++) {
+        x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
+        x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
+      }
     }
 #pragma unroll
     for (int c = 0; c < HD / 32; c++)
