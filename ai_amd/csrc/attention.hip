@@ -60,6 +60,7 @@ struct VarlenParams {
   float* out;
   const int32_t* cu;
   const int32_t* items;  // triples (seq, q0, head)
+  const int32_t* ext;    // null, or per item (sequence's first packed row, length, first tile, 0)
   int32_t H, Hkv;
   int32_t window;
   float scale;
@@ -140,8 +141,16 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   const int q0 = p.items[3 * item + 1];
   const int h = p.items[3 * item + 2];
   const int hk = h / (p.H / p.Hkv);
-  const int L = p.cu[seq + 1] - p.cu[seq];
-  const int64_t start = p.cu[seq] - p.row0;  // the sequence's first row in qkv and out
+  int32_t seq_row, L;  // the sequence's first packed row and length
+  if (p.ext) {
+    const int4 e = reinterpret_cast<const int4*>(p.ext)[item];
+    seq_row = e.x;
+    L = e.y;
+  } else {
+    seq_row = p.cu[seq];
+    L = p.cu[seq + 1] - seq_row;
+  }
+  const int64_t start = seq_row - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
   const int dofs = half * HALF;
   const float* qbase = p.qkv + (int64_t)start * W + (int64_t)h * HD + dofs;
@@ -439,6 +448,7 @@ struct TilesParams {
   const int32_t* cu;     // cu_seqlens
   const int32_t* cut;    // first tile of each sequence
   const int32_t* items;  // triples (sequence, first row, kv head)
+  const int32_t* ext;    // null, or per item (sequence's first packed row, length, first tile, 0)
   int32_t H, Hkv;
   int32_t window;
   float scale;
@@ -512,8 +522,18 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   const int rb = p.items[3 * item + 1];
   const int hk = p.items[3 * item + 2];
   const int G = p.H / p.Hkv;
-  const int L = p.cu[seq + 1] - p.cu[seq];
-  const int64_t start = p.cu[seq] - p.row0;  // the sequence's first row in qkv and out
+  int32_t seq_row, L, seq_tile;  // the sequence's first packed row, length and first key tile
+  if (p.ext) {
+    const int4 e = reinterpret_cast<const int4*>(p.ext)[item];
+    seq_row = e.x;
+    L = e.y;
+    seq_tile = e.z;
+  } else {
+    seq_row = p.cu[seq];
+    L = p.cu[seq + 1] - seq_row;
+    seq_tile = p.cut[seq];
+  }
+  const int64_t start = seq_row - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
   const int nrows = G * L;
   const int row = rb + 16 * rbw + lq;
@@ -536,7 +556,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     tb = nb;
   }
 
-  const uint16_t* img0 = p.img + ((int64_t)p.cut[seq] * p.Hkv + hk) * (2 * TL_IMG);
+  const uint16_t* img0 = p.img + ((int64_t)seq_tile * p.Hkv + hk) * (2 * TL_IMG);
   const int64_t tstride = (int64_t)p.Hkv * 2 * TL_IMG;
   // 48 loads of 1 KB per image, six per wave
   auto issue = [&](const uint16_t* src, uint16_t* dst) {
@@ -962,7 +982,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   if (!qvalid) return;
   const int OW = p.H * HD;
   if (p.kparts > 1) {
-    const int64_t arow = p.cu[seq] + tok;  // absolute packed row
+    const int64_t arow = seq_row + tok;  // absolute packed row
     float* orow = p.part + ((int64_t)part * p.rows + arow) * OW + (int64_t)head * HD + 16 * NDB * hf + 4 * g;
 #pragma unroll
     for (int db = 0; db < NDB; db++) *reinterpret_cast<f32x4*>(orow + 16 * db) = oacc[db];
@@ -1238,7 +1258,7 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
     return set_error(ctx, FA_ERR_ARG, "attention: %d key parts (1..%d, > 1 needs a partial buffer)", a.kparts,
                      kMaxKeyParts);
   VarlenParams p;
-  p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items; p.row0 = a.row0;
+  p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items; p.ext = a.item_ext; p.row0 = a.row0;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
   p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
   const dim3 grid((unsigned)((int64_t)n_items * a.kparts));
@@ -1284,6 +1304,7 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
                      kMaxKeyParts);
   TilesParams p;
   p.qkv = a.qkv; p.img = a.img; p.out = a.out; p.cu = a.cu_seqlens; p.cut = a.cu_tiles; p.items = d_items;
+  p.ext = a.item_ext;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
   p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
   p.gq = a.gq; p.cs = a.cos_t; p.sn = a.sin_t; p.eps = a.eps;

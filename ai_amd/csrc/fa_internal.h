@@ -270,6 +270,10 @@ struct AttnVarlenArgs {
   int32_t window;
   float scale;
   int64_t row0 = 0;  // packed row held by qkv's and out's first row (items' sequences start at or after it)
+  // optional, per work item (16-byte aligned): the first packed row of the
+  // item's sequence, its length, its first key tile, 0; read beside the item
+  // instead of through cu_seqlens (one dependent load less before q and K/V)
+  const int32_t* item_ext = nullptr;
   // kparts > 1 (at most kMaxKeyParts): every item's keys are cut into kparts
   // runs, one workgroup each, summed by a second pass; part holds
   // attention_part_floats(kparts, rows, H, D) floats and rows is the row
@@ -306,6 +310,7 @@ struct AttnTilesArgs {
   float* out;
   const int32_t* cu_seqlens;
   const int32_t* cu_tiles;
+  const int32_t* item_ext = nullptr;  // as AttnVarlenArgs::item_ext
   int32_t H, Hkv;
   int32_t window;
   float scale;

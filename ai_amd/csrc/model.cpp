@@ -877,7 +877,12 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   const int64_t n_items_t = ap.n_items_t, n_items = ap.n_items_t + ap.n_items_v, n_tiles = ap.n_tiles;
   const int hkv_t = ap.hkv_t, kparts_t = ap.kparts_t, kparts_v = ap.kparts_v, waves_t = ap.waves_t;
   const int tkeys = pin.tile_keys;
-  const size_t plan_ints = 2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles;
+  // plan buffer: cu_seqlens, items, first tile per sequence, tile ->
+  // sequence, then (16-byte aligned) each item's extent: its sequence's
+  // first packed row, length and first tile, read by the attention kernels
+  // beside the item instead of through the sequence tables
+  const size_t ext_off = (2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles + 3) & ~(size_t)3;
+  const size_t plan_ints = ext_off + 4 * (size_t)n_items;
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
     m->plan_pending = false;
@@ -901,6 +906,16 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     for (int q = cut_h[b]; q < cut_h[b + 1]; q++) tseq_h[q] = b;
   }
   fa::plan_items(pin, ap, items_h, m->seq_order);
+  {
+    int32_t* ext_h = m->plan_host + ext_off;
+    for (int64_t i = 0; i < n_items; i++) {
+      const int b = items_h[3 * i];
+      ext_h[4 * i] = cu_h[b];
+      ext_h[4 * i + 1] = lengths[b];
+      ext_h[4 * i + 2] = cut_h[b];
+      ext_h[4 * i + 3] = 0;
+    }
+  }
   const int64_t* group_items_t = ap.group_items_t;
   const int64_t* group_items_v = ap.group_items_v;
   int rc;
@@ -909,6 +924,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   int32_t* items_d = cu_d + (B + 1);
   int32_t* cut_d = items_d + 3 * n_items;
   int32_t* tseq_d = cut_d + (B + 1);
+  const int32_t* ext_d = cu_d + ext_off;  // [n_items][4], 16-byte aligned
   int32_t* row_src_d = cu_d + plan_ints;   // [M] b*T + t
   int32_t* pos_d = row_src_d + M;          // [M] t
   FA_HIP_CHECK(ctx, hipMemcpyAsync(cu_d, m->plan_host, plan_ints * 4, hipMemcpyHostToDevice, ctx->stream));
@@ -1059,6 +1075,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     {
       fa::AttnVarlenArgs a;
       a.qkv = qkvr; a.out = attr; a.row0 = r0; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
+      a.item_ext = ext_d + 4 * ((items_v - items_d) / 3);
       a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
       a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
       if (kparts_v > 1) {
@@ -1080,6 +1097,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       if (tiles) {
         fa::AttnTilesArgs at;
         at.qkv = qkvr; at.img = img; at.out = attr; at.row0 = r0; at.cu_seqlens = cu_d; at.cu_tiles = cut_d;
+        at.item_ext = ext_d + 4 * ((items_t - items_d) / 3);
         at.H = H; at.Hkv = Hkv; at.window = a.window; at.scale = a.scale;
         at.gq = L.g_q; at.eps = eps; at.cos_t = L.cos_t; at.sin_t = L.sin_t; at.waves = waves_t;
         if (kparts_t > 1) {
