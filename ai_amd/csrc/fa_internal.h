@@ -239,7 +239,7 @@ int launch_embed_gather(fa_ctx* ctx, const int32_t* d_ids, const int32_t* d_row_
                         float* xn, hipStream_t s);
 
 // q/k RMSNorm with (1+g) and RoPE on the packed qkv buffer [rows x (H+2*Hkv)*D],
-// in place; positions from d_pos.
+// in place; positions from d_pos (null: row i is position i, the rows being one sequence).
 // With norm_v, the Hkv value heads are RMS-normalised too (unit gain, no
 // rotation). D is 256 or 512. qkv2 (optional): the second K part of a
 // K-split q|k|v product (same layout), added to qkv first, values included.
@@ -298,11 +298,13 @@ int attention_varlen_qblock();
 // [tile][Hkv][2][3*32*256] bf16. Tile tt of sequence b (d_cu_tiles[b] <= tt
 // < d_cu_tiles[b+1], every sequence starting a tile) holds its tokens 32 (tt
 // - d_cu_tiles[b]) .. +31 (their positions, for RoPE); d_tile_seq[tt] = b.
-// qkv starts at packed row row0.
+// qkv starts at packed row row0. d_tile_ext (optional, 16-byte aligned): per
+// tile (first packed row, keys, first key's position, 0), read in place of
+// the three tables (one dependent load less before the rows).
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
                     const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
                     const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
-                    hipStream_t s, bool norm_v = false);
+                    hipStream_t s, bool norm_v = false, const int32_t* d_tile_ext = nullptr);
 
 struct AttnTilesArgs {
   const float* qkv;       // raw q read here (rows of the launch start at packed row row0)

@@ -878,11 +878,12 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   const int hkv_t = ap.hkv_t, kparts_t = ap.kparts_t, kparts_v = ap.kparts_v, waves_t = ap.waves_t;
   const int tkeys = pin.tile_keys;
   // plan buffer: cu_seqlens, items, first tile per sequence, tile ->
-  // sequence, then (16-byte aligned) each item's extent: its sequence's
-  // first packed row, length and first tile, read by the attention kernels
-  // beside the item instead of through the sequence tables
+  // sequence, then (16-byte aligned) each item's extent (its sequence's
+  // first packed row, length and first tile) and each key tile's (its first
+  // packed row, keys, first key's position), read by the attention and the
+  // key/value image kernels instead of through the sequence tables
   const size_t ext_off = (2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles + 3) & ~(size_t)3;
-  const size_t plan_ints = ext_off + 4 * (size_t)n_items;
+  const size_t plan_ints = ext_off + 4 * (size_t)(n_items + n_tiles);
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
     m->plan_pending = false;
@@ -915,6 +916,15 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       ext_h[4 * i + 2] = cut_h[b];
       ext_h[4 * i + 3] = 0;
     }
+    int32_t* text_h = ext_h + 4 * n_items;
+    for (int b = 0; b < B; b++)
+      for (int q = cut_h[b]; q < cut_h[b + 1]; q++) {
+        const int t0 = tkeys * (q - cut_h[b]);
+        text_h[4 * q] = cu_h[b] + t0;
+        text_h[4 * q + 1] = std::min(tkeys, lengths[b] - t0);
+        text_h[4 * q + 2] = t0;
+        text_h[4 * q + 3] = 0;
+      }
   }
   const int64_t* group_items_t = ap.group_items_t;
   const int64_t* group_items_v = ap.group_items_v;
@@ -925,6 +935,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   int32_t* cut_d = items_d + 3 * n_items;
   int32_t* tseq_d = cut_d + (B + 1);
   const int32_t* ext_d = cu_d + ext_off;  // [n_items][4], 16-byte aligned
+  const int32_t* text_d = ext_d + 4 * n_items;  // [n_tiles][4]
   int32_t* row_src_d = cu_d + plan_ints;   // [M] b*T + t
   int32_t* pos_d = row_src_d + M;          // [M] t
   FA_HIP_CHECK(ctx, hipMemcpyAsync(cu_d, m->plan_host, plan_ints * 4, hipMemcpyHostToDevice, ctx->stream));
@@ -1062,12 +1073,14 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       fa::Probe pr(m, FA_K_QKNORM_ROPE, 0,
                    (double)rows * (v2 ? 3 : 2) * Hkv * 4.0 * D + (double)ntl * Hkv * 2 * 3 * 32 * 256 * 2);
       if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, L.cos_t, L.sin_t, cu_d, cut_d, tseq_d,
-                                    cut_h[b0], (int32_t)ntl, img, st, v2)))
+                                    cut_h[b0], (int32_t)ntl, img, st, v2, text_d)))
         return rc;
       pr.done();
     } else {
       fa::Probe pr(m, FA_K_QKNORM_ROPE, 0, (double)rows * (H + (v2 ? 2 : 1) * Hkv) * D * 8.0);
-      if ((rc = fa::launch_qknorm_rope(ctx, qkvr, rows, H, Hkv, D, L.g_q, L.g_k, eps, pos_d + r0, L.cos_t, L.sin_t,
+      // a group of one sequence: row i is token i, no position table
+      const int32_t* gpos = b1 - b0 == 1 ? nullptr : pos_d + r0;
+      if ((rc = fa::launch_qknorm_rope(ctx, qkvr, rows, H, Hkv, D, L.g_q, L.g_k, eps, gpos, L.cos_t, L.sin_t,
                                        st, v2, qkv2)))
         return rc;
       pr.done();

@@ -185,7 +185,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
   const int width = (H + 2 * Hkv) * D;
   float* p = qkv + row * width + (int64_t)head * D;
   // every load is issued before the reduction: the head's values, its gains
-  // and the token's RoPE table row (one dependent step through pos)
+  // and the token's RoPE table row (one dependent step through pos, none
+  // without it)
   f32x4 v[NQ], gg[NQ];
   const float* g = head < H ? gq : gk;
   const bool rot = head < H + Hkv;
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_kernel(float* __restrict__ qk
 #pragma unroll
     for (int c = 0; c < NQ; c++) gg[c] = *reinterpret_cast<const f32x4*>(g + c * 256 + lane * 4);
   }
-  const int t = pos[row];
+  const int t = pos ? pos[row] : (int)row;  // null: the rows are one sequence's tokens 0, 1, ...
   const int i0 = D == 256 ? (lane & 31) * 4 : lane * 4;
   f32x4 cv = {0.f, 0.f, 0.f, 0.f}, svv = {0.f, 0.f, 0.f, 0.f};
   if (rot) {
@@ -310,6 +311,7 @@ struct KvTilesParams {
   float eps;
   const float *cs, *sn;
   const int32_t *cu, *cut, *tile_seq;
+  const int32_t* tile_ext;  // null, or per tile (first packed row, keys, first key's position, 0)
   int t_lo, tiles;
   uint16_t* img;
   int norm_v;  // values RMS-normed with unit gain first (EmbeddingGemma 2, gemma2.go)
@@ -325,12 +327,26 @@ constexpr int kVtStride = 132;
 // keys 16*half + w, + 4, ..., 4 dims per lane; rows past the sequence are
 // clamped to its last token (every load issued up front, none conditional)
 // and written as zeros.
+// The tile's first qkv row, its first key's position and its key count.
+__device__ __forceinline__ void tile_extent(const KvTilesParams& a, int tile, int64_t& r_first, int& t0, int& n) {
+  if (a.tile_ext) {
+    const int4 e = reinterpret_cast<const int4*>(a.tile_ext)[tile];
+    r_first = e.x - a.row0;
+    n = e.y;
+    t0 = e.z;
+  } else {
+    const int sq = a.tile_seq[tile];
+    t0 = 32 * (tile - a.cut[sq]);
+    n = min(32, a.cu[sq + 1] - a.cu[sq] - t0);
+    r_first = a.cu[sq] - a.row0 + t0;
+  }
+}
+
 __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int half_, int wave, int lane) {
   constexpr int D = 256, half = D / 2;
-  const int sq = a.tile_seq[tile];
-  const int t0 = 32 * (tile - a.cut[sq]);
-  const int n = min(32, a.cu[sq + 1] - a.cu[sq] - t0);
-  const int64_t r_first = a.cu[sq] - a.row0 + t0;  // qkv row of the tile's first token
+  int64_t r_first;  // qkv row of the tile's first token
+  int t0, n;
+  tile_extent(a, tile, r_first, t0, n);
   const int width = (a.H + 2 * a.Hkv) * D;
   uint16_t* kimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg);
   const f32x4 gg = *reinterpret_cast<const f32x4*>(a.gk + lane * 4);
@@ -384,10 +400,9 @@ __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int h
 __device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int hk, int half_, int wave, int lane,
                                            float (*Vt)[kVtStride]) {
   constexpr int D = 256;
-  const int sq = a.tile_seq[tile];
-  const int t0 = 32 * (tile - a.cut[sq]);
-  const int n = min(32, a.cu[sq + 1] - a.cu[sq] - t0);
-  const int64_t r_first = a.cu[sq] - a.row0 + t0;
+  int64_t r_first;
+  int t0, n;
+  tile_extent(a, tile, r_first, t0, n);
   const int width = (a.H + 2 * a.Hkv) * D;
   uint16_t* vimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg) + kTileImg;
   float2 v[8];
@@ -661,12 +676,13 @@ int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int3
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
                     const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
                     const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
-                    hipStream_t s, bool norm_v) {
+                    hipStream_t s, bool norm_v, const int32_t* d_tile_ext) {
   if (tiles == 0) return FA_OK;
   KvTilesParams a;
   a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.cs = cos_t; a.sn = sin_t;
   a.cu = d_cu_seqlens; a.cut = d_cu_tiles; a.tile_seq = d_tile_seq; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
   a.norm_v = norm_v ? 1 : 0;
+  a.tile_ext = d_tile_ext;
   hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
