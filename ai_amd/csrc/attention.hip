@@ -58,9 +58,8 @@ constexpr float kNegBig = -1e30f;
 struct VarlenParams {
   const float* qkv;
   float* out;
-  const int32_t* cu;
   const int32_t* items;  // triples (seq, q0, head)
-  const int32_t* ext;    // null, or per item (sequence's first packed row, length, first tile, 0)
+  const int32_t* ext;    // per item (sequence's first packed row, length, first tile, 0)
   int32_t H, Hkv;
   int32_t window;
   float scale;
@@ -137,19 +136,11 @@ __global__ __launch_bounds__(DL_NT) void attention_varlen_kernel(VarlenParams p)
   const int lq = lane & 15;
 
   const int item = blockIdx.x / p.kparts, part = blockIdx.x % p.kparts;
-  const int seq = p.items[3 * item];
   const int q0 = p.items[3 * item + 1];
   const int h = p.items[3 * item + 2];
   const int hk = h / (p.H / p.Hkv);
-  int32_t seq_row, L;  // the sequence's first packed row and length
-  if (p.ext) {
-    const int4 e = reinterpret_cast<const int4*>(p.ext)[item];
-    seq_row = e.x;
-    L = e.y;
-  } else {
-    seq_row = p.cu[seq];
-    L = p.cu[seq + 1] - seq_row;
-  }
+  const int4 e = reinterpret_cast<const int4*>(p.ext)[item];
+  const int32_t seq_row = e.x, L = e.y;  // the sequence's first packed row and length
   const int64_t start = seq_row - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
   const int dofs = half * HALF;
@@ -445,10 +436,8 @@ struct TilesParams {
   const float* qkv;
   const uint16_t* img;   // [tile][Hkv][key image | value image]
   float* out;
-  const int32_t* cu;     // cu_seqlens
-  const int32_t* cut;    // first tile of each sequence
   const int32_t* items;  // triples (sequence, first row, kv head)
-  const int32_t* ext;    // null, or per item (sequence's first packed row, length, first tile, 0)
+  const int32_t* ext;    // per item (sequence's first packed row, length, first tile, 0)
   int32_t H, Hkv;
   int32_t window;
   float scale;
@@ -518,21 +507,11 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   const int lq = lane & 15, g = lane >> 4;
 
   const int item = blockIdx.x / p.kparts, part = blockIdx.x % p.kparts;
-  const int seq = p.items[3 * item];
   const int rb = p.items[3 * item + 1];
   const int hk = p.items[3 * item + 2];
   const int G = p.H / p.Hkv;
-  int32_t seq_row, L, seq_tile;  // the sequence's first packed row, length and first key tile
-  if (p.ext) {
-    const int4 e = reinterpret_cast<const int4*>(p.ext)[item];
-    seq_row = e.x;
-    L = e.y;
-    seq_tile = e.z;
-  } else {
-    seq_row = p.cu[seq];
-    L = p.cu[seq + 1] - seq_row;
-    seq_tile = p.cut[seq];
-  }
+  const int4 e = reinterpret_cast<const int4*>(p.ext)[item];
+  const int32_t seq_row = e.x, L = e.y, seq_tile = e.z;  // the sequence's first packed row, length and first key tile
   const int64_t start = seq_row - p.row0;  // the sequence's first row in qkv and out
   const int W = (p.H + 2 * p.Hkv) * HD;
   const int nrows = G * L;
@@ -1258,7 +1237,8 @@ int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const in
     return set_error(ctx, FA_ERR_ARG, "attention: %d key parts (1..%d, > 1 needs a partial buffer)", a.kparts,
                      kMaxKeyParts);
   VarlenParams p;
-  p.qkv = a.qkv; p.out = a.out; p.cu = a.cu_seqlens; p.items = d_items; p.ext = a.item_ext; p.row0 = a.row0;
+  if (!a.item_ext) return set_error(ctx, FA_ERR_ARG, "attention: no item extents");
+  p.qkv = a.qkv; p.out = a.out; p.items = d_items; p.ext = a.item_ext; p.row0 = a.row0;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale;
   p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
   const dim3 grid((unsigned)((int64_t)n_items * a.kparts));
@@ -1302,9 +1282,9 @@ int launch_attention_tiles(fa_ctx* ctx, const AttnTilesArgs& a, const int32_t* d
   if (a.kparts < 1 || a.kparts > kMaxKeyParts || (a.kparts > 1 && (!a.part || a.rows <= 0 || a.nrows <= 0)))
     return set_error(ctx, FA_ERR_ARG, "attention: %d key parts (1..%d, > 1 needs a partial buffer)", a.kparts,
                      kMaxKeyParts);
+  if (!a.item_ext) return set_error(ctx, FA_ERR_ARG, "attention: no item extents");
   TilesParams p;
-  p.qkv = a.qkv; p.img = a.img; p.out = a.out; p.cu = a.cu_seqlens; p.cut = a.cu_tiles; p.items = d_items;
-  p.ext = a.item_ext;
+  p.qkv = a.qkv; p.img = a.img; p.out = a.out; p.items = d_items; p.ext = a.item_ext;
   p.H = a.H; p.Hkv = a.Hkv; p.window = a.window; p.scale = a.scale; p.row0 = a.row0;
   p.kparts = a.kparts; p.rows = a.rows; p.part = a.part;
   p.gq = a.gq; p.cs = a.cos_t; p.sn = a.sin_t; p.eps = a.eps;

@@ -260,19 +260,18 @@ int launch_residual_norm(fa_ctx* ctx, const float* o, float* x, float* xn, int64
                          const float* o2 = nullptr, float scale = 1.f, int n2 = 1, int64_t pstride = 0);
 
 // Fused varlen attention over packed tokens. qkv [rows x (H+2Hkv)*D]; out
-// [rows x H*D]; cu_seqlens [nseq+1]; window: keys with |i-j| >= window are
-// masked (window <= 0: none).
+// [rows x H*D]; window: keys with |i-j| >= window are masked (window <= 0:
+// none).
 struct AttnVarlenArgs {
   const float* qkv;
   float* out;
-  const int32_t* cu_seqlens;
-  int32_t nseq, max_len, H, Hkv, D;
+  int32_t H, Hkv, D;
   int32_t window;
   float scale;
   int64_t row0 = 0;  // packed row held by qkv's and out's first row (items' sequences start at or after it)
-  // optional, per work item (16-byte aligned): the first packed row of the
+  // per work item (16-byte aligned, required): the first packed row of the
   // item's sequence, its length, its first key tile, 0; read beside the item
-  // instead of through cu_seqlens (one dependent load less before q and K/V)
+  // (no dependent load through a sequence table before q and K/V)
   const int32_t* item_ext = nullptr;
   // kparts > 1 (at most kMaxKeyParts): every item's keys are cut into kparts
   // runs, one workgroup each, summed by a second pass; part holds
@@ -287,7 +286,8 @@ inline int64_t attention_part_floats(int kparts, int64_t rows, int H, int D) {
   return (int64_t)kparts * rows * H * (D + 2);
 }
 // d_items holds n_items triples (sequence, first query, head): one work item
-// per query block of attention_varlen_qblock() queries and head.
+// per query block of attention_varlen_qblock() queries and head; a.item_ext
+// its n_items extents.
 int launch_attention_varlen_items(fa_ctx* ctx, const AttnVarlenArgs& a, const int32_t* d_items, int32_t n_items,
                                   hipStream_t s);
 // Queries per workgroup of the varlen kernel (the item granularity).
@@ -295,24 +295,20 @@ int attention_varlen_qblock();
 // head_dim 256, split-bf16 attention over key/value tile images: writes,
 // for tiles [t_lo, t_lo + tiles), the key image (keys normed, gained,
 // rotated) and value image of each (tile, kv head) into img
-// [tile][Hkv][2][3*32*256] bf16. Tile tt of sequence b (d_cu_tiles[b] <= tt
-// < d_cu_tiles[b+1], every sequence starting a tile) holds its tokens 32 (tt
-// - d_cu_tiles[b]) .. +31 (their positions, for RoPE); d_tile_seq[tt] = b.
-// qkv starts at packed row row0. d_tile_ext (optional, 16-byte aligned): per
-// tile (first packed row, keys, first key's position, 0), read in place of
-// the three tables (one dependent load less before the rows).
+// [tile][Hkv][2][3*32*256] bf16. Every sequence starts a tile; tile tt
+// holds up to 32 consecutive tokens of one sequence, described by
+// d_tile_ext[4 tt ..] (16-byte aligned): its first token's packed row, its
+// token count (1..32), its first token's position in the sequence (for
+// RoPE), 0. qkv starts at packed row row0.
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
-                    const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
-                    const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
-                    hipStream_t s, bool norm_v = false, const int32_t* d_tile_ext = nullptr);
+                    const float* cos_t, const float* sin_t, const int32_t* d_tile_ext, int32_t t_lo, int32_t tiles,
+                    uint16_t* img, hipStream_t s, bool norm_v = false);
 
 struct AttnTilesArgs {
   const float* qkv;       // raw q read here (rows of the launch start at packed row row0)
   const uint16_t* img;    // launch_kv_tiles's images
   float* out;
-  const int32_t* cu_seqlens;
-  const int32_t* cu_tiles;
-  const int32_t* item_ext = nullptr;  // as AttnVarlenArgs::item_ext
+  const int32_t* item_ext = nullptr;  // as AttnVarlenArgs::item_ext (required)
   int32_t H, Hkv;
   int32_t window;
   float scale;

@@ -877,12 +877,12 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   const int64_t n_items_t = ap.n_items_t, n_items = ap.n_items_t + ap.n_items_v, n_tiles = ap.n_tiles;
   const int hkv_t = ap.hkv_t, kparts_t = ap.kparts_t, kparts_v = ap.kparts_v, waves_t = ap.waves_t;
   const int tkeys = pin.tile_keys;
-  // plan buffer: cu_seqlens, items, first tile per sequence, tile ->
-  // sequence, then (16-byte aligned) each item's extent (its sequence's
-  // first packed row, length and first tile) and each key tile's (its first
-  // packed row, keys, first key's position), read by the attention and the
-  // key/value image kernels instead of through the sequence tables
-  const size_t ext_off = (2 * (size_t)(B + 1) + 3 * (size_t)n_items + (size_t)n_tiles + 3) & ~(size_t)3;
+  // plan buffer: cu_seqlens, items, first tile per sequence, then (16-byte
+  // aligned) each item's extent (its sequence's first packed row, length and
+  // first tile) and each key tile's (its first packed row, keys, first key's
+  // position), which the attention and the key/value image kernels read
+  // beside the item or tile (no dependent load through a sequence table)
+  const size_t ext_off = (2 * (size_t)(B + 1) + 3 * (size_t)n_items + 3) & ~(size_t)3;
   const size_t plan_ints = ext_off + 4 * (size_t)(n_items + n_tiles);
   if (m->plan_pending) {
     FA_HIP_CHECK(ctx, hipEventSynchronize(m->plan_done));  // previous upload has read the pinned buffer
@@ -898,13 +898,11 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   int32_t* cu_h = m->plan_host;
   int32_t* items_h = m->plan_host + (B + 1);
   int32_t* cut_h = items_h + 3 * n_items;
-  int32_t* tseq_h = cut_h + (B + 1);
   cu_h[0] = 0;
   cut_h[0] = 0;
   for (int b = 0; b < B; b++) {
     cu_h[b + 1] = cu_h[b] + lengths[b];
     cut_h[b + 1] = cut_h[b] + (ap.any_tiles ? (lengths[b] + tkeys - 1) / tkeys : 0);
-    for (int q = cut_h[b]; q < cut_h[b + 1]; q++) tseq_h[q] = b;
   }
   fa::plan_items(pin, ap, items_h, m->seq_order);
   {
@@ -932,8 +930,6 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
   if ((rc = m->plan_dev.ensure(ctx, plan_ints * 4 + (size_t)M * 8))) return rc;
   int32_t* cu_d = m->plan_dev.as<int32_t>();
   int32_t* items_d = cu_d + (B + 1);
-  int32_t* cut_d = items_d + 3 * n_items;
-  int32_t* tseq_d = cut_d + (B + 1);
   const int32_t* ext_d = cu_d + ext_off;  // [n_items][4], 16-byte aligned
   const int32_t* text_d = ext_d + 4 * n_items;  // [n_tiles][4]
   int32_t* row_src_d = cu_d + plan_ints;   // [M] b*T + t
@@ -1072,8 +1068,8 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       // the other half of its keys' values for the sum of squares)
       fa::Probe pr(m, FA_K_QKNORM_ROPE, 0,
                    (double)rows * (v2 ? 3 : 2) * Hkv * 4.0 * D + (double)ntl * Hkv * 2 * 3 * 32 * 256 * 2);
-      if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, L.cos_t, L.sin_t, cu_d, cut_d, tseq_d,
-                                    cut_h[b0], (int32_t)ntl, img, st, v2, text_d)))
+      if ((rc = fa::launch_kv_tiles(ctx, qkvr, r0, H, Hkv, L.g_k, eps, L.cos_t, L.sin_t, text_d, cut_h[b0],
+                                    (int32_t)ntl, img, st, v2)))
         return rc;
       pr.done();
     } else {
@@ -1087,7 +1083,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
     }
     {
       fa::AttnVarlenArgs a;
-      a.qkv = qkvr; a.out = attr; a.row0 = r0; a.cu_seqlens = cu_d; a.nseq = B; a.max_len = T;
+      a.qkv = qkvr; a.out = attr; a.row0 = r0;
       a.item_ext = ext_d + 4 * ((items_v - items_d) / 3);
       a.H = H; a.Hkv = Hkv; a.D = D; a.scale = att_scale;
       a.window = (sliding && c.sliding_window > 0) ? wbound : 0;
@@ -1109,7 +1105,7 @@ int forward(fa_model* m, const int32_t* d_ids, const int32_t* lengths, int32_t B
       fa::Probe pr(m, FA_K_ATTENTION, pairs * 4.0 * H * D, 0);
       if (tiles) {
         fa::AttnTilesArgs at;
-        at.qkv = qkvr; at.img = img; at.out = attr; at.row0 = r0; at.cu_seqlens = cu_d; at.cu_tiles = cut_d;
+        at.qkv = qkvr; at.img = img; at.out = attr; at.row0 = r0;
         at.item_ext = ext_d + 4 * ((items_t - items_d) / 3);
         at.H = H; at.Hkv = Hkv; at.window = a.window; at.scale = a.scale;
         at.gq = L.g_q; at.eps = eps; at.cos_t = L.cos_t; at.sin_t = L.sin_t; at.waves = waves_t;

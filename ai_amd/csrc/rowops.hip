@@ -310,8 +310,7 @@ struct KvTilesParams {
   const float* gk;
   float eps;
   const float *cs, *sn;
-  const int32_t *cu, *cut, *tile_seq;
-  const int32_t* tile_ext;  // null, or per tile (first packed row, keys, first key's position, 0)
+  const int32_t* tile_ext;  // per tile (first packed row, keys, first key's position, 0)
   int t_lo, tiles;
   uint16_t* img;
   int norm_v;  // values RMS-normed with unit gain first (EmbeddingGemma 2, gemma2.go)
@@ -329,17 +328,10 @@ constexpr int kVtStride = 132;
 // and written as zeros.
 // The tile's first qkv row, its first key's position and its key count.
 __device__ __forceinline__ void tile_extent(const KvTilesParams& a, int tile, int64_t& r_first, int& t0, int& n) {
-  if (a.tile_ext) {
-    const int4 e = reinterpret_cast<const int4*>(a.tile_ext)[tile];
-    r_first = e.x - a.row0;
-    n = e.y;
-    t0 = e.z;
-  } else {
-    const int sq = a.tile_seq[tile];
-    t0 = 32 * (tile - a.cut[sq]);
-    n = min(32, a.cu[sq + 1] - a.cu[sq] - t0);
-    r_first = a.cu[sq] - a.row0 + t0;
-  }
+  const int4 e = reinterpret_cast<const int4*>(a.tile_ext)[tile];
+  r_first = e.x - a.row0;
+  n = e.y;
+  t0 = e.z;
 }
 
 __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int half_, int wave, int lane) {
@@ -674,15 +666,14 @@ int launch_l2norm(fa_ctx* ctx, const float* y, int32_t nseq, int32_t width, int3
 }
 
 int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int32_t Hkv, const float* gk, float eps,
-                    const float* cos_t, const float* sin_t, const int32_t* d_cu_seqlens,
-                    const int32_t* d_cu_tiles, const int32_t* d_tile_seq, int32_t t_lo, int32_t tiles, uint16_t* img,
-                    hipStream_t s, bool norm_v, const int32_t* d_tile_ext) {
+                    const float* cos_t, const float* sin_t, const int32_t* d_tile_ext, int32_t t_lo, int32_t tiles,
+                    uint16_t* img, hipStream_t s, bool norm_v) {
   if (tiles == 0) return FA_OK;
+  if (!d_tile_ext) return set_error(ctx, FA_ERR_ARG, "key/value tiles: no tile extents");
   KvTilesParams a;
   a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.cs = cos_t; a.sn = sin_t;
-  a.cu = d_cu_seqlens; a.cut = d_cu_tiles; a.tile_seq = d_tile_seq; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
+  a.tile_ext = d_tile_ext; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
   a.norm_v = norm_v ? 1 : 0;
-  a.tile_ext = d_tile_ext;
   hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
