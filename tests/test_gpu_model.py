@@ -360,6 +360,23 @@ def test_random_batches_across_plan_rules(models, seed):
     compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens), f"random batch {seed}")
 
 
+@pytest.mark.parametrize("lengths", [[128], [64], [1], [40, 17, 3], [100, 60], [7] * 20])
+def test_few_row_fused_qk_norm(models, lengths):
+    """Few-row batches (up to 160 tokens on one stream): the q|k|v product
+    in two K parts (the second in the o product's planes), added by the q/k
+    norm pass, the o and down products in four K parts, the fp32 attention's
+    key runs. Every row against the oracle, and the hidden states after
+    layers 1, 12 and 24 of the first and last sequences."""
+    gm, om = models
+    rng = np.random.default_rng(9000 + sum(lengths))
+    lens = np.array(lengths, np.int32)
+    ids = rng.integers(3, 262144, (len(lens), int(lens.max()))).astype(np.int32)
+    ids[:, 0] = 2
+    ids[np.arange(ids.shape[1])[None, :] >= lens[:, None]] = 0
+    compare(gm.embed_ids(ids, lens), oracle_embed(om, ids, lens), f"few rows {lengths}")
+    compare_states(gm, om, ids, lens, sorted({0, len(lens) - 1}), f"few rows {lengths} states", layers=[1, 12, -1])
+
+
 @pytest.mark.parametrize("lengths", [[1], [1] * 5, [1, 2048, 1, 33]])
 def test_one_token_sequences(models, lengths):
     """Sequences of a single token (only the BOS id): alone, five in a batch
