@@ -570,7 +570,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     // of a sequence): the wave issues its share of each image load and
     // takes part in every barrier of the loop below, in the same order,
     // and computes nothing
-    if constexpr (DS == 2) dl_barrier<0xC07F>();  // the q halves' exchange below
+    if constexpr (DS == 2) dl_barrier<0xC07F>();  // the pairs' q row exchange below
     if (tb < te) {
       for (int tt = tb; tt < te; tt++) {
         dl_barrier<0x0F70>();
@@ -585,7 +585,78 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   }
 
   bf16x8 qt[3][NC];
-  {
+  if constexpr (DS == 2) {
+    // Wave pairs: each wave norms (RMSNorm, gain) and rotates (RoPE at the
+    // token's position) 8 of the pair's 16 rows, all 256 dims: lane l takes
+    // row 8 hf + l / 8 and dims 16 (l mod 8) .. + 15 and the same + 128
+    // (RoPE's pairs in the lane; the row's sum of squares over its eight
+    // lanes), and stores them in LDS (the value buffers, free until the
+    // first tile's value loads; 16 KB per pair, 16-byte chunk k of row r at
+    // position k ^ (r mod 16)); after the barrier each wave reads its dim
+    // half of all 16 rows. Each wave norms and rotates 8 rows, not 16.
+    const int rho = 8 * hf + (lane >> 3), s8 = lane & 7;
+    const int row2 = rb + 16 * rbw + rho;
+    const bool valid2 = row2 < nrows;
+    const int tok2 = (valid2 ? row2 : rb) / G;
+    const int head2 = hk * G + (valid2 ? row2 : rb) % G;
+    const float* qr = p.qkv + (start + tok2) * W + (int64_t)head2 * HD + 16 * s8;
+    f32x4 lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      lo[j] = *reinterpret_cast<const f32x4*>(qr + 4 * j);
+      hi[j] = *reinterpret_cast<const f32x4*>(qr + HD / 2 + 4 * j);
+    }
+    const float* gr = p.gq + 16 * s8;
+    const float* cr = p.cs + (int64_t)tok2 * (HD / 2) + 16 * s8;
+    const float* sr = p.sn + (int64_t)tok2 * (HD / 2) + 16 * s8;
+    f32x4 ga[4], gb[4], co[4], si[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      ga[j] = *reinterpret_cast<const f32x4*>(gr + 4 * j);
+      gb[j] = *reinterpret_cast<const f32x4*>(gr + HD / 2 + 4 * j);
+      co[j] = *reinterpret_cast<const f32x4*>(cr + 4 * j);
+      si[j] = *reinterpret_cast<const f32x4*>(sr + 4 * j);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) ss = fmaf(lo[j][e], lo[j][e], ss);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) ss = fmaf(hi[j][e], hi[j][e], ss);
+    // the row's eight lanes: xor 1 and 2 within the quad, then the other
+    // quad through the half-row mirror (each sum commutes exactly, so every
+    // lane of the row gets the same bits)
+    ss = ss + dpp_f32<0xB1>(ss);   // quad_perm [1, 0, 3, 2]
+    ss = ss + dpp_f32<0x4E>(ss);   // quad_perm [2, 3, 0, 1]
+    ss = ss + dpp_f32<0x141>(ss);  // row_half_mirror
+    const float inv = rms_inv(ss, HD, p.eps);
+    f32x4* qs = reinterpret_cast<f32x4*>((rbw < 3 ? Vs0 : Vs1) + (rbw % 3) * 8192);  // the pair's 16 rows
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      f32x4 yl, yh;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float a = lo[j][e] * inv * ga[j][e], b = hi[j][e] * inv * gb[j][e];
+        yl[e] = a * co[j][e] - b * si[j][e];  // y_i = x_i c - x_{i+h} s
+        yh[e] = a * si[j][e] + b * co[j][e];  // y_{i+h} = x_i s + x_{i+h} c
+      }
+      const int k = 4 * s8 + j;  // the 16-byte chunk of dims 16 s8 + 4 j
+      qs[rho * 64 + (k ^ (rho & 15))] = yl;
+      qs[rho * 64 + ((k + 32) ^ (rho & 15))] = yh;
+    }
+    dl_barrier<0xC07F>();  // lgkmcnt(0): the pair's rows written; the first key image stays in flight
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      // the wave's dim half (chunks NC * hf ..): dims 32 (NC hf + c) + 8 g ..
+      const int k = 8 * (NC * hf + c) + 2 * g;
+      f32x4 x0 = qs[lq * 64 + (k ^ lq)], x1 = qs[lq * 64 + ((k + 1) ^ lq)];
+      if (!qvalid) x0 = x1 = f32x4{0.f, 0.f, 0.f, 0.f};
+      split_pack8(x0, x1, qt[0][c], qt[1][c], qt[2][c]);
+    }
+  } else {
     // q normed (RMSNorm, gain) and rotated (RoPE at the token's position)
     // as it is loaded: the row's dims are spread over the four lanes with
     // this lq (sum of squares: two exchanges), and dims i and i + 128 sit in
@@ -593,52 +664,10 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     const float* qr = p.qkv + (start + tok) * W + (int64_t)head * HD + 8 * g;
     f32x4 x[HD / 32][2];
     float ss = 0.f;
-    if constexpr (DS == 2) {
-      // Wave pairs: each wave loads its own half of the rows' dims (chunks
-      // NC * hf ..) and the halves swap through LDS (the value buffers, free
-      // until the first tile's value loads, which follow that tile's first
-      // barrier): half the q bytes from memory at the launch's start, where
-      // every workgroup loads its q rows at once. Same values, same sums.
-      f32x4* xs = reinterpret_cast<f32x4*>((wave < 6 ? Vs0 : Vs1) + (wave % 6) * 4096);  // 8 KB per wave
-      const int pw = wave ^ RB;
-      const f32x4* xp = reinterpret_cast<const f32x4*>((pw < 6 ? Vs0 : Vs1) + (pw % 6) * 4096);
-      if (hf == 0) {
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
-          x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
-          x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
-          xs[(2 * c) * 64 + lane] = x[c][0];
-          xs[(2 * c + 1) * 64 + lane] = x[c][1];
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-          x[NC + c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * (NC + c));
-          x[NC + c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * (NC + c) + 4);
-          xs[(2 * c) * 64 + lane] = x[NC + c][0];
-          xs[(2 * c + 1) * 64 + lane] = x[NC + c][1];
-        }
-      }
-      dl_barrier<0xC07F>();  // lgkmcnt(0): every half written; the first key image stays in flight
-      if (hf == 0) {
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-          x[NC + c][0] = xp[(2 * c) * 64 + lane];
-          x[NC + c][1] = xp[(2 * c + 1) * 64 + lane];
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-          x[c][0] = xp[(2 * c) * 64 + lane];
-          x[c][1] = xp[(2 * c + 1) * 64 + lane];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < HD / 32; c++) {
-        x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
-        x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
-      }
+    for (int c = 0; c < HD / 32; c++) {
+      x[c][0] = *reinterpret_cast<const f32x4*>(qr + 32 * c);
+      x[c][1] = *reinterpret_cast<const f32x4*>(qr + 32 * c + 4);
     }
 #pragma unroll
     for (int c = 0; c < HD / 32; c++)
@@ -669,14 +698,7 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
     }
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-      // the wave's dim half (chunks NC * hf ..)
       f32x4 x0 = x[c][0], x1 = x[c][1];
-      if constexpr (DS == 2) {
-        if (hf) {
-          x0 = x[NC + c][0];
-          x1 = x[NC + c][1];
-        }
-      }
       if (!qvalid) x0 = x1 = f32x4{0.f, 0.f, 0.f, 0.f};
       split_pack8(x0, x1, qt[0][c], qt[1][c], qt[2][c]);
     }
