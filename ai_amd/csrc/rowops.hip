@@ -322,10 +322,10 @@ constexpr int kTileImg = 3 * 32 * 256;  // bf16 per key or value image
 // 16c + dim mod 64, all distinct, since 4 * 132 = 16 (mod 64)
 constexpr int kVtStride = 132;
 
-// Keys 16*half .. 16*half + 15 of the key image of (tile, hk): wave w takes
-// keys 16*half + w, + 4, ..., 4 dims per lane; rows past the sequence are
-// clamped to its last token (every load issued up front, none conditional)
-// and written as zeros.
+// Keys 4 KPW part .. + 4 KPW - 1 of the key image of (tile, hk): wave w
+// takes keys 4 KPW part + w, + 4, ... (KPW of them), 4 dims per lane; rows
+// past the sequence are clamped to its last token (every load issued up
+// front, none conditional) and written as zeros.
 // The tile's first qkv row, its first key's position and its key count.
 __device__ __forceinline__ void tile_extent(const KvTilesParams& a, int tile, int64_t& r_first, int& t0, int& n) {
   const int4 e = reinterpret_cast<const int4*>(a.tile_ext)[tile];
@@ -334,8 +334,10 @@ __device__ __forceinline__ void tile_extent(const KvTilesParams& a, int tile, in
   t0 = e.z;
 }
 
-__device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int half_, int wave, int lane) {
+template <int KPW>
+__device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int hk, int part, int wave, int lane) {
   constexpr int D = 256, half = D / 2;
+  const int kb = 4 * KPW * part;
   int64_t r_first;  // qkv row of the tile's first token
   int t0, n;
   tile_extent(a, tile, r_first, t0, n);
@@ -343,18 +345,18 @@ __device__ __forceinline__ void key_tile(const KvTilesParams& a, int tile, int h
   uint16_t* kimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg);
   const f32x4 gg = *reinterpret_cast<const f32x4*>(a.gk + lane * 4);
   const int i0 = (lane & 31) * 4;
-  f32x4 v[4], c[4], sv[4];
+  f32x4 v[KPW], c[KPW], sv[KPW];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int64_t row = r_first + min(16 * half_ + wave + 4 * j, n - 1);
+  for (int j = 0; j < KPW; j++) {
+    const int64_t row = r_first + min(kb + wave + 4 * j, n - 1);
     v[j] = *reinterpret_cast<const f32x4*>(a.qkv + row * width + (int64_t)(a.H + hk) * D + lane * 4);
-    const int t = t0 + min(16 * half_ + wave + 4 * j, n - 1);  // the key's position in its sequence
+    const int t = t0 + min(kb + wave + 4 * j, n - 1);  // the key's position in its sequence
     c[j] = *reinterpret_cast<const f32x4*>(a.cs + (int64_t)t * half + i0);
     sv[j] = *reinterpret_cast<const f32x4*>(a.sn + (int64_t)t * half + i0);
   }
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int k = 16 * half_ + wave + 4 * j;
+  for (int j = 0; j < KPW; j++) {
+    const int k = kb + wave + 4 * j;
     f32x4 x[1] = {v[j]};
     const float inv = rms_inv(sumsq<1>(x), D, a.eps);
     x[0].x = x[0].x * inv * gg.x; x[0].y = x[0].y * inv * gg.y;
@@ -452,20 +454,77 @@ __device__ __forceinline__ void value_tile(const KvTilesParams& a, int tile, int
   }
 }
 
-// Blocks 4i + j of (tile t_lo + i / Hkv, kv head i % Hkv): j = 0, 1 the
-// key image's two halves of 16 keys, j = 2, 3 the value image's two halves
-// of 128 dims (half-tile blocks: twice the blocks of whole-image ones, so
-// more of a launch's loads are in flight).
+// Dims 64 q .. 64 q + 63 of the value image of (tile, hk) (values not
+// normed): lane l loads dims 2 (l mod 32), + 1 of keys w + 4 (2 j + l / 32)
+// into LDS, then each thread transposes, splits and stores one 16-byte
+// chunk (8 slots of one dim and term), as value_tile does for 128 dims.
+__device__ __forceinline__ void value_quarter(const KvTilesParams& a, int tile, int hk, int q, int wave, int lane,
+                                              float (*Vt)[kVtStride]) {
+  constexpr int D = 256;
+  int64_t r_first;
+  int t0, n;
+  tile_extent(a, tile, r_first, t0, n);
+  const int width = (a.H + 2 * a.Hkv) * D;
+  uint16_t* vimg = a.img + ((int64_t)tile * a.Hkv + hk) * (2 * kTileImg) + kTileImg;
+  const float* vsrc = a.qkv + (int64_t)(a.H + a.Hkv + hk) * D + 64 * q + (lane & 31) * 2;
+  float2 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int64_t row = r_first + min(wave + 4 * (2 * j + (lane >> 5)), n - 1);
+    v[j] = *reinterpret_cast<const float2*>(vsrc + row * width);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int k = wave + 4 * (2 * j + (lane >> 5));
+    *reinterpret_cast<float2*>(&Vt[k][(lane & 31) * 2]) = k < n ? v[j] : make_float2(0.f, 0.f);
+  }
+  __syncthreads();
+  const int u = wave * 64 + lane;
+  const int dl = u >> 2, c = u & 3;  // local dim, chunk of 8 slots: keys 4c .. 4c+3, 16 + 4c .. 16 + 4c+3
+  const int d = 64 * q + dl;
+  uint32_t th[8], tm[8], tl[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const Split3 sp = split3(Vt[(e >> 2) * 16 + 4 * c + (e & 3)][dl]);
+    th[e] = sp.h;
+    tm[e] = sp.m;
+    tl[e] = sp.l;
+  }
+  uint16_t* o = vimg + d * 32 + ((c ^ ((d >> 1) & 3)) * 8);
+  *reinterpret_cast<uint4*>(o) = make_uint4(pack_hi16(th[0], th[1]), pack_hi16(th[2], th[3]),
+                                            pack_hi16(th[4], th[5]), pack_hi16(th[6], th[7]));
+  *reinterpret_cast<uint4*>(o + 32 * D) = make_uint4(pack_hi16(tm[0], tm[1]), pack_hi16(tm[2], tm[3]),
+                                                     pack_hi16(tm[4], tm[5]), pack_hi16(tm[6], tm[7]));
+  *reinterpret_cast<uint4*>(o + 64 * D) = make_uint4(pack_hi16(tl[0], tl[1]), pack_hi16(tl[2], tl[3]),
+                                                     pack_hi16(tl[4], tl[5]), pack_hi16(tl[6], tl[7]));
+}
+
+// QUARTERS (values not normed): blocks 8i + j of (tile t_lo + i / Hkv, kv
+// head i % Hkv), j = 0..3 the key image's quarters of 8 keys, 4..7 the
+// value image's quarters of 64 dims. Else (values RMS-normed, each block
+// needing all of a key's dims) blocks 4i + j, j = 0, 1 the key image's
+// halves of 16 keys, 2, 3 the value image's halves of 128 dims. Smaller
+// blocks: more of a launch's loads in flight, a shorter serial chain per
+// block.
+template <bool QUARTERS>
 __global__ __launch_bounds__(256) void kv_tiles_kernel(KvTilesParams a) {
   __shared__ __attribute__((aligned(16))) float Vt[32][kVtStride];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t b = blockIdx.x;
-  const int tile = a.t_lo + (int)(b / (4 * a.Hkv)), hk = (int)((b >> 2) % a.Hkv);
-  const int part = (int)(b & 3);
-  if (part >= 2)
-    value_tile(a, tile, hk, part - 2, wave, lane, Vt);
-  else
-    key_tile(a, tile, hk, part, wave, lane);
+  constexpr int P = QUARTERS ? 8 : 4;  // blocks per (tile, kv head)
+  const int tile = a.t_lo + (int)(b / (P * a.Hkv)), hk = (int)((b / P) % a.Hkv);
+  const int part = (int)(b % P);
+  if constexpr (QUARTERS) {
+    if (part >= 4)
+      value_quarter(a, tile, hk, part - 4, wave, lane, Vt);
+    else
+      key_tile<2>(a, tile, hk, part, wave, lane);
+  } else {
+    if (part >= 2)
+      value_tile(a, tile, hk, part - 2, wave, lane, Vt);
+    else
+      key_tile<4>(a, tile, hk, part, wave, lane);
+  }
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, int64_t n) {
@@ -674,7 +733,10 @@ int launch_kv_tiles(fa_ctx* ctx, const float* qkv, int64_t row0, int32_t H, int3
   a.qkv = qkv; a.row0 = row0; a.H = H; a.Hkv = Hkv; a.gk = gk; a.eps = eps; a.cs = cos_t; a.sn = sin_t;
   a.tile_ext = d_tile_ext; a.t_lo = t_lo; a.tiles = tiles; a.img = img;
   a.norm_v = norm_v ? 1 : 0;
-  hipLaunchKernelGGL(kv_tiles_kernel, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
+  if (norm_v)
+    hipLaunchKernelGGL(kv_tiles_kernel<false>, dim3((unsigned)(4 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(kv_tiles_kernel<true>, dim3((unsigned)(8 * (int64_t)tiles * Hkv)), dim3(256), 0, s, a);
   FA_CHECK_LAUNCH(ctx);
   return FA_OK;
 }
