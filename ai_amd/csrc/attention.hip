@@ -503,7 +503,8 @@ __global__ __launch_bounds__(64 * TL_W, TL_W == 8 ? 2 : 1) void attention_tiles_
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rbw = wave % RB, hf = wave / RB;  // the wave's row block and dim half
+  // the wave's row block and dim half (single waves: the whole head)
+  const int rbw = wave % RB, hf = DS == 2 ? wave / RB : 0;
   const int lq = lane & 15, g = lane >> 4;
 
   const int item = blockIdx.x / p.kparts, part = blockIdx.x % p.kparts;
