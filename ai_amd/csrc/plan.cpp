@@ -63,23 +63,34 @@ void plan_attention(const AttnPlanIn& in, AttnPlan& p) {
   // 160 (192) 6.34 vs 6.49; EmbeddingGemma 2 at C2 (202) 4.15 vs 4.17; C3,
   // C4, C5 (from 271 items) 4-9 % slower with four. Below half a round the
   // key runs spread the work instead.
-  // On one stream with at most half a round of 128-row items (the key runs'
-  // regime), 64-row items on eight waves in head-dimension pairs win while
-  // the sequences stay under 1 536 tokens (MI355X, per forward: 1 025
+  // On one stream with at most half a round of 128-row items (the key
+  // runs' regime), 64-row items on eight waves in head-dimension pairs win
+  // while the sequences stay under 1 536 tokens (MI355X, per forward: 1 025
   // tokens -5.6 %, one 1 100-token sequence -4.3 %, 8 x 160 -8.5 %, 5 x 300
   // -7.4 %, 3 x 512 -2.9 %, 3 x 600 -1.2 %, 6 x 200 + 100 -10 %): twice
   // the items fill more CUs, each with two waves per SIMD. One 2 048-token
   // sequence loses 2 % (its items' key runs halve: 2 of 32 tiles instead of
-  // 5 of 13), so it keeps 128-row items.
+  // 5 of 13), so it keeps 128-row items. Between half a round and 0.6 of
+  // a round, pairs only for ragged batches (the longest sequence at least
+  // 1.25x the mean): one round of 128-row items takes as long as its
+  // longest item, which the pairs halve while the short items fill their
+  // partial second round (the C2 batch, 143 items, on one stream: 5.605 ->
+  // 5.519 ms per forward, attention 1.13 -> 1.03 ms); with equal lengths
+  // that second round is only added time (36 x 160: 5.39 -> 5.67, 43 x
+  // 128: 5.21 -> 5.45 ms). From two rounds (C3, C5) the 128-row items stay
+  // 20-30 % faster.
   if (p.any_tiles) {
-    int64_t n8 = 0;
+    int64_t n8 = 0, sum_len = 0;
     int max_len = 0;
     for (int b = 0; b < in.B; b++) {
       n8 += ((int64_t)p.Gt * in.lengths[b] + 127) / 128 * p.hkv_t;
       max_len = std::max(max_len, (int)in.lengths[b]);
+      sum_len += in.lengths[b];
     }
+    const bool ragged = 4LL * max_len * in.B >= 5 * sum_len;
     if (in.groups > 1 && 2 * n8 > in.cus && 5 * n8 <= 3LL * in.cus) p.waves_t = 4;
-    if (in.groups == 1 && 2 * n8 <= in.cus && max_len < 1536) p.waves_t = 4;
+    if (in.groups == 1 && max_len < 1536 && (2 * n8 <= in.cus || (ragged && 5 * n8 <= 3LL * in.cus)))
+      p.waves_t = 4;
     if (in.forced_rows) p.waves_t = in.forced_rows / 16;
   }
   const int istep_t = 16 * p.waves_t;

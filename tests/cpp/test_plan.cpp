@@ -226,12 +226,23 @@ TEST(TestTileWaves) {
     if (c.p.n_tiles != (int64_t)tc.n * ((tc.len + 31) / 32)) FATAL("key tiles %lld", (long long)c.p.n_tiles);
     check_items(c);
   }
-  // the same batch on one stream (no micro-batches): eight waves
+  // the same batch on one stream (no micro-batches): eight waves (equal
+  // lengths: the pairs' second round would only add time)
   Case c;
   c.lengths = repeat(36, 160);
   run(c, eg300m(), 1);
   if (c.p.waves_t != 8 || c.p.n_items_t != 36 * 4) FATAL("one stream: %d waves, %lld items", c.p.waves_t, (long long)c.p.n_items_t);
   check_items(c);
+  // a ragged batch at the same fill on one stream (longest 1.25x the mean
+  // or more): pairs. 20 x 100 + 14 x 220 tokens: 20 x 3 + 14 x 6 = 144
+  // items of 128 rows (0.56 of a round), mean 149, longest 220
+  Case r;
+  r.lengths = repeat(20, 100);
+  for (int i = 0; i < 14; i++) r.lengths.push_back(220);
+  run(r, eg300m(), 1);
+  if (r.p.waves_t != 4 || r.p.n_items_t != 20 * 5 + 14 * 11)
+    FATAL("ragged one stream: %d waves, %lld items", r.p.waves_t, (long long)r.p.n_items_t);
+  check_items(r);
 }
 
 // one stream, at most half a round of 128-row items, sequences under 1 536

@@ -129,6 +129,22 @@ def test_c2_all_rows(models):
     compare(gm.embed_ids(b.ids, b.lengths), oracle_embed(om, b.ids, b.lengths), "C2 all")
 
 
+def test_c2_one_stream_profiling_pass(models):
+    """With profiling on (fa_gemma_set_profiling) the forward runs on one
+    stream with full-batch launches: at C2 the tile attention's 143 items of
+    128 rows fill 0.56 of a round and the batch is ragged, so the plan takes
+    64-row items on head-dimension wave pairs. Every row against the
+    oracle, then the default (micro-batched) forward again."""
+    gm, om = models
+    b = S.make_batch("C2")
+    gm.set_profiling(True)
+    try:
+        got = gm.embed_ids(b.ids, b.lengths)
+    finally:
+        gm.set_profiling(False)
+    compare(got, oracle_embed(om, b.ids, b.lengths), "C2 one stream (profiling)")
+
+
 def test_c2_layer_states(models):
     """Hidden states after every layer at C2, for sequences of the first,
     middle and last micro-batch groups."""
